@@ -1,0 +1,401 @@
+"""Loads ``libdimq_hip.so`` (the gfx950 C-ABI library) and registers the ops.
+
+Importing this module is what ``ops.is_available()`` tests, exactly as the
+reference's ``dimq_backend/ops.py:12-18`` tests ``import dimq_backend._C``.
+The import fails loudly (OSError / RuntimeError) when the library is missing;
+nothing here falls back to a CPU implementation.
+
+Ops registered in the ``dimq`` namespace on the CUDA dispatch key (HIP tensors
+use it in ROCm PyTorch):
+
+* the reference's six schemas, verbatim (``dimq_cuda_backend/csrc/dimq_ops.cpp:38-43``);
+* generalised ops for b in {2,3,4,8}, per-channel codebooks and weight-only
+  GEMM/conv (``pack_bits``, ``unpack_bits``, ``hard_quantize``,
+  ``build_product_table_grouped``, ``linear_codebook``, ``conv2d_codebook``).
+
+Each op validates its tensors in Python (same messages as the reference's
+TORCH_CHECKs), allocates the output with ``torch.empty`` and passes raw device
+pointers plus the current HIP stream to the ``extern "C"`` entry point.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch  # must be imported first: the HIP runtime comes from torch's libamdhip64
+
+_LIB_PATH = Path(__file__).resolve().parent / "libdimq_hip.so"
+
+if not _LIB_PATH.exists():
+    raise ImportError(
+        f"{_LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+        "or `make -C dimq_amd/csrc`"
+    )
+
+lib = ctypes.CDLL(str(_LIB_PATH))
+
+F32, F16, BF16, F64, U8 = 0, 1, 2, 3, 4
+NCHW, NHWC = 0, 1
+VARIANT_AUTO, VARIANT_SMALL_M, VARIANT_MFMA = 0, 1, 2
+
+_DT = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.float64: F64, torch.uint8: U8}
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_dbl = ctypes.c_double
+
+_SIGS = {
+    "dimq_last_error": (ctypes.c_char_p, []),
+    "dimq_abi_version": (_int, []),
+    "dimq_pack_u4": (_int, [_vp, _i64, _vp, _vp]),
+    "dimq_unpack_u4": (_int, [_vp, _i64, _i64, _vp, _vp]),
+    "dimq_quantize_activation_u4": (_int, [_vp, _int, _i64, _dbl, _i64, _vp, _vp]),
+    "dimq_build_product_table": (_int, [_vp, _int, _i64, _dbl, _i64, _vp, _vp]),
+    "dimq_linear_lut": (_int, [_vp, _int, _i64, _vp, _i64, _vp, _int, _i64, _dbl, _i64, _vp, _int, _i64, _i64, _i64,
+                               _vp, _vp]),
+    "dimq_conv2d_lut": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _int, _i64, _dbl, _i64, _vp, _int,
+                               _i64] + [_i64] * 11 + [_vp, _vp]),
+    "dimq_pack_bits": (_int, [_vp, _i64, _int, _vp, _vp]),
+    "dimq_unpack_bits": (_int, [_vp, _i64, _i64, _int, _vp, _vp]),
+    "dimq_hard_quantize": (_int, [_vp, _int, _i64, _i64, _vp, _i64, _int, _vp, _vp, _vp]),
+    "dimq_build_product_table_grouped": (_int, [_vp, _int, _i64, _i64, _dbl, _i64, _vp, _vp]),
+    "dimq_linear_codebook": (_int, [_vp, _int, _i64, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _vp, _int, _i64,
+                                    _vp, _int, _int, _vp]),
+    "dimq_conv2d_codebook": (_int, [_vp, _int, _int, _i64, _i64, _i64, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64,
+                                    _vp, _int] + [_i64] * 10 + [_vp, _int, _int, _int, _vp]),
+}
+
+for _name, (_res, _args) in _SIGS.items():
+    _fn = getattr(lib, _name)  # AttributeError here = the library lacks a declared entry point
+    _fn.restype = _res
+    _fn.argtypes = _args
+
+
+def exported_symbols() -> list[str]:
+    return sorted(_SIGS)
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        msg = lib.dimq_last_error().decode(errors="replace")
+        raise RuntimeError(msg)
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _dtype(t: torch.Tensor) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise RuntimeError(f"unsupported dtype {t.dtype}") from None
+
+
+def _require_cuda(t: torch.Tensor, msg: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(msg)
+
+
+# ---------------------------------------------------------------------------
+# reference ops (csrc/dimq_pack.cu, dimq_product_table.cu, dimq_gemm_lut.cu, dimq_conv2d_lut.cu)
+# ---------------------------------------------------------------------------
+
+def pack_u4_impl(indices: torch.Tensor) -> torch.Tensor:
+    _require_cuda(indices, "pack_u4 expects a CUDA tensor")
+    if indices.dtype != torch.uint8:
+        raise RuntimeError("pack_u4 expects uint8 indices")
+    flat = indices.contiguous().view(-1)
+    out = torch.empty(((flat.numel() + 1) // 2,), dtype=torch.uint8, device=flat.device)
+    with torch.cuda.device(flat.device):
+        _check(lib.dimq_pack_u4(_ptr(flat), flat.numel(), _ptr(out), _stream(flat.device)))
+    return out
+
+
+def unpack_u4_impl(packed: torch.Tensor, numel: int) -> torch.Tensor:
+    _require_cuda(packed, "unpack_u4 expects a CUDA tensor")
+    if packed.dtype != torch.uint8:
+        raise RuntimeError("unpack_u4 expects uint8 packed data")
+    if numel < 0:
+        raise RuntimeError("numel must be non-negative")
+    if packed.numel() < (numel + 1) // 2:
+        raise RuntimeError("packed tensor is too small for requested numel")
+    flat = packed.contiguous().view(-1)
+    out = torch.empty((numel,), dtype=torch.uint8, device=flat.device)
+    with torch.cuda.device(flat.device):
+        _check(lib.dimq_unpack_u4(_ptr(flat), flat.numel(), numel, _ptr(out), _stream(flat.device)))
+    return out
+
+
+def quantize_activation_u4_impl(x: torch.Tensor, act_scale: float, act_zp: int) -> torch.Tensor:
+    _require_cuda(x, "quantize_activation_u4 expects a CUDA tensor")
+    if not x.is_floating_point():
+        raise RuntimeError("quantize_activation_u4 expects floating input")
+    xc = x.contiguous()
+    out = torch.empty(xc.shape, dtype=torch.uint8, device=xc.device)
+    with torch.cuda.device(xc.device):
+        _check(lib.dimq_quantize_activation_u4(_ptr(xc), _dtype(xc), xc.numel(), float(act_scale), int(act_zp),
+                                               _ptr(out), _stream(xc.device)))
+    return out
+
+
+def build_product_table_impl(codebook: torch.Tensor, act_scale: float, act_zp: int) -> torch.Tensor:
+    _require_cuda(codebook, "build_product_table expects a CUDA tensor")
+    if not codebook.is_floating_point():
+        raise RuntimeError("build_product_table expects floating codebook")
+    cb = codebook.contiguous().view(-1)
+    table = torch.empty((16, 16), dtype=torch.float32, device=cb.device)
+    with torch.cuda.device(cb.device):
+        _check(lib.dimq_build_product_table(_ptr(cb), _dtype(cb), cb.numel(), float(act_scale), int(act_zp),
+                                            _ptr(table), _stream(cb.device)))
+    return table
+
+
+def _bias_args(bias: torch.Tensor | None, n: int, what: str):
+    if bias is None:
+        return None, None, F32, 0
+    _require_cuda(bias, "bias must be CUDA when provided")
+    if bias.numel() != n:
+        raise RuntimeError(f"bias numel must equal {what}")
+    b = bias.contiguous()
+    return b, _ptr(b), _dtype(b), b.numel()
+
+
+def linear_lut_impl(x, packed_w, codebook, act_scale, act_zp, bias, out_features, in_features):
+    _require_cuda(x, "linear_lut expects CUDA input")
+    _require_cuda(packed_w, "linear_lut expects CUDA packed_weight")
+    _require_cuda(codebook, "linear_lut expects CUDA codebook")
+    if not x.is_floating_point():
+        raise RuntimeError("linear_lut expects floating input")
+    if packed_w.dtype != torch.uint8:
+        raise RuntimeError("packed_weight must be uint8")
+    if not codebook.is_floating_point():
+        raise RuntimeError("codebook must be floating point")
+    if codebook.numel() != 16:
+        raise RuntimeError("codebook must have 16 entries for W4")
+    if out_features <= 0 or in_features <= 0:
+        raise RuntimeError("linear dimensions must be positive")
+    if x.numel() % in_features != 0:
+        raise RuntimeError("input numel must be divisible by in_features")
+    if x.dim() == 0 or x.size(-1) != in_features:
+        raise RuntimeError("input last dimension must equal in_features")
+    xc = x.contiguous()
+    pw = packed_w.contiguous().view(-1)
+    cb = codebook.contiguous().view(-1)
+    b, bp, bdt, bn = _bias_args(bias, out_features, "out_features")
+    M = xc.numel() // in_features
+    y = torch.empty((M, out_features), dtype=torch.float32, device=xc.device)
+    with torch.cuda.device(xc.device):
+        _check(lib.dimq_linear_lut(_ptr(xc), _dtype(xc), M, _ptr(pw), pw.numel(), _ptr(cb), _dtype(cb), cb.numel(),
+                                   float(act_scale), int(act_zp), bp, bdt, bn, out_features, in_features, _ptr(y),
+                                   _stream(xc.device)))
+    return y.view(*x.shape[:-1], out_features)
+
+
+def conv2d_lut_impl(x, packed_w, codebook, act_scale, act_zp, bias, out_channels, in_channels_per_group, kernel_h,
+                    kernel_w, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w, groups):
+    _require_cuda(x, "conv2d_lut expects CUDA input")
+    if x.dim() != 4:
+        raise RuntimeError("conv2d_lut expects NCHW input")
+    _require_cuda(packed_w, "conv2d_lut expects CUDA packed_weight")
+    _require_cuda(codebook, "conv2d_lut expects CUDA codebook")
+    if not x.is_floating_point():
+        raise RuntimeError("conv2d_lut expects floating input")
+    if packed_w.dtype != torch.uint8:
+        raise RuntimeError("packed_weight must be uint8")
+    if not codebook.is_floating_point():
+        raise RuntimeError("codebook must be floating point")
+    xc = x.contiguous()
+    pw = packed_w.contiguous().view(-1)
+    cb = codebook.contiguous().view(-1)
+    B, C, H, W = xc.shape
+    b, bp, bdt, bn = _bias_args(bias, out_channels, "out_channels")
+    oh = (H + 2 * pad_h - dilation_h * (kernel_h - 1) - 1) // stride_h + 1 if stride_h > 0 else 0
+    ow = (W + 2 * pad_w - dilation_w * (kernel_w - 1) - 1) // stride_w + 1 if stride_w > 0 else 0
+    y = torch.empty((B, out_channels, max(oh, 0), max(ow, 0)), dtype=torch.float32, device=xc.device)
+    with torch.cuda.device(xc.device):
+        _check(lib.dimq_conv2d_lut(_ptr(xc), _dtype(xc), B, C, H, W, _ptr(pw), pw.numel(), _ptr(cb), _dtype(cb),
+                                   cb.numel(), float(act_scale), int(act_zp), bp, bdt, bn, out_channels,
+                                   in_channels_per_group, kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w,
+                                   dilation_h, dilation_w, groups, _ptr(y), _stream(xc.device)))
+    return y
+
+
+# ---------------------------------------------------------------------------
+# generalised ops
+# ---------------------------------------------------------------------------
+
+def pack_bits_impl(indices: torch.Tensor, bits: int) -> torch.Tensor:
+    _require_cuda(indices, "pack_bits expects a CUDA tensor")
+    if indices.dtype != torch.uint8:
+        raise RuntimeError("pack_bits expects uint8 indices")
+    flat = indices.contiguous().view(-1)
+    out = torch.empty(((flat.numel() * bits + 7) // 8,), dtype=torch.uint8, device=flat.device)
+    with torch.cuda.device(flat.device):
+        _check(lib.dimq_pack_bits(_ptr(flat), flat.numel(), int(bits), _ptr(out), _stream(flat.device)))
+    return out
+
+
+def unpack_bits_impl(packed: torch.Tensor, numel: int, bits: int) -> torch.Tensor:
+    _require_cuda(packed, "unpack_bits expects a CUDA tensor")
+    if packed.dtype != torch.uint8:
+        raise RuntimeError("unpack_bits expects uint8 packed data")
+    if numel < 0:
+        raise RuntimeError("numel must be non-negative")
+    flat = packed.contiguous().view(-1)
+    out = torch.empty((numel,), dtype=torch.uint8, device=flat.device)
+    with torch.cuda.device(flat.device):
+        _check(lib.dimq_unpack_bits(_ptr(flat), flat.numel(), numel, int(bits), _ptr(out), _stream(flat.device)))
+    return out
+
+
+def hard_quantize_impl(w: torch.Tensor, centers: torch.Tensor, per_channel: bool):
+    _require_cuda(w, "hard_quantize expects a CUDA tensor")
+    _require_cuda(centers, "hard_quantize expects CUDA centers")
+    wc = w.contiguous()
+    if wc.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        wc = wc.float()
+    c = centers.detach().float().contiguous()
+    if per_channel:
+        if c.dim() != 2 or wc.dim() == 0 or c.size(0) != wc.size(0):
+            raise RuntimeError("per-channel centers must be [out_channels, K]")
+        rows, K = c.size(0), c.size(1)
+    else:
+        rows, K = 1, c.numel()
+    row_len = wc.numel() // rows if rows else 0
+    idx = torch.empty(wc.shape, dtype=torch.uint8, device=wc.device)
+    vals = torch.empty(wc.shape, dtype=wc.dtype, device=wc.device)
+    with torch.cuda.device(wc.device):
+        _check(lib.dimq_hard_quantize(_ptr(wc), _dtype(wc), rows, row_len, _ptr(c), K, int(bool(per_channel)),
+                                      _ptr(idx), _ptr(vals), _stream(wc.device)))
+    return idx, vals
+
+
+def build_product_table_grouped_impl(codebook: torch.Tensor, act_scale: float, act_zp: int) -> torch.Tensor:
+    _require_cuda(codebook, "build_product_table expects a CUDA tensor")
+    cb = codebook.contiguous()
+    G, Kc = (1, cb.numel()) if cb.dim() <= 1 else (cb.size(0), cb.numel() // max(cb.size(0), 1))
+    out = torch.empty((G, Kc, 16), dtype=torch.float32, device=cb.device)
+    with torch.cuda.device(cb.device):
+        _check(lib.dimq_build_product_table_grouped(_ptr(cb), _dtype(cb), G, Kc, float(act_scale), int(act_zp),
+                                                    _ptr(out), _stream(cb.device)))
+    return out
+
+
+def _cb_shape(codebook: torch.Tensor, n: int):
+    if codebook.dim() == 2 and codebook.size(0) == n and n != 1:
+        return codebook.size(0), codebook.size(1)
+    if codebook.dim() == 2 and codebook.size(0) == 1:
+        return 1, codebook.size(1)
+    if codebook.dim() <= 1:
+        return 1, codebook.numel()
+    raise RuntimeError("codebook must be [K] (per layer) or [out_features, K] (per channel)")
+
+
+def linear_codebook_impl(x, packed_w, codebook, bits, bias, out_features, in_features, out_dtype=None, variant=0):
+    _require_cuda(x, "linear_codebook expects CUDA input")
+    _require_cuda(packed_w, "linear_codebook expects CUDA packed_weight")
+    _require_cuda(codebook, "linear_codebook expects CUDA codebook")
+    if x.dim() == 0 or x.size(-1) != in_features:
+        raise RuntimeError("input last dimension must equal in_features")
+    if packed_w.dtype != torch.uint8:
+        raise RuntimeError("packed_weight must be uint8")
+    xc = x.contiguous()
+    pw = packed_w.contiguous().view(-1)
+    cb = codebook.contiguous()
+    rows, size = _cb_shape(cb, out_features)
+    b, bp, bdt, _ = _bias_args(bias, out_features, "out_features")
+    odt = x.dtype if out_dtype is None else out_dtype
+    M = xc.numel() // in_features if in_features else 0
+    y = torch.empty((M, out_features), dtype=odt, device=xc.device)
+    with torch.cuda.device(xc.device):
+        _check(lib.dimq_linear_codebook(_ptr(xc), _dtype(xc), M, in_features, _ptr(pw), pw.numel(), int(bits),
+                                        _ptr(cb), _dtype(cb), rows, size, bp, bdt, out_features, _ptr(y), _dtype(y),
+                                        int(variant), _stream(xc.device)))
+    return y.view(*x.shape[:-1], out_features)
+
+
+def conv2d_codebook_impl(x, packed_w, codebook, bits, bias, out_channels, in_channels_per_group, kernel_h, kernel_w,
+                         stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w, groups, out_dtype=None, variant=0):
+    _require_cuda(x, "conv2d_codebook expects CUDA input")
+    if x.dim() != 4:
+        raise RuntimeError("conv2d_codebook expects a 4-D input")
+    _require_cuda(packed_w, "conv2d_codebook expects CUDA packed_weight")
+    _require_cuda(codebook, "conv2d_codebook expects CUDA codebook")
+    if packed_w.dtype != torch.uint8:
+        raise RuntimeError("packed_weight must be uint8")
+    B, C, H, W = x.shape
+    if C != in_channels_per_group * groups:
+        raise RuntimeError("input channels do not match weight/groups")
+    channels_last = (not x.is_contiguous()) and x.is_contiguous(memory_format=torch.channels_last)
+    if channels_last:
+        xc, layout = x, NHWC
+    else:
+        xc, layout = x.contiguous(), NCHW
+    pw = packed_w.contiguous().view(-1)
+    cb = codebook.contiguous()
+    rows, size = _cb_shape(cb, out_channels)
+    b, bp, bdt, _ = _bias_args(bias, out_channels, "out_channels")
+    oh = (H + 2 * pad_h - dilation_h * (kernel_h - 1) - 1) // stride_h + 1 if stride_h > 0 else 0
+    ow = (W + 2 * pad_w - dilation_w * (kernel_w - 1) - 1) // stride_w + 1 if stride_w > 0 else 0
+    odt = x.dtype if out_dtype is None else out_dtype
+    mf = torch.channels_last if channels_last else torch.contiguous_format
+    y = torch.empty((B, out_channels, max(oh, 0), max(ow, 0)), dtype=odt, device=xc.device, memory_format=mf)
+    with torch.cuda.device(xc.device):
+        _check(lib.dimq_conv2d_codebook(_ptr(xc), _dtype(xc), layout, B, C, H, W, _ptr(pw), pw.numel(), int(bits),
+                                        _ptr(cb), _dtype(cb), rows, size, bp, bdt, out_channels, kernel_h, kernel_w,
+                                        stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w, groups, _ptr(y),
+                                        _dtype(y), layout, int(variant), _stream(xc.device)))
+    return y
+
+
+# ---------------------------------------------------------------------------
+# torch.library registration
+# ---------------------------------------------------------------------------
+
+_SCHEMAS = {
+    # verbatim from dimq_cuda_backend/csrc/dimq_ops.cpp:38-43
+    "pack_u4": ("pack_u4(Tensor indices) -> Tensor", pack_u4_impl),
+    "unpack_u4": ("unpack_u4(Tensor packed, int numel) -> Tensor", unpack_u4_impl),
+    "quantize_activation_u4": ("quantize_activation_u4(Tensor x, float act_scale, int act_zp) -> Tensor",
+                               quantize_activation_u4_impl),
+    "build_product_table": ("build_product_table(Tensor codebook, float act_scale, int act_zp) -> Tensor",
+                            build_product_table_impl),
+    "linear_lut": ("linear_lut(Tensor x, Tensor packed_w, Tensor codebook, float act_scale, int act_zp, Tensor? bias, "
+                   "int out_features, int in_features) -> Tensor", linear_lut_impl),
+    "conv2d_lut": ("conv2d_lut(Tensor x, Tensor packed_w, Tensor codebook, float act_scale, int act_zp, Tensor? bias, "
+                   "int out_channels, int in_channels_per_group, int kernel_h, int kernel_w, int stride_h, "
+                   "int stride_w, int pad_h, int pad_w, int dilation_h, int dilation_w, int groups) -> Tensor",
+                   conv2d_lut_impl),
+    # generalised ops
+    "pack_bits": ("pack_bits(Tensor indices, int bits) -> Tensor", pack_bits_impl),
+    "unpack_bits": ("unpack_bits(Tensor packed, int numel, int bits) -> Tensor", unpack_bits_impl),
+    "hard_quantize": ("hard_quantize(Tensor w, Tensor centers, bool per_channel) -> (Tensor, Tensor)",
+                      hard_quantize_impl),
+    "build_product_table_grouped": ("build_product_table_grouped(Tensor codebook, float act_scale, int act_zp) "
+                                    "-> Tensor", build_product_table_grouped_impl),
+    "linear_codebook": ("linear_codebook(Tensor x, Tensor packed_w, Tensor codebook, int bits, Tensor? bias, "
+                        "int out_features, int in_features, ScalarType? out_dtype=None, int variant=0) -> Tensor",
+                        linear_codebook_impl),
+    "conv2d_codebook": ("conv2d_codebook(Tensor x, Tensor packed_w, Tensor codebook, int bits, Tensor? bias, "
+                        "int out_channels, int in_channels_per_group, int kernel_h, int kernel_w, int stride_h, "
+                        "int stride_w, int pad_h, int pad_w, int dilation_h, int dilation_w, int groups, "
+                        "ScalarType? out_dtype=None, int variant=0) -> Tensor", conv2d_codebook_impl),
+}
+
+
+def _register() -> torch.library.Library:
+    lib_def = torch.library.Library("dimq", "DEF")
+    for name, (schema, impl) in _SCHEMAS.items():
+        lib_def.define(schema)
+        lib_def.impl(name, impl, "CUDA")
+    return lib_def
+
+
+_LIBRARY = _register()

@@ -1,0 +1,107 @@
+// Shared device/host helpers of libdimq_hip.so (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_bf16.h>
+#include <stdint.h>
+
+#include "../../include/dimq_hip.h"
+
+namespace dimq {
+
+// ---------------------------------------------------------------- errors
+// Thread-local message store (capi.hip).
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+#define DIMQ_CHECK(cond, ...)                                  \
+  do {                                                         \
+    if (!(cond)) return ::dimq::set_error(DIMQ_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+inline int dtype_size(int dt) {
+  switch (dt) {
+    case DIMQ_F32: return 4;
+    case DIMQ_F16: return 2;
+    case DIMQ_BF16: return 2;
+    case DIMQ_F64: return 8;
+    case DIMQ_U8: return 1;
+  }
+  return 0;
+}
+
+inline bool is_float_dtype(int dt) {
+  return dt == DIMQ_F32 || dt == DIMQ_F16 || dt == DIMQ_BF16 || dt == DIMQ_F64;
+}
+
+// ---------------------------------------------------------------- device scalars
+// Raw 16-bit storage types; conversions are explicit.
+struct f16raw { uint16_t v; };
+struct bf16raw { uint16_t v; };
+
+__device__ __forceinline__ float bf16_bits_to_float(uint32_t b) {
+  return __uint_as_float(b << 16);
+}
+
+__device__ __forceinline__ float f16_bits_to_float(uint32_t b) {
+  _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)b);
+  return (float)h;
+}
+
+// fp32 -> fp16 bits, round to nearest even.
+__device__ __forceinline__ uint32_t float_to_f16_bits(float x) {
+  _Float16 h = (_Float16)x;
+  return (uint32_t)__builtin_bit_cast(uint16_t, h);
+}
+
+// fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
+__device__ __forceinline__ uint32_t float_to_bf16_bits(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// Load element i of a float tensor of runtime dtype as fp32.
+__device__ __forceinline__ float load_as_float(const void* p, int dt, int64_t i) {
+  switch (dt) {
+    case DIMQ_F32: return reinterpret_cast<const float*>(p)[i];
+    case DIMQ_F16: return f16_bits_to_float(reinterpret_cast<const uint16_t*>(p)[i]);
+    case DIMQ_BF16: return bf16_bits_to_float(reinterpret_cast<const uint16_t*>(p)[i]);
+    case DIMQ_F64: return (float)reinterpret_cast<const double*>(p)[i];
+  }
+  return 0.0f;
+}
+
+__device__ __forceinline__ void store_from_float(void* p, int dt, int64_t i, float v) {
+  switch (dt) {
+    case DIMQ_F32: reinterpret_cast<float*>(p)[i] = v; break;
+    case DIMQ_F16: reinterpret_cast<uint16_t*>(p)[i] = (uint16_t)float_to_f16_bits(v); break;
+    case DIMQ_BF16: reinterpret_cast<uint16_t*>(p)[i] = (uint16_t)float_to_bf16_bits(v); break;
+    case DIMQ_F64: reinterpret_cast<double*>(p)[i] = (double)v; break;
+  }
+}
+
+// u4 activation code: clamp(rint(x / s) + zp, 0, 15), IEEE divide
+// (dimq_backend/reference.py:11-21).
+__device__ __forceinline__ int quantize_u4(float x, float s, int zp) {
+  float q = __builtin_rintf(x / s) + (float)zp;
+  q = q < 0.0f ? 0.0f : q;
+  q = q > 15.0f ? 15.0f : q;
+  return (int)q;
+}
+
+// v_perm_b32: byte i of the result = byte sel.byte[i] of the 8-byte value
+// {hi:lo} (0..3 pick lo, 4..7 pick hi).
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+constexpr int kWave = 64;
+
+}  // namespace dimq

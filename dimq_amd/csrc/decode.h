@@ -1,0 +1,144 @@
+// Register-resident codebook decode for the matrix-core kernels.
+//
+// A lane that feeds the MFMA B operand owns one weight row n (its column of
+// the 16x16 tile) and, per 128-wide k step, one contiguous chunk of 32 packed
+// indices (4*b bytes).  The row's codebook (2^b fp16 entries, b <= 4) lives in
+// VGPRs as two byte planes: L holds the low bytes of the entries, H the high
+// bytes (entry e at byte e%4 of dword e/4).  v_perm_b32 then performs four
+// table lookups per instruction, so decoding costs no LDS traffic:
+//
+//   lo = perm(L[1], L[0], D)     // D = 4 index bytes (3-bit: entries 0..7)
+//   hi = perm(H[1], H[0], D)
+//   V01 = perm(hi, lo, 0x05010400)   -> fp16 pair (D.b0, D.b1)
+//   V23 = perm(hi, lo, 0x07030602)   -> fp16 pair (D.b2, D.b3)
+//
+// Each bit width extracts its index bytes with a few shifts and masks, in an
+// order ("slot order") that is cheapest for it; the A operand is written to
+// LDS in the same order (kperm16), so that the dot products pair up.
+#pragma once
+
+#include "common.h"
+
+namespace dimq {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Slot order: slot u of a 16-wide k group holds k offset kperm16(bits, u).
+//  b=4: each packed dword holds 8 nibbles; (w & 0x0f0f0f0f) yields the even
+//       k, ((w >> 4) & 0x0f0f0f0f) the odd k.
+//  b=2: (w >> 2j) & 0x03030303 yields k = {j, 4+j, 8+j, 12+j}.
+//  b=3, b=8: natural order.
+__host__ __device__ constexpr int kperm16(int bits, int u) {
+  if (bits == 4) {
+    const int g = u & 8, j = u & 7;
+    return g + (j < 4 ? 2 * j : 2 * (j - 4) + 1);
+  }
+  if (bits == 2) {
+    // u = 8h + 4p + t  ->  k = 4t + 2h + p
+    const int h = u >> 3, p = (u >> 2) & 1, t = u & 3;
+    return 4 * t + 2 * h + p;
+  }
+  return u;
+}
+
+template <int BITS>
+struct CodebookRegs {
+  static constexpr int kPlanes = (BITS >= 2 && BITS <= 4) ? (1 << BITS) / 4 : 1;
+  uint32_t L[kPlanes];
+  uint32_t H[kPlanes];
+};
+
+// Fill the byte planes from 2^b fp16 bit patterns.
+template <int BITS>
+__device__ __forceinline__ void set_planes(CodebookRegs<BITS>& cb, const uint32_t* h16) {
+#pragma unroll
+  for (int q = 0; q < CodebookRegs<BITS>::kPlanes; ++q) {
+    uint32_t l = 0, h = 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint32_t e = (4 * q + t < (1 << BITS)) ? h16[4 * q + t] : 0u;
+      l |= (e & 0xffu) << (8 * t);
+      h |= ((e >> 8) & 0xffu) << (8 * t);
+    }
+    cb.L[q] = l;
+    cb.H[q] = h;
+  }
+}
+
+// Four lookups: D holds four index bytes; returns the fp16 pairs (b0,b1), (b2,b3).
+template <int BITS>
+__device__ __forceinline__ void lookup4(const CodebookRegs<BITS>& cb, uint32_t D, uint32_t& v01, uint32_t& v23) {
+  uint32_t lo, hi;
+  if constexpr (BITS == 2) {
+    lo = perm(cb.L[0], cb.L[0], D);
+    hi = perm(cb.H[0], cb.H[0], D);
+  } else if constexpr (BITS == 3) {
+    lo = perm(cb.L[1], cb.L[0], D);
+    hi = perm(cb.H[1], cb.H[0], D);
+  } else {
+    const uint32_t s = D & 0x07070707u;
+    // byte i of sel2 = i + 4 * bit3(D.byte_i): picks the upper half table
+    const uint32_t sel2 = ((D >> 1) & 0x04040404u) | 0x03020100u;
+    const uint32_t la = perm(cb.L[1], cb.L[0], s), lb = perm(cb.L[3], cb.L[2], s);
+    const uint32_t ha = perm(cb.H[1], cb.H[0], s), hb = perm(cb.H[3], cb.H[2], s);
+    lo = perm(lb, la, sel2);
+    hi = perm(hb, ha, sel2);
+  }
+  v01 = perm(hi, lo, 0x05010400u);
+  v23 = perm(hi, lo, 0x07030602u);
+}
+
+// 12-bit group of four 3-bit fields -> four bytes.
+__device__ __forceinline__ uint32_t spread3x4(uint32_t y) {
+  uint32_t t = ((y << 10) | y) & 0x003f003fu;
+  return ((t << 5) | t) & 0x07070707u;
+}
+
+// Decode sub-step s (slots 8s..8s+7 of the lane's 32-index chunk c[]) into a
+// B fragment (8 fp16 in slot order).  BITS in {2,3,4}.
+template <int BITS>
+__device__ __forceinline__ half8 decode_sub(const uint32_t (&c)[BITS], int s, const CodebookRegs<BITS>& cb) {
+  uint32_t D0, D1;
+  if constexpr (BITS == 4) {
+    const uint32_t w = c[s];
+    D0 = w & 0x0f0f0f0fu;
+    D1 = (w >> 4) & 0x0f0f0f0fu;
+  } else if constexpr (BITS == 2) {
+    const uint32_t w = c[s >> 1];
+    const int sh = 4 * (s & 1);
+    D0 = (w >> sh) & 0x03030303u;
+    D1 = (w >> (sh + 2)) & 0x03030303u;
+  } else {
+    uint32_t G;
+    if (s == 0) G = c[0];
+    else if (s == 1) G = __builtin_amdgcn_alignbit(c[1], c[0], 24);
+    else if (s == 2) G = __builtin_amdgcn_alignbit(c[2], c[1], 16);
+    else G = c[2] >> 8;
+    D0 = spread3x4(G & 0xfffu);
+    D1 = spread3x4((G >> 12) & 0xfffu);
+  }
+  uint32_t r0, r1, r2, r3;
+  lookup4<BITS>(cb, D0, r0, r1);
+  lookup4<BITS>(cb, D1, r2, r3);
+  const u32x4 r = {r0, r1, r2, r3};
+  return __builtin_bit_cast(half8, r);
+}
+
+__device__ __forceinline__ floatx4 mfma16x16x32(half8 a, half8 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Power-of-two exponent e such that max|c| * 2^e lies in [2^14, 2^15):
+// keeps fp16 codebook entries away from subnormals and from overflow.
+__device__ __forceinline__ int cb_exponent(float maxabs) {
+  if (!(maxabs > 0.0f) || !__builtin_isfinite(maxabs)) return 0;
+  int ex;
+  (void)frexpf(maxabs, &ex);
+  int e = 15 - ex;
+  e = e > 100 ? 100 : (e < -100 ? -100 : e);
+  return e;
+}
+
+}  // namespace dimq

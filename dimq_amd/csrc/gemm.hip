@@ -1,0 +1,150 @@
+// Host side of the codebook Linear: argument checks (with the reference's
+// messages where one exists, csrc/dimq_gemm_lut.cu:66-79), tile selection and
+// launch.
+#include "gemm_kernel.h"
+
+namespace dimq {
+namespace {
+
+constexpr int64_t kCUs = 256;
+
+}  // namespace
+
+int gemm_pick_tile(int64_t M, int64_t N, int variant) {
+  if (variant == DIMQ_VARIANT_SMALL_M) return kTile16x16;
+  if (variant == DIMQ_VARIANT_AUTO && M <= 16) return kTile16x16;
+  const int64_t big = ((M + 127) / 128) * ((N + 255) / 256);
+  if (big >= kCUs) return kTile128x64;
+  return kTile64x32;
+}
+
+namespace {
+
+template <bool A4>
+int dispatch(const GemmArgs& p, int bits, int xt, int tile, hipStream_t s) {
+#define DIMQ_XT_CASES(B)                                                   \
+  switch (xt) {                                                            \
+    case DIMQ_F32: return launch_gemm_tile<B, DIMQ_F32, A4>(p, tile, s);   \
+    case DIMQ_F16: return launch_gemm_tile<B, DIMQ_F16, A4>(p, tile, s);   \
+    case DIMQ_BF16: return launch_gemm_tile<B, DIMQ_BF16, A4>(p, tile, s); \
+  }                                                                        \
+  break;
+  if constexpr (A4) {
+    switch (xt) {
+      case DIMQ_F32: return launch_gemm_tile<4, DIMQ_F32, true>(p, tile, s);
+      case DIMQ_F16: return launch_gemm_tile<4, DIMQ_F16, true>(p, tile, s);
+      case DIMQ_BF16: return launch_gemm_tile<4, DIMQ_BF16, true>(p, tile, s);
+      case DIMQ_F64: return launch_gemm_tile<4, DIMQ_F64, true>(p, tile, s);
+    }
+  } else {
+    switch (bits) {
+      case 2: DIMQ_XT_CASES(2)
+      case 3: DIMQ_XT_CASES(3)
+      case 4: DIMQ_XT_CASES(4)
+      case 8: DIMQ_XT_CASES(8)
+    }
+  }
+#undef DIMQ_XT_CASES
+  return set_error(DIMQ_ERR_UNSUPPORTED, "unsupported dtype/bit-width combination (x dtype %d, bits %d)", xt, bits);
+}
+
+}  // namespace
+
+int gemm_dispatch(const GemmArgs& p, int bits, int xt, bool a4, int tile, hipStream_t s) {
+  return a4 ? dispatch<true>(p, bits, xt, tile, s) : dispatch<false>(p, bits, xt, tile, s);
+}
+
+int linear_codebook_impl(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed_w,
+                         int bits, const void* codebook, int cb_dtype, int64_t cb_rows, int64_t cb_size,
+                         const void* bias, int bias_dtype, int64_t N, void* y, int y_dtype, int64_t ldy,
+                         int variant, hipStream_t s) {
+  GemmArgs p{};
+  p.x = x;
+  p.M = M;
+  p.K = K;
+  p.ldx = ldx;
+  p.w = packed_w;
+  p.N = N;
+  p.cb = codebook;
+  p.cb_dt = cb_dtype;
+  p.cb_rows = cb_rows;
+  p.cb_size = static_cast<int>(cb_size);
+  p.bias = bias;
+  p.bias_dt = bias_dtype;
+  p.y = y;
+  p.y_dt = y_dtype;
+  p.ldy = ldy;
+  p.act_scale = 1.0f;
+  p.act_zp = 0;
+  p.fast_b = (K % 32 == 0) && aligned(packed_w, 16);
+  const int xs = dtype_size(x_dtype);
+  p.vec_a = aligned(x, 16) && ((ldx * xs) % 16 == 0);
+  p.groups = 1;
+  if (M == 0 || N == 0) return DIMQ_OK;
+  return dispatch<false>(p, bits, x_dtype, gemm_pick_tile(M, N, variant), s);
+}
+
+}  // namespace dimq
+
+using namespace dimq;
+
+extern "C" int dimq_linear_codebook(const void* x, int x_dtype, int64_t M, int64_t K, const uint8_t* packed_w,
+                                    int64_t packed_numel, int bits, const void* codebook, int cb_dtype,
+                                    int64_t cb_rows, int64_t cb_size, const void* bias, int bias_dtype, int64_t N,
+                                    void* y, int y_dtype, int variant, void* stream) {
+  if (!(bits == 2 || bits == 3 || bits == 4 || bits == 8))
+    return set_error(DIMQ_ERR_UNSUPPORTED, "bits must be one of 2, 3, 4, 8 (got %d)", bits);
+  DIMQ_CHECK(x_dtype == DIMQ_F32 || x_dtype == DIMQ_F16 || x_dtype == DIMQ_BF16,
+             "linear_codebook expects fp32, fp16 or bf16 input");
+  DIMQ_CHECK(y_dtype == DIMQ_F32 || y_dtype == DIMQ_F16 || y_dtype == DIMQ_BF16,
+             "linear_codebook output dtype must be fp32, fp16 or bf16");
+  DIMQ_CHECK(is_float_dtype(cb_dtype), "codebook must be floating point");
+  DIMQ_CHECK(bias == nullptr || is_float_dtype(bias_dtype), "bias must be floating point");
+  DIMQ_CHECK(M >= 0 && N > 0 && K > 0, "linear dimensions must be positive");
+  DIMQ_CHECK(cb_rows == 1 || cb_rows == N, "codebook must have 1 (per layer) or out_features (per channel) rows");
+  DIMQ_CHECK(cb_size >= 1 && cb_size <= (1 << bits), "codebook rows must hold between 1 and 2^bits entries");
+  DIMQ_CHECK(packed_numel >= (N * K * bits + 7) / 8, "packed_weight is too small for out_features * in_features");
+  DIMQ_CHECK(variant >= DIMQ_VARIANT_AUTO && variant <= DIMQ_VARIANT_MFMA, "unknown kernel variant %d", variant);
+  return linear_codebook_impl(x, x_dtype, M, K, K, packed_w, bits, codebook, cb_dtype, cb_rows, cb_size, bias,
+                              bias_dtype, N, y, y_dtype, N, variant, as_stream(stream));
+}
+
+extern "C" int dimq_linear_lut(const void* x, int x_dtype, int64_t M, const uint8_t* packed_w, int64_t packed_numel,
+                               const void* codebook, int cb_dtype, int64_t cb_numel, double act_scale,
+                               int64_t act_zp, const void* bias, int bias_dtype, int64_t bias_numel,
+                               int64_t out_features, int64_t in_features, float* y, void* stream) {
+  DIMQ_CHECK(is_float_dtype(x_dtype), "linear_lut expects floating input");
+  DIMQ_CHECK(is_float_dtype(cb_dtype), "codebook must be floating point");
+  DIMQ_CHECK(cb_numel == 16, "codebook must have 16 entries for W4");
+  DIMQ_CHECK(act_scale > 0.0, "act_scale must be positive");
+  DIMQ_CHECK(act_zp >= 0 && act_zp <= 15, "act_zero_point must be in [0, 15]");
+  DIMQ_CHECK(out_features > 0 && in_features > 0, "linear dimensions must be positive");
+  DIMQ_CHECK(M >= 0, "input numel must be divisible by in_features");
+  DIMQ_CHECK(packed_numel >= (out_features * in_features + 1) / 2,
+             "packed_weight is too small for out_features * in_features");
+  if (bias) DIMQ_CHECK(bias_numel == out_features, "bias numel must equal out_features");
+  DIMQ_CHECK(bias == nullptr || is_float_dtype(bias_dtype), "bias must be floating point");
+  if (M == 0) return DIMQ_OK;
+  GemmArgs p{};
+  p.x = x;
+  p.M = M;
+  p.K = in_features;
+  p.ldx = in_features;
+  p.w = packed_w;
+  p.N = out_features;
+  p.cb = codebook;
+  p.cb_dt = cb_dtype;
+  p.cb_rows = 1;
+  p.cb_size = 16;
+  p.bias = bias;
+  p.bias_dt = bias_dtype;
+  p.y = y;
+  p.y_dt = DIMQ_F32;
+  p.ldy = out_features;
+  p.act_scale = static_cast<float>(act_scale);
+  p.act_zp = static_cast<int>(act_zp);
+  p.fast_b = (in_features % 32 == 0) && aligned(packed_w, 16);
+  p.vec_a = aligned(x, 16) && ((in_features * dtype_size(x_dtype)) % 16 == 0);
+  p.groups = 1;
+  return dispatch<true>(p, 4, x_dtype, kTile64x32, as_stream(stream));
+}

@@ -1,0 +1,535 @@
+// Dequant + MFMA codebook GEMM: y[M,N] = x[M,K] . W_hat[N,K]^T (+ bias),
+// W_hat[n,k] = C[n or 0][idx[n,k]], idx a b-bit LSB-first stream.
+//
+// Work-group = 256 threads = 4 waves; tile BM x (4*WN).  The 4 waves split the
+// tile's columns: wave w owns columns [w*WN, (w+1)*WN) and all BM rows, so a
+// weight is decoded by exactly one lane per work-group and B never touches LDS:
+// each lane streams its row's packed chunk (4*b bytes per 128-wide k step)
+// from HBM into VGPRs and decodes it with v_perm lookups into its
+// codebook byte planes (decode.h).  The activation tile (BM x 128 fp16) is
+// staged in LDS, double-buffered, written in the bit width's slot order, and
+// read back as 16-byte MFMA A fragments (v_mfma_f32_16x16x32_f16, fp32
+// accumulation).
+//
+// A4 (the reference's linear_lut, W4A4): the A operand is the integer
+// q - zp (exact in fp16) and the 16-entry fp32 codebook enters as an fp16
+// hi + lo pair (two MFMAs), so products are exact and the epilogue applies
+// s * 2^-e.
+#pragma once
+
+#include "decode.h"
+
+namespace dimq {
+
+constexpr int kKM = 128;         // k per pipeline step
+constexpr int kAPad = 8;         // fp16 padding per LDS row (bank spread)
+constexpr int kLDA = kKM + kAPad;
+
+struct GemmArgs {
+  const void* x;
+  int64_t M, K, ldx;
+  const uint8_t* w;
+  int64_t N;
+  const void* cb;
+  int cb_dt;
+  int64_t cb_rows;
+  int cb_size;
+  const void* bias;
+  int bias_dt;
+  void* y;
+  int y_dt;
+  int64_t ldy;
+  float act_scale;
+  int act_zp;
+  int fast_b;  // K % 32 == 0 and packed stream 16-byte aligned
+  int vec_a;   // x rows allow 16-element vector loads
+  // implicit-GEMM convolution (conv != 0): M = B*OH*OW, N = OC/groups per
+  // group (blockIdx.z), K = ICg*KH*KW in conv_kcrs order (ci, kh, kw).
+  int conv;
+  int x_layout, y_layout;  // DIMQ_NCHW / DIMQ_NHWC
+  int64_t cB, cC, cH, cW, cOH, cOW, cOC, cICg;
+  int cKH, cKW, csh, csw, cph, cpw, cdh, cdw;
+  int groups;  // grid z (1 for Linear)
+};
+
+// Output element offset of (row m, global column n).
+__device__ __forceinline__ int64_t out_offset(const GemmArgs& p, int64_t m, int64_t n) {
+  if (!p.conv) return m * p.ldy + n;
+  if (p.y_layout == DIMQ_NHWC) return m * p.cOC + n;
+  const int64_t hw = p.cOH * p.cOW;
+  const int64_t b = m / hw;
+  const int64_t r = m - b * hw;
+  return (b * p.cOC + n) * hw + r;
+}
+
+// im2col gather of 16 consecutive k (conv_kcrs order) for output pixel m.
+__device__ __forceinline__ void gather16_conv(const GemmArgs& p, int xt, int64_t m, int64_t k0, int64_t cbase,
+                                              float v[16]) {
+  const int64_t hw = p.cOH * p.cOW;
+  const int64_t b = m / hw;
+  const int64_t r = m - b * hw;
+  const int oh = static_cast<int>(r / p.cOW);
+  const int ow = static_cast<int>(r - (int64_t)oh * p.cOW);
+  const int khw = p.cKH * p.cKW;
+  int ci = static_cast<int>(k0 / khw);
+  int t = static_cast<int>(k0 - (int64_t)ci * khw);
+  int kh = t / p.cKW;
+  int kw = t - kh * p.cKW;
+  const int64_t K = p.K;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    float val = 0.0f;
+    if (k0 + j < K) {
+      const int ih = oh * p.csh - p.cph + kh * p.cdh;
+      const int iw = ow * p.csw - p.cpw + kw * p.cdw;
+      if (ih >= 0 && ih < p.cH && iw >= 0 && iw < p.cW) {
+        const int64_t c = cbase + ci;
+        const int64_t off = (p.x_layout == DIMQ_NHWC) ? ((b * p.cH + ih) * p.cW + iw) * p.cC + c
+                                                      : ((b * p.cC + c) * p.cH + ih) * p.cW + iw;
+        val = load_as_float(p.x, xt, off);
+      }
+    }
+    v[j] = val;
+    if (++kw == p.cKW) {
+      kw = 0;
+      if (++kh == p.cKH) {
+        kh = 0;
+        ++ci;
+      }
+    }
+  }
+}
+
+// ---- activation tile loader --------------------------------------------------
+template <int XT>
+__device__ __forceinline__ void load16_as_float(const void* x, int64_t off, bool vec, int64_t kvalid, float v[16]) {
+  if constexpr (XT == DIMQ_F32) {
+    const float* p = reinterpret_cast<const float*>(x) + off;
+    if (vec) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 t = reinterpret_cast<const float4*>(p)[q];
+        v[4 * q] = t.x; v[4 * q + 1] = t.y; v[4 * q + 2] = t.z; v[4 * q + 3] = t.w;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j] = (j < kvalid) ? p[j] : 0.0f;
+    }
+  } else if constexpr (XT == DIMQ_F64) {
+    // the reference op accepts double activations and quantizes x.float()
+    const double* p = reinterpret_cast<const double*>(x) + off;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = (j < kvalid) ? (float)p[j] : 0.0f;
+  } else {
+    const uint16_t* p = reinterpret_cast<const uint16_t*>(x) + off;
+    uint32_t r[8];
+    if (vec) {
+      const uint4 a = reinterpret_cast<const uint4*>(p)[0];
+      const uint4 b = reinterpret_cast<const uint4*>(p)[1];
+      r[0] = a.x; r[1] = a.y; r[2] = a.z; r[3] = a.w; r[4] = b.x; r[5] = b.y; r[6] = b.z; r[7] = b.w;
+    } else {
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        const uint32_t lo = (2 * d < kvalid) ? p[2 * d] : 0u;
+        const uint32_t hi = (2 * d + 1 < kvalid) ? p[2 * d + 1] : 0u;
+        r[d] = lo | (hi << 16);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t bits = (r[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+      v[j] = (XT == DIMQ_F16) ? f16_bits_to_float(bits) : bf16_bits_to_float(bits);
+    }
+  }
+}
+
+// 16 activations starting at (row gm, column k0) -> 8 dwords of fp16 pairs in
+// the slot order of BITS.
+template <int BITS, int XT, bool A4>
+__device__ __forceinline__ void load_a_group(const GemmArgs& p, int64_t gm, int64_t k0, int64_t cbase,
+                                             uint32_t out[8]) {
+  float v[16];
+  if (p.conv) {
+    if (gm < p.M && k0 < p.K) {
+      gather16_conv(p, XT, gm, k0, cbase, v);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j] = 0.0f;
+    }
+  } else if (gm < p.M && k0 < p.K) {
+    const int64_t kvalid = p.K - k0;
+    const bool vec = p.vec_a && kvalid >= 16;
+    load16_as_float<XT>(p.x, gm * p.ldx + k0, vec, kvalid, v);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = 0.0f;
+  }
+  uint32_t h[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    float t = v[j];
+    if constexpr (A4) {
+      const bool live = (gm < p.M) && (k0 + j < p.K);
+      t = live ? (float)(quantize_u4(t, p.act_scale, p.act_zp) - p.act_zp) : 0.0f;
+    }
+    h[j] = float_to_f16_bits(t);
+  }
+#pragma unroll
+  for (int d = 0; d < 8; ++d) out[d] = h[kperm16(BITS, 2 * d)] | (h[kperm16(BITS, 2 * d + 1)] << 16);
+}
+
+// ---- packed weight chunk loader ---------------------------------------------
+// 32 indices of row n starting at column k (k % 32 == 0) -> BITS dwords laid
+// out as if the chunk started on a byte boundary.  Columns >= K read as 0.
+template <int BITS>
+__device__ __forceinline__ void load_b_chunk(const GemmArgs& p, int64_t nl, int64_t n, int64_t k, uint32_t c[BITS]) {
+#pragma unroll
+  for (int w = 0; w < BITS; ++w) c[w] = 0u;
+  if (nl >= p.N || k >= p.K) return;
+  if (p.fast_b) {
+    const uint8_t* src = p.w + (((n * p.K + k) * BITS) >> 3);
+    if constexpr (BITS == 2) {
+      const uint2 t = *reinterpret_cast<const uint2*>(src);
+      c[0] = t.x; c[1] = t.y;
+    } else if constexpr (BITS == 3) {
+      c[0] = reinterpret_cast<const uint32_t*>(src)[0];
+      c[1] = reinterpret_cast<const uint32_t*>(src)[1];
+      c[2] = reinterpret_cast<const uint32_t*>(src)[2];
+    } else if constexpr (BITS == 4) {
+      const uint4 t = *reinterpret_cast<const uint4*>(src);
+      c[0] = t.x; c[1] = t.y; c[2] = t.z; c[3] = t.w;
+    } else {
+      const uint4 t0 = reinterpret_cast<const uint4*>(src)[0];
+      const uint4 t1 = reinterpret_cast<const uint4*>(src)[1];
+      c[0] = t0.x; c[1] = t0.y; c[2] = t0.z; c[3] = t0.w;
+      c[4] = t1.x; c[5] = t1.y; c[6] = t1.z; c[7] = t1.w;
+    }
+  } else {
+    // generic: rows are not byte aligned in the stream (K*b % 8 != 0) or K % 32 != 0
+    const int64_t kv = p.K - k;
+    for (int i = 0; i < 32; ++i) {
+      if (i >= kv) break;
+      const int64_t bit = (n * p.K + k + i) * BITS;
+      const uint8_t* b = p.w + (bit >> 3);
+      const int sh = static_cast<int>(bit & 7);
+      uint32_t v = b[0] >> sh;
+      if (sh + BITS > 8) v |= (uint32_t)b[1] << (8 - sh);
+      v &= (1u << BITS) - 1u;
+      const int ob = i * BITS;
+      c[ob >> 5] |= v << (ob & 31);
+      if ((ob & 31) + BITS > 32) c[(ob >> 5) + 1] |= v >> (32 - (ob & 31));
+    }
+  }
+}
+
+// ---- codebook setup ------------------------------------------------------------
+// Loads row `row` (cb_size entries, any float dtype), scales by 2^e, rounds to
+// fp16 (A4: hi + lo pair).  Returns e.
+template <int BITS, bool A4>
+__device__ __forceinline__ int load_codebook_row(const GemmArgs& p, int64_t row, bool valid, CodebookRegs<BITS>& hi,
+                                                 CodebookRegs<BITS>& lo) {
+  constexpr int E = 1 << BITS;
+  float c[E];
+  float mx = 0.0f;
+#pragma unroll
+  for (int j = 0; j < E; ++j) {
+    c[j] = (valid && j < p.cb_size) ? load_as_float(p.cb, p.cb_dt, row * p.cb_size + j) : 0.0f;
+    mx = fmaxf(mx, fabsf(c[j]));
+  }
+  const int e = cb_exponent(mx);
+  uint32_t h16[E], l16[E];
+#pragma unroll
+  for (int j = 0; j < E; ++j) {
+    const float cs = ldexpf(c[j], e);
+    h16[j] = float_to_f16_bits(cs);
+    if constexpr (A4) l16[j] = float_to_f16_bits(cs - f16_bits_to_float(h16[j]));
+  }
+  set_planes<BITS>(hi, h16);
+  if constexpr (A4) set_planes<BITS>(lo, l16);
+  return e;
+}
+
+template <int BITS, int BM, int WN, int XT, bool A4>
+__global__ __launch_bounds__(256) void gemm_cb_kernel(const GemmArgs p) {
+  static_assert(BITS >= 2 && BITS <= 4, "register codebooks hold at most 16 entries");
+  constexpr int MB = BM / 16;
+  constexpr int NB = WN / 16;
+  constexpr int NCB = A4 ? 2 : 1;
+  constexpr int A_TASKS = BM * (kKM / 16);
+  constexpr int A_PER_T = (A_TASKS + 255) / 256;
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kLDA];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 15;
+  const int g = lane >> 4;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * BM;
+  const int64_t nw0 = static_cast<int64_t>(blockIdx.x) * (4 * WN) + wave * WN;
+  const int64_t nz = static_cast<int64_t>(blockIdx.z) * p.N;      // first weight row of this group
+  const int64_t cbase = static_cast<int64_t>(blockIdx.z) * p.cICg;  // first input channel of this group
+
+  CodebookRegs<BITS> cb[NB][NCB];
+  float colscale[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int64_t n = nw0 + nb * 16 + col;
+    const int64_t row = (p.cb_rows == 1) ? 0 : nz + n;
+    const int e = load_codebook_row<BITS, A4>(p, row, n < p.N, cb[nb][0], cb[nb][NCB - 1]);
+    colscale[nb] = ldexpf(A4 ? p.act_scale : 1.0f, -e);
+  }
+
+  floatx4 acc[MB][NB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const int64_t nk = (p.K + kKM - 1) / kKM;
+  uint32_t a_st[A_PER_T][8];
+  uint32_t bc[NB][BITS], bn[NB][BITS];
+
+  auto load_a = [&](int64_t kt) {
+#pragma unroll
+    for (int i = 0; i < A_PER_T; ++i) {
+      const int task = tid + 256 * i;
+      if (A_TASKS % 256 == 0 || task < A_TASKS) {
+        const int m = task >> 3, kg = task & 7;
+        load_a_group<BITS, XT, A4>(p, m0 + m, kt * kKM + 16 * kg, cbase, a_st[i]);
+      }
+    }
+  };
+  auto store_a = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_PER_T; ++i) {
+      const int task = tid + 256 * i;
+      if (A_TASKS % 256 == 0 || task < A_TASKS) {
+        const int m = task >> 3, kg = task & 7;
+        uint4* dst = reinterpret_cast<uint4*>(&As[buf][m * kLDA + 16 * kg]);
+        dst[0] = make_uint4(a_st[i][0], a_st[i][1], a_st[i][2], a_st[i][3]);
+        dst[1] = make_uint4(a_st[i][4], a_st[i][5], a_st[i][6], a_st[i][7]);
+      }
+    }
+  };
+  auto load_b = [&](int64_t kt, uint32_t (&dst)[NB][BITS]) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+      load_b_chunk<BITS>(p, nw0 + nb * 16 + col, nz + nw0 + nb * 16 + col, kt * kKM + 32 * g, dst[nb]);
+  };
+
+  load_a(0);
+  store_a(0);
+  load_b(0, bc);
+  __syncthreads();
+
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    const int buf = static_cast<int>(kt & 1);
+    const bool more = kt + 1 < nk;
+    if (more) {
+      load_a(kt + 1);
+      load_b(kt + 1, bn);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      half8 bf[NB][NCB];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int c = 0; c < NCB; ++c) bf[nb][c] = decode_sub<BITS>(bc[nb], s, cb[nb][c]);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const half8 af = *reinterpret_cast<const half8*>(&As[buf][(mb * 16 + col) * kLDA + 32 * g + 8 * s]);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int c = 0; c < NCB; ++c) acc[mb][nb] = mfma16x16x32(af, bf[nb][c], acc[mb][nb]);
+      }
+    }
+    if (more) {
+      store_a(buf ^ 1);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int w = 0; w < BITS; ++w) bc[nb][w] = bn[nb][w];
+    }
+    __syncthreads();
+  }
+
+  // epilogue: lane holds rows 4g..4g+3 of column `col` of each 16x16 block
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int64_t n = nw0 + nb * 16 + col;
+    if (n >= p.N) continue;
+    const float b = p.bias ? load_as_float(p.bias, p.bias_dt, nz + n) : 0.0f;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t m = m0 + mb * 16 + 4 * g + i;
+        if (m < p.M) store_from_float(p.y, p.y_dt, out_offset(p, m, nz + n), acc[mb][nb][i] * colscale[nb] + b);
+      }
+    }
+  }
+}
+
+// 8-bit codebooks (256 entries) are too large for registers: the work-group's
+// 4*WN rows are staged in LDS as fp16 and looked up with ds_read_u16.
+template <int BM, int WN, int XT>
+__global__ __launch_bounds__(256) void gemm_cb8_kernel(const GemmArgs p) {
+  constexpr int BITS = 8;
+  constexpr int MB = BM / 16;
+  constexpr int NB = WN / 16;
+  constexpr int ROWS = 4 * WN;
+  constexpr int A_TASKS = BM * (kKM / 16);
+  constexpr int A_PER_T = (A_TASKS + 255) / 256;
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kLDA];
+  __shared__ uint16_t cbs[ROWS * 256];
+  __shared__ float rscale[ROWS];
+  __shared__ float rmax[ROWS][4];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 15;
+  const int g = lane >> 4;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * BM;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * ROWS;
+  const int64_t nw0 = n0 + wave * WN;
+  const int64_t nz = static_cast<int64_t>(blockIdx.z) * p.N;
+  const int64_t cbase = static_cast<int64_t>(blockIdx.z) * p.cICg;
+
+  // codebook rows -> LDS (fp16, scaled by a per-row power of two)
+  for (int r = tid / 4; r < ROWS; r += 64) {
+    const int part = tid & 3;
+    const int64_t n = n0 + r;
+    const int64_t row = (p.cb_rows == 1) ? 0 : nz + n;
+    float mx = 0.0f;
+    for (int j = part; j < 256; j += 4) {
+      const float c = (n < p.N && j < p.cb_size) ? load_as_float(p.cb, p.cb_dt, row * p.cb_size + j) : 0.0f;
+      mx = fmaxf(mx, fabsf(c));
+    }
+    rmax[r][part] = mx;
+  }
+  __syncthreads();
+  for (int r = tid / 4; r < ROWS; r += 64) {
+    const int part = tid & 3;
+    const int64_t n = n0 + r;
+    const int64_t row = (p.cb_rows == 1) ? 0 : nz + n;
+    const float mx = fmaxf(fmaxf(rmax[r][0], rmax[r][1]), fmaxf(rmax[r][2], rmax[r][3]));
+    const int e = cb_exponent(mx);
+    for (int j = part; j < 256; j += 4) {
+      const float c = (n < p.N && j < p.cb_size) ? load_as_float(p.cb, p.cb_dt, row * p.cb_size + j) : 0.0f;
+      cbs[r * 256 + j] = (uint16_t)float_to_f16_bits(ldexpf(c, e));
+    }
+    if (part == 0) rscale[r] = ldexpf(1.0f, -e);
+  }
+
+  floatx4 acc[MB][NB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const int64_t nk = (p.K + kKM - 1) / kKM;
+  uint32_t a_st[A_PER_T][8];
+  uint32_t bc[NB][BITS], bn[NB][BITS];
+  auto load_a = [&](int64_t kt) {
+#pragma unroll
+    for (int i = 0; i < A_PER_T; ++i) {
+      const int task = tid + 256 * i;
+      if (A_TASKS % 256 == 0 || task < A_TASKS) {
+        const int m = task >> 3, kg = task & 7;
+        load_a_group<BITS, XT, false>(p, m0 + m, kt * kKM + 16 * kg, cbase, a_st[i]);
+      }
+    }
+  };
+  auto store_a = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_PER_T; ++i) {
+      const int task = tid + 256 * i;
+      if (A_TASKS % 256 == 0 || task < A_TASKS) {
+        const int m = task >> 3, kg = task & 7;
+        uint4* dst = reinterpret_cast<uint4*>(&As[buf][m * kLDA + 16 * kg]);
+        dst[0] = make_uint4(a_st[i][0], a_st[i][1], a_st[i][2], a_st[i][3]);
+        dst[1] = make_uint4(a_st[i][4], a_st[i][5], a_st[i][6], a_st[i][7]);
+      }
+    }
+  };
+  auto load_b = [&](int64_t kt, uint32_t (&dst)[NB][BITS]) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+      load_b_chunk<BITS>(p, nw0 + nb * 16 + col, nz + nw0 + nb * 16 + col, kt * kKM + 32 * g, dst[nb]);
+  };
+
+  load_a(0);
+  store_a(0);
+  load_b(0, bc);
+  __syncthreads();
+
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    const int buf = static_cast<int>(kt & 1);
+    const bool more = kt + 1 < nk;
+    if (more) {
+      load_a(kt + 1);
+      load_b(kt + 1, bn);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      half8 bf[NB];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const uint16_t* rowp = &cbs[(wave * WN + nb * 16 + col) * 256];
+        u32x4 r;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const uint32_t w = bc[nb][2 * s + (d >> 1)];
+          const int sh = 16 * (d & 1);
+          r[d] = (uint32_t)rowp[(w >> sh) & 0xffu] | ((uint32_t)rowp[(w >> (sh + 8)) & 0xffu] << 16);
+        }
+        bf[nb] = __builtin_bit_cast(half8, r);
+      }
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const half8 af = *reinterpret_cast<const half8*>(&As[buf][(mb * 16 + col) * kLDA + 32 * g + 8 * s]);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = mfma16x16x32(af, bf[nb], acc[mb][nb]);
+      }
+    }
+    if (more) {
+      store_a(buf ^ 1);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int w = 0; w < BITS; ++w) bc[nb][w] = bn[nb][w];
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int64_t n = nw0 + nb * 16 + col;
+    if (n >= p.N) continue;
+    const float sc = rscale[wave * WN + nb * 16 + col];
+    const float b = p.bias ? load_as_float(p.bias, p.bias_dt, nz + n) : 0.0f;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t m = m0 + mb * 16 + 4 * g + i;
+        if (m < p.M) store_from_float(p.y, p.y_dt, out_offset(p, m, nz + n), acc[mb][nb][i] * sc + b);
+      }
+    }
+  }
+}
+
+// Tile shapes: (BM, WN); the work-group covers BM x 4*WN.
+enum TileId { kTile128x64 = 0, kTile64x32 = 1, kTile16x16 = 2, kTileCount = 3 };
+
+template <int BITS, int XT, bool A4>
+int launch_gemm_tile(const GemmArgs& p, int tile, hipStream_t s);
+
+// gemm.hip
+int gemm_pick_tile(int64_t M, int64_t N, int variant);
+int gemm_dispatch(const GemmArgs& p, int bits, int xt, bool a4, int tile, hipStream_t s);
+
+}  // namespace dimq

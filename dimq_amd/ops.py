@@ -1,0 +1,181 @@
+"""Python entry points for the DIMQ operators (MI355X HIP backend).
+
+Mirrors ``dimq_backend/ops.py`` (reference ``dimq_cuda_backend/dimq_backend/ops.py:12-125``):
+same function names, arguments and errors, with ``is_available()`` testing that
+the HIP library (``dimq_amd._C``) loads.  The generalised operators for
+b-bit / per-channel / weight-only layers are added alongside.
+"""
+
+from __future__ import annotations
+
+import importlib
+from functools import lru_cache
+from typing import Sequence
+
+import torch
+
+
+@lru_cache(maxsize=1)
+def _extension_available() -> bool:
+    try:
+        importlib.import_module("dimq_amd._C")
+    except Exception:
+        return False
+    return True
+
+
+def is_available() -> bool:
+    """Return whether the compiled HIP library is loadable (ops.py:21-24)."""
+
+    return _extension_available()
+
+
+def require_extension() -> None:
+    if not is_available():
+        raise RuntimeError(
+            "dimq_amd HIP library is not available. "
+            "Build it with `make -C dimq_amd/csrc` (or `python -c 'import __graft_entry__ as g; g.build()'`)."
+        )
+
+
+def pack_u4(indices: torch.Tensor) -> torch.Tensor:
+    require_extension()
+    return torch.ops.dimq.pack_u4(indices)
+
+
+def unpack_u4(packed: torch.Tensor, numel: int) -> torch.Tensor:
+    require_extension()
+    return torch.ops.dimq.unpack_u4(packed, int(numel))
+
+
+def quantize_activation_u4(x: torch.Tensor, act_scale: float, act_zero_point: int) -> torch.Tensor:
+    require_extension()
+    return torch.ops.dimq.quantize_activation_u4(x, float(act_scale), int(act_zero_point))
+
+
+def build_product_table(codebook: torch.Tensor, act_scale: float, act_zero_point: int) -> torch.Tensor:
+    require_extension()
+    return torch.ops.dimq.build_product_table(codebook, float(act_scale), int(act_zero_point))
+
+
+def dimq_linear_lut(
+    x: torch.Tensor,
+    packed_weight: torch.Tensor,
+    codebook: torch.Tensor,
+    act_scale: float,
+    act_zero_point: int,
+    bias: torch.Tensor | None,
+    out_features: int,
+    in_features: int,
+) -> torch.Tensor:
+    require_extension()
+    return torch.ops.dimq.linear_lut(
+        x, packed_weight, codebook, float(act_scale), int(act_zero_point), bias, int(out_features), int(in_features)
+    )
+
+
+def dimq_conv2d_lut(
+    x: torch.Tensor,
+    packed_weight: torch.Tensor,
+    codebook: torch.Tensor,
+    act_scale: float,
+    act_zero_point: int,
+    bias: torch.Tensor | None,
+    weight_shape: Sequence[int],
+    stride: Sequence[int],
+    padding: Sequence[int],
+    dilation: Sequence[int],
+    groups: int,
+) -> torch.Tensor:
+    require_extension()
+    out_channels, cin_per_group, kernel_h, kernel_w = [int(v) for v in weight_shape]
+    stride_h, stride_w = _pair(stride)
+    pad_h, pad_w = _pair(padding)
+    dil_h, dil_w = _pair(dilation)
+    return torch.ops.dimq.conv2d_lut(
+        x, packed_weight, codebook, float(act_scale), int(act_zero_point), bias, out_channels, cin_per_group,
+        kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w, dil_h, dil_w, int(groups),
+    )
+
+
+# ---------------------------------------------------------------------------
+# generalised operators (no reference counterpart: the reference is W4A4 only)
+# ---------------------------------------------------------------------------
+
+VARIANTS = {"auto": 0, "small_m": 1, "mfma": 2}
+
+
+def pack_bits(indices: torch.Tensor, bits: int) -> torch.Tensor:
+    require_extension()
+    return torch.ops.dimq.pack_bits(indices, int(bits))
+
+
+def unpack_bits(packed: torch.Tensor, numel: int, bits: int) -> torch.Tensor:
+    require_extension()
+    return torch.ops.dimq.unpack_bits(packed, int(numel), int(bits))
+
+
+def hard_quantize(w: torch.Tensor, centers: torch.Tensor, per_channel: bool = False):
+    """Nearest-centre (indices, values), quant/dimq.py:197-221 semantics."""
+    require_extension()
+    return torch.ops.dimq.hard_quantize(w, centers, bool(per_channel))
+
+
+def build_product_table_grouped(codebook: torch.Tensor, act_scale: float, act_zero_point: int) -> torch.Tensor:
+    require_extension()
+    return torch.ops.dimq.build_product_table_grouped(codebook, float(act_scale), int(act_zero_point))
+
+
+def dimq_linear_codebook(
+    x: torch.Tensor,
+    packed_weight: torch.Tensor,
+    codebook: torch.Tensor,
+    bits: int,
+    bias: torch.Tensor | None,
+    out_features: int,
+    in_features: int,
+    *,
+    out_dtype: torch.dtype | None = None,
+    variant: str = "auto",
+) -> torch.Tensor:
+    """y = x @ W_hat^T + bias with W_hat[n, k] = codebook[n or 0, idx[n, k]]."""
+    require_extension()
+    return torch.ops.dimq.linear_codebook(
+        x, packed_weight, codebook, int(bits), bias, int(out_features), int(in_features), out_dtype,
+        VARIANTS[variant],
+    )
+
+
+def dimq_conv2d_codebook(
+    x: torch.Tensor,
+    packed_weight: torch.Tensor,
+    codebook: torch.Tensor,
+    bits: int,
+    bias: torch.Tensor | None,
+    weight_shape: Sequence[int],
+    stride: Sequence[int],
+    padding: Sequence[int],
+    dilation: Sequence[int],
+    groups: int,
+    *,
+    out_dtype: torch.dtype | None = None,
+    variant: str = "auto",
+) -> torch.Tensor:
+    """Weight-only codebook conv2d; NCHW or channels_last input, output in the same memory format."""
+    require_extension()
+    out_channels, cin_per_group, kernel_h, kernel_w = [int(v) for v in weight_shape]
+    stride_h, stride_w = _pair(stride)
+    pad_h, pad_w = _pair(padding)
+    dil_h, dil_w = _pair(dilation)
+    return torch.ops.dimq.conv2d_codebook(
+        x, packed_weight, codebook, int(bits), bias, out_channels, cin_per_group, kernel_h, kernel_w, stride_h,
+        stride_w, pad_h, pad_w, dil_h, dil_w, int(groups), out_dtype, VARIANTS[variant],
+    )
+
+
+def _pair(value: Sequence[int] | int) -> tuple[int, int]:
+    if isinstance(value, int):
+        return int(value), int(value)
+    if len(value) != 2:
+        raise ValueError(f"expected pair, got {value!r}")
+    return int(value[0]), int(value[1])

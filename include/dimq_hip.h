@@ -1,0 +1,159 @@
+/*
+ * dimq_hip.h — C ABI of libdimq_hip.so, the MI355X (gfx950) DIMQ packed-index
+ * inference library.
+ *
+ * Every entry point takes raw device pointers, element counts and a HIP stream
+ * (hipStream_t passed as void*; NULL = the legacy default stream), launches
+ * asynchronously on that stream, and returns DIMQ_OK (0) or an error code.  On
+ * error dimq_last_error() returns a thread-local message; the message text of
+ * the reference's TORCH_CHECKs is kept where a reference check exists.  No
+ * entry point allocates device memory: outputs are caller-allocated.
+ *
+ * Citations are relative to the fengchao32/DIMQ tree.  The reference binds its
+ * six ops through TORCH_LIBRARY(dimq) (dimq_cuda_backend/csrc/dimq_ops.cpp:37-53);
+ * the dimq_* functions in section 1 replace those CUDA impls one for one, with
+ * the tensor arguments flattened to pointer + size + dtype.
+ */
+#ifndef DIMQ_HIP_H_
+#define DIMQ_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types of tensors crossing the boundary. */
+enum dimq_dtype {
+  DIMQ_F32 = 0,
+  DIMQ_F16 = 1,
+  DIMQ_BF16 = 2,
+  DIMQ_F64 = 3,
+  DIMQ_U8 = 4
+};
+
+/* Return codes. */
+enum dimq_status {
+  DIMQ_OK = 0,
+  DIMQ_ERR_INVALID = 1,     /* argument check failed (reference: TORCH_CHECK) */
+  DIMQ_ERR_UNSUPPORTED = 2, /* dtype / bit-width / layout not implemented */
+  DIMQ_ERR_HIP = 3          /* HIP runtime error at launch */
+};
+
+/* Conv activation layouts. */
+enum dimq_layout { DIMQ_NCHW = 0, DIMQ_NHWC = 1 };
+
+/* Kernel variant selector for the weight-only ops. */
+enum dimq_variant {
+  DIMQ_VARIANT_AUTO = 0,
+  DIMQ_VARIANT_SMALL_M = 1, /* register-codebook gather, 16-row tiles (decode / GEMV) */
+  DIMQ_VARIANT_MFMA = 2     /* dequant-to-fp16 + MFMA, 64/128-row tiles */
+};
+
+/* Thread-local message of the last failing call on this thread. */
+const char* dimq_last_error(void);
+/* ABI version of this header (bumped on incompatible changes). */
+int dimq_abi_version(void);
+
+/* ---------------------------------------------------------------------------
+ * 1. The reference's ops (dimq_cuda_backend/csrc/dimq_ops.cpp:38-43)
+ * ------------------------------------------------------------------------- */
+
+/* pack_u4: replaces pack_u4_cuda (csrc/dimq_pack.cu:52-67).  packed receives
+ * (numel+1)/2 bytes, packed[j] = idx[2j]&15 | (idx[2j+1]&15)<<4. */
+int dimq_pack_u4(const uint8_t* indices, int64_t numel, uint8_t* packed, void* stream);
+
+/* unpack_u4: replaces unpack_u4_cuda (csrc/dimq_pack.cu:69-85). */
+int dimq_unpack_u4(const uint8_t* packed, int64_t packed_numel, int64_t numel, uint8_t* indices,
+                   void* stream);
+
+/* quantize_activation_u4: replaces quantize_activation_u4_cuda
+ * (csrc/dimq_pack.cu:87-109).  x_dtype in {F32, F16, BF16, F64}; out u8. */
+int dimq_quantize_activation_u4(const void* x, int x_dtype, int64_t numel, double act_scale,
+                                int64_t act_zp, uint8_t* out, void* stream);
+
+/* build_product_table: replaces build_product_table_cuda
+ * (csrc/dimq_product_table.cu:29-46).  table receives [16,16] fp32. */
+int dimq_build_product_table(const void* codebook, int cb_dtype, int64_t cb_numel, double act_scale,
+                             int64_t act_zp, float* table, void* stream);
+
+/* linear_lut: replaces linear_lut_cuda (csrc/dimq_gemm_lut.cu:58-117).
+ * x [M, in_features] row-major; packed_w u4 [out_features*in_features];
+ * 16-entry per-layer codebook; bias (nullable) [out_features];
+ * y [M, out_features] fp32.  y = sum_k P[w,a] + bias, P = C[w]*s*(a-zp). */
+int dimq_linear_lut(const void* x, int x_dtype, int64_t M, const uint8_t* packed_w, int64_t packed_numel,
+                    const void* codebook, int cb_dtype, int64_t cb_numel, double act_scale, int64_t act_zp,
+                    const void* bias, int bias_dtype, int64_t bias_numel, int64_t out_features,
+                    int64_t in_features, float* y, void* stream);
+
+/* conv2d_lut: replaces conv2d_lut_cuda (csrc/dimq_conv2d_lut.cu:90-186).
+ * x NCHW [B,C,H,W]; packed_w u4 in conv_kcrs order [OC, C/groups, KH, KW];
+ * y NCHW fp32 [B, OC, OH, OW]. */
+int dimq_conv2d_lut(const void* x, int x_dtype, int64_t B, int64_t C, int64_t H, int64_t W,
+                    const uint8_t* packed_w, int64_t packed_numel, const void* codebook, int cb_dtype,
+                    int64_t cb_numel, double act_scale, int64_t act_zp, const void* bias, int bias_dtype,
+                    int64_t bias_numel, int64_t out_channels, int64_t in_channels_per_group, int64_t kernel_h,
+                    int64_t kernel_w, int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                    int64_t dilation_h, int64_t dilation_w, int64_t groups, float* y, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * 2. Generalised ops for the BASELINE configurations: b in {2,3,4,8} bits,
+ *    per-layer or per-output-channel codebooks, weight-only GEMM/conv.
+ *    The reference has no kernel for these (it is W4A4-only); their
+ *    semantics are those of dequantize-then-F.linear / F.conv2d
+ *    (dimq_backend/reference.py:47-56,91-144; quant/dimq_wrapper.py:189-197,237-240).
+ * ------------------------------------------------------------------------- */
+
+/* LSB-first b-bit packing, generalising pack_u4_indices
+ * (dimq_backend/export.py:38-55): index i occupies bits [b*i, b*i+b).
+ * packed receives ceil(numel*bits/8) bytes; values are masked to b bits. */
+int dimq_pack_bits(const uint8_t* indices, int64_t numel, int bits, uint8_t* packed, void* stream);
+
+/* Inverse of dimq_pack_bits, generalising unpack_u4_indices (export.py:58-78). */
+int dimq_unpack_bits(const uint8_t* packed, int64_t packed_numel, int64_t numel, int bits,
+                     uint8_t* indices, void* stream);
+
+/* Nearest-centre assignment, quant/dimq.py:197-221 (hard_quantize_weight) and
+ * dimq_backend/export.py:24-35: idx = argmin_j (w - c_j)^2 in fp32, first
+ * minimum wins; a NaN distance wins (first NaN), as torch.argmin.
+ * w [rows, row_len] (w_dtype F32/F16/BF16); centers fp32 [rows, n_centers]
+ * when per_channel, else [n_centers] shared by every row; n_centers <= 256.
+ * values (nullable) receives centers[idx] in w_dtype. */
+int dimq_hard_quantize(const void* w, int w_dtype, int64_t rows, int64_t row_len, const float* centers,
+                       int64_t n_centers, int per_channel, uint8_t* indices, void* values, void* stream);
+
+/* Per-channel product table, generalising build_product_table
+ * (dimq_backend/reference.py:32-44): table [G, Kc, 16] fp32,
+ * table[g][w][a] = C[g][w] * (s * (a - zp)). */
+int dimq_build_product_table_grouped(const void* codebook, int cb_dtype, int64_t groups, int64_t kc,
+                                     double act_scale, int64_t act_zp, float* table, void* stream);
+
+/* Weight-only codebook Linear: y[M,N] = x[M,K] . W_hat[N,K]^T + bias.
+ * packed_w: LSB-first b-bit stream of the row-major [N,K] index matrix;
+ * codebook [cb_rows, cb_size] with cb_rows in {1 (per layer), N (per output
+ * channel)} and cb_size <= 2^bits; x_dtype/y_dtype in {F32, F16, BF16};
+ * bias (nullable, any float dtype) [N]; fp32 accumulation.
+ * Inputs are rounded to fp16 for the matrix cores (exact for fp16 and for
+ * bf16 values within the fp16 range; fp32 is rounded to nearest); the
+ * codebook is scaled per row by a power of two before rounding to fp16. */
+int dimq_linear_codebook(const void* x, int x_dtype, int64_t M, int64_t K, const uint8_t* packed_w,
+                         int64_t packed_numel, int bits, const void* codebook, int cb_dtype, int64_t cb_rows,
+                         int64_t cb_size, const void* bias, int bias_dtype, int64_t N, void* y, int y_dtype,
+                         int variant, void* stream);
+
+/* Weight-only codebook Conv2d (zero padding, stride, dilation, groups).
+ * x [B,C,H,W] in x_layout (NCHW or NHWC memory order); y [B,OC,OH,OW] in
+ * y_layout; packed_w: b-bit stream of the conv_kcrs index tensor
+ * [OC, C/groups, KH, KW] (dimq_backend/export.py:232). */
+int dimq_conv2d_codebook(const void* x, int x_dtype, int x_layout, int64_t B, int64_t C, int64_t H, int64_t W,
+                         const uint8_t* packed_w, int64_t packed_numel, int bits, const void* codebook,
+                         int cb_dtype, int64_t cb_rows, int64_t cb_size, const void* bias, int bias_dtype,
+                         int64_t out_channels, int64_t kernel_h, int64_t kernel_w, int64_t stride_h,
+                         int64_t stride_w, int64_t pad_h, int64_t pad_w, int64_t dilation_h, int64_t dilation_w,
+                         int64_t groups, void* y, int y_dtype, int y_layout, int variant, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DIMQ_HIP_H_ */

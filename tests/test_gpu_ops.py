@@ -1,0 +1,334 @@
+"""GPU parity: every HIP entry point against the CPU oracle on the same inputs.
+
+Inputs are generated on the CPU with seeded torch.Generator and copied to the
+device.  Integer work (codec, index assignment, activation codes) must be
+bit-exact; W4A4 LUT ops follow the reference's tolerance (rtol = atol = 1e-5,
+dimq_cuda_backend/tests/test_cuda_ops.py:64,93); weight-only GEMM/conv must
+satisfy max|y - ref| / max|ref| <= 2e-3 against dequantize-then-F.linear /
+F.conv2d in fp32 on the CPU.
+"""
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.conftest import announce
+
+pytestmark = pytest.mark.gpu
+GOLD = Path(__file__).resolve().parent / "golden"
+TOL = 2e-3
+
+
+def _ops():
+    from dimq_amd import ops
+
+    return ops
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+# ---------------------------------------------------------------- codec
+def test_codec_golden_vectors_gpu(gpu):
+    ops = _ops()
+    cases = json.loads((GOLD / "codec_vectors.json").read_text())
+    for c in cases:
+        announce(f"codec golden bits={c['bits']} n={len(c['indices'])}")
+        idx = torch.tensor(c["indices"], dtype=torch.uint8, device=gpu)
+        packed = ops.pack_bits(idx, c["bits"])
+        assert packed.cpu().numpy().tobytes().hex(" ") == c["packed"], (c["bits"], len(c["indices"]))
+        back = ops.unpack_bits(packed, idx.numel(), c["bits"])
+        assert torch.equal(back, idx)
+        if c["bits"] == 4:
+            assert torch.equal(ops.pack_u4(idx), packed)
+            assert torch.equal(ops.unpack_u4(packed, idx.numel()), idx)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 8])
+def test_codec_random_sizes_and_offsets(gpu, bits):
+    ops = _ops()
+    g = _gen(bits)
+    for n in (0, 1, 31, 32, 33, 1000, 4097, 123457):
+        announce(f"codec random bits={bits} n={n}")
+        idx = torch.randint(0, 1 << bits, (n + 5,), generator=g, dtype=torch.uint8)
+        for off in (0, 3):  # an offset view exercises the unaligned path
+            sub = idx[off:off + n]
+            packed = ops.pack_bits(sub.to(gpu), bits).cpu()
+            assert np.array_equal(packed.numpy(), oracle.pack_bits(sub, bits))
+            big = torch.zeros(packed.numel() + 7, dtype=torch.uint8)
+            big[off:off + packed.numel()] = packed
+            back = ops.unpack_bits(big[off:off + packed.numel()].to(gpu), n, bits).cpu()
+            assert torch.equal(back, sub)
+
+
+def test_codec_masks_out_of_range_values(gpu):
+    ops = _ops()
+    idx = torch.tensor([0x1F, 0x2E, 0xFF], dtype=torch.uint8, device=gpu)
+    assert ops.pack_u4(idx).cpu().tolist() == [0xEF, 0x0F]
+
+
+def test_codec_errors(gpu):
+    ops = _ops()
+    with pytest.raises(RuntimeError, match="packed tensor is too small"):
+        ops.unpack_u4(torch.zeros(2, dtype=torch.uint8, device=gpu), 5)
+    with pytest.raises(RuntimeError, match="uint8"):
+        ops.pack_u4(torch.zeros(4, dtype=torch.int32, device=gpu))
+    with pytest.raises(RuntimeError, match="bits must be one of"):
+        ops.pack_bits(torch.zeros(4, dtype=torch.uint8, device=gpu), 5)
+
+
+def test_codec_stress_2p27_3bit_round_trip(gpu):
+    """cfg5: 2^27 random 3-bit indices, bit-exact pack/unpack round trip; packed bytes checked on a slice."""
+    ops = _ops()
+    announce("codec stress 2^27 3-bit")
+    n = 1 << 27
+    idx = torch.randint(0, 8, (n,), generator=_gen(5), dtype=torch.uint8)
+    d = idx.to(gpu)
+    packed = ops.pack_bits(d, 3)
+    assert packed.numel() == n * 3 // 8
+    back = ops.unpack_bits(packed, n, 3)
+    assert torch.equal(back, d)
+    sl = slice(1 << 20, (1 << 20) + 4096)  # a 4096-index window on a 3-byte boundary
+    ref = oracle.pack_bits(idx[sl], 3)
+    byte0 = (1 << 20) * 3 // 8
+    assert np.array_equal(packed[byte0:byte0 + ref.size].cpu().numpy(), ref)
+
+
+# ---------------------------------------------------------------- hard quantization
+def test_hard_quantize_golden_and_random(gpu):
+    ops = _ops()
+    for c in json.loads((GOLD / "hardquant_vectors.json").read_text()):
+        announce(f"hardquant golden {c['source']}")
+        idx, val = ops.hard_quantize(torch.tensor(c["w"], device=gpu), torch.tensor(c["centers"], device=gpu))
+        assert idx.cpu().tolist() == c["idx"], c["source"]
+    g = _gen(11)
+    for K in (4, 8, 16, 256):
+        for per_channel in (False, True):
+            announce(f"hardquant random K={K} pc={per_channel}")
+            w = torch.randn(37, 301, generator=g) * 0.02
+            c = torch.randn(37 if per_channel else 1, K, generator=g) * 0.02
+            cc = c if per_channel else c[0]
+            idx, val = ops.hard_quantize(w.to(gpu), cc.to(gpu), per_channel)
+            want_idx, want_val = oracle.hard_quantize(w, cc, per_channel=per_channel)
+            assert np.array_equal(idx.cpu().numpy(), want_idx)
+            assert np.array_equal(val.cpu().numpy(), want_val)
+
+
+def test_hard_quantize_nan_inf(gpu):
+    ops = _ops()
+    w = torch.tensor([0.5, float("nan"), 2.0, float("inf")])
+    for c in (torch.tensor([0.0, float("nan"), 1.0, 3.0]), torch.tensor([0.0, 1.0, 3.0])):
+        idx, _ = ops.hard_quantize(w.to(gpu), c.to(gpu), False)
+        assert idx.cpu().tolist() == ((w[:, None] - c[None, :]) ** 2).argmin(1).tolist()
+
+
+def test_hard_quantize_half_inputs(gpu):
+    ops = _ops()
+    w = (torch.randn(64, 50, generator=_gen(3)) * 0.1)
+    c = torch.randn(64, 16, generator=_gen(4)) * 0.1
+    for dt in (torch.float16, torch.bfloat16):
+        idx, val = ops.hard_quantize(w.to(dt).to(gpu), c.to(gpu), True)
+        want, wv = oracle.hard_quantize(w.to(dt).float(), c, per_channel=True)
+        assert np.array_equal(idx.cpu().numpy(), want)
+        assert torch.equal(val.cpu(), torch.from_numpy(wv).to(dt))
+
+
+# ---------------------------------------------------------------- activation quantization / product table
+def test_quantize_activation_golden_and_dtypes(gpu):
+    ops = _ops()
+    for c in json.loads((GOLD / "actquant_vectors.json").read_text()):
+        q = ops.quantize_activation_u4(torch.tensor(c["x"], device=gpu), c["scale"], c["zp"])
+        assert q.cpu().tolist() == c["q"], c["source"]
+    x = torch.randn(3, 1001, generator=_gen(2)) * 2
+    for dt in (torch.float32, torch.float16, torch.bfloat16, torch.float64):
+        q = ops.quantize_activation_u4(x.to(dt).to(gpu), 0.2, 7)
+        assert q.shape == x.shape
+        assert np.array_equal(q.cpu().numpy(), oracle.quantize_act_u4(x.to(dt).float(), 0.2, 7))
+    with pytest.raises(RuntimeError, match="act_zero_point must be in"):
+        ops.quantize_activation_u4(x.to(gpu), 0.2, 16)
+    with pytest.raises(RuntimeError, match="act_scale must be positive"):
+        ops.quantize_activation_u4(x.to(gpu), 0.0, 3)
+
+
+def test_product_table(gpu):
+    ops = _ops()
+    c = json.loads((GOLD / "product_table_vectors.json").read_text())[0]
+    cb = torch.linspace(-1.0, 1.0, 16, dtype=torch.float16)
+    t = ops.build_product_table(cb.to(gpu), 0.125, 8).cpu()
+    assert torch.equal(t, torch.tensor(c["table"]))
+    g = torch.randn(7, 16, generator=_gen(8))
+    tg = ops.build_product_table_grouped(g.to(gpu), 0.37, 5).cpu().numpy()
+    assert np.array_equal(tg, oracle.product_table(g, 0.37, 5))
+    with pytest.raises(RuntimeError, match="exactly 16 codebook entries"):
+        ops.build_product_table(torch.zeros(8, device=gpu), 0.1, 3)
+
+
+# ---------------------------------------------------------------- W4A4 LUT ops (the reference ops)
+def test_linear_lut_reference_recipe(gpu):
+    ops = _ops()
+    r = json.loads((GOLD / "w4a4_recipes.json").read_text())["linear"]
+    idx = np.array(r["indices"], np.uint8)
+    packed = torch.from_numpy(oracle.pack_bits(idx, 4))
+    y = ops.dimq_linear_lut(torch.tensor(r["x"], device=gpu), packed.to(gpu), torch.tensor(r["codebook"], device=gpu),
+                            r["scale"], r["zp"], torch.tensor(r["bias"], device=gpu), 6, 11)
+    torch.testing.assert_close(y.cpu(), torch.tensor(r["y"]), rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("M,N,K", [(4, 11, 6), (1, 64, 128), (37, 130, 96), (200, 300, 768), (64, 33, 250)])
+@pytest.mark.parametrize("xdt", [torch.float32, torch.float16, torch.float64])
+def test_linear_lut_vs_oracle(gpu, M, N, K, xdt):
+    ops = _ops()
+    announce(f"linear_lut M={M} N={N} K={K} {xdt}")
+    g = _gen(M * 7 + N)
+    x = torch.randn(M, K, generator=g).to(xdt)
+    idx = torch.randint(0, 16, (N, K), generator=g, dtype=torch.uint8)
+    cb = torch.linspace(-0.5, 0.5, 16) + 0.01 * torch.randn(16, generator=g)
+    bias = torch.randn(N, generator=g)
+    packed = torch.from_numpy(oracle.pack_bits(idx, 4))
+    y = ops.dimq_linear_lut(x.to(gpu), packed.to(gpu), cb.to(gpu), 0.2, 7, bias.to(gpu), N, K)
+    ref = oracle.linear_lut(x.float(), packed, cb, 0.2, 7, bias, N, K)
+    torch.testing.assert_close(y.cpu(), torch.from_numpy(ref), rtol=1e-5, atol=1e-5)
+
+
+def test_linear_lut_leading_dims_and_errors(gpu):
+    ops = _ops()
+    x = torch.randn(2, 3, 32, generator=_gen(1))
+    idx = torch.randint(0, 16, (8, 32), generator=_gen(2), dtype=torch.uint8)
+    packed = torch.from_numpy(oracle.pack_bits(idx, 4)).to(gpu)
+    cb = torch.linspace(-1, 1, 16, device=gpu)
+    y = ops.dimq_linear_lut(x.to(gpu), packed, cb, 0.25, 8, None, 8, 32)
+    assert y.shape == (2, 3, 8) and y.dtype == torch.float32
+    ref = oracle.linear_lut(x, packed.cpu(), cb.cpu(), 0.25, 8, None, 8, 32)
+    torch.testing.assert_close(y.cpu(), torch.from_numpy(ref), rtol=1e-5, atol=1e-5)
+    with pytest.raises(RuntimeError, match="codebook must have 16 entries for W4"):
+        ops.dimq_linear_lut(x.to(gpu), packed, cb[:8], 0.25, 8, None, 8, 32)
+    with pytest.raises(RuntimeError, match="packed_weight is too small"):
+        ops.dimq_linear_lut(x.to(gpu), packed[:10], cb, 0.25, 8, None, 8, 32)
+    with pytest.raises(RuntimeError, match="input last dimension must equal in_features"):
+        ops.dimq_linear_lut(x.to(gpu), packed, cb, 0.25, 8, None, 16, 16)
+
+
+def test_conv2d_lut_reference_recipe(gpu):
+    ops = _ops()
+    r = json.loads((GOLD / "w4a4_recipes.json").read_text())["conv2d"]
+    idx = np.array(r["indices"], np.uint8)
+    packed = torch.from_numpy(oracle.pack_bits(idx, 4))
+    y = ops.dimq_conv2d_lut(torch.tensor(r["x"], device=gpu), packed.to(gpu), torch.tensor(r["codebook"], device=gpu),
+                            r["scale"], r["zp"], torch.tensor(r["bias"], device=gpu), idx.shape, r["stride"],
+                            r["padding"], r["dilation"], r["groups"])
+    torch.testing.assert_close(y.cpu(), torch.tensor(r["y"]), rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("case", [
+    dict(B=2, C=4, H=9, W=8, OC=6, KH=3, KW=3, s=(1, 1), p=(1, 1), d=(1, 1), g=1),
+    dict(B=1, C=6, H=11, W=7, OC=4, KH=3, KW=2, s=(2, 1), p=(1, 0), d=(1, 2), g=2),
+    dict(B=3, C=16, H=8, W=8, OC=32, KH=1, KW=1, s=(2, 2), p=(0, 0), d=(1, 1), g=1),
+])
+def test_conv2d_lut_vs_oracle(gpu, case):
+    ops = _ops()
+    announce(f"conv2d_lut {case}")
+    g = _gen(case["C"] * 13 + case["OC"])
+    x = torch.randn(case["B"], case["C"], case["H"], case["W"], generator=g)
+    shape = (case["OC"], case["C"] // case["g"], case["KH"], case["KW"])
+    idx = torch.randint(0, 16, shape, generator=g, dtype=torch.uint8)
+    cb = torch.linspace(-0.7, 0.6, 16)
+    bias = torch.randn(case["OC"], generator=g)
+    packed = torch.from_numpy(oracle.pack_bits(idx, 4))
+    y = ops.dimq_conv2d_lut(x.to(gpu), packed.to(gpu), cb.to(gpu), 0.25, 7, bias.to(gpu), shape, case["s"], case["p"],
+                            case["d"], case["g"])
+    ref = oracle.conv2d_lut(x, packed, cb, 0.25, 7, bias, shape, case["s"], case["p"], case["d"], case["g"])
+    torch.testing.assert_close(y.cpu(), torch.from_numpy(ref), rtol=1e-5, atol=1e-5)
+
+
+# ---------------------------------------------------------------- weight-only codebook Linear
+def _codebook_case(N, K, bits, per_channel, g, cb_entries=None):
+    Kc = cb_entries or (1 << bits)
+    rows = N if per_channel else 1
+    cb = (torch.randn(rows, Kc, generator=g) * 0.05).sort(dim=1).values
+    idx = torch.randint(0, Kc, (N, K), generator=g, dtype=torch.uint8)
+    packed = torch.from_numpy(oracle.pack_bits(idx, bits))
+    return cb if per_channel else cb[0], idx, packed
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 8])
+@pytest.mark.parametrize("M,N,K", [(1, 64, 128), (3, 5, 13), (16, 200, 256), (33, 96, 160), (300, 260, 512)])
+def test_linear_codebook_bits_shapes(gpu, bits, M, N, K):
+    ops = _ops()
+    for per_channel in (True, False):
+        announce(f"linear_codebook bits={bits} M={M} N={N} K={K} pc={per_channel}")
+        g = _gen(bits * 1000 + M + N + K)
+        cb, idx, packed = _codebook_case(N, K, bits, per_channel, g)
+        x = torch.randn(M, K, generator=g)
+        bias = torch.randn(N, generator=g) * 0.1
+        y = ops.dimq_linear_codebook(x.to(gpu), packed.to(gpu), cb.to(gpu), bits, bias.to(gpu), N, K,
+                                     out_dtype=torch.float32)
+        ref = oracle.linear_dequant_reference(x, packed, bits, cb, N, K, bias)
+        assert oracle.rel_err(y, ref) <= TOL, (bits, M, N, K, per_channel, oracle.rel_err(y, ref))
+
+
+@pytest.mark.parametrize("xdt", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("odt", [torch.float32, torch.float16, torch.bfloat16])
+def test_linear_codebook_dtypes(gpu, xdt, odt):
+    ops = _ops()
+    g = _gen(77)
+    N, K, M = 192, 384, 130
+    cb, idx, packed = _codebook_case(N, K, 4, True, g)
+    x = torch.randn(M, K, generator=g).to(xdt)
+    bias = (torch.randn(N, generator=g) * 0.1).to(xdt)
+    for variant in ("auto", "small_m", "mfma"):
+        announce(f"linear_codebook dtypes {xdt}->{odt} {variant}")
+        y = ops.dimq_linear_codebook(x.to(gpu), packed.to(gpu), cb.to(gpu).to(xdt), 4, bias.to(gpu), N, K,
+                                     out_dtype=odt, variant=variant)
+        assert y.dtype == odt
+        ref = oracle.linear_dequant_reference(x.float(), packed, 4, cb.to(xdt).float(), N, K, bias.float())
+        tol = TOL if odt == torch.float32 else 4e-3  # a 16-bit output alone rounds at 2^-9 relative
+        assert oracle.rel_err(y.float(), ref) <= tol, (xdt, odt, variant, oracle.rel_err(y.float(), ref))
+
+
+def test_linear_codebook_small_codebook_and_errors(gpu):
+    ops = _ops()
+    g = _gen(5)
+    cb, idx, packed = _codebook_case(40, 64, 3, True, g, cb_entries=5)  # fewer entries than 2^b
+    x = torch.randn(7, 64, generator=g)
+    y = ops.dimq_linear_codebook(x.to(gpu), packed.to(gpu), cb.to(gpu), 3, None, 40, 64)
+    ref = oracle.linear_dequant_reference(x, packed, 3, cb, 40, 64)
+    assert oracle.rel_err(y, ref) <= TOL
+    with pytest.raises(RuntimeError, match="packed_weight is too small"):
+        ops.dimq_linear_codebook(x.to(gpu), packed[:5].to(gpu), cb.to(gpu), 3, None, 40, 64)
+    with pytest.raises(RuntimeError, match="codebook rows must hold"):
+        ops.dimq_linear_codebook(x.to(gpu), packed.to(gpu), torch.zeros(40, 9, device=gpu), 3, None, 40, 64)
+
+
+# ---------------------------------------------------------------- weight-only codebook Conv2d
+@pytest.mark.parametrize("case", [
+    dict(B=2, C=16, H=10, W=9, OC=32, KH=3, KW=3, s=(1, 1), p=(1, 1), d=(1, 1), g=1, bits=2),
+    dict(B=1, C=8, H=13, W=11, OC=8, KH=3, KW=3, s=(2, 2), p=(1, 1), d=(1, 1), g=1, bits=4),
+    dict(B=2, C=3, H=23, W=23, OC=16, KH=7, KW=7, s=(2, 2), p=(3, 3), d=(1, 1), g=1, bits=8),
+    dict(B=2, C=12, H=9, W=9, OC=16, KH=1, KW=1, s=(2, 2), p=(0, 0), d=(1, 1), g=1, bits=4),
+    dict(B=1, C=8, H=9, W=10, OC=12, KH=3, KW=3, s=(1, 2), p=(2, 1), d=(2, 1), g=4, bits=3),
+])
+@pytest.mark.parametrize("layout", ["nchw", "nhwc"])
+def test_conv2d_codebook_vs_oracle(gpu, case, layout):
+    ops = _ops()
+    announce(f"conv2d_codebook {case} {layout}")
+    g = _gen(case["C"] * 31 + case["OC"] + case["bits"])
+    shape = (case["OC"], case["C"] // case["g"], case["KH"], case["KW"])
+    x = torch.randn(case["B"], case["C"], case["H"], case["W"], generator=g).half()
+    cb, idx, packed = _codebook_case(case["OC"], int(np.prod(shape[1:])), case["bits"], True, g)
+    bias = torch.randn(case["OC"], generator=g) * 0.1
+    xd = x.to(gpu)
+    if layout == "nhwc":
+        xd = xd.to(memory_format=torch.channels_last)
+    y = ops.dimq_conv2d_codebook(xd, packed.to(gpu), cb.to(gpu), case["bits"], bias.to(gpu), shape, case["s"],
+                                 case["p"], case["d"], case["g"], out_dtype=torch.float32)
+    if layout == "nhwc":
+        assert y.is_contiguous(memory_format=torch.channels_last)
+    ref = oracle.conv2d_dequant_reference(x.float(), packed, case["bits"], cb, shape, bias, case["s"], case["p"],
+                                          case["d"], case["g"])
+    assert y.shape == ref.shape
+    assert oracle.rel_err(y.float(), ref) <= TOL, oracle.rel_err(y.float(), ref)

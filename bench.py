@@ -1,0 +1,370 @@
+"""Benchmark of the DIMQ packed-index hot path on one MI355X.
+
+Default workload: BASELINE configs[1] (cfg2), the ResNet-18 layer1 3x3 conv
+with a 2-bit per-output-channel codebook: x fp16 [32,64,56,56] (ReLU of
+N(0,1)), W [64,64,3,3] Kaiming-normal, stride 1, pad 1, no bias, y fp32.
+One step = one LUT conv launch over one batch.  Other workloads:
+``--config cfg1|cfg5|codec``.
+
+Timing: inputs are resident in HBM before the timed region; R buffer sets
+(> 512 MB in total, so the 256 MB MALL cannot serve repeats) are rotated; the
+steps are captured once in a HIP graph (torch.cuda.CUDAGraph) so the GPU runs
+them back to back, and HIP events on the launch stream bracket the K timed
+steps.  Prints ONE JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+METRIC = "LUT-GEMM/conv TFLOP/s + % roofline; ViT-B/16 4-bit bs64 images/s"
+
+
+# ---------------------------------------------------------------------------
+# workloads
+# ---------------------------------------------------------------------------
+
+def _conv_weight_cfg2(g):
+    w = torch.randn(64, 64, 3, 3, generator=g) * math.sqrt(2.0 / 576.0)  # kaiming_normal_, fan_in 576
+    return w
+
+
+def make_cfg2(dev, rotations):
+    from dimq_amd import ops
+    from dimq_amd.codebook import assign_indices, init_centers_per_channel
+    from dimq_amd.export import pack_indices
+
+    g = torch.Generator().manual_seed(1)
+    w = _conv_weight_cfg2(g)
+    centers = init_centers_per_channel(w, 4)                      # [64, 4] fp32
+    idx = assign_indices(w, centers)                              # GPU kernel
+    packed = pack_indices(idx, 2).to(dev)                         # GPU kernel
+    prepared = ops.prepare_conv_weight(packed, 2, (64, 64, 3, 3))  # one-time kernel-layout repack
+    cb = centers.to(dev)
+    xs = [torch.relu(torch.randn(32, 64, 56, 56, generator=g)).half().to(dev) for _ in range(rotations)]
+
+    def step(i):
+        return ops.dimq_conv2d_codebook(xs[i], packed, cb, 2, None, (64, 64, 3, 3), (1, 1), (1, 1), (1, 1), 1,
+                                        out_dtype=torch.float32, prepared_weight=prepared)
+
+    x_bytes = 32 * 64 * 56 * 56 * 2
+    y_bytes = 32 * 64 * 56 * 56 * 4
+    alg_bytes = x_bytes + y_bytes + packed.numel() + cb.numel() * 4
+    flops = 2.0 * 32 * 56 * 56 * 64 * 64 * 9
+
+    def cpu_step(sample_batch):
+        import oracle
+        return oracle.conv2d_dequant_reference(xs[0][:sample_batch].cpu().float(), packed.cpu(), 2, centers,
+                                               (64, 64, 3, 3), None, 1, 1, 1, 1)
+
+    def check():
+        import oracle
+        y = step(0)
+        ref = oracle.conv2d_dequant_reference(xs[0].cpu().float(), packed.cpu(), 2, centers, (64, 64, 3, 3), None,
+                                              1, 1, 1, 1)
+        return oracle.rel_err(y, ref)
+
+    return dict(
+        name="cfg2",
+        workload="ResNet-18 layer1 conv3x3: x fp16 [32,64,56,56] (ReLU N(0,1)), W [64,64,3,3] Kaiming-normal, "
+                 "2-bit per-output-channel codebook (4 centroids/row, quantile init), stride 1, pad 1, no bias, "
+                 "y fp32 NCHW",
+        step=step, flops=flops, alg_bytes=alg_bytes, bound="hbm", dtype="fp16",
+        unit="TFLOP/s", per_step_units=flops / 1e12, cpu_step=cpu_step, cpu_full_batch=32, check=check,
+        extra_config={"global_batch": 32, "in_shape": [32, 64, 56, 56], "weight_shape": [64, 64, 3, 3],
+                      "bits": 2, "codebook": "per_channel"},
+        per_set_bytes=x_bytes + y_bytes,
+    )
+
+
+def make_cfg1(dev, rotations):
+    from dimq_amd import ops
+    from dimq_amd.codebook import assign_indices, init_centers_per_channel
+    from dimq_amd.export import pack_indices
+
+    g = torch.Generator().manual_seed(0)
+    w = torch.randn(3072, 768, generator=g) * 0.02
+    b = torch.randn(3072, generator=g) * 0.02
+    centers = init_centers_per_channel(w, 16)
+    packed = pack_indices(assign_indices(w, centers), 4).to(dev)
+    cb = centers.to(dev)
+    bias = b.to(dev)
+    xs = [torch.randn(1576, 768, generator=g).to(dev) for _ in range(rotations)]
+
+    def step(i):
+        return ops.dimq_linear_codebook(xs[i], packed, cb, 4, bias, 3072, 768, out_dtype=torch.float32)
+
+    alg_bytes = 1576 * 768 * 4 + packed.numel() + cb.numel() * 4 + 3072 * 4 + 1576 * 3072 * 4
+    flops = 2.0 * 1576 * 3072 * 768
+
+    def cpu_step(sample_rows):
+        import oracle
+        return oracle.linear_dequant_reference(xs[0][:sample_rows].cpu(), packed.cpu(), 4, centers, 3072, 768, b)
+
+    def check():
+        import oracle
+        return oracle.rel_err(step(0), oracle.linear_dequant_reference(xs[0].cpu(), packed.cpu(), 4, centers, 3072,
+                                                                       768, b))
+
+    return dict(
+        name="cfg1",
+        workload="ViT-B/16 MLP fc1 Linear: X fp32 [1576,768], W [3072,768] N(0,0.02), 4-bit per-output-channel "
+                 "codebook (16 centroids/row, quantile init), bias, Y fp32",
+        step=step, flops=flops, alg_bytes=alg_bytes, bound="hbm", dtype="fp16",
+        unit="TFLOP/s", per_step_units=flops / 1e12, cpu_step=cpu_step, cpu_full_batch=1576, check=check,
+        extra_config={"M": 1576, "N": 3072, "K": 768, "bits": 4, "codebook": "per_channel"},
+        per_set_bytes=1576 * 768 * 4 + 1576 * 3072 * 4,
+    )
+
+
+def make_cfg5(dev, rotations, M=16):
+    from dimq_amd import ops
+    from dimq_amd.codebook import assign_indices, init_centers_per_channel
+    from dimq_amd.export import pack_indices
+
+    g = torch.Generator().manual_seed(4)
+    w = torch.randn(4096, 4096, generator=g) * 0.02
+    centers = init_centers_per_channel(w, 8)
+    cb = centers.to(dev)
+    # weights rotate too (6.3 MB packed each) so that repeats stream from HBM
+    packs = [pack_indices(assign_indices(w, centers), 3).to(dev)]
+    for _ in range(rotations - 1):
+        packs.append(packs[0].clone())
+    xs = [torch.randn(M, 4096, generator=g).bfloat16().to(dev) for _ in range(rotations)]
+
+    def step(i):
+        return ops.dimq_linear_codebook(xs[i], packs[i], cb, 3, None, 4096, 4096, out_dtype=torch.float32)
+
+    alg_bytes = packs[0].numel() + cb.numel() * 4 + M * 4096 * 2 + M * 4096 * 4
+    flops = 2.0 * M * 4096 * 4096
+
+    def cpu_step(sample_rows):
+        import oracle
+        return oracle.linear_dequant_reference(xs[0][:sample_rows].cpu().float(), packs[0].cpu(), 3, centers, 4096,
+                                               4096)
+
+    def check():
+        import oracle
+        return oracle.rel_err(step(0), oracle.linear_dequant_reference(xs[0].cpu().float(), packs[0].cpu(), 3,
+                                                                       centers, 4096, 4096))
+
+    return dict(
+        name=f"cfg5_m{M}",
+        workload=f"decode GEMV: X bf16 [{M},4096], W [4096,4096] N(0,0.02), 3-bit per-output-channel codebook "
+                 "(8 centroids/row), Y fp32",
+        step=step, flops=flops, alg_bytes=alg_bytes, bound="hbm", dtype="fp16",
+        unit="TFLOP/s", per_step_units=flops / 1e12, cpu_step=cpu_step, cpu_full_batch=M, check=check,
+        extra_config={"M": M, "N": 4096, "K": 4096, "bits": 3, "codebook": "per_channel"},
+        per_set_bytes=packs[0].numel() + M * 4096 * 6,
+    )
+
+
+def make_codec(dev, rotations, direction="unpack"):
+    from dimq_amd import ops
+
+    n = 1 << 27
+    g = torch.Generator().manual_seed(5)
+    idx = torch.randint(0, 8, (n,), generator=g, dtype=torch.uint8)
+    base = idx.to(dev)
+    packed0 = ops.pack_bits(base, 3)
+    srcs = [base if i == 0 else base.clone() for i in range(rotations)] if direction == "pack" else \
+        [packed0 if i == 0 else packed0.clone() for i in range(rotations)]
+
+    if direction == "pack":
+        def step(i):
+            return ops.pack_bits(srcs[i], 3)
+    else:
+        def step(i):
+            return ops.unpack_bits(srcs[i], n, 3)
+
+    alg_bytes = n + n * 3 // 8
+
+    def cpu_step(sample):
+        import oracle
+        sub = idx[:sample].numpy()
+        return oracle.pack_bits(sub, 3) if direction == "pack" else oracle.unpack_bits(
+            oracle.pack_bits(sub, 3), sample, 3)
+
+    def check():
+        back = ops.unpack_bits(ops.pack_bits(base, 3), n, 3)
+        return 0.0 if torch.equal(back, base) else 1.0
+
+    return dict(
+        name=f"codec_{direction}",
+        workload=f"3-bit codec {direction}: 2^27 uniform random indices <-> 50,331,648 packed bytes",
+        step=step, flops=0.0, alg_bytes=alg_bytes, bound="hbm", dtype="u8",
+        unit="GB/s", per_step_units=alg_bytes / 1e9, cpu_step=cpu_step, cpu_full_batch=n, check=check,
+        extra_config={"numel": n, "bits": 3},
+        per_set_bytes=alg_bytes,
+    )
+
+
+WORKLOADS = {"cfg2": make_cfg2, "cfg1": make_cfg1, "cfg5": make_cfg5, "codec": make_codec}
+
+
+# ---------------------------------------------------------------------------
+# timing
+# ---------------------------------------------------------------------------
+
+def time_gpu(wl, rotations, steps, warmup):
+    """Captures `rotations` steps in one HIP graph, replays it; returns ms per step from HIP events."""
+    step = wl["step"]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(rotations):      # eager warm-up outside capture
+            step(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(rotations):
+            step(i)
+    replays = max(1, steps // rotations)
+    rem = steps - replays * rotations
+    graph_rem = None
+    if rem:
+        graph_rem = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph_rem):
+            for i in range(rem):
+                step(i)
+    for _ in range(max(1, warmup // rotations)):
+        graph.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    if graph_rem is not None:
+        graph_rem.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / (replays * rotations + rem)
+    return ms, replays * rotations + rem
+
+
+def time_cpu(wl, budget_s=15.0):
+    """Times the oracle's CPU path (dequantize, then torch CPU fp32 conv/linear) on a bounded sample."""
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    full = wl["cpu_full_batch"]
+    sample = full
+    t0 = time.perf_counter()
+    wl["cpu_step"](sample)
+    one = time.perf_counter() - t0
+    # shrink the sample until one call takes at most ~budget/8
+    while one > budget_s / 8 and sample > 1:
+        sample = max(1, sample // 2)
+        t0 = time.perf_counter()
+        wl["cpu_step"](sample)
+        one = time.perf_counter() - t0
+    for _ in range(2):
+        wl["cpu_step"](sample)
+    times = []
+    t_end = time.perf_counter() + budget_s * 0.6
+    while len(times) < 10 or (time.perf_counter() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        wl["cpu_step"](sample)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 10 and time.perf_counter() > t_end:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    frac = sample / full
+    value = wl["per_step_units"] * frac / med
+    try:
+        model = [l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name")][0]
+    except Exception:
+        model = "unknown"
+    return dict(value=value, unit=wl["unit"], cores=threads, kind="port",
+                sample=f"{sample}/{full} of one step ({wl['name']}), median of {len(times)} runs after 3 warm-ups; "
+                       f"oracle dequantize + torch CPU fp32; {model}")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1600)
+    ap.add_argument("--warmup", type=int, default=160)
+    ap.add_argument("--config", default="cfg2", choices=sorted(WORKLOADS))
+    ap.add_argument("--m", type=int, default=16, help="rows for cfg5")
+    ap.add_argument("--direction", default="unpack", choices=["pack", "unpack"])
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-check", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (every box has one GPU). "
+              "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    dev = torch.device("cuda:0")
+    make = WORKLOADS[args.config]
+    kw = {}
+    if args.config == "cfg5":
+        kw["M"] = args.m
+    if args.config == "codec":
+        kw["direction"] = args.direction
+    # rotate buffer sets totalling > 512 MB
+    probe = make(dev, 1, **kw)
+    rotations = max(2, min(64, math.ceil(512e6 / probe["per_set_bytes"]) + 1))
+    del probe
+    torch.cuda.empty_cache()
+    wl = make(dev, rotations, **kw)
+
+    err = None if args.no_check else wl["check"]()
+    ms, steps = time_gpu(wl, rotations, args.steps, args.warmup)
+    sec = ms / 1e3
+    value = wl["per_step_units"] / sec
+    if wl["bound"] == "hbm":
+        achieved = wl["alg_bytes"] / sec / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None}
+    else:
+        achieved = wl["flops"] / sec / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None}
+    traffic_file = ROOT / "profiles" / f"traffic_{wl['name']}.json"
+    if traffic_file.exists():
+        roof["traffic"] = json.loads(traffic_file.read_text()).get("traffic_bytes_per_launch")
+    cpu = None if args.no_cpu else time_cpu(wl)
+    out = {
+        "metric": METRIC,
+        "value": round(value, 4),
+        "unit": wl["unit"],
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": wl["dtype"],
+        "data": "synthetic (seeded CPU torch.Generator, copied to HBM before timing)",
+        "config": {"workload": wl["workload"], "name": wl["name"], "rotated_buffer_sets": rotations,
+                   "algorithmic_bytes_per_step": wl["alg_bytes"], "flops_per_step": wl["flops"],
+                   "parity_max_rel_err": err, **wl["extra_config"]},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

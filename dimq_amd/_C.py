@@ -63,8 +63,10 @@ _SIGS = {
     "dimq_build_product_table_grouped": (_int, [_vp, _int, _i64, _i64, _dbl, _i64, _vp, _vp]),
     "dimq_linear_codebook": (_int, [_vp, _int, _i64, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _vp, _int, _i64,
                                     _vp, _int, _int, _vp]),
-    "dimq_conv2d_codebook": (_int, [_vp, _int, _int, _i64, _i64, _i64, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64,
-                                    _vp, _int] + [_i64] * 10 + [_vp, _int, _int, _int, _vp]),
+    "dimq_conv2d_prepared_words": (_i64, [_i64, _i64, _i64, _i64, _int]),
+    "dimq_conv2d_prepare_weight": (_int, [_vp, _i64, _int, _i64, _i64, _i64, _i64, _vp, _i64, _vp]),
+    "dimq_conv2d_codebook": (_int, [_vp, _int, _int, _i64, _i64, _i64, _i64, _vp, _i64, _int, _vp, _i64, _vp, _int,
+                                    _i64, _i64, _vp, _int] + [_i64] * 10 + [_vp, _int, _int, _int, _vp]),
 }
 
 for _name, (_res, _args) in _SIGS.items():
@@ -321,8 +323,28 @@ def linear_codebook_impl(x, packed_w, codebook, bits, bias, out_features, in_fea
     return y.view(*x.shape[:-1], out_features)
 
 
+def prepare_conv_weight_impl(packed_w, bits, out_channels, in_channels, kernel_h, kernel_w):
+    _require_cuda(packed_w, "prepare_conv_weight expects a CUDA tensor")
+    if packed_w.dtype != torch.uint8:
+        raise RuntimeError("packed_weight must be uint8")
+    words = int(lib.dimq_conv2d_prepared_words(out_channels, in_channels, kernel_h, kernel_w, int(bits)))
+    if words <= 0:
+        raise RuntimeError(f"no kernel layout for C={in_channels} KH={kernel_h} KW={kernel_w} bits={bits}")
+    pw = packed_w.contiguous().view(-1)
+    out = torch.empty((words,), dtype=torch.int32, device=pw.device)
+    with torch.cuda.device(pw.device):
+        _check(lib.dimq_conv2d_prepare_weight(_ptr(pw), pw.numel(), int(bits), out_channels, in_channels, kernel_h,
+                                              kernel_w, _ptr(out), words, _stream(pw.device)))
+    return out
+
+
+def prepared_conv_words(out_channels, in_channels, kernel_h, kernel_w, bits) -> int:
+    return int(lib.dimq_conv2d_prepared_words(out_channels, in_channels, kernel_h, kernel_w, int(bits)))
+
+
 def conv2d_codebook_impl(x, packed_w, codebook, bits, bias, out_channels, in_channels_per_group, kernel_h, kernel_w,
-                         stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w, groups, out_dtype=None, variant=0):
+                         stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w, groups, out_dtype=None, variant=0,
+                         prepared_w=None):
     _require_cuda(x, "conv2d_codebook expects CUDA input")
     if x.dim() != 4:
         raise RuntimeError("conv2d_codebook expects a 4-D input")
@@ -347,9 +369,15 @@ def conv2d_codebook_impl(x, packed_w, codebook, bits, bias, out_channels, in_cha
     odt = x.dtype if out_dtype is None else out_dtype
     mf = torch.channels_last if channels_last else torch.contiguous_format
     y = torch.empty((B, out_channels, max(oh, 0), max(ow, 0)), dtype=odt, device=xc.device, memory_format=mf)
+    if prepared_w is not None:
+        _require_cuda(prepared_w, "prepared_w must be CUDA when provided")
+        prep = prepared_w.contiguous()
+        prep_ptr, prep_words = _ptr(prep), prep.numel()
+    else:
+        prep_ptr, prep_words = None, 0
     with torch.cuda.device(xc.device):
         _check(lib.dimq_conv2d_codebook(_ptr(xc), _dtype(xc), layout, B, C, H, W, _ptr(pw), pw.numel(), int(bits),
-                                        _ptr(cb), _dtype(cb), rows, size, bp, bdt, out_channels, kernel_h, kernel_w,
+                                        prep_ptr, prep_words, _ptr(cb), _dtype(cb), rows, size, bp, bdt, out_channels, kernel_h, kernel_w,
                                         stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w, groups, _ptr(y),
                                         _dtype(y), layout, int(variant), _stream(xc.device)))
     return y
@@ -386,7 +414,10 @@ _SCHEMAS = {
     "conv2d_codebook": ("conv2d_codebook(Tensor x, Tensor packed_w, Tensor codebook, int bits, Tensor? bias, "
                         "int out_channels, int in_channels_per_group, int kernel_h, int kernel_w, int stride_h, "
                         "int stride_w, int pad_h, int pad_w, int dilation_h, int dilation_w, int groups, "
-                        "ScalarType? out_dtype=None, int variant=0) -> Tensor", conv2d_codebook_impl),
+                        "ScalarType? out_dtype=None, int variant=0, Tensor? prepared_w=None) -> Tensor",
+                        conv2d_codebook_impl),
+    "prepare_conv_weight": ("prepare_conv_weight(Tensor packed_w, int bits, int out_channels, int in_channels, "
+                            "int kernel_h, int kernel_w) -> Tensor", prepare_conv_weight_impl),
 }
 
 

@@ -112,9 +112,31 @@ extern "C" int dimq_conv2d_lut(const void* x, int x_dtype, int64_t B, int64_t C,
   return gemm_dispatch(p, 4, x_dtype, true, kTile64x32, as_stream(stream));
 }
 
+extern "C" int64_t dimq_conv2d_prepared_words(int64_t out_channels, int64_t in_channels, int64_t kernel_h,
+                                              int64_t kernel_w, int bits) {
+  if (!halo_weight_supported(in_channels, kernel_h, kernel_w, bits) || out_channels <= 0) return 0;
+  return halo_prepared_words(out_channels, in_channels, kernel_h, kernel_w, bits);
+}
+
+extern "C" int dimq_conv2d_prepare_weight(const uint8_t* packed_w, int64_t packed_numel, int bits,
+                                          int64_t out_channels, int64_t in_channels, int64_t kernel_h,
+                                          int64_t kernel_w, uint32_t* prepared_w, int64_t prepared_words,
+                                          void* stream) {
+  if (!halo_weight_supported(in_channels, kernel_h, kernel_w, bits))
+    return set_error(DIMQ_ERR_UNSUPPORTED, "no kernel layout for C=%lld KH=%lld KW=%lld bits=%d",
+                     (long long)in_channels, (long long)kernel_h, (long long)kernel_w, bits);
+  DIMQ_CHECK(out_channels > 0, "channel counts must be positive");
+  const int64_t wnumel = out_channels * in_channels * kernel_h * kernel_w;
+  DIMQ_CHECK(packed_numel >= (wnumel * bits + 7) / 8, "packed_weight is too small for requested conv weight shape");
+  DIMQ_CHECK(prepared_words >= halo_prepared_words(out_channels, in_channels, kernel_h, kernel_w, bits),
+             "prepared weight buffer is too small");
+  return launch_prepare(packed_w, out_channels, in_channels, kernel_h, kernel_w, bits, prepared_w,
+                        as_stream(stream));
+}
+
 extern "C" int dimq_conv2d_codebook(const void* x, int x_dtype, int x_layout, int64_t B, int64_t C, int64_t H,
                                     int64_t W, const uint8_t* packed_w, int64_t packed_numel, int bits,
-                                    const void* codebook, int cb_dtype, int64_t cb_rows, int64_t cb_size,
+                                    const uint32_t* prepared_w, int64_t prepared_words, const void* codebook, int cb_dtype, int64_t cb_rows, int64_t cb_size,
                                     const void* bias, int bias_dtype, int64_t out_channels, int64_t kernel_h,
                                     int64_t kernel_w, int64_t stride_h, int64_t stride_w, int64_t pad_h,
                                     int64_t pad_w, int64_t dilation_h, int64_t dilation_w, int64_t groups, void* y,
@@ -141,7 +163,17 @@ extern "C" int dimq_conv2d_codebook(const void* x, int x_dtype, int x_layout, in
   DIMQ_CHECK(packed_numel >= (wnumel * bits + 7) / 8, "packed_weight is too small for requested conv weight shape");
   DIMQ_CHECK(variant >= DIMQ_VARIANT_AUTO && variant <= DIMQ_VARIANT_MFMA, "unknown kernel variant %d", variant);
   if (s.B * s.OC * s.OH * s.OW == 0) return DIMQ_OK;
+  if (prepared_w != nullptr && variant != DIMQ_VARIANT_SMALL_M && aligned(x, 16) &&
+      halo_eligible(s.C, s.KH, s.KW, s.sh, s.sw, s.dh, s.dw, s.groups, s.OH, s.OW, bits, x_dtype)) {
+    DIMQ_CHECK(prepared_words >= halo_prepared_words(s.OC, s.C, s.KH, s.KW, bits),
+               "prepared weight buffer is too small");
+    return launch_conv_halo(x, x_dtype, x_layout, s.B, s.C, s.H, s.W, prepared_w, bits, codebook, cb_dtype, cb_rows,
+                            cb_size, bias, bias_dtype, s.OC, s.KH, s.KW, s.sh, s.ph, s.pw, s.OH, s.OW, y, y_dtype,
+                            y_layout, as_stream(stream));
+  }
   GemmArgs p = conv_args(s, x, x_layout, packed_w, codebook, cb_dtype, cb_rows, cb_size, bias, bias_dtype, y,
                          y_dtype, y_layout);
-  return gemm_dispatch(p, bits, x_dtype, false, gemm_pick_tile(p.M, p.N, variant), as_stream(stream));
+  int tile = gemm_pick_tile(p.M, p.N, variant);
+  if (tile == kTileGemv) tile = kTile16x16;  // the GEMV kernel has no im2col/group support
+  return gemm_dispatch(p, bits, x_dtype, false, tile, as_stream(stream));
 }

@@ -11,8 +11,8 @@ constexpr int64_t kCUs = 256;
 }  // namespace
 
 int gemm_pick_tile(int64_t M, int64_t N, int variant) {
-  if (variant == DIMQ_VARIANT_SMALL_M) return kTile16x16;
-  if (variant == DIMQ_VARIANT_AUTO && M <= 16) return kTile16x16;
+  if (variant == DIMQ_VARIANT_SMALL_M) return M <= 16 ? kTileGemv : kTile16x16;
+  if (variant == DIMQ_VARIANT_AUTO && M <= 16) return kTileGemv;
   const int64_t big = ((M + 127) / 128) * ((N + 255) / 256);
   if (big >= kCUs) return kTile128x64;
   return kTile64x32;

@@ -178,6 +178,22 @@ __device__ __forceinline__ void load_a_group(const GemmArgs& p, int64_t gm, int6
   for (int d = 0; d < 8; ++d) out[d] = h[kperm16(BITS, 2 * d)] | (h[kperm16(BITS, 2 * d + 1)] << 16);
 }
 
+// ---- tile scheduling -------------------------------------------------------------
+// The grid is 1-D over Mt x Nt tiles (n fastest).  Work-groups are dispatched
+// round-robin over the 8 XCDs (each with its own L2), so work-group i runs on
+// XCD i % 8.  The remap hands every XCD a contiguous run of tiles, i.e. whole
+// rows of N-tiles over a few M-tiles: that XCD then reads only its own slab
+// of x and the packed weight, both of which stay resident in its L2.
+__device__ __forceinline__ void tile_coords(int64_t n_tiles, int64_t& mt, int64_t& nt) {
+  constexpr int kXCD = 8;
+  const int64_t T = gridDim.x;
+  int64_t pid = blockIdx.x;
+  const int64_t per = T / kXCD;
+  if (pid < per * kXCD) pid = (pid % kXCD) * per + pid / kXCD;
+  mt = pid / n_tiles;
+  nt = pid - mt * n_tiles;
+}
+
 // ---- packed weight chunk loader ---------------------------------------------
 // 32 indices of row n starting at column k (k % 32 == 0) -> BITS dwords laid
 // out as if the chunk started on a byte boundary.  Columns >= K read as 0.
@@ -264,8 +280,10 @@ __global__ __launch_bounds__(256) void gemm_cb_kernel(const GemmArgs p) {
   const int wave = tid >> 6;
   const int col = lane & 15;
   const int g = lane >> 4;
-  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * BM;
-  const int64_t nw0 = static_cast<int64_t>(blockIdx.x) * (4 * WN) + wave * WN;
+  int64_t mt, nt;
+  tile_coords((p.N + 4 * WN - 1) / (4 * WN), mt, nt);
+  const int64_t m0 = mt * BM;
+  const int64_t nw0 = nt * (4 * WN) + wave * WN;
   const int64_t nz = static_cast<int64_t>(blockIdx.z) * p.N;      // first weight row of this group
   const int64_t cbase = static_cast<int64_t>(blockIdx.z) * p.cICg;  // first input channel of this group
 
@@ -392,8 +410,10 @@ __global__ __launch_bounds__(256) void gemm_cb8_kernel(const GemmArgs p) {
   const int wave = tid >> 6;
   const int col = lane & 15;
   const int g = lane >> 4;
-  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * BM;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * ROWS;
+  int64_t mt, nt;
+  tile_coords((p.N + ROWS - 1) / ROWS, mt, nt);
+  const int64_t m0 = mt * BM;
+  const int64_t n0 = nt * ROWS;
   const int64_t nw0 = n0 + wave * WN;
   const int64_t nz = static_cast<int64_t>(blockIdx.z) * p.N;
   const int64_t cbase = static_cast<int64_t>(blockIdx.z) * p.cICg;
@@ -522,11 +542,88 @@ __global__ __launch_bounds__(256) void gemm_cb8_kernel(const GemmArgs p) {
   }
 }
 
+// Small-M variant (M <= 16, decode / GEMV shapes).  A work-group of WPW waves
+// owns 16 weight rows and the whole K range; wave w takes the 128-wide k steps
+// kt = w, w + WPW, ...  so WPW waves per work-group (16 per CU) keep enough
+// loads in flight to hide HBM latency, which is what bounds these shapes.
+// The activation rows (16 lanes x 32 values per step) are read straight from
+// global memory (L2-resident, shared by all work-groups), converted and put in
+// slot order in registers; partial sums of the WPW waves meet in LDS.
+template <int BITS, int XT, int WPW>
+__global__ __launch_bounds__(WPW * 64) void gemv_cb_kernel(const GemmArgs p) {
+  static_assert(BITS >= 2 && BITS <= 4, "register codebooks hold at most 16 entries");
+  __shared__ floatx4 red[WPW][64];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 15;
+  const int g = lane >> 4;
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * 16 + col;
+  const int64_t row = (p.cb_rows == 1) ? 0 : n;
+  CodebookRegs<BITS> cb;
+  const int e = load_codebook_row<BITS, false>(p, row, n < p.N, cb, cb);
+  const float colscale = ldexpf(1.0f, -e);
+  const int64_t nk = (p.K + kKM - 1) / kKM;
+  const bool arow = col < p.M;
+  floatx4 acc = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  uint32_t bc[BITS];
+  uint32_t av[16];  // 32 fp16 activations in slot order
+  auto load_step = [&](int64_t kt, uint32_t (&bdst)[BITS], uint32_t (&adst)[16]) {
+    load_b_chunk<BITS>(p, n, n, kt * kKM + 32 * g, bdst);
+    const int64_t k0 = kt * kKM + 32 * g;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t t[8];
+      load_a_group<BITS, XT, false>(p, arow ? (int64_t)col : p.M, k0 + 16 * h, 0, t);
+#pragma unroll
+      for (int d = 0; d < 8; ++d) adst[8 * h + d] = t[d];
+    }
+  };
+  for (int64_t kt = wave; kt < nk; kt += WPW) {
+    load_step(kt, bc, av);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const u32x4 a4 = {av[4 * s], av[4 * s + 1], av[4 * s + 2], av[4 * s + 3]};
+      const half8 bf = decode_sub<BITS>(bc, s, cb);
+      acc = mfma16x16x32(__builtin_bit_cast(half8, a4), bf, acc);
+    }
+  }
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0) {
+    floatx4 t = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < WPW; ++w) t += red[w][lane];
+    if (n < p.N) {
+      const float b = p.bias ? load_as_float(p.bias, p.bias_dt, n) : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t m = 4 * g + i;
+        if (m < p.M) store_from_float(p.y, p.y_dt, m * p.ldy + n, t[i] * colscale + b);
+      }
+    }
+  }
+}
+
 // Tile shapes: (BM, WN); the work-group covers BM x 4*WN.
-enum TileId { kTile128x64 = 0, kTile64x32 = 1, kTile16x16 = 2, kTileCount = 3 };
+enum TileId { kTile128x64 = 0, kTile64x32 = 1, kTile16x16 = 2, kTileGemv = 3, kTileCount = 4 };
 
 template <int BITS, int XT, bool A4>
 int launch_gemm_tile(const GemmArgs& p, int tile, hipStream_t s);
+
+// conv_halo.hip
+int64_t halo_prepared_words(int64_t OC, int64_t C, int64_t KH, int64_t KW, int bits);
+int64_t halo_tile_rows(int64_t C, int64_t KH, int64_t KW, int64_t stride, int64_t OH, int64_t OW);
+bool halo_weight_supported(int64_t C, int64_t KH, int64_t KW, int bits);
+bool halo_eligible(int64_t C, int64_t KH, int64_t KW, int64_t sh, int64_t sw, int64_t dh, int64_t dw,
+                   int64_t groups, int64_t OH, int64_t OW, int bits, int x_dtype);
+int launch_conv_halo(const void* x, int x_dtype, int x_layout, int64_t B, int64_t C, int64_t H, int64_t W,
+                     const uint32_t* kw, int bits, const void* cb, int cb_dtype, int64_t cb_rows, int64_t cb_size,
+                     const void* bias, int bias_dtype, int64_t OC, int64_t KH, int64_t KW, int64_t stride,
+                     int64_t ph, int64_t pw, int64_t OH, int64_t OW, void* y, int y_dtype, int y_layout,
+                     hipStream_t s);
+int launch_prepare(const uint8_t* src, int64_t OC, int64_t C, int64_t KH, int64_t KW, int bits, uint32_t* out,
+                   hipStream_t s);
 
 // gemm.hip
 int gemm_pick_tile(int64_t M, int64_t N, int variant);

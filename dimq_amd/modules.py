@@ -151,12 +151,25 @@ class DIMQCodebookConv2d(nn.Module):
         self.groups = int(groups)
         self.out_dtype = out_dtype
         self.variant = variant
+        self._prepared = None      # kernel-layout weight, built once on the GPU
+        self._prepared_key = None
+
+    def prepared_weight(self) -> torch.Tensor | None:
+        """Kernel-layout copy of packed_weight (conv_halo kernel), built on first use."""
+        if self.groups != 1:
+            return None
+        key = (self.packed_weight.data_ptr(), self.packed_weight.device)
+        if self._prepared_key != key:
+            self._prepared = ops.prepare_conv_weight(self.packed_weight, self.bits, self.weight_shape)
+            self._prepared_key = key
+        return self._prepared
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         _require_gpu(x, self.packed_weight, True, "DIMQCodebookConv2d")
         return ops.dimq_conv2d_codebook(x, self.packed_weight, self.codebook, self.bits, self.bias,
                                         self.weight_shape, self.stride, self.padding, self.dilation, self.groups,
-                                        out_dtype=self.out_dtype, variant=self.variant)
+                                        out_dtype=self.out_dtype, variant=self.variant,
+                                        prepared_weight=self.prepared_weight())
 
     @classmethod
     @torch.no_grad()

@@ -160,8 +160,12 @@ def dimq_conv2d_codebook(
     *,
     out_dtype: torch.dtype | None = None,
     variant: str = "auto",
+    prepared_weight: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """Weight-only codebook conv2d; NCHW or channels_last input, output in the same memory format."""
+    """Weight-only codebook conv2d; NCHW or channels_last input, output in the same memory format.
+
+    ``prepared_weight`` (from :func:`prepare_conv_weight`) enables the LDS-halo
+    kernel for the shapes it supports."""
     require_extension()
     out_channels, cin_per_group, kernel_h, kernel_w = [int(v) for v in weight_shape]
     stride_h, stride_w = _pair(stride)
@@ -169,8 +173,19 @@ def dimq_conv2d_codebook(
     dil_h, dil_w = _pair(dilation)
     return torch.ops.dimq.conv2d_codebook(
         x, packed_weight, codebook, int(bits), bias, out_channels, cin_per_group, kernel_h, kernel_w, stride_h,
-        stride_w, pad_h, pad_w, dil_h, dil_w, int(groups), out_dtype, VARIANTS[variant],
+        stride_w, pad_h, pad_w, dil_h, dil_w, int(groups), out_dtype, VARIANTS[variant], prepared_weight,
     )
+
+
+def prepare_conv_weight(packed_weight: torch.Tensor, bits: int, weight_shape: Sequence[int]) -> torch.Tensor | None:
+    """Kernel-layout copy of a conv_kcrs packed weight, or None when the shape has no kernel layout."""
+    require_extension()
+    from . import _C
+
+    out_channels, cin, kernel_h, kernel_w = [int(v) for v in weight_shape]
+    if _C.prepared_conv_words(out_channels, cin, kernel_h, kernel_w, int(bits)) <= 0:
+        return None
+    return torch.ops.dimq.prepare_conv_weight(packed_weight, int(bits), out_channels, cin, kernel_h, kernel_w)
 
 
 def _pair(value: Sequence[int] | int) -> tuple[int, int]:

@@ -141,12 +141,28 @@ int dimq_linear_codebook(const void* x, int x_dtype, int64_t M, int64_t K, const
                          int64_t cb_size, const void* bias, int bias_dtype, int64_t N, void* y, int y_dtype,
                          int variant, void* stream);
 
+/* Words of the kernel-layout weight of a conv (0 when the shape has no
+ * kernel layout: supported are C in {64, 128}, 3x3 or 1x1, bits in {2,3,4}). */
+int64_t dimq_conv2d_prepared_words(int64_t out_channels, int64_t in_channels, int64_t kernel_h, int64_t kernel_w,
+                                   int bits);
+
+/* One-time repack of a conv_kcrs b-bit index stream into the kernel layout
+ * read by the LDS-halo conv kernel (per output channel and lane group, the
+ * indices of each (kh, kw, 32-channel) step in decode order).  Same bytes
+ * of information; done when a layer is loaded, not per call. */
+int dimq_conv2d_prepare_weight(const uint8_t* packed_w, int64_t packed_numel, int bits, int64_t out_channels,
+                               int64_t in_channels, int64_t kernel_h, int64_t kernel_w, uint32_t* prepared_w,
+                               int64_t prepared_words, void* stream);
+
 /* Weight-only codebook Conv2d (zero padding, stride, dilation, groups).
  * x [B,C,H,W] in x_layout (NCHW or NHWC memory order); y [B,OC,OH,OW] in
  * y_layout; packed_w: b-bit stream of the conv_kcrs index tensor
- * [OC, C/groups, KH, KW] (dimq_backend/export.py:232). */
+ * [OC, C/groups, KH, KW] (dimq_backend/export.py:232).  prepared_w
+ * (nullable): the same weights in kernel layout; when given and the shape
+ * fits, the LDS-halo kernel runs, otherwise the implicit-GEMM kernel. */
 int dimq_conv2d_codebook(const void* x, int x_dtype, int x_layout, int64_t B, int64_t C, int64_t H, int64_t W,
-                         const uint8_t* packed_w, int64_t packed_numel, int bits, const void* codebook,
+                         const uint8_t* packed_w, int64_t packed_numel, int bits, const uint32_t* prepared_w,
+                         int64_t prepared_words, const void* codebook,
                          int cb_dtype, int64_t cb_rows, int64_t cb_size, const void* bias, int bias_dtype,
                          int64_t out_channels, int64_t kernel_h, int64_t kernel_w, int64_t stride_h,
                          int64_t stride_w, int64_t pad_h, int64_t pad_w, int64_t dilation_h, int64_t dilation_w,

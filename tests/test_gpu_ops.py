@@ -332,3 +332,81 @@ def test_conv2d_codebook_vs_oracle(gpu, case, layout):
                                           case["d"], case["g"])
     assert y.shape == ref.shape
     assert oracle.rel_err(y.float(), ref) <= TOL, oracle.rel_err(y.float(), ref)
+
+
+# ---------------------------------------------------------------- HIP graph replay
+def test_graph_replay_matches_eager(gpu):
+    """Kernels captured in a HIP graph give the eager result on every replay (bench.py times graphs)."""
+    ops = _ops()
+    g = _gen(123)
+    cb, idx, packed = _codebook_case(128, 256, 4, True, g)
+    x = torch.randn(64, 256, generator=g).to(gpu)
+    cbc = (torch.randn(16, 4, generator=g) * 0.1).sort(dim=1).values.to(gpu)
+    pc = torch.from_numpy(oracle.pack_bits(torch.randint(0, 4, (16, 144), generator=g, dtype=torch.uint8), 2)).to(gpu)
+    xc = torch.randn(2, 16, 10, 10, generator=g).half().to(gpu)
+    packed, cb = packed.to(gpu), cb.to(gpu)
+
+    def run():
+        y1 = ops.dimq_linear_codebook(x, packed, cb, 4, None, 128, 256)
+        y2 = ops.dimq_conv2d_codebook(xc, pc, cbc, 2, None, (16, 16, 3, 3), (1, 1), (1, 1), (1, 1), 1,
+                                      out_dtype=torch.float32)
+        return y1, y2
+
+    e1, e2 = run()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        o1, o2 = run()
+    for r in range(3):
+        o1.zero_()
+        o2.zero_()
+        _ = (x * 2).sum()  # unrelated eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o1, e1) and torch.equal(o2, e2), f"replay {r}"
+
+
+# ---------------------------------------------------------------- LDS-halo conv (prepared weights)
+@pytest.mark.parametrize("case", [
+    dict(B=2, C=64, H=56, W=56, OC=64, K=3, s=1, bits=2, dt=torch.float16),    # cfg2 geometry (smaller batch)
+    dict(B=1, C=64, H=17, W=13, OC=128, K=3, s=1, bits=4, dt=torch.bfloat16),
+    dict(B=2, C=128, H=28, W=28, OC=64, K=3, s=1, bits=3, dt=torch.float16),
+    dict(B=2, C=64, H=56, W=56, OC=128, K=3, s=2, bits=2, dt=torch.float16),
+    dict(B=3, C=128, H=14, W=14, OC=64, K=1, s=2, bits=4, dt=torch.float16),
+    dict(B=1, C=64, H=9, W=300, OC=64, K=3, s=1, bits=2, dt=torch.float16),    # OW > 256: falls back
+])
+@pytest.mark.parametrize("layout", ["nchw", "nhwc"])
+def test_conv2d_halo_prepared_vs_oracle(gpu, case, layout):
+    ops = _ops()
+    announce(f"conv halo {case} {layout}")
+    g = _gen(case["C"] + case["OC"] * 3 + case["bits"] + case["s"])
+    K = case["K"]
+    pad = K // 2
+    shape = (case["OC"], case["C"], K, K)
+    x = torch.relu(torch.randn(case["B"], case["C"], case["H"], case["W"], generator=g)).to(case["dt"])
+    cb, idx, packed = _codebook_case(case["OC"], case["C"] * K * K, case["bits"], True, g)
+    bias = torch.randn(case["OC"], generator=g) * 0.1
+    xd = x.to(gpu)
+    if layout == "nhwc":
+        xd = xd.to(memory_format=torch.channels_last)
+    pd = packed.to(gpu)
+    prep = ops.prepare_conv_weight(pd, case["bits"], shape)
+    assert prep is not None
+    y = ops.dimq_conv2d_codebook(xd, pd, cb.to(gpu), case["bits"], bias.to(gpu), shape, (case["s"],) * 2,
+                                 (pad, pad), (1, 1), 1, out_dtype=torch.float32, prepared_weight=prep)
+    ref = oracle.conv2d_dequant_reference(x.float(), packed, case["bits"], cb, shape, bias, case["s"], pad, 1, 1)
+    assert y.shape == ref.shape
+    assert oracle.rel_err(y.float(), ref) <= TOL, oracle.rel_err(y.float(), ref)
+    y2 = ops.dimq_conv2d_codebook(xd, pd, cb.to(gpu), case["bits"], bias.to(gpu), shape, (case["s"],) * 2,
+                                  (pad, pad), (1, 1), 1, out_dtype=torch.float32)
+    assert oracle.rel_err(y, y2) <= 1e-5  # prepared (halo) and generic implicit-GEMM paths agree
+
+
+def test_conv2d_prepare_unsupported_returns_none(gpu):
+    ops = _ops()
+    assert ops.prepare_conv_weight(torch.zeros(100, dtype=torch.uint8, device=gpu), 2, (16, 48, 3, 3)) is None
+    assert ops.prepare_conv_weight(torch.zeros(100, dtype=torch.uint8, device=gpu), 8, (16, 64, 3, 3)) is None

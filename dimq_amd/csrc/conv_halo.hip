@@ -9,15 +9,16 @@
 // formed: the MFMA operand for (pixel, kh, kw, 8 channels) is one ds_read_b128
 // at the pixel's shifted position.
 //
+// The matrix cores run v_mfma_f32_32x32x16_f16 (measured on MI355X: ~2.2
+// PFLOP/s sustained against ~1.2 for the 16x16x32 shape).  One MFMA covers 32
+// pixels x 32 output channels x 16 input channels; lane l holds 8 channels
+// (group g = l / 32) of pixel / output channel l % 32.
+//
 // Weights arrive in a "kernel layout" (dimq_conv2d_prepare_weight): for every
 // output channel n and lane group g, the b-bit indices of the sub-steps
-// t = (kh, kw, 32-channel chunk) x 8 channels, ordered so that the v_perm
+// t = (kh, kw, 16-channel chunk) x 8 channels, ordered so that the v_perm
 // decode of decode.h yields channels in natural order.  Each lane keeps its
-// rows' packed indices and codebook byte planes in VGPRs for the whole tile.
-//
-// The MFMA computes D[oc][pixel] (weights as the A operand), so lane l ends
-// with 4 output channels of pixel l%16 and the fp32 NCHW stores of 16 lanes
-// are 64-byte contiguous runs.
+// row's packed indices and codebook byte planes in VGPRs for the whole tile.
 #include "decode.h"
 
 #include <algorithm>
@@ -43,194 +44,315 @@ struct HaloArgs {
   int y_dt, y_layout;
 };
 
-template <int BITS>
-__device__ __forceinline__ void load_cb_row(const HaloArgs& p, int row, bool valid, CodebookRegs<BITS>& cb, int& e) {
-  constexpr int E = 1 << BITS;
-  float c[E];
-  float mx = 0.0f;
-#pragma unroll
-  for (int j = 0; j < E; ++j) {
-    c[j] = (valid && j < p.cb_size) ? load_as_float(p.cb, p.cb_dt, (int64_t)row * p.cb_size + j) : 0.0f;
-    mx = fmaxf(mx, fabsf(c[j]));
-  }
-  e = cb_exponent(mx);
-  uint32_t h16[E];
-#pragma unroll
-  for (int j = 0; j < E; ++j) h16[j] = float_to_f16_bits(ldexpf(c[j], e));
-  set_planes<BITS>(cb, h16);
-}
-
 __device__ __forceinline__ uint32_t to_f16_bits(uint32_t raw, int dt) {
   return dt == DIMQ_F16 ? raw : float_to_f16_bits(bf16_bits_to_float(raw));
 }
 
-// T = KH*KW*CC sub-steps of 32 channels; CC = C / 32.
-template <int BITS, int CC, int STRIDE, int KHW>
+// Four consecutive outputs of one lane: one 16-byte (fp32) or 8-byte (16-bit)
+// store when `vec`, element stores otherwise.
+__device__ __forceinline__ void store4(void* y, int dt, int64_t off, const float v[4], bool vec) {
+  if (vec && dt == DIMQ_F32) {
+    *reinterpret_cast<float4*>(reinterpret_cast<float*>(y) + off) = make_float4(v[0], v[1], v[2], v[3]);
+  } else if (vec) {
+    uint32_t h[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) h[i] = dt == DIMQ_F16 ? float_to_f16_bits(v[i]) : float_to_bf16_bits(v[i]);
+    *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(y) + off) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) store_from_float(y, dt, off + i, v[i]);
+  }
+}
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ floatx16 mfma32x32x16(half8 a, half8 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// T = KH*KW*CC16 sub-steps of 16 channels; CC16 = C / 16.
+// Waves: wn = wave & 1 owns output channels [32*wn, 32*wn + 32) of the tile,
+// wm = wave >> 1 owns the 32-pixel m-blocks wm, wm + 2, wm + 4, wm + 6, so one
+// decoded weight fragment feeds 4 MFMAs.
+// PXROWS: MFMA rows are pixels (lane holds 4 consecutive pixels of one output
+// channel: contiguous in NCHW); otherwise rows are output channels (lane holds
+// 4 consecutive channels of one pixel: contiguous in NHWC).
+template <int BITS, int CC16, int STRIDE, int KHW, bool PXROWS>
 __global__ __launch_bounds__(256) void conv_halo_kernel(const HaloArgs p) {
-  constexpr int T = KHW * CC;
+  constexpr int T = KHW * CC16;
   constexpr int CHUNKS = (T + 3) / 4;
-  constexpr int WPL = CHUNKS * BITS;  // packed words per lane per output row
-  constexpr int NB = 4;               // 64 output channels per work-group
-  constexpr int MBW = 4;              // m-blocks (16 pixels) per wave, at most
+  constexpr int WPL = CHUNKS * BITS;  // packed words per lane
+  constexpr int MBW = 4;              // 32-pixel m-blocks per wave (256 pixels per tile)
   extern __shared__ __attribute__((aligned(16))) uint16_t halo[];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int col = lane & 15;
-  const int g = lane >> 4;
+  const int col = lane & 31;
+  const int g = lane >> 5;
   const int tile = blockIdx.x;
   const int b = tile / p.tiles_h;
   const int oh0 = (tile - b * p.tiles_h) * p.TH;
   const int oc0 = blockIdx.y * 64;
-  const int C = CC * 32;
+  const int C = CC16 * 16;
+  const int wn = wave & 1;
+  const int wm = wave >> 1;
+  const int ocl = oc0 + 32 * wn + col;  // this lane's weight row
 
-  // ---- stage the input halo: rows ih = oh0*S - pad + r, cols iw = -pad + c
+  // ---- codebooks of the 64 output rows -> LDS (fp32), then byte planes
+  constexpr int E = 1 << BITS;
+  __shared__ float cbs[64 * E];
+  stage_codebook<E>(p.cb, p.cb_dt, p.cb_rows, p.cb_size, oc0, 64, p.OC, cbs, tid, 256);
+
+  // ---- weights: this lane's packed words (independent loads)
+  uint32_t wreg[WPL];
+  {
+    const int oc = min(ocl, p.OC - 1);
+    const uint32_t* src = p.kw + ((int64_t)oc * 2 + g) * WPL;
+#pragma unroll
+    for (int w = 0; w < WPL; ++w) wreg[w] = src[w];
+  }
+
+  // ---- stage the input halo: halo row r <-> ih = oh0*S - pad_h + r,
+  //      halo col hc <-> iw = hc - pad_w.  Zero outside the image.
   const int ih0 = oh0 * STRIDE - p.pad_h;
-  const int rows_valid = p.IH_t;
-  if (p.x_layout == DIMQ_NCHW) {
-    // task = (channel pair, halo row, 8 halo columns)
-    const int cg = (p.IW_t + 7) / 8;
-    const int tasks = (C / 2) * rows_valid * cg;
-    for (int t = tid; t < tasks; t += 256) {
-      const int c8 = t % cg;
-      const int rest = t / cg;
-      const int r = rest % rows_valid;
-      const int c2 = rest / rows_valid;
-      const int ih = ih0 + r;
-      const int cbase = c8 * 8;
-      uint32_t v0[8], v1[8];
+  if (p.x_layout == DIMQ_NCHW && (p.W & 7) == 0) {
+    // task = (8-channel octet, halo row, 8 input columns): eight 16-byte row
+    // loads, an 8x8 transpose in registers, eight 16-byte LDS stores.
+    const int qn = p.W / 8;
+    const int tasks = (C / 8) * p.IH_t * qn;
+    constexpr int TPT = 2;  // tasks in flight per thread
+    for (int t0 = 0; t0 < tasks; t0 += 256 * TPT) {
+      uint4 v[TPT][8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int iw = cbase + j - p.pad_w;
-        uint32_t a = 0, bb = 0;
-        if (ih >= 0 && ih < p.H && iw >= 0 && iw < p.W) {
-          const int64_t off = (((int64_t)b * p.C + 2 * c2) * p.H + ih) * p.W + iw;
-          a = reinterpret_cast<const uint16_t*>(p.x)[off];
-          bb = reinterpret_cast<const uint16_t*>(p.x)[off + (int64_t)p.H * p.W];
-          a = to_f16_bits(a, p.x_dt);
-          bb = to_f16_bits(bb, p.x_dt);
+      for (int u = 0; u < TPT; ++u) {
+        const int t = t0 + u * 256 + tid;
+        const int tt = t < tasks ? t : 0;
+        const int co = tt % (C / 8);
+        const int rest = tt / (C / 8);
+        const int q = rest % qn;
+        const int r = rest / qn;
+        const int ih = ih0 + r;
+        const bool live = t < tasks && ih >= 0 && ih < p.H;
+        const int ihc = live ? ih : 0;
+        const uint16_t* src = reinterpret_cast<const uint16_t*>(p.x) +
+                              (((int64_t)b * p.C + 8 * co) * p.H + ihc) * p.W + 8 * q;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          v[u][c] = *reinterpret_cast<const uint4*>(src + (int64_t)c * p.H * p.W);
+          if (!live) v[u][c] = make_uint4(0, 0, 0, 0);
         }
-        v0[j] = a;
-        v1[j] = bb;
       }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int hc = cbase + j;
-        if (hc < p.IW_t)
-          *reinterpret_cast<uint32_t*>(&halo[(r * p.IW_t + hc) * p.CP + 2 * c2]) = v0[j] | (v1[j] << 16);
+      for (int u = 0; u < TPT; ++u) {
+        const int t = t0 + u * 256 + tid;
+        if (t >= tasks) continue;
+        const int co = t % (C / 8);
+        const int rest = t / (C / 8);
+        const int q = rest % qn;
+        const int r = rest / qn;
+        uint32_t in[8][4];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          uint32_t w4[4] = {v[u][c].x, v[u][c].y, v[u][c].z, v[u][c].w};
+          if (p.x_dt != DIMQ_F16) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+              w4[k] = to_f16_bits(w4[k] & 0xffffu, p.x_dt) | (to_f16_bits(w4[k] >> 16, p.x_dt) << 16);
+          }
+#pragma unroll
+          for (int k = 0; k < 4; ++k) in[c][k] = w4[k];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          // pixel j: channels 2w, 2w+1 from half (j&1) of word j/2 of rows 2w, 2w+1
+          const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+          const uint4 o = make_uint4(perm(in[1][j >> 1], in[0][j >> 1], sel), perm(in[3][j >> 1], in[2][j >> 1], sel),
+                                     perm(in[5][j >> 1], in[4][j >> 1], sel), perm(in[7][j >> 1], in[6][j >> 1], sel));
+          const int hc = 8 * q + j + p.pad_w;
+          if (hc < p.IW_t) *reinterpret_cast<uint4*>(&halo[(r * p.IW_t + hc) * p.CP + 8 * co]) = o;
+        }
       }
+    }
+    // zero the padding columns (hc < pad_w, hc >= pad_w + W)
+    const int npad = p.IW_t - p.W;
+    const int ztasks = p.IH_t * (npad > 0 ? npad : 0) * (C / 8);
+    for (int t = tid; t < ztasks; t += 256) {
+      const int co = t % (C / 8);
+      const int rest = t / (C / 8);
+      const int pc = rest % npad;
+      const int r = rest / npad;
+      const int hc = pc < p.pad_w ? pc : p.W + pc;
+      if (hc < p.IW_t) *reinterpret_cast<uint4*>(&halo[(r * p.IW_t + hc) * p.CP + 8 * co]) = make_uint4(0, 0, 0, 0);
+    }
+  } else if (p.x_layout == DIMQ_NCHW) {
+    // any width: task = (channel pair, halo row, halo column)
+    const int tasks = (C / 2) * p.IH_t * p.IW_t;
+    for (int t = tid; t < tasks; t += 256) {
+      const int hc = t % p.IW_t;
+      const int rest = t / p.IW_t;
+      const int r = rest % p.IH_t;
+      const int c2 = rest / p.IH_t;
+      const int ih = ih0 + r, iw = hc - p.pad_w;
+      uint32_t a = 0, bb = 0;
+      if (ih >= 0 && ih < p.H && iw >= 0 && iw < p.W) {
+        const int64_t off = (((int64_t)b * p.C + 2 * c2) * p.H + ih) * p.W + iw;
+        a = to_f16_bits(reinterpret_cast<const uint16_t*>(p.x)[off], p.x_dt);
+        bb = to_f16_bits(reinterpret_cast<const uint16_t*>(p.x)[off + (int64_t)p.H * p.W], p.x_dt);
+      }
+      *reinterpret_cast<uint32_t*>(&halo[(r * p.IW_t + hc) * p.CP + 2 * c2]) = a | (bb << 16);
     }
   } else {
     // NHWC: task = (halo pixel, 8 channels) -> one 16-byte load, one 16-byte LDS store
-    const int tasks = rows_valid * p.IW_t * (C / 8);
-    for (int t = tid; t < tasks; t += 256) {
-      const int c8 = t % (C / 8);
-      const int pix = t / (C / 8);
-      const int r = pix / p.IW_t;
-      const int hc = pix - r * p.IW_t;
-      const int ih = ih0 + r;
-      const int iw = hc - p.pad_w;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (ih >= 0 && ih < p.H && iw >= 0 && iw < p.W) {
-        const int64_t off = (((int64_t)b * p.H + ih) * p.W + iw) * p.C + 8 * c8;
-        v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p.x) + off);
-        if (p.x_dt != DIMQ_F16) {
-          uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+    const int tasks = p.IH_t * p.IW_t * (C / 8);
+    constexpr int TPT = 4;
+    for (int t0 = 0; t0 < tasks; t0 += 256 * TPT) {
+      uint4 v[TPT];
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            w4[q] = to_f16_bits(w4[q] & 0xffffu, p.x_dt) | (to_f16_bits(w4[q] >> 16, p.x_dt) << 16);
-          v = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-        }
+      for (int u = 0; u < TPT; ++u) {
+        const int t = t0 + u * 256 + tid;
+        const int tt = t < tasks ? t : 0;
+        const int c8 = tt % (C / 8);
+        const int pix = tt / (C / 8);
+        const int r = pix / p.IW_t;
+        const int hc = pix - r * p.IW_t;
+        const int ih = ih0 + r;
+        const int iw = hc - p.pad_w;
+        const bool live = t < tasks && ih >= 0 && ih < p.H && iw >= 0 && iw < p.W;
+        const int64_t off = live ? (((int64_t)b * p.H + ih) * p.W + iw) * p.C + 8 * c8 : 0;
+        v[u] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p.x) + off);
+        if (!live) v[u] = make_uint4(0, 0, 0, 0);
       }
-      *reinterpret_cast<uint4*>(&halo[(r * p.IW_t + hc) * p.CP + 8 * c8]) = v;
+#pragma unroll
+      for (int u = 0; u < TPT; ++u) {
+        const int t = t0 + u * 256 + tid;
+        if (t >= tasks) continue;
+        const int c8 = t % (C / 8);
+        const int pix = t / (C / 8);
+        uint4 o = v[u];
+        if (p.x_dt != DIMQ_F16) {
+          uint32_t w4[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+            w4[k] = to_f16_bits(w4[k] & 0xffffu, p.x_dt) | (to_f16_bits(w4[k] >> 16, p.x_dt) << 16);
+          o = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        }
+        *reinterpret_cast<uint4*>(&halo[pix * p.CP + 8 * c8]) = o;
+      }
     }
   }
-
-  // ---- weights and codebooks for this lane's 4 output rows
-  uint32_t wreg[NB][WPL];
-  CodebookRegs<BITS> cbr[NB];
-  float scale[NB];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const int oc = oc0 + nb * 16 + col;
-    const bool valid = oc < p.OC;
-    const uint32_t* src = p.kw + ((int64_t)oc * 4 + g) * WPL;
-#pragma unroll
-    for (int w = 0; w < WPL; ++w) wreg[nb][w] = valid ? src[w] : 0u;
-    int e;
-    load_cb_row<BITS>(p, p.cb_rows == 1 ? 0 : oc, valid, cbr[nb], e);
-    scale[nb] = ldexpf(1.0f, -e);
+  __syncthreads();
+  CodebookRegs<BITS> cbr;
+  float scale;
+  {
+    const int rl = (p.cb_rows == 1) ? 0 : 32 * wn + col;
+    const int e = planes_from_lds<BITS, false>(cbs + rl * E, cbr, cbr);
+    scale = ldexpf(1.0f, -e);
   }
 
-  // ---- this lane's pixels: m-blocks mb = wave + 4*q
+  // ---- this lane's pixels: m-blocks mb = wm + 2*q (pixels past the tile read
+  //      pixel 0 and are never stored, so the loop below has no branches)
   const int P = min(p.TH, p.OH - oh0) * p.OW;
-  const int MBT = (P + 15) / 16;
   int base[MBW];
 #pragma unroll
   for (int q = 0; q < MBW; ++q) {
-    const int mb = wave + 4 * q;
-    int pix = mb * 16 + col;
+    int pix = (wm + 2 * q) * 32 + col;
     if (pix >= P) pix = 0;
     const int r = pix / p.OW;
     const int c = pix - r * p.OW;
     base[q] = ((r * STRIDE) * p.IW_t + c * STRIDE) * p.CP + 8 * g;
   }
-  __syncthreads();
 
-  floatx4 acc[MBW][NB];
+  floatx16 acc[MBW];
 #pragma unroll
   for (int q = 0; q < MBW; ++q)
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[q][nb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < 16; ++i) acc[q][i] = 0.0f;
 
 #pragma unroll
   for (int t = 0; t < T; ++t) {
-    const int khw = t / CC;
-    const int cc = t - khw * CC;
+    const int khw = t / CC16;
+    const int cc = t - khw * CC16;
     const int kh = (KHW == 9) ? khw / 3 : 0;
     const int kw = (KHW == 9) ? khw - 3 * kh : 0;
-    const int koff = (kh * p.IW_t + kw) * p.CP + 32 * cc;
-    half8 wf[NB];
+    const int koff = (kh * p.IW_t + kw) * p.CP + 16 * cc;
+    uint32_t chunk[BITS];
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      uint32_t chunk[BITS];
+    for (int w = 0; w < BITS; ++w) chunk[w] = wreg[(t >> 2) * BITS + w];
+    const half8 wf = decode_sub<BITS>(chunk, t & 3, cbr);
+    half8 xf[MBW];
 #pragma unroll
-      for (int w = 0; w < BITS; ++w) chunk[w] = wreg[nb][(t >> 2) * BITS + w];
-      wf[nb] = decode_sub<BITS>(chunk, t & 3, cbr[nb]);
-    }
+    for (int q = 0; q < MBW; ++q) xf[q] = *reinterpret_cast<const half8*>(&halo[base[q] + koff]);
 #pragma unroll
-    for (int q = 0; q < MBW; ++q) {
-      if (wave + 4 * q < MBT) {
-        const half8 xf = *reinterpret_cast<const half8*>(&halo[base[q] + koff]);
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) acc[q][nb] = mfma16x16x32(wf[nb], xf, acc[q][nb]);
-      }
-    }
+    for (int q = 0; q < MBW; ++q) acc[q] = PXROWS ? mfma32x32x16(xf[q], wf, acc[q]) : mfma32x32x16(wf, xf[q], acc[q]);
   }
 
-  // ---- epilogue: lane holds D[oc = nb*16 + 4g + i][pixel = mb*16 + col]
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int orow = 4 * g + i;
-      const float sc = __shfl(scale[nb], orow, 64);
-      const int oc = oc0 + nb * 16 + orow;
-      if (oc >= p.OC) continue;
-      const float bv = p.bias ? load_as_float(p.bias, p.bias_dt, oc) : 0.0f;
+  // ---- epilogue: acc[q][4j + i] = D[row 8j + 4g + i][col], 32x32 block q
+  const int64_t ohw = (int64_t)p.OH * p.OW;
+  if constexpr (PXROWS) {
+    // rows are pixels mb*32 + 8j + 4g + i, column = output channel ocl.
+    // NCHW offset of (oc, pixel) = (b*OC + oc)*OH*OW + oh0*OW + pixel.
+    if (ocl < p.OC) {
+      const bool vec = (ohw % 4 == 0) && (p.OW % 4 == 0) && (p.y_layout == DIMQ_NCHW);
+      const float bv = p.bias ? load_as_float(p.bias, p.bias_dt, ocl) : 0.0f;
+      const int64_t chan = ((int64_t)b * p.OC + ocl) * ohw + (int64_t)oh0 * p.OW;
 #pragma unroll
       for (int q = 0; q < MBW; ++q) {
-        const int mb = wave + 4 * q;
-        const int pix = mb * 16 + col;
-        if (mb < MBT && pix < P) {
-          const int r = pix / p.OW;
-          const int c = pix - r * p.OW;
-          const int oh = oh0 + r;
-          const int64_t off = p.y_layout == DIMQ_NCHW
-                                  ? (((int64_t)b * p.OC + oc) * p.OH + oh) * p.OW + c
-                                  : (((int64_t)b * p.OH + oh) * p.OW + c) * p.OC + oc;
-          store_from_float(p.y, p.y_dt, off, acc[q][nb][i] * sc + bv);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int pix0 = (wm + 2 * q) * 32 + 8 * j + 4 * g;
+          if (pix0 >= P) continue;
+          float v[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] = acc[q][4 * j + i] * scale + bv;
+          if (p.y_layout == DIMQ_NCHW && pix0 + 4 <= P) {
+            store4(p.y, p.y_dt, chan + pix0, v, vec);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              if (pix0 + i < P) {
+                const int64_t off = p.y_layout == DIMQ_NCHW
+                                        ? chan + pix0 + i
+                                        : ((int64_t)b * ohw + (int64_t)oh0 * p.OW + pix0 + i) * p.OC + ocl;
+                store_from_float(p.y, p.y_dt, off, v[i]);
+              }
+            }
+          }
+        }
+      }
+    }
+  } else {
+    // rows are output channels oc0 + 32*wn + 8j + 4g + i, column = pixel mb*32 + col.
+    // NHWC offset of (pixel, oc) = (b*OH*OW + oh0*OW + pixel)*OC + oc.
+    const bool vec = (p.OC % 4 == 0) && (p.y_layout == DIMQ_NHWC);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int ocb = oc0 + 32 * wn + 8 * j + 4 * g;
+      float sc[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sc[i] = __shfl(scale, 8 * j + 4 * g + i, 32);
+        bv[i] = (p.bias && ocb + i < p.OC) ? load_as_float(p.bias, p.bias_dt, ocb + i) : 0.0f;
+      }
+#pragma unroll
+      for (int q = 0; q < MBW; ++q) {
+        const int pix = (wm + 2 * q) * 32 + col;
+        if (pix >= P) continue;
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = acc[q][4 * j + i] * sc[i] + bv[i];
+        const int64_t pbase = (int64_t)b * ohw + (int64_t)oh0 * p.OW + pix;
+        if (p.y_layout == DIMQ_NHWC && ocb + 4 <= p.OC) {
+          store4(p.y, p.y_dt, pbase * p.OC + ocb, v, vec);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (ocb + i < p.OC) {
+              const int64_t off = p.y_layout == DIMQ_NHWC ? pbase * p.OC + ocb + i
+                                                          : ((int64_t)b * p.OC + ocb + i) * ohw + (int64_t)oh0 * p.OW + pix;
+              store_from_float(p.y, p.y_dt, off, v[i]);
+            }
+          }
         }
       }
     }
@@ -238,8 +360,8 @@ __global__ __launch_bounds__(256) void conv_halo_kernel(const HaloArgs p) {
 }
 
 // ---- weight preparation: conv_kcrs b-bit stream -> kernel layout
-// out[((n*4 + g)*CHUNKS + chunk)*BITS + w]: sub-steps t = 4*chunk + s, slot j
-// holds channel c = 32*(t % CC) + 8*g + j at (kh, kw) = divmod(t / CC, KW),
+// out[((n*2 + g)*CHUNKS + chunk)*BITS + w]: sub-steps t = 4*chunk + s, slot j
+// holds channel c = 16*(t % CC16) + 8*g + j at (kh, kw) = divmod(t / CC16, KW),
 // at the field position that decode_sub<BITS>(chunk, s) reads as slot j.
 template <int BITS>
 __device__ __forceinline__ int field_of(int s, int j) {
@@ -257,11 +379,11 @@ template <int BITS>
 __global__ void prepare_kernel(const uint8_t* __restrict__ src, int OC, int C, int KH, int KW, int CC, int T,
                                int chunks, uint32_t* __restrict__ out) {
   const int64_t id = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t total = (int64_t)OC * 4 * chunks;
+  const int64_t total = (int64_t)OC * 2 * chunks;
   if (id >= total) return;
   const int chunk = static_cast<int>(id % chunks);
-  const int g = static_cast<int>((id / chunks) % 4);
-  const int n = static_cast<int>(id / (4 * chunks));
+  const int g = static_cast<int>((id / chunks) % 2);
+  const int n = static_cast<int>(id / (2 * chunks));
   uint32_t words[BITS];
 #pragma unroll
   for (int w = 0; w < BITS; ++w) words[w] = 0;
@@ -273,7 +395,7 @@ __global__ void prepare_kernel(const uint8_t* __restrict__ src, int OC, int C, i
     const int kh = khw / KW;
     const int kw = khw - kh * KW;
     for (int j = 0; j < 8; ++j) {
-      const int c = 32 * cc + 8 * g + j;
+      const int c = 16 * cc + 8 * g + j;
       const int64_t i = (((int64_t)n * C + c) * KH + kh) * KW + kw;
       const int64_t bit = i * BITS;
       uint32_t v = src[bit >> 3] >> (bit & 7);
@@ -293,25 +415,28 @@ template <int BITS, int CC, int STRIDE>
 int launch_halo(const HaloArgs& p, hipStream_t s) {
   const size_t lds = (size_t)p.IH_t * p.IW_t * p.CP * sizeof(uint16_t);
   const dim3 grid(static_cast<unsigned>(p.B * p.tiles_h), static_cast<unsigned>((p.OC + 63) / 64));
+  const bool pxrows = p.y_layout == DIMQ_NCHW;
   if (p.KH == 3) {
-    hipLaunchKernelGGL((conv_halo_kernel<BITS, CC, STRIDE, 9>), grid, dim3(256), lds, s, p);
+    if (pxrows) hipLaunchKernelGGL((conv_halo_kernel<BITS, CC, STRIDE, 9, true>), grid, dim3(256), lds, s, p);
+    else hipLaunchKernelGGL((conv_halo_kernel<BITS, CC, STRIDE, 9, false>), grid, dim3(256), lds, s, p);
   } else {
-    hipLaunchKernelGGL((conv_halo_kernel<BITS, CC, STRIDE, 1>), grid, dim3(256), lds, s, p);
+    if (pxrows) hipLaunchKernelGGL((conv_halo_kernel<BITS, CC, STRIDE, 1, true>), grid, dim3(256), lds, s, p);
+    else hipLaunchKernelGGL((conv_halo_kernel<BITS, CC, STRIDE, 1, false>), grid, dim3(256), lds, s, p);
   }
   return check_launch("conv2d_codebook (halo)");
 }
 
 template <int BITS>
-int launch_halo_cc(const HaloArgs& p, int CC, int stride, hipStream_t s) {
-  if (CC == 2) return stride == 1 ? launch_halo<BITS, 2, 1>(p, s) : launch_halo<BITS, 2, 2>(p, s);
-  return stride == 1 ? launch_halo<BITS, 4, 1>(p, s) : launch_halo<BITS, 4, 2>(p, s);
+int launch_halo_cc(const HaloArgs& p, int CC16, int stride, hipStream_t s) {
+  if (CC16 == 4) return stride == 1 ? launch_halo<BITS, 4, 1>(p, s) : launch_halo<BITS, 4, 2>(p, s);
+  return stride == 1 ? launch_halo<BITS, 8, 1>(p, s) : launch_halo<BITS, 8, 2>(p, s);
 }
 
 }  // namespace
 
 int64_t halo_prepared_words(int64_t OC, int64_t C, int64_t KH, int64_t KW, int bits) {
-  const int64_t T = KH * KW * (C / 32);
-  return OC * 4 * ((T + 3) / 4) * bits;
+  const int64_t T = KH * KW * (C / 16);
+  return OC * 2 * ((T + 3) / 4) * bits;
 }
 
 // Output rows per tile: at most 256 pixels (16 m-blocks over 4 waves) and a
@@ -366,7 +491,7 @@ int launch_conv_halo(const void* x, int x_dtype, int x_layout, int64_t B, int64_
   p.CP = (int)C + 8;
   p.tiles_h = (int)((OH + p.TH - 1) / p.TH);
   p.kw = kw;
-  const int64_t T = KH * KW * (C / 32);
+  const int64_t T = KH * KW * (C / 16);
   p.words_per_lane = (int)(((T + 3) / 4) * bits);
   p.cb = cb;
   p.cb_dt = cb_dtype;
@@ -377,7 +502,7 @@ int launch_conv_halo(const void* x, int x_dtype, int x_layout, int64_t B, int64_
   p.y = y;
   p.y_dt = y_dtype;
   p.y_layout = y_layout;
-  const int CC = (int)(C / 32);
+  const int CC = (int)(C / 16);
   switch (bits) {
     case 2: return launch_halo_cc<2>(p, CC, (int)stride, s);
     case 3: return launch_halo_cc<3>(p, CC, (int)stride, s);
@@ -387,10 +512,10 @@ int launch_conv_halo(const void* x, int x_dtype, int x_layout, int64_t B, int64_
 
 int launch_prepare(const uint8_t* src, int64_t OC, int64_t C, int64_t KH, int64_t KW, int bits, uint32_t* out,
                    hipStream_t s) {
-  const int CC = (int)(C / 32);
+  const int CC = (int)(C / 16);
   const int T = (int)(KH * KW * CC);
   const int chunks = (T + 3) / 4;
-  const int64_t total = OC * 4 * chunks;
+  const int64_t total = OC * 2 * chunks;
   const unsigned blocks = static_cast<unsigned>((total + 255) / 256);
   switch (bits) {
     case 2: hipLaunchKernelGGL(prepare_kernel<2>, dim3(blocks), dim3(256), 0, s, src, (int)OC, (int)C, (int)KH,

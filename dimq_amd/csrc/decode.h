@@ -141,4 +141,77 @@ __device__ __forceinline__ int cb_exponent(float maxabs) {
   return e;
 }
 
+// Cooperative staging of codebook rows into LDS as fp32.
+// Rows [row0, row0 + R) (or only row 0 for a per-layer codebook) with
+// cb_size entries each are written to lds[r * E + j], entries j >= cb_size
+// and rows >= n_rows as 0.  Eight independent loads per thread are issued
+// before any is used, on a dtype branch taken once, so the few hundred loads
+// of a work-group overlap instead of queueing one latency after another.
+template <int E>
+__device__ __forceinline__ void stage_codebook(const void* cb, int dt, int64_t cb_rows, int cb_size, int64_t row0,
+                                               int R, int64_t n_rows, float* lds, int tid, int nthreads) {
+  const int Rr = (cb_rows == 1) ? 1 : R;
+  const int total = Rr * E;
+  for (int base = 0; base < total; base += 8 * nthreads) {
+    float v[8];
+    int64_t off[8];
+    bool ok[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = base + u * nthreads + tid;
+      const int r = i / E, j = i % E;
+      const int64_t row = (cb_rows == 1) ? 0 : row0 + r;
+      ok[u] = i < total && j < cb_size && (cb_rows == 1 || row < n_rows);
+      off[u] = ok[u] ? row * cb_size + j : 0;
+    }
+    if (dt == DIMQ_F32) {
+      const float* p = reinterpret_cast<const float*>(cb);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = p[off[u]];
+    } else if (dt == DIMQ_F16) {
+      const uint16_t* p = reinterpret_cast<const uint16_t*>(cb);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = f16_bits_to_float(p[off[u]]);
+    } else if (dt == DIMQ_BF16) {
+      const uint16_t* p = reinterpret_cast<const uint16_t*>(cb);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = bf16_bits_to_float(p[off[u]]);
+    } else {
+      const double* p = reinterpret_cast<const double*>(cb);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = (float)p[off[u]];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = base + u * nthreads + tid;
+      if (i < total) lds[i] = ok[u] ? v[u] : 0.0f;
+    }
+  }
+}
+
+// Byte planes (and the power-of-two exponent) of one staged codebook row.
+// A4 (hi_lo): second plane set holds the fp16 residual c - fp16(c).
+template <int BITS, bool HI_LO>
+__device__ __forceinline__ int planes_from_lds(const float* row, CodebookRegs<BITS>& hi, CodebookRegs<BITS>& lo) {
+  constexpr int E = 1 << BITS;
+  float c[E];
+  float mx = 0.0f;
+#pragma unroll
+  for (int j = 0; j < E; ++j) {
+    c[j] = row[j];
+    mx = fmaxf(mx, fabsf(c[j]));
+  }
+  const int e = cb_exponent(mx);
+  uint32_t h16[E], l16[E];
+#pragma unroll
+  for (int j = 0; j < E; ++j) {
+    const float cs = ldexpf(c[j], e);
+    h16[j] = float_to_f16_bits(cs);
+    if constexpr (HI_LO) l16[j] = float_to_f16_bits(cs - f16_bits_to_float(h16[j]));
+  }
+  set_planes<BITS>(hi, h16);
+  if constexpr (HI_LO) set_planes<BITS>(lo, l16);
+  return e;
+}
+
 }  // namespace dimq

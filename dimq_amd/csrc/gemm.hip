@@ -1,6 +1,8 @@
 // Host side of the codebook Linear: argument checks (with the reference's
 // messages where one exists, csrc/dimq_gemm_lut.cu:66-79), tile selection and
 // launch.
+#include <stdlib.h>
+
 #include "gemm_kernel.h"
 
 namespace dimq {
@@ -9,6 +11,14 @@ namespace {
 constexpr int64_t kCUs = 256;
 
 }  // namespace
+
+// Fast-path tiles need K % 128 == 0, aligned rows/streams and a Linear layout.
+int gemm_fast_tile(int tile, const GemmArgs& p, int bits) {
+  if (bits == 8 || p.conv || !p.fast_b || !p.vec_a || p.K % kKM != 0) return tile;
+  if (tile == kTile128x64) return kTileFast128x64;
+  if (tile == kTile64x32) return kTileFast64x32;
+  return tile;
+}
 
 int gemm_pick_tile(int64_t M, int64_t N, int variant) {
   if (variant == DIMQ_VARIANT_SMALL_M) return M <= 16 ? kTileGemv : kTile16x16;
@@ -81,7 +91,12 @@ int linear_codebook_impl(const void* x, int x_dtype, int64_t M, int64_t K, int64
   p.vec_a = aligned(x, 16) && ((ldx * xs) % 16 == 0);
   p.groups = 1;
   if (M == 0 || N == 0) return DIMQ_OK;
-  return dispatch<false>(p, bits, x_dtype, gemm_pick_tile(M, N, variant), s);
+  const char* force = getenv("DIMQ_GEMM_TILE");  // A/B runs: force a tile id
+  int tile = force ? atoi(force) : gemm_fast_tile(gemm_pick_tile(M, N, variant), p, bits);
+  if (tile < 0 || tile >= kTileCount) tile = gemm_pick_tile(M, N, variant);
+  if (tile >= kTileFast128x64 && gemm_fast_tile(kTile64x32, p, bits) == kTile64x32) tile = gemm_pick_tile(M, N, variant);
+  if (tile == kTileGemv && (M > 16 || bits == 8)) tile = gemm_pick_tile(M, N, DIMQ_VARIANT_MFMA);
+  return dispatch<false>(p, bits, x_dtype, tile, s);
 }
 
 }  // namespace dimq
@@ -146,5 +161,6 @@ extern "C" int dimq_linear_lut(const void* x, int x_dtype, int64_t M, const uint
   p.fast_b = (in_features % 32 == 0) && aligned(packed_w, 16);
   p.vec_a = aligned(x, 16) && ((in_features * dtype_size(x_dtype)) % 16 == 0);
   p.groups = 1;
-  return dispatch<true>(p, 4, x_dtype, kTile64x32, as_stream(stream));
+  const int tile = (x_dtype != DIMQ_F64) ? gemm_fast_tile(kTile64x32, p, 4) : kTile64x32;
+  return dispatch<true>(p, 4, x_dtype, tile, as_stream(stream));
 }

@@ -15,10 +15,21 @@ int launch_gemm_tile(const GemmArgs& p, int tile, hipStream_t s) {
     else if (tile == kTile64x32) hipLaunchKernelGGL((gemm_cb8_kernel<64, 16, XT>), g1(gy64, 64), dim3(256), 0, s, p);
     else hipLaunchKernelGGL((gemm_cb8_kernel<16, 16, XT>), g1(gy16, 64), dim3(256), 0, s, p);
   } else if constexpr (A4) {
-    hipLaunchKernelGGL((gemm_cb_kernel<BITS, 64, 32, XT, true>), g1(gy64, 128),
-                       dim3(256), 0, s, p);
+    if (tile == kTileFast64x32)
+      hipLaunchKernelGGL((gemm_fast_kernel<BITS, 64, 32, XT, true>), g1(gy64, 128), dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((gemm_cb_kernel<BITS, 64, 32, XT, true>), g1(gy64, 128),
+                         dim3(256), 0, s, p);
   } else {
-    if (tile == kTileGemv)
+    if (tile == kTileFast128x64)
+      hipLaunchKernelGGL((gemm_fast_kernel<BITS, 128, 64, XT, false>), g1(gy128, 256), dim3(256), 0, s, p);
+    else if (tile == kTileFast64x32)
+      hipLaunchKernelGGL((gemm_fast_kernel<BITS, 64, 32, XT, false>), g1(gy64, 128), dim3(256), 0, s, p);
+    else if (tile == kTileFast128x32)
+      hipLaunchKernelGGL((gemm_fast_kernel<BITS, 128, 32, XT, false>), g1(gy128, 128), dim3(256), 0, s, p);
+    else if (tile == kTileFast64x64)
+      hipLaunchKernelGGL((gemm_fast_kernel<BITS, 64, 64, XT, false>), g1(gy64, 256), dim3(256), 0, s, p);
+    else if (tile == kTileGemv)
       hipLaunchKernelGGL((gemv_cb_kernel<BITS, XT, 16>), dim3(static_cast<unsigned>((p.N + 15) / 16)), dim3(1024), 0,
                          s, p);
     else if (tile == kTile128x64)

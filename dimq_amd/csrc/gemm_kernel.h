@@ -287,15 +287,31 @@ __global__ __launch_bounds__(256) void gemm_cb_kernel(const GemmArgs p) {
   const int64_t nz = static_cast<int64_t>(blockIdx.z) * p.N;      // first weight row of this group
   const int64_t cbase = static_cast<int64_t>(blockIdx.z) * p.cICg;  // first input channel of this group
 
+  constexpr int E = 1 << BITS;
+  float* cbs = reinterpret_cast<float*>(&As[1][0]);
+  {
+    const int64_t n0 = nt * (4 * WN);
+    if constexpr (4 * WN * E * 4 <= BM * kLDA * 2) {
+      stage_codebook<E>(p.cb, p.cb_dt, p.cb_rows, p.cb_size, nz + n0, 4 * WN, nz + p.N, cbs, tid, 256);
+    }
+  }
+  __syncthreads();
   CodebookRegs<BITS> cb[NB][NCB];
   float colscale[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     const int64_t n = nw0 + nb * 16 + col;
-    const int64_t row = (p.cb_rows == 1) ? 0 : nz + n;
-    const int e = load_codebook_row<BITS, A4>(p, row, n < p.N, cb[nb][0], cb[nb][NCB - 1]);
+    int e;
+    if constexpr (4 * WN * E * 4 <= BM * kLDA * 2) {
+      const int rl = (p.cb_rows == 1) ? 0 : wave * WN + nb * 16 + col;
+      e = planes_from_lds<BITS, A4>(cbs + rl * E, cb[nb][0], cb[nb][NCB - 1]);
+    } else {
+      const int64_t row = (p.cb_rows == 1) ? 0 : nz + n;
+      e = load_codebook_row<BITS, A4>(p, row, n < p.N, cb[nb][0], cb[nb][NCB - 1]);
+    }
     colscale[nb] = ldexpf(A4 ? p.act_scale : 1.0f, -e);
   }
+  __syncthreads();
 
   floatx4 acc[MB][NB];
 #pragma unroll
@@ -559,9 +575,13 @@ __global__ __launch_bounds__(WPW * 64) void gemv_cb_kernel(const GemmArgs p) {
   const int col = lane & 15;
   const int g = lane >> 4;
   const int64_t n = static_cast<int64_t>(blockIdx.x) * 16 + col;
-  const int64_t row = (p.cb_rows == 1) ? 0 : n;
+  constexpr int E = 1 << BITS;
+  __shared__ float cbs[16 * E];
+  stage_codebook<E>(p.cb, p.cb_dt, p.cb_rows, p.cb_size, static_cast<int64_t>(blockIdx.x) * 16, 16, p.N, cbs, tid,
+                    WPW * 64);
+  __syncthreads();
   CodebookRegs<BITS> cb;
-  const int e = load_codebook_row<BITS, false>(p, row, n < p.N, cb, cb);
+  const int e = planes_from_lds<BITS, false>(cbs + ((p.cb_rows == 1) ? 0 : col * E), cb, cb);
   const float colscale = ldexpf(1.0f, -e);
   const int64_t nk = (p.K + kKM - 1) / kKM;
   const bool arow = col < p.M;
@@ -605,8 +625,236 @@ __global__ __launch_bounds__(WPW * 64) void gemv_cb_kernel(const GemmArgs p) {
   }
 }
 
+// ---- fast Linear kernel -------------------------------------------------------
+// Same tiling as gemm_cb_kernel, for the shapes the BASELINE layers have:
+// Linear, K % 128 == 0, x rows 16-byte aligned, packed stream 16-byte aligned.
+// Those guarantees let the main loop be straight-line code, which is what
+// lets the compiler keep loads in flight across the compute of a step:
+//  * loads are raw (no conversion) into registers, issued two steps ahead for
+//    the weights and one step ahead for the activations;
+//  * conversion to fp16 and the LDS write ("commit") happen after the compute
+//    of the current step;
+//  * out-of-range rows/columns are clamped for loading and masked on store, so
+//    no load sits under a branch;
+//  * the k loop is unrolled twice so the two weight register sets ping-pong
+//    without copies.
+template <int XT>
+struct RawA {
+  static constexpr int kWords = (XT == DIMQ_F32) ? 16 : 8;  // 16 activations
+  uint32_t w[kWords];
+};
+
+template <int XT>
+__device__ __forceinline__ void issue_a16(const void* x, int64_t off, RawA<XT>& r) {
+  if constexpr (XT == DIMQ_F32) {
+    const uint4* s = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(x) + off);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint4 t = s[q];
+      r.w[4 * q] = t.x; r.w[4 * q + 1] = t.y; r.w[4 * q + 2] = t.z; r.w[4 * q + 3] = t.w;
+    }
+  } else {
+    const uint4* s = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(x) + off);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint4 t = s[q];
+      r.w[4 * q] = t.x; r.w[4 * q + 1] = t.y; r.w[4 * q + 2] = t.z; r.w[4 * q + 3] = t.w;
+    }
+  }
+}
+
+// 16 raw activations -> 8 dwords of fp16 pairs in the slot order of BITS.
+template <int BITS, int XT, bool A4>
+__device__ __forceinline__ void convert_a16(const RawA<XT>& r, float s, int zp, uint32_t out[8]) {
+  uint32_t h[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    float v;
+    if constexpr (XT == DIMQ_F32) v = __uint_as_float(r.w[j]);
+    else {
+      const uint32_t bits = (r.w[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+      v = (XT == DIMQ_F16) ? f16_bits_to_float(bits) : bf16_bits_to_float(bits);
+    }
+    if constexpr (A4) v = (float)(quantize_u4(v, s, zp) - zp);
+    h[j] = float_to_f16_bits(v);
+  }
+#pragma unroll
+  for (int d = 0; d < 8; ++d) out[d] = h[kperm16(BITS, 2 * d)] | (h[kperm16(BITS, 2 * d + 1)] << 16);
+}
+
+template <int BITS>
+__device__ __forceinline__ void issue_b_fast(const uint8_t* w, int64_t n, int64_t K, int64_t k, uint32_t c[BITS]) {
+  const uint8_t* src = w + (((n * K + k) * BITS) >> 3);
+  if constexpr (BITS == 2) {
+    const uint2 t = *reinterpret_cast<const uint2*>(src);
+    c[0] = t.x; c[1] = t.y;
+  } else if constexpr (BITS == 3) {
+    c[0] = reinterpret_cast<const uint32_t*>(src)[0];
+    c[1] = reinterpret_cast<const uint32_t*>(src)[1];
+    c[2] = reinterpret_cast<const uint32_t*>(src)[2];
+  } else {
+    const uint4 t = *reinterpret_cast<const uint4*>(src);
+    c[0] = t.x; c[1] = t.y; c[2] = t.z; c[3] = t.w;
+  }
+}
+
+template <int BITS, int BM, int WN, int XT, bool A4>
+__global__ __launch_bounds__(256) void gemm_fast_kernel(const GemmArgs p) {
+  static_assert(BITS >= 2 && BITS <= 4, "register codebooks hold at most 16 entries");
+  static_assert(BM >= 32, "at least one 16-wide activation group per thread");
+  constexpr int MB = BM / 16;
+  constexpr int NB = WN / 16;
+  constexpr int NCB = A4 ? 2 : 1;
+  constexpr int A_PER_T = BM * (kKM / 16) / 256;
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kLDA];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 15;
+  const int g = lane >> 4;
+  int64_t mt, nt;
+  tile_coords((p.N + 4 * WN - 1) / (4 * WN), mt, nt);
+  const int64_t m0 = mt * BM;
+  const int64_t nw0 = nt * (4 * WN) + wave * WN;
+
+  // codebook rows of the work-group's 4*WN columns, staged through As[1]
+  // (first written by the main loop, after the barrier that ends the prologue)
+  constexpr int E = 1 << BITS;
+  static_assert(4 * WN * E * 4 <= BM * kLDA * 2, "codebook staging fits in one A buffer");
+  float* cbs = reinterpret_cast<float*>(&As[1][0]);
+  const int64_t n0 = nt * (4 * WN);
+  stage_codebook<E>(p.cb, p.cb_dt, p.cb_rows, p.cb_size, n0, 4 * WN, p.N, cbs, tid, 256);
+  __syncthreads();
+  CodebookRegs<BITS> cb[NB][NCB];
+  float colscale[NB];
+  int64_t brow[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int64_t n = nw0 + nb * 16 + col;
+    brow[nb] = n < p.N ? n : p.N - 1;
+    const int rl = (p.cb_rows == 1) ? 0 : wave * WN + nb * 16 + col;
+    const int e = planes_from_lds<BITS, A4>(cbs + rl * E, cb[nb][0], cb[nb][NCB - 1]);
+    colscale[nb] = ldexpf(A4 ? p.act_scale : 1.0f, -e);
+  }
+  // activation tasks: (row m, 16-wide group kg) per thread
+  int64_t aoff[A_PER_T];
+  int alds[A_PER_T];
+#pragma unroll
+  for (int i = 0; i < A_PER_T; ++i) {
+    const int task = tid + 256 * i;
+    const int m = task >> 3, kg = task & 7;
+    const int64_t row = (m0 + m < p.M) ? m0 + m : p.M - 1;
+    aoff[i] = row * p.ldx + 16 * kg;
+    alds[i] = m * kLDA + 16 * kg;
+  }
+
+  floatx4 acc[MB][NB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const int64_t nk = p.K / kKM;
+  // two raw activation register sets (even / odd steps) and two weight sets
+  RawA<XT> ra0[A_PER_T], ra1[A_PER_T];
+  uint32_t b0[NB][BITS], b1[NB][BITS];
+
+  auto issue_a = [&](int64_t kt, RawA<XT> (&dst)[A_PER_T]) {
+    const int64_t k = (kt < nk ? kt : nk - 1) * kKM;
+#pragma unroll
+    for (int i = 0; i < A_PER_T; ++i) issue_a16<XT>(p.x, aoff[i] + k, dst[i]);
+  };
+  auto commit_a = [&](int buf, const RawA<XT> (&src)[A_PER_T]) {
+#pragma unroll
+    for (int i = 0; i < A_PER_T; ++i) {
+      uint32_t o[8];
+      convert_a16<BITS, XT, A4>(src[i], p.act_scale, p.act_zp, o);
+      uint4* dst = reinterpret_cast<uint4*>(&As[buf][alds[i]]);
+      dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
+      dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+    }
+  };
+  auto issue_b = [&](int64_t kt, uint32_t (&dst)[NB][BITS]) {
+    const int64_t k = (kt < nk ? kt : nk - 1) * kKM + 32 * g;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) issue_b_fast<BITS>(p.w, brow[nb], p.K, k, dst[nb]);
+  };
+  auto compute = [&](int buf, const uint32_t (&bq)[NB][BITS]) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      half8 af[MB];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        af[mb] = *reinterpret_cast<const half8*>(&As[buf][(mb * 16 + col) * kLDA + 32 * g + 8 * s]);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+        for (int c = 0; c < NCB; ++c) {
+          const half8 bf = decode_sub<BITS>(bq[nb], s, cb[nb][c]);
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) acc[mb][nb] = mfma16x16x32(af[mb], bf, acc[mb][nb]);
+        }
+      }
+    }
+  };
+
+  // Pipeline: activations are committed to LDS two compute phases after
+  // their loads were issued, weights are consumed two phases after theirs.
+  // sched_barrier keeps the compiler from hoisting a commit (which waits for
+  // its loads) into the compute phase before it.
+  issue_a(0, ra0);
+  issue_b(0, b0);
+  issue_a(1, ra1);
+  issue_b(1, b1);
+  commit_a(0, ra0);
+  issue_a(2, ra0);
+  __syncthreads();
+  int64_t kt = 0;
+  for (; kt + 2 <= nk; kt += 2) {
+    compute(0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    commit_a(1, ra1);
+    issue_a(kt + 3, ra1);
+    issue_b(kt + 2, b0);
+    __syncthreads();
+    compute(1, b1);
+    __builtin_amdgcn_sched_barrier(0);
+    commit_a(0, ra0);
+    issue_a(kt + 4, ra0);
+    issue_b(kt + 3, b1);
+    __syncthreads();
+  }
+  if (kt < nk) compute(0, b0);
+
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int64_t n = nw0 + nb * 16 + col;
+    if (n >= p.N) continue;
+    const float b = p.bias ? load_as_float(p.bias, p.bias_dt, n) : 0.0f;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t m = m0 + mb * 16 + 4 * g + i;
+        if (m < p.M) store_from_float(p.y, p.y_dt, m * p.ldy + n, acc[mb][nb][i] * colscale[nb] + b);
+      }
+    }
+  }
+}
+
 // Tile shapes: (BM, WN); the work-group covers BM x 4*WN.
-enum TileId { kTile128x64 = 0, kTile64x32 = 1, kTile16x16 = 2, kTileGemv = 3, kTileCount = 4 };
+enum TileId {
+  kTile128x64 = 0,
+  kTile64x32 = 1,
+  kTile16x16 = 2,
+  kTileGemv = 3,
+  kTileFast128x64 = 4,
+  kTileFast64x32 = 5,
+  kTileFast128x32 = 6,
+  kTileFast64x64 = 7,
+  kTileCount = 8
+};
 
 template <int BITS, int XT, bool A4>
 int launch_gemm_tile(const GemmArgs& p, int tile, hipStream_t s);

@@ -192,11 +192,15 @@ def make_codec(dev, rotations, direction="unpack"):
 
     alg_bytes = n + n * 3 // 8
 
+    idx_np = idx.numpy()
+    packed_np = packed0.cpu().numpy()
+
     def cpu_step(sample):
         import oracle
-        sub = idx[:sample].numpy()
-        return oracle.pack_bits(sub, 3) if direction == "pack" else oracle.unpack_bits(
-            oracle.pack_bits(sub, 3), sample, 3)
+        if direction == "pack":
+            return oracle.pack_bits(idx_np[:sample], 3)
+        sample -= sample % 8                      # whole 3-byte groups
+        return oracle.unpack_bits(packed_np[:sample * 3 // 8], sample, 3)
 
     def check():
         back = ops.unpack_bits(ops.pack_bits(base, 3), n, 3)
@@ -212,7 +216,32 @@ def make_codec(dev, rotations, direction="unpack"):
     )
 
 
-WORKLOADS = {"cfg2": make_cfg2, "cfg1": make_cfg1, "cfg5": make_cfg5, "codec": make_codec}
+def make_copy(dev, rotations):
+    """Calibration only: a plain 256 MiB device-to-device copy, whose HBM bytes are known exactly.
+
+    Used to scale the FETCH_SIZE / WRITE_SIZE counters of the other workloads."""
+    n = 256 << 20
+    srcs = [torch.randint(0, 255, (n,), dtype=torch.uint8, device=dev) for _ in range(rotations)]
+    dst = torch.empty(n, dtype=torch.uint8, device=dev)
+
+    def step(i):
+        return dst.copy_(srcs[i])
+
+    def check():
+        return 0.0 if torch.equal(step(0), srcs[0]) else 1.0
+
+    def cpu_step(sample):
+        return srcs[0][:sample].cpu().clone()
+
+    return dict(
+        name="copy", workload="calibration: 256 MiB uint8 device copy (torch copy_)",
+        step=step, flops=0.0, alg_bytes=2 * n, bound="hbm", dtype="u8",
+        unit="GB/s", per_step_units=2 * n / 1e9, cpu_step=cpu_step, cpu_full_batch=n, check=check,
+        extra_config={"bytes": n}, per_set_bytes=n,
+    )
+
+
+WORKLOADS = {"cfg2": make_cfg2, "cfg1": make_cfg1, "cfg5": make_cfg5, "codec": make_codec, "copy": make_copy}
 
 
 # ---------------------------------------------------------------------------

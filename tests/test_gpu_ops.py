@@ -377,7 +377,10 @@ def test_graph_replay_matches_eager(gpu):
     dict(B=2, C=128, H=28, W=28, OC=64, K=3, s=1, bits=3, dt=torch.float16),
     dict(B=2, C=64, H=56, W=56, OC=128, K=3, s=2, bits=2, dt=torch.float16),
     dict(B=3, C=128, H=14, W=14, OC=64, K=1, s=2, bits=4, dt=torch.float16),
-    dict(B=1, C=64, H=9, W=300, OC=64, K=3, s=1, bits=2, dt=torch.float16),    # OW > 256: falls back
+    dict(B=1, C=64, H=9, W=300, OC=64, K=3, s=1, bits=2, dt=torch.float16),    # wide rows: implicit-GEMM fallback
+    dict(B=2, C=128, H=56, W=56, OC=64, K=3, s=2, bits=2, dt=torch.float16),   # window staged without prefetch
+    dict(B=32, C=64, H=56, W=56, OC=64, K=3, s=1, bits=2, dt=torch.float16),   # cfg2 shape: 8 bands per image
+    dict(B=3, C=64, H=20, W=12, OC=192, K=3, s=1, bits=4, dt=torch.float16),   # 3 channel blocks, odd bands
 ])
 @pytest.mark.parametrize("layout", ["nchw", "nhwc"])
 def test_conv2d_halo_prepared_vs_oracle(gpu, case, layout):

@@ -1,0 +1,146 @@
+"""CPU-only checks of the host side: the C-ABI library's exports, its host-only
+entry points and error returns, the torch.library registration, and the
+host-side codebook initialisation (quant/dimq.py:88-194)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "dimq_hip.h"
+
+
+def _header_decls():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    decls = {}
+    for m in re.finditer(r"\b(?:int|int64_t|const char\s*\*)\s+(dimq_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = [p.strip() for p in m.group(2).split(",") if p.strip() and p.strip() != "void"]
+        decls[m.group(1)] = len(params)
+    return decls
+
+
+@pytest.fixture(scope="module")
+def capi():
+    from dimq_amd import _C
+    return _C
+
+
+def test_header_declares_every_entry_point_the_binding_uses(capi):
+    decls = _header_decls()
+    assert len(decls) >= 16
+    assert set(decls) == set(capi.exported_symbols())
+    for name, nargs in decls.items():
+        assert len(capi._SIGS[name][1]) == nargs, name
+
+
+def test_library_exports_every_declared_symbol(capi):
+    lib = ctypes.CDLL(str(capi._LIB_PATH))
+    for name in _header_decls():
+        assert hasattr(lib, name), name
+
+
+def test_host_only_entry_points(capi):
+    lib = capi.lib
+    assert lib.dimq_abi_version() == 1
+    # kernel-layout words: OC * 2 lane groups * ceil(T/4) words-groups * bits, T = KH*KW*C/16
+    assert lib.dimq_conv2d_prepared_words(64, 64, 3, 3, 2) == 64 * 2 * 9 * 2
+    assert lib.dimq_conv2d_prepared_words(128, 128, 1, 1, 4) == 128 * 2 * 2 * 4
+    assert lib.dimq_conv2d_prepared_words(64, 64, 3, 3, 8) == 0      # bits without a kernel layout
+    assert lib.dimq_conv2d_prepared_words(64, 48, 3, 3, 2) == 0      # channels without a kernel layout
+    assert lib.dimq_conv2d_prepared_words(64, 64, 5, 5, 2) == 0
+
+
+def test_argument_errors_return_codes_without_touching_the_gpu(capi):
+    lib = capi.lib
+    assert lib.dimq_pack_bits(None, 0, 5, None, None) == 2                 # DIMQ_ERR_UNSUPPORTED
+    assert b"bits must be one of 2, 3, 4, 8" in lib.dimq_last_error()
+    assert lib.dimq_unpack_bits(None, 1, 16, 4, None, None) == 1           # DIMQ_ERR_INVALID
+    assert lib.dimq_last_error() == b"packed tensor is too small for requested numel"  # dimq_pack.cu:73
+    assert lib.dimq_pack_bits(None, -1, 4, None, None) == 1
+    assert lib.dimq_pack_bits(None, 8, 4, None, None) == 1                 # null pointers with numel > 0
+
+
+def test_ops_have_no_cpu_kernel(capi):
+    # the reference registers CUDA impls only (dimq_ops.cpp:46-53): CPU tensors raise a dispatcher error
+    with pytest.raises(NotImplementedError):
+        torch.ops.dimq.pack_u4(torch.zeros(4, dtype=torch.uint8))
+    with pytest.raises(NotImplementedError):
+        torch.ops.dimq.unpack_u4(torch.zeros(2, dtype=torch.uint8), 4)
+
+
+def test_reference_schemas_registered_verbatim(capi):
+    # dimq_cuda_backend/csrc/dimq_ops.cpp:37-42
+    schemas = {
+        "pack_u4": "pack_u4(Tensor indices) -> Tensor",
+        "unpack_u4": "unpack_u4(Tensor packed, int numel) -> Tensor",
+        "quantize_activation_u4": "quantize_activation_u4(Tensor x, float act_scale, int act_zp) -> Tensor",
+        "build_product_table": "build_product_table(Tensor codebook, float act_scale, int act_zp) -> Tensor",
+        "linear_lut": "linear_lut(Tensor x, Tensor packed_w, Tensor codebook, float act_scale, int act_zp, "
+                      "Tensor? bias, int out_features, int in_features) -> Tensor",
+        "conv2d_lut": "conv2d_lut(Tensor x, Tensor packed_w, Tensor codebook, float act_scale, int act_zp, "
+                      "Tensor? bias, int out_channels, int in_channels_per_group, int kernel_h, int kernel_w, "
+                      "int stride_h, int stride_w, int pad_h, int pad_w, int dilation_h, int dilation_w, "
+                      "int groups) -> Tensor",
+    }
+    for name, schema in schemas.items():
+        got = str(getattr(torch.ops.dimq, name).default._schema)
+        assert got.replace("dimq::", "") == schema
+
+
+# ---------------------------------------------------------------------------
+# codebook initialisation (host)
+# ---------------------------------------------------------------------------
+
+def test_quantile_centers_closed_form():
+    from dimq_amd.codebook import init_centers_1d
+    w = torch.arange(5, dtype=torch.float32)            # quantiles at 1/4, 1/2, 3/4 -> 1, 2, 3
+    c = init_centers_1d(w, 3, "quantile")
+    assert torch.allclose(c, torch.tensor([1.0, 2.0, 3.0]), atol=1e-6)
+
+
+def test_postprocess_spreads_duplicate_centers_and_keeps_mean():
+    from dimq_amd.codebook import init_centers_1d
+    g = torch.Generator().manual_seed(7)
+    w = torch.randn(147, generator=g)                  # ResNet stem row: 256 centres > 147 weights
+    c = init_centers_1d(w, 256, "quantile")
+    q = torch.quantile(w, torch.linspace(0, 1, 258)[1:-1])
+    assert c.shape == (256,)
+    assert bool((c[1:] > c[:-1]).all())                # strictly increasing after the min-gap pass
+    assert abs(float(c.mean() - q.mean())) < 1e-6      # re-centred on the quantiles' mean
+    gap = float(torch.maximum(w.max() - w.min(), w.std(unbiased=False))) * 1e-6
+    assert float((c[1:] - c[:-1]).min()) >= gap * 0.5
+
+
+def test_constant_row_min_gap_behaviour():
+    from dimq_amd.codebook import init_centers_1d
+    # span = sigma = 0 -> min_gap = 1e-6 * 1e-6 = 1e-12 (quant/dimq.py:182-190)
+    c0 = init_centers_1d(torch.zeros(10), 4, "quantile")
+    assert bool((c0[1:] > c0[:-1]).all())
+    assert torch.allclose(c0[1:] - c0[:-1], torch.full((3,), 1e-12), rtol=1e-3, atol=0)
+    assert abs(float(c0.mean())) < 1e-15
+    # at 0.25 the 1e-12 gap is below fp32 resolution: the centres stay equal, as in the reference
+    c1 = init_centers_1d(torch.full((10,), 0.25), 4, "quantile")
+    assert torch.equal(c1, torch.full((4,), 0.25))
+
+
+def test_per_channel_init_equals_row_wise_reference_recipe():
+    from dimq_amd.codebook import init_centers_1d, init_centers_per_channel
+    g = torch.Generator().manual_seed(3)
+    w = torch.randn(48, 16, 3, 3, generator=g) * 0.05
+    w[5] = 0.125                                       # a constant row exercises the min-gap path
+    pc = init_centers_per_channel(w, 4)
+    ref = torch.stack([init_centers_1d(r, 4, "quantile") for r in w.reshape(48, -1)])
+    assert torch.allclose(pc, ref, rtol=0, atol=1e-7)
+
+
+def test_kmeans_init_converges_to_cluster_means():
+    from dimq_amd.codebook import init_centers_1d
+    w = torch.cat([torch.full((50,), -1.0), torch.full((50,), 0.0), torch.full((50,), 2.0)])
+    w = w + torch.linspace(-0.01, 0.01, 150)
+    c = init_centers_1d(w, 3, "kmeans")
+    assert torch.allclose(c, torch.tensor([-1.0, 0.0, 2.0]), atol=0.02)

@@ -42,7 +42,7 @@ def _conv_weight_cfg2(g):
     return w
 
 
-def make_cfg2(dev, rotations):
+def make_cfg2(dev, rotations, layout="nchw"):
     from dimq_amd import ops
     from dimq_amd.codebook import assign_indices, init_centers_per_channel
     from dimq_amd.export import pack_indices
@@ -54,7 +54,9 @@ def make_cfg2(dev, rotations):
     packed = pack_indices(idx, 2).to(dev)                         # GPU kernel
     prepared = ops.prepare_conv_weight(packed, 2, (64, 64, 3, 3))  # one-time kernel-layout repack
     cb = centers.to(dev)
-    xs = [torch.relu(torch.randn(32, 64, 56, 56, generator=g)).half().to(dev) for _ in range(rotations)]
+    mf = torch.channels_last if layout == "nhwc" else torch.contiguous_format
+    xs = [torch.relu(torch.randn(32, 64, 56, 56, generator=g)).half().to(dev).contiguous(memory_format=mf)
+          for _ in range(rotations)]
 
     def step(i):
         return ops.dimq_conv2d_codebook(xs[i], packed, cb, 2, None, (64, 64, 3, 3), (1, 1), (1, 1), (1, 1), 1,
@@ -81,11 +83,11 @@ def make_cfg2(dev, rotations):
         name="cfg2",
         workload="ResNet-18 layer1 conv3x3: x fp16 [32,64,56,56] (ReLU N(0,1)), W [64,64,3,3] Kaiming-normal, "
                  "2-bit per-output-channel codebook (4 centroids/row, quantile init), stride 1, pad 1, no bias, "
-                 "y fp32 NCHW",
+                 f"y fp32 {layout.upper()}",
         step=step, flops=flops, alg_bytes=alg_bytes, bound="hbm", dtype="fp16",
         unit="TFLOP/s", per_step_units=flops / 1e12, cpu_step=cpu_step, cpu_full_batch=32, check=check,
         extra_config={"global_batch": 32, "in_shape": [32, 64, 56, 56], "weight_shape": [64, 64, 3, 3],
-                      "bits": 2, "codebook": "per_channel"},
+                      "bits": 2, "codebook": "per_channel", "layout": layout},
         per_set_bytes=x_bytes + y_bytes,
     )
 
@@ -216,6 +218,84 @@ def make_codec(dev, rotations, direction="unpack"):
     )
 
 
+def _cast_float_params(model, dtype):
+    """Unquantized parameters (embeddings, LayerNorm, head, ...) to `dtype`; codebook layers keep fp32 codebooks."""
+    from dimq_amd.modules import DIMQCodebookConv2d, DIMQCodebookLinear
+    for mod in model.modules():
+        if isinstance(mod, (DIMQCodebookConv2d, DIMQCodebookLinear)):
+            continue
+        for name, prm in list(mod._parameters.items()):
+            if prm is not None:
+                mod._parameters[name] = torch.nn.Parameter(prm.detach().to(dtype), requires_grad=False)
+    return model
+
+
+def _model_workload(name, workload, dev, rotations, qmodel, xs_cpu, flops_per_image, dtype_name, mf, extra):
+    """Shared plumbing of the end-to-end model workloads: graph-replayed forward, images/s."""
+    batch = xs_cpu.shape[0]
+    xdt = torch.bfloat16 if dtype_name == "bf16" else torch.float16
+    xs = [xs_cpu.to(dev).to(xdt).contiguous(memory_format=mf) for _ in range(rotations)]
+    qmodel.eval()
+
+    @torch.no_grad()
+    def step(i):
+        return qmodel(xs[i])
+
+    def cpu_model():
+        import oracle
+        if "cpu" not in _model_workload.cache:
+            _model_workload.cache["cpu"] = oracle.dequantized_model(qmodel)
+        return _model_workload.cache["cpu"]
+
+    @torch.no_grad()
+    def cpu_step(sample):
+        return cpu_model()(xs_cpu[:sample].float())
+
+    @torch.no_grad()
+    def check():
+        import oracle
+        n = 2
+        ref = cpu_model()(xs_cpu[:n].float())
+        out = qmodel(xs[0][:n]).float().cpu()
+        return oracle.rel_err(out, ref)
+
+    return dict(
+        name=name, workload=workload, step=step, flops=flops_per_image * batch, alg_bytes=0, bound="mfma",
+        dtype=dtype_name, unit="images/s", per_step_units=float(batch), cpu_step=cpu_step, cpu_full_batch=batch,
+        check=check, extra_config={"global_batch": batch, **extra},
+        per_set_bytes=xs_cpu.numel() * 2,
+    )
+
+
+_model_workload.cache = {}
+
+
+def make_vit(dev, rotations):
+    from dimq_amd.bench_models import quantize_vit, vit_b16, vit_flops
+    g = torch.Generator().manual_seed(3)
+    xs_cpu = torch.randn(64, 3, 224, 224, generator=g)
+    m = vit_b16().to(dev)
+    m = _cast_float_params(quantize_vit(m, 4, out_dtype=torch.bfloat16), torch.bfloat16)
+    return _model_workload(
+        "vit_b16", "ViT-B/16 forward, bs64, 3x224x224 N(0,1): qkv/proj/fc1/fc2 4-bit per-output-channel codebooks "
+        "(N(0,0.02) weights); patch embedding, LayerNorm, softmax, attention (SDPA) and head in bf16",
+        dev, rotations, m, xs_cpu, vit_flops(1), "bf16", torch.contiguous_format,
+        {"model": "vit_b16", "image": 224, "bits": 4, "codebook": "per_channel"})
+
+
+def make_resnet18(dev, rotations):
+    from dimq_amd.bench_models import quantize_resnet18, resnet18, resnet18_flops
+    g = torch.Generator().manual_seed(2)
+    xs_cpu = torch.randn(128, 3, 224, 224, generator=g)
+    m = resnet18().to(dev).to(memory_format=torch.channels_last)
+    m = _cast_float_params(quantize_resnet18(m, out_dtype=torch.float16), torch.float16)
+    return _model_workload(
+        "resnet18", "ResNet-18 forward, bs128, 3x224x224 N(0,1), BN folded: 8-bit stem and fc, 2-bit 3x3 convs, "
+        "4-bit 1x1 downsample (per-output-channel codebooks); fp16 channels_last activations",
+        dev, rotations, m, xs_cpu, resnet18_flops(1), "fp16", torch.channels_last,
+        {"model": "resnet18", "image": 224, "bits": "8/2/4/8", "codebook": "per_channel"})
+
+
 def make_copy(dev, rotations):
     """Calibration only: a plain 256 MiB device-to-device copy, whose HBM bytes are known exactly.
 
@@ -241,7 +321,9 @@ def make_copy(dev, rotations):
     )
 
 
-WORKLOADS = {"cfg2": make_cfg2, "cfg1": make_cfg1, "cfg5": make_cfg5, "codec": make_codec, "copy": make_copy}
+FIXED_ROTATIONS = {"vit": 4, "resnet18": 4}
+WORKLOADS = {"cfg2": make_cfg2, "cfg1": make_cfg1, "cfg5": make_cfg5, "codec": make_codec, "copy": make_copy,
+             "vit": make_vit, "resnet18": make_resnet18}
 
 
 # ---------------------------------------------------------------------------
@@ -333,6 +415,9 @@ def main():
     ap.add_argument("--config", default="cfg2", choices=sorted(WORKLOADS))
     ap.add_argument("--m", type=int, default=16, help="rows for cfg5")
     ap.add_argument("--direction", default="unpack", choices=["pack", "unpack"])
+    ap.add_argument("--layout", default="nchw", choices=["nchw", "nhwc"], help="cfg2 activation layout")
+    ap.add_argument("--rotations", type=int, default=0,
+                    help="buffer sets to rotate (0 = enough for > 512 MB; smaller values let the MALL serve repeats)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-check", action="store_true")
     args = ap.parse_args()
@@ -350,9 +435,18 @@ def main():
         kw["M"] = args.m
     if args.config == "codec":
         kw["direction"] = args.direction
+    if args.config == "cfg2":
+        kw["layout"] = args.layout
     # rotate buffer sets totalling > 512 MB
-    probe = make(dev, 1, **kw)
-    rotations = max(2, min(64, math.ceil(512e6 / probe["per_set_bytes"]) + 1))
+    if args.config in FIXED_ROTATIONS:
+        # end-to-end models: inputs rotate over a few sets; the packed weights are re-read every step
+        probe = {"per_set_bytes": 1}
+        rotations = FIXED_ROTATIONS[args.config]
+    else:
+        probe = make(dev, 1, **kw)
+        rotations = max(2, min(64, math.ceil(512e6 / probe["per_set_bytes"]) + 1))
+    if args.rotations > 0:
+        rotations = args.rotations
     del probe
     torch.cuda.empty_cache()
     wl = make(dev, rotations, **kw)

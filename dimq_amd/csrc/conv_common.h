@@ -1,0 +1,133 @@
+// Pieces shared by the two LDS-halo conv kernels (conv_halo.hip,
+// conv_stream.hip): the argument block, the 32x32x16 MFMA, the epilogue of
+// one 32x32 output block and the XCD-aware tile order.
+#pragma once
+
+#include "decode.h"
+
+namespace dimq {
+
+struct HaloArgs {
+  const void* x;
+  int x_dt, x_layout;
+  int B, C, H, W, OC, OH, OW;
+  int KH, KW, pad_h, pad_w;
+  int TH;              // output rows per tile (band)
+  int IH_t, IW_t, CP;  // halo tile rows, cols, channel pitch (fp16 elements)
+  int tiles_h;         // ceil(OH / TH): tiles (bands) per image
+  int NR;              // streaming kernel: input rows held in the LDS ring (power of two)
+  int SR;              // streaming kernel: input rows one step adds at most (LDS staging rows)
+  const uint32_t* kw;  // kernel-layout weights
+  int words_per_lane;  // ceil(T/4) * BITS
+  const void* cb;
+  int cb_dt, cb_rows, cb_size;
+  const void* bias;
+  int bias_dt;
+  void* y;
+  int y_dt, y_layout;
+};
+
+// Streaming kernel (conv_stream.hip): shapes it runs, LDS bytes, launch.
+bool stream_supported(const HaloArgs& p, int stride, int bits);
+int launch_conv_stream(HaloArgs p, int stride, int bits, hipStream_t s);
+
+namespace {
+
+__device__ __forceinline__ uint32_t to_f16_bits(uint32_t raw, int dt) {
+  return dt == DIMQ_F16 ? raw : float_to_f16_bits(bf16_bits_to_float(raw));
+}
+
+// Four consecutive outputs of one lane: one 16-byte (fp32) or 8-byte (16-bit)
+// store when `vec`, element stores otherwise.
+__device__ __forceinline__ void store4(void* y, int dt, int64_t off, const float v[4], bool vec) {
+  if (vec && dt == DIMQ_F32) {
+    *reinterpret_cast<float4*>(reinterpret_cast<float*>(y) + off) = make_float4(v[0], v[1], v[2], v[3]);
+  } else if (vec) {
+    uint32_t h[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) h[i] = dt == DIMQ_F16 ? float_to_f16_bits(v[i]) : float_to_bf16_bits(v[i]);
+    *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(y) + off) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) store_from_float(y, dt, off + i, v[i]);
+  }
+}
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ floatx16 mfma32x32x16(half8 a, half8 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Work-group index -> tile, so that the tiles of one XCD (work-groups are
+// dealt to the 8 XCDs round-robin) are consecutive row bands: the halo rows
+// two bands share are then read once into that XCD's L2.
+__device__ __forceinline__ int xcd_tile(int bid, int n) {
+  return (n % 8 == 0) ? (bid % 8) * (n / 8) + bid / 8 : bid;
+}
+
+// Epilogue of one 32x32 MFMA block.  PXROWS: rows = pixels pix0 + 8j + 4g + i
+// of output channel ocl (lane column); else rows = output channels
+// ocr + 8j + 4g + i of pixel pix (lane column).
+template <bool PXROWS>
+__device__ __forceinline__ void store_block(const HaloArgs& p, const floatx16& acc, int b, int oh0, int P, int mb,
+                                            int col, int g, int ocl, int ocr, float scale, float bv) {
+  const int64_t ohw = (int64_t)p.OH * p.OW;
+  if constexpr (PXROWS) {
+    if (ocl >= p.OC) return;
+    const bool vec = (ohw % 4 == 0) && (p.OW % 4 == 0) && (p.y_layout == DIMQ_NCHW);
+    const int64_t chan = ((int64_t)b * p.OC + ocl) * ohw + (int64_t)oh0 * p.OW;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int pix0 = mb * 32 + 8 * j + 4 * g;
+      if (pix0 >= P) continue;
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = acc[4 * j + i] * scale + bv;
+      if (p.y_layout == DIMQ_NCHW && pix0 + 4 <= P) {
+        store4(p.y, p.y_dt, chan + pix0, v, vec);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (pix0 + i < P) {
+            const int64_t off = p.y_layout == DIMQ_NCHW
+                                    ? chan + pix0 + i
+                                    : ((int64_t)b * ohw + (int64_t)oh0 * p.OW + pix0 + i) * p.OC + ocl;
+            store_from_float(p.y, p.y_dt, off, v[i]);
+          }
+        }
+      }
+    }
+  } else {
+    const int pix = mb * 32 + col;
+    const bool vec = (p.OC % 4 == 0) && (p.y_layout == DIMQ_NHWC);
+    const int64_t pbase = (int64_t)b * ohw + (int64_t)oh0 * p.OW + pix;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int ocb = ocr + 8 * j + 4 * g;
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float sc = __shfl(scale, 8 * j + 4 * g + i, 32);
+        const float bb = __shfl(bv, 8 * j + 4 * g + i, 32);
+        v[i] = acc[4 * j + i] * sc + bb;
+      }
+      if (pix >= P) continue;
+      if (p.y_layout == DIMQ_NHWC && ocb + 4 <= p.OC) {
+        store4(p.y, p.y_dt, pbase * p.OC + ocb, v, vec);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (ocb + i < p.OC) {
+            const int64_t off = p.y_layout == DIMQ_NHWC ? pbase * p.OC + ocb + i
+                                                        : ((int64_t)b * p.OC + ocb + i) * ohw + (int64_t)oh0 * p.OW + pix;
+            store_from_float(p.y, p.y_dt, off, v[i]);
+          }
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+}  // namespace dimq

@@ -19,103 +19,21 @@
 // t = (kh, kw, 16-channel chunk) x 8 channels, ordered so that the v_perm
 // decode of decode.h yields channels in natural order.  Each lane keeps its
 // row's packed indices and codebook byte planes in VGPRs for the whole tile.
-#include "decode.h"
+#include "conv_common.h"
+
+#include <stdlib.h>
 
 #include <algorithm>
 
 namespace dimq {
 namespace {
 
-struct HaloArgs {
-  const void* x;
-  int x_dt, x_layout;
-  int B, C, H, W, OC, OH, OW;
-  int KH, KW, pad_h, pad_w;
-  int TH;              // output rows per tile
-  int IH_t, IW_t, CP;  // halo tile rows, cols, channel pitch (fp16 elements)
-  int tiles_h;         // ceil(OH / TH)
-  const uint32_t* kw;  // kernel-layout weights
-  int words_per_lane;  // ceil(T/4) * BITS
-  const void* cb;
-  int cb_dt, cb_rows, cb_size;
-  const void* bias;
-  int bias_dt;
-  void* y;
-  int y_dt, y_layout;
-};
-
-__device__ __forceinline__ uint32_t to_f16_bits(uint32_t raw, int dt) {
-  return dt == DIMQ_F16 ? raw : float_to_f16_bits(bf16_bits_to_float(raw));
-}
-
-// Four consecutive outputs of one lane: one 16-byte (fp32) or 8-byte (16-bit)
-// store when `vec`, element stores otherwise.
-__device__ __forceinline__ void store4(void* y, int dt, int64_t off, const float v[4], bool vec) {
-  if (vec && dt == DIMQ_F32) {
-    *reinterpret_cast<float4*>(reinterpret_cast<float*>(y) + off) = make_float4(v[0], v[1], v[2], v[3]);
-  } else if (vec) {
-    uint32_t h[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) h[i] = dt == DIMQ_F16 ? float_to_f16_bits(v[i]) : float_to_bf16_bits(v[i]);
-    *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(y) + off) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) store_from_float(y, dt, off + i, v[i]);
-  }
-}
-
-typedef float floatx16 __attribute__((ext_vector_type(16)));
-
-__device__ __forceinline__ floatx16 mfma32x32x16(half8 a, half8 b, floatx16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-}
-
-// T = KH*KW*CC16 sub-steps of 16 channels; CC16 = C / 16.
-// Waves: wn = wave & 1 owns output channels [32*wn, 32*wn + 32) of the tile,
-// wm = wave >> 1 owns the 32-pixel m-blocks wm, wm + 2, wm + 4, wm + 6, so one
-// decoded weight fragment feeds 4 MFMAs.
-// PXROWS: MFMA rows are pixels (lane holds 4 consecutive pixels of one output
-// channel: contiguous in NCHW); otherwise rows are output channels (lane holds
-// 4 consecutive channels of one pixel: contiguous in NHWC).
-template <int BITS, int CC16, int STRIDE, int KHW, bool PXROWS>
-__global__ __launch_bounds__(256) void conv_halo_kernel(const HaloArgs p) {
-  constexpr int T = KHW * CC16;
-  constexpr int CHUNKS = (T + 3) / 4;
-  constexpr int WPL = CHUNKS * BITS;  // packed words per lane
-  constexpr int MBW = 4;              // 32-pixel m-blocks per wave (256 pixels per tile)
-  extern __shared__ __attribute__((aligned(16))) uint16_t halo[];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int col = lane & 31;
-  const int g = lane >> 5;
-  const int tile = blockIdx.x;
-  const int b = tile / p.tiles_h;
-  const int oh0 = (tile - b * p.tiles_h) * p.TH;
-  const int oc0 = blockIdx.y * 64;
-  const int C = CC16 * 16;
-  const int wn = wave & 1;
-  const int wm = wave >> 1;
-  const int ocl = oc0 + 32 * wn + col;  // this lane's weight row
-
-  // ---- codebooks of the 64 output rows -> LDS (fp32), then byte planes
-  constexpr int E = 1 << BITS;
-  __shared__ float cbs[64 * E];
-  stage_codebook<E>(p.cb, p.cb_dt, p.cb_rows, p.cb_size, oc0, 64, p.OC, cbs, tid, 256);
-
-  // ---- weights: this lane's packed words (independent loads)
-  uint32_t wreg[WPL];
-  {
-    const int oc = min(ocl, p.OC - 1);
-    const uint32_t* src = p.kw + ((int64_t)oc * 2 + g) * WPL;
-#pragma unroll
-    for (int w = 0; w < WPL; ++w) wreg[w] = src[w];
-  }
-
-  // ---- stage the input halo: halo row r <-> ih = oh0*S - pad_h + r,
-  //      halo col hc <-> iw = hc - pad_w.  Zero outside the image.
-  const int ih0 = oh0 * STRIDE - p.pad_h;
+// Stages the input rows of one tile into LDS as fp16 [row][col][channel]
+// (channel pitch p.CP), zero outside the image: halo row r <-> input row
+// ih0 + r, halo column hc <-> input column hc - pad_w.  256 threads.
+template <int CC16>
+__device__ __forceinline__ void stage_halo(const HaloArgs& p, int b, int ih0, uint16_t* halo, int tid) {
+  constexpr int C = CC16 * 16;
   if (p.x_layout == DIMQ_NCHW && (p.W & 7) == 0) {
     // task = (8-channel octet, halo row, 8 input columns): eight 16-byte row
     // loads, an 8x8 transpose in registers, eight 16-byte LDS stores.
@@ -241,6 +159,52 @@ __global__ __launch_bounds__(256) void conv_halo_kernel(const HaloArgs p) {
       }
     }
   }
+}
+
+// T = KH*KW*CC16 sub-steps of 16 channels; CC16 = C / 16.
+// Waves: wn = wave & 1 owns output channels [32*wn, 32*wn + 32) of the tile,
+// wm = wave >> 1 owns the 32-pixel m-blocks wm, wm + 2, wm + 4, wm + 6, so one
+// decoded weight fragment feeds 4 MFMAs.
+// PXROWS: MFMA rows are pixels (lane holds 4 consecutive pixels of one output
+// channel: contiguous in NCHW); otherwise rows are output channels (lane holds
+// 4 consecutive channels of one pixel: contiguous in NHWC).
+template <int BITS, int CC16, int STRIDE, int KHW, bool PXROWS>
+__global__ __launch_bounds__(256) void conv_halo_kernel(const HaloArgs p) {
+  constexpr int T = KHW * CC16;
+  constexpr int CHUNKS = (T + 3) / 4;
+  constexpr int WPL = CHUNKS * BITS;  // packed words per lane
+  constexpr int MBW = 4;              // 32-pixel m-blocks per wave (256 pixels per tile)
+  extern __shared__ __attribute__((aligned(16))) uint16_t halo[];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 31;
+  const int g = lane >> 5;
+  const int tile = blockIdx.x;
+  const int b = tile / p.tiles_h;
+  const int oh0 = (tile - b * p.tiles_h) * p.TH;
+  const int oc0 = blockIdx.y * 64;
+  const int C = CC16 * 16;
+  const int wn = wave & 1;
+  const int wm = wave >> 1;
+  const int ocl = oc0 + 32 * wn + col;  // this lane's weight row
+
+  // ---- codebooks of the 64 output rows -> LDS (fp32), then byte planes
+  constexpr int E = 1 << BITS;
+  __shared__ float cbs[64 * E];
+  stage_codebook<E>(p.cb, p.cb_dt, p.cb_rows, p.cb_size, oc0, 64, p.OC, cbs, tid, 256);
+
+  // ---- weights: this lane's packed words (independent loads)
+  uint32_t wreg[WPL];
+  {
+    const int oc = min(ocl, p.OC - 1);
+    const uint32_t* src = p.kw + ((int64_t)oc * 2 + g) * WPL;
+#pragma unroll
+    for (int w = 0; w < WPL; ++w) wreg[w] = src[w];
+  }
+
+  stage_halo<CC16>(p, b, oh0 * STRIDE - p.pad_h, halo, tid);
   __syncthreads();
   CodebookRegs<BITS> cbr;
   float scale;
@@ -411,19 +375,21 @@ __global__ void prepare_kernel(const uint8_t* __restrict__ src, int OC, int C, i
   for (int w = 0; w < BITS; ++w) dst[w] = words[w];
 }
 
+template <int BITS, int CC, int STRIDE, int KHW>
+int launch_halo_k(const HaloArgs& p, dim3 grid, size_t lds, hipStream_t s) {
+  if (p.y_layout == DIMQ_NCHW)
+    hipLaunchKernelGGL((conv_halo_kernel<BITS, CC, STRIDE, KHW, true>), grid, dim3(256), lds, s, p);
+  else
+    hipLaunchKernelGGL((conv_halo_kernel<BITS, CC, STRIDE, KHW, false>), grid, dim3(256), lds, s, p);
+  return check_launch("conv2d_codebook (halo)");
+}
+
 template <int BITS, int CC, int STRIDE>
 int launch_halo(const HaloArgs& p, hipStream_t s) {
   const size_t lds = (size_t)p.IH_t * p.IW_t * p.CP * sizeof(uint16_t);
   const dim3 grid(static_cast<unsigned>(p.B * p.tiles_h), static_cast<unsigned>((p.OC + 63) / 64));
-  const bool pxrows = p.y_layout == DIMQ_NCHW;
-  if (p.KH == 3) {
-    if (pxrows) hipLaunchKernelGGL((conv_halo_kernel<BITS, CC, STRIDE, 9, true>), grid, dim3(256), lds, s, p);
-    else hipLaunchKernelGGL((conv_halo_kernel<BITS, CC, STRIDE, 9, false>), grid, dim3(256), lds, s, p);
-  } else {
-    if (pxrows) hipLaunchKernelGGL((conv_halo_kernel<BITS, CC, STRIDE, 1, true>), grid, dim3(256), lds, s, p);
-    else hipLaunchKernelGGL((conv_halo_kernel<BITS, CC, STRIDE, 1, false>), grid, dim3(256), lds, s, p);
-  }
-  return check_launch("conv2d_codebook (halo)");
+  return p.KH == 3 ? launch_halo_k<BITS, CC, STRIDE, 9>(p, grid, lds, s)
+                   : launch_halo_k<BITS, CC, STRIDE, 1>(p, grid, lds, s);
 }
 
 template <int BITS>
@@ -502,6 +468,9 @@ int launch_conv_halo(const void* x, int x_dtype, int x_layout, int64_t B, int64_
   p.y = y;
   p.y_dt = y_dtype;
   p.y_layout = y_layout;
+  const char* force = getenv("DIMQ_CONV_KERNEL");  // A/B runs: 0 = one-shot halo kernel
+  if (stream_supported(p, (int)stride, bits) && !(force && atoi(force) == 0))
+    return launch_conv_stream(p, (int)stride, bits, s);
   const int CC = (int)(C / 16);
   switch (bits) {
     case 2: return launch_halo_cc<2>(p, CC, (int)stride, s);

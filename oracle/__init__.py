@@ -281,3 +281,38 @@ def rel_err(y, ref) -> float:
         return float(np.abs(y - ref).max()) if y.size else 0.0
     return float(np.abs(y - ref).max() / denom)
 
+
+
+def dequantized_model(qmodel):
+    """CPU fp32 copy of a model whose weight-only codebook layers are replaced by
+    plain nn.Linear / nn.Conv2d holding W_hat = C[idx] (reference.py:47-56): the
+    dequantize-then-F.linear/F.conv2d reference of an end-to-end forward."""
+    import copy
+
+    import torch
+    import torch.nn as nn
+
+    from dimq_amd.modules import DIMQCodebookConv2d, DIMQCodebookLinear
+
+    m = copy.deepcopy(qmodel).cpu().float()
+    for name, mod in list(m.named_modules()):
+        if isinstance(mod, DIMQCodebookLinear):
+            new = nn.Linear(mod.in_features, mod.out_features, bias=mod.bias is not None)
+            w = dequantize(mod.packed_weight, mod.bits, mod.codebook.float(), mod.out_features, mod.in_features)
+            new.weight.data = torch.from_numpy(w)
+        elif isinstance(mod, DIMQCodebookConv2d):
+            oc, cin, kh, kw = mod.weight_shape
+            new = nn.Conv2d(cin * mod.groups, oc, (kh, kw), mod.stride, mod.padding, mod.dilation, mod.groups,
+                            bias=mod.bias is not None)
+            w = dequantize(mod.packed_weight, mod.bits, mod.codebook.float(), oc, cin * kh * kw)
+            new.weight.data = torch.from_numpy(w).reshape(oc, cin, kh, kw)
+        else:
+            continue
+        if mod.bias is not None:
+            new.bias.data = mod.bias.detach().float().cpu()
+        parent = m
+        parts = name.split(".")
+        for part in parts[:-1]:
+            parent = parent._modules[part]
+        parent._modules[parts[-1]] = new
+    return m.eval()

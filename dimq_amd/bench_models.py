@@ -75,8 +75,15 @@ class ViT(nn.Module):
         self.ln = nn.LayerNorm(dim, eps=1e-6)
         self.head = nn.Linear(dim, classes)
 
+    def embed(self, x: torch.Tensor) -> torch.Tensor:
+        """Patch embedding: a stride-16 16x16 conv is a GEMM over the unfolded patches."""
+        b, c, h, w = x.shape
+        p = self.patch
+        patches = x.reshape(b, c, h // p, p, w // p, p).permute(0, 2, 4, 1, 3, 5).reshape(b, (h // p) * (w // p), -1)
+        return F.linear(patches, self.conv_proj.weight.reshape(self.conv_proj.out_channels, -1), self.conv_proj.bias)
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        x = self.conv_proj(x).flatten(2).transpose(1, 2)
+        x = self.embed(x)
         x = torch.cat([self.class_token.expand(x.shape[0], -1, -1), x], dim=1) + self.pos_embedding
         for blk in self.blocks:
             x = blk(x)

@@ -96,26 +96,18 @@ __device__ __forceinline__ uint32_t spread3x4(uint32_t y) {
   return ((t << 5) | t) & 0x07070707u;
 }
 
-// Decode sub-step s (slots 8s..8s+7 of the lane's 32-index chunk c[]) into a
-// B fragment (8 fp16 in slot order).  BITS in {2,3,4}.
+// Eight fields already at the bottom of G (4-bit: 8 nibbles; 2-bit: fields
+// at bits 0,2 + 8i; 3-bit: 24 bits) -> B fragment (8 fp16 in slot order).
 template <int BITS>
-__device__ __forceinline__ half8 decode_sub(const uint32_t (&c)[BITS], int s, const CodebookRegs<BITS>& cb) {
+__device__ __forceinline__ half8 decode_word(uint32_t G, const CodebookRegs<BITS>& cb) {
   uint32_t D0, D1;
   if constexpr (BITS == 4) {
-    const uint32_t w = c[s];
-    D0 = w & 0x0f0f0f0fu;
-    D1 = (w >> 4) & 0x0f0f0f0fu;
+    D0 = G & 0x0f0f0f0fu;
+    D1 = (G >> 4) & 0x0f0f0f0fu;
   } else if constexpr (BITS == 2) {
-    const uint32_t w = c[s >> 1];
-    const int sh = 4 * (s & 1);
-    D0 = (w >> sh) & 0x03030303u;
-    D1 = (w >> (sh + 2)) & 0x03030303u;
+    D0 = G & 0x03030303u;
+    D1 = (G >> 2) & 0x03030303u;
   } else {
-    uint32_t G;
-    if (s == 0) G = c[0];
-    else if (s == 1) G = __builtin_amdgcn_alignbit(c[1], c[0], 24);
-    else if (s == 2) G = __builtin_amdgcn_alignbit(c[2], c[1], 16);
-    else G = c[2] >> 8;
     D0 = spread3x4(G & 0xfffu);
     D1 = spread3x4((G >> 12) & 0xfffu);
   }
@@ -124,6 +116,24 @@ __device__ __forceinline__ half8 decode_sub(const uint32_t (&c)[BITS], int s, co
   lookup4<BITS>(cb, D1, r2, r3);
   const u32x4 r = {r0, r1, r2, r3};
   return __builtin_bit_cast(half8, r);
+}
+
+// Decode sub-step s (slots 8s..8s+7 of the lane's 32-index chunk c[]) into a
+// B fragment (8 fp16 in slot order).  BITS in {2,3,4}.
+template <int BITS>
+__device__ __forceinline__ half8 decode_sub(const uint32_t (&c)[BITS], int s, const CodebookRegs<BITS>& cb) {
+  uint32_t G;
+  if constexpr (BITS == 4) {
+    G = c[s];
+  } else if constexpr (BITS == 2) {
+    G = c[s >> 1] >> (4 * (s & 1));
+  } else {
+    if (s == 0) G = c[0];
+    else if (s == 1) G = __builtin_amdgcn_alignbit(c[1], c[0], 24);
+    else if (s == 2) G = __builtin_amdgcn_alignbit(c[2], c[1], 16);
+    else G = c[2] >> 8;
+  }
+  return decode_word<BITS>(G, cb);
 }
 
 __device__ __forceinline__ floatx4 mfma16x16x32(half8 a, half8 b, floatx4 c) {

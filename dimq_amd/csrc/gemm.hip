@@ -3,6 +3,7 @@
 // launch.
 #include <stdlib.h>
 
+#include "gemm_big.h"
 #include "gemm_kernel.h"
 
 namespace dimq {
@@ -18,6 +19,18 @@ int gemm_fast_tile(int tile, const GemmArgs& p, int bits) {
   if (tile == kTile128x64) return kTileFast128x64;
   if (tile == kTile64x32) return kTileFast64x32;
   return tile;
+}
+
+// Large-tile kernels (gemm_big.h) for Linear shapes with M > 64, K % 64 == 0
+// and aligned rows/streams.  Measured on the ViT-B/16 shapes (M = 12,608) and
+// cfg1: the deep-pipeline 128x128 tile (7) is fastest for K < 2048, the 2x2
+// 128x128 tile (2) for K >= 2048.  Returns -1 when the shape does not qualify.
+int gemm_big_tile(const GemmArgs& p, int bits, int variant) {
+  if (variant == DIMQ_VARIANT_SMALL_M || p.conv || !(bits == 2 || bits == 3 || bits == 4)) return -1;
+  if (p.M <= 64 || p.K % 64 != 0 || !p.fast_b || !p.vec_a) return -1;
+  const char* force = getenv("DIMQ_GEMM_BIG");  // A/B runs: -1 = off, 0..7 = tile
+  if (force) return (atoi(force) >= 0 && atoi(force) <= 7) ? atoi(force) : -1;
+  return p.K >= 2048 ? 2 : 7;
 }
 
 int gemm_pick_tile(int64_t M, int64_t N, int variant) {
@@ -91,6 +104,14 @@ int linear_codebook_impl(const void* x, int x_dtype, int64_t M, int64_t K, int64
   p.vec_a = aligned(x, 16) && ((ldx * xs) % 16 == 0);
   p.groups = 1;
   if (M == 0 || N == 0) return DIMQ_OK;
+  const int big = gemm_big_tile(p, bits, variant);
+  if (big >= 0) {
+    switch (bits) {
+      case 2: return launch_big_b2(p, x_dtype, big, s);
+      case 3: return launch_big_b3(p, x_dtype, big, s);
+      default: return launch_big_b4(p, x_dtype, big, s);
+    }
+  }
   const char* force = getenv("DIMQ_GEMM_TILE");  // A/B runs: force a tile id
   int tile = force ? atoi(force) : gemm_fast_tile(gemm_pick_tile(M, N, variant), p, bits);
   if (tile < 0 || tile >= kTileCount) tile = gemm_pick_tile(M, N, variant);

@@ -1,0 +1,557 @@
+// Large-tile codebook GEMM for the MFMA-bound Linear shapes (ViT-B/16
+// qkv/proj/fc1/fc2 at M = 12,608, BASELINE cfg1): y[M,N] = x[M,K] W_hat^T + b.
+//
+// Work-group = WGM x WGN waves; wave (wm, wn) owns a (MBLK*32) x (NBLK*32)
+// block of the (WGM*MBLK*32) x (WGN*NBLK*32) tile.  With WGM = 1 every weight
+// column is decoded by exactly one wave.  The MFMA
+// is v_mfma_f32_32x32x16_f16 with the *weights* as the A operand (rows =
+// output columns n) and the activations as the B operand (columns = rows m),
+// so each lane's accumulator holds 4 consecutive n of one m: 16-byte stores
+// into row-major y.
+//
+// Per 64-wide k stage:
+//   * activations: raw 16-byte global loads issued one stage ahead into
+//     registers, converted to fp16 in the k-slot order of the weight decoder
+//     (fp16: byte selects; bf16: v_cvt_pkrtz, exact for every bf16 value in
+//     the fp16 range; fp32: round to nearest) and written to a
+//     double-buffered LDS tile (row pitch 72 halves: the 16-byte reads of 16
+//     consecutive rows hit distinct bank groups);
+//   * weights: each lane loads its row's 64 packed indices (8*BITS bytes,
+//     one stage ahead) and decodes one 8-index word per k16 step with v_perm
+//     lookups into the row's codebook byte planes held in VGPRs; one decoded
+//     fragment feeds MBLK MFMAs.
+// Codebook rows are scaled by a power of two before rounding to fp16; the
+// epilogue multiplies by 2^-e and adds the bias.
+#pragma once
+
+#include "gemm_kernel.h"
+
+namespace dimq {
+namespace {
+
+typedef float floatx16g __attribute__((ext_vector_type(16)));
+
+constexpr int kBigKS = 64;           // k per pipeline stage
+constexpr int kBigLDA = kBigKS + 8;  // LDS row pitch (halves)
+
+__device__ __forceinline__ floatx16g mfma32(half8 a, half8 b, floatx16g c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// 64 indices of row n from column k0 (K % 64 == 0): 8*BITS bytes, 16-byte
+// aligned for BITS 2 and 4, 8-byte aligned for BITS 3.
+template <int BITS>
+__device__ __forceinline__ void issue_b_stage(const uint8_t* w, int64_t n, int64_t K, int64_t k0,
+                                              uint32_t (&c)[2 * BITS]) {
+  const uint8_t* src = w + (((n * K + k0) * BITS) >> 3);
+  if constexpr (BITS == 3) {
+    const uint2* s2 = reinterpret_cast<const uint2*>(src);
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const uint2 t = s2[q];
+      c[2 * q] = t.x;
+      c[2 * q + 1] = t.y;
+    }
+  } else {
+    const uint4* s4 = reinterpret_cast<const uint4*>(src);
+#pragma unroll
+    for (int q = 0; q < BITS / 2; ++q) {
+      const uint4 t = s4[q];
+      c[4 * q] = t.x;
+      c[4 * q + 1] = t.y;
+      c[4 * q + 2] = t.z;
+      c[4 * q + 3] = t.w;
+    }
+  }
+}
+
+// Field word of k16 step s of the stage for lane group g: sub-step u = 2s + g
+// of the stage's two 32-index chunks (slot order of decode_sub).
+template <int BITS>
+__device__ __forceinline__ uint32_t stage_word(const uint32_t (&c)[2 * BITS], int s, int g) {
+  const int t = s & 1;                     // sub-steps 2t + g of chunk s >> 1
+  const uint32_t* ch = c + (s >> 1) * BITS;
+  if constexpr (BITS == 4) {
+    return g ? ch[2 * t + 1] : ch[2 * t];
+  } else if constexpr (BITS == 2) {
+    return ch[t] >> (4 * g);
+  } else {
+    if (t == 0) return g ? __builtin_amdgcn_alignbit(ch[1], ch[0], 24) : ch[0];
+    return g ? (ch[2] >> 8) : __builtin_amdgcn_alignbit(ch[2], ch[1], 16);
+  }
+}
+
+// 16 raw activations -> 8 dwords of fp16 pairs in the slot order of BITS.
+template <int BITS, int XT>
+__device__ __forceinline__ void convert_a16_big(const RawA<XT>& r, uint32_t out[8]) {
+  if constexpr (XT == DIMQ_F32) {
+    convert_a16<BITS, XT, false>(r, 1.0f, 0, out);
+  } else {
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if constexpr (XT == DIMQ_F16) {
+        w[i] = r.w[i];
+      } else {
+        const auto h2 = __builtin_amdgcn_cvt_pkrtz(__uint_as_float(r.w[i] << 16), __uint_as_float(r.w[i] & 0xffff0000u));
+        w[i] = __builtin_bit_cast(uint32_t, h2);
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const int a = kperm16(BITS, 2 * d), b = kperm16(BITS, 2 * d + 1);
+      if ((a >> 1) == (b >> 1) && (a & 1) == 0 && (b & 1) == 1) {
+        out[d] = w[a >> 1];
+      } else {
+        // low half <- half (a & 1) of word a/2, high half <- half (b & 1) of word b/2
+        const uint32_t sel = ((a & 1) ? 0x0302u : 0x0100u) | ((b & 1) ? 0x07060000u : 0x05040000u);
+        out[d] = perm(w[b >> 1], w[a >> 1], sel);
+      }
+    }
+  }
+}
+
+template <int BITS, int XT, int WGM, int WGN, int MBLK, int NBLK>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_big_kernel(const GemmArgs p) {
+  static_assert(BITS >= 2 && BITS <= 4, "register codebooks hold at most 16 entries");
+  constexpr int NT = 64 * WGM * WGN;
+  constexpr int BM = WGM * MBLK * 32;
+  constexpr int BN = WGN * NBLK * 32;
+  constexpr int E = 1 << BITS;
+  constexpr int A_TASKS = BM * (kBigKS / 16) / NT;  // 16-element groups per thread
+  static_assert(A_TASKS * NT == BM * (kBigKS / 16), "tile rows must split evenly over the threads");
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kBigLDA];
+  __shared__ float cbs[BN * E];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 31;
+  const int g = lane >> 5;
+  const int wm = wave / WGN;
+  const int wn = wave - wm * WGN;
+  int64_t mt, nt;
+  tile_coords((p.N + BN - 1) / BN, mt, nt);
+  const int64_t m0 = mt * BM;
+  const int64_t n0 = nt * BN;
+
+  stage_codebook<E>(p.cb, p.cb_dt, p.cb_rows, p.cb_size, n0, BN, p.N, cbs, tid, NT);
+  __syncthreads();
+  CodebookRegs<BITS> cb[NBLK];
+  float rscale[NBLK];
+  int64_t brow[NBLK];
+#pragma unroll
+  for (int nb = 0; nb < NBLK; ++nb) {
+    const int nl = wn * NBLK * 32 + nb * 32 + col;
+    brow[nb] = n0 + nl < p.N ? n0 + nl : p.N - 1;
+    const int rl = (p.cb_rows == 1) ? 0 : nl;
+    const int e = planes_from_lds<BITS, false>(cbs + rl * E, cb[nb], cb[nb]);
+    rscale[nb] = ldexpf(1.0f, -e);
+  }
+
+  // activation tasks: (row m, 16-wide group kg) per thread, 4 groups per row
+  int64_t aoff[A_TASKS];
+  int alds[A_TASKS];
+#pragma unroll
+  for (int i = 0; i < A_TASKS; ++i) {
+    const int task = tid + NT * i;
+    const int m = task >> 2, kg = task & 3;
+    const int64_t row = (m0 + m < p.M) ? m0 + m : p.M - 1;
+    aoff[i] = row * p.ldx + 16 * kg;
+    alds[i] = m * kBigLDA + 16 * kg;
+  }
+
+  floatx16g acc[MBLK][NBLK];
+#pragma unroll
+  for (int mb = 0; mb < MBLK; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NBLK; ++nb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[mb][nb][i] = 0.0f;
+
+  const int64_t nk = p.K / kBigKS;
+  RawA<XT> ra[A_TASKS];
+  uint32_t b0[NBLK][2 * BITS], b1[NBLK][2 * BITS];
+
+  auto issue_a = [&](int64_t kt) {
+    const int64_t k = (kt < nk ? kt : nk - 1) * kBigKS;
+#pragma unroll
+    for (int i = 0; i < A_TASKS; ++i) issue_a16<XT>(p.x, aoff[i] + k, ra[i]);
+  };
+  auto commit_a = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_TASKS; ++i) {
+      uint32_t o[8];
+      convert_a16_big<BITS, XT>(ra[i], o);
+      uint4* dst = reinterpret_cast<uint4*>(&As[buf][alds[i]]);
+      dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
+      dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+    }
+  };
+  auto issue_b = [&](int64_t kt, uint32_t (&dst)[NBLK][2 * BITS]) {
+    const int64_t k = (kt < nk ? kt : nk - 1) * kBigKS;
+#pragma unroll
+    for (int nb = 0; nb < NBLK; ++nb) issue_b_stage<BITS>(p.w, brow[nb], p.K, k, dst[nb]);
+  };
+  const uint16_t* arow = nullptr;  // this lane's activation row in a stage tile
+  // activation fragments: double-buffered across the four k16 steps (the
+  // reads of step s+1 go out under the MFMAs of step s) for small wave tiles;
+  // large ones (>= 12 MFMAs per step) read each step's fragments at its start
+  // and let the first MFMAs cover the later reads
+  constexpr bool XDB = MBLK * NBLK < 12;
+  auto compute = [&](int buf, const uint32_t (&bq)[NBLK][2 * BITS]) {
+    arow = &As[buf][(wm * MBLK * 32 + col) * kBigLDA + 8 * g];
+    half8 xf[XDB ? 2 : 1][MBLK];
+    if constexpr (XDB) {
+#pragma unroll
+      for (int mb = 0; mb < MBLK; ++mb) xf[0][mb] = *reinterpret_cast<const half8*>(arow + mb * 32 * kBigLDA);
+    }
+#pragma unroll
+    for (int s = 0; s < kBigKS / 16; ++s) {
+      const int cur = XDB ? (s & 1) : 0;
+      if constexpr (XDB) {
+        if (s + 1 < kBigKS / 16) {
+#pragma unroll
+          for (int mb = 0; mb < MBLK; ++mb)
+            xf[(s + 1) & 1][mb] = *reinterpret_cast<const half8*>(arow + mb * 32 * kBigLDA + 16 * (s + 1));
+        }
+      } else {
+#pragma unroll
+        for (int mb = 0; mb < MBLK; ++mb)
+          xf[0][mb] = *reinterpret_cast<const half8*>(arow + mb * 32 * kBigLDA + 16 * s);
+      }
+#pragma unroll
+      for (int nb = 0; nb < NBLK; ++nb) {
+        const half8 wf = decode_word<BITS>(stage_word<BITS>(bq[nb], s, g), cb[nb]);
+#pragma unroll
+        for (int mb = 0; mb < MBLK; ++mb) acc[mb][nb] = mfma32(wf, xf[cur][mb], acc[mb][nb]);
+      }
+    }
+    if constexpr (XDB) {
+      // order: first reads; then per step its decode, and its MFMAs paired
+      // with the next step's reads
+      __builtin_amdgcn_sched_group_barrier(0x100, MBLK, 0);
+#pragma unroll
+      for (int s = 0; s < kBigKS / 16; ++s) {
+        __builtin_amdgcn_sched_group_barrier(0x002, 12 * NBLK, 0);
+#pragma unroll
+        for (int i = 0; i < MBLK * NBLK; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if (s + 1 < kBigKS / 16 && i < MBLK) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+      }
+    }
+  };
+
+  // Pipeline (two stages per loop trip so the weight register sets alternate
+  // without copies): loads for stage kt+1 are in flight while stage kt
+  // computes; sched_barriers keep those loads ahead of the MFMAs and the
+  // commit, which waits for them, after the MFMAs.
+  issue_a(0);
+  issue_b(0, b0);
+  commit_a(0);
+  __syncthreads();
+  int64_t kt = 0;
+  for (; kt + 2 <= nk; kt += 2) {
+    issue_a(kt + 1);
+    issue_b(kt + 1, b1);
+    __builtin_amdgcn_sched_barrier(0);  // loads go out before the MFMAs, not after
+    compute(0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    commit_a(1);
+    __syncthreads();
+    issue_a(kt + 2);
+    issue_b(kt + 2, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(1, b1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (kt + 2 < nk) commit_a(0);
+    __syncthreads();
+  }
+  if (kt < nk) compute(0, b0);
+
+  // epilogue: acc[mb][nb][4j + i] = y[m][n], m = block row m0 + wm*MBLK*32 +
+  // mb*32 + col, n = n0 + wn*NBLK*32 + nb*32 + 8j + 4g + i
+  const bool vec = p.ldy % 4 == 0 && p.y_dt != DIMQ_F64;
+#pragma unroll
+  for (int nb = 0; nb < NBLK; ++nb) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int nl = 8 * j + 4 * g;
+      const int64_t n = n0 + wn * NBLK * 32 + nb * 32 + nl;
+      float sc[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sc[i] = __shfl(rscale[nb], nl + i, 32);
+        bv[i] = (p.bias && n + i < p.N) ? load_as_float(p.bias, p.bias_dt, n + i) : 0.0f;
+      }
+#pragma unroll
+      for (int mb = 0; mb < MBLK; ++mb) {
+        const int64_t m = m0 + wm * MBLK * 32 + mb * 32 + col;
+        if (m >= p.M) continue;
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = acc[mb][nb][4 * j + i] * sc[i] + bv[i];
+        const int64_t off = m * p.ldy + n;
+        if (vec && n + 4 <= p.N) {
+          if (p.y_dt == DIMQ_F32) {
+            *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.y) + off) = make_float4(v[0], v[1], v[2], v[3]);
+          } else {
+            uint32_t h[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) h[i] = p.y_dt == DIMQ_F16 ? float_to_f16_bits(v[i]) : float_to_bf16_bits(v[i]);
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.y) + off) =
+                make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (n + i < p.N) store_from_float(p.y, p.y_dt, off + i, v[i]);
+        }
+      }
+    }
+  }
+}
+
+typedef __attribute__((address_space(3))) void lds_void_g;
+
+// Deep-pipeline variant for one wave per SIMD: 4 waves side by side in n
+// (wave tile (MBLK*32) x 32), activations two stages ahead in registers,
+// packed weights through a 3-stage LDS ring filled with global_load_lds
+// (no registers held by the weight loads).
+template <int BITS, int XT, int MBLK>
+__global__ __launch_bounds__(256) void gemm_deep_kernel(const GemmArgs p) {
+  static_assert(BITS >= 2 && BITS <= 4, "register codebooks hold at most 16 entries");
+  constexpr int BM = MBLK * 32;
+  constexpr int BN = 128;
+  constexpr int E = 1 << BITS;
+  constexpr int A_TASKS = BM * (kBigKS / 16) / 256;
+  constexpr int RB = 8 * BITS;                  // packed bytes of one row per stage
+  constexpr int BSTAGE = BN * RB;               // bytes of one weight stage
+  constexpr int DSZ = BITS == 4 ? 16 : 4;       // global_load_lds size
+  constexpr int DPT = BSTAGE / DSZ / 256;       // loads per thread per stage
+  static_assert(DPT * DSZ * 256 == BSTAGE, "weight stage splits evenly over the threads");
+  constexpr int RING = 3;
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kBigLDA];
+  __shared__ __attribute__((aligned(16))) uint8_t Bs[RING][BSTAGE];
+  __shared__ float cbs[BN * E];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 31;
+  const int g = lane >> 5;
+  int64_t mt, nt;
+  tile_coords((p.N + BN - 1) / BN, mt, nt);
+  const int64_t m0 = mt * BM;
+  const int64_t n0 = nt * BN;
+
+  stage_codebook<E>(p.cb, p.cb_dt, p.cb_rows, p.cb_size, n0, BN, p.N, cbs, tid, 256);
+  __syncthreads();
+  CodebookRegs<BITS> cb;
+  float rscale;
+  const int nl = wave * 32 + col;  // this lane's weight row within the tile
+  {
+    const int rl = (p.cb_rows == 1) ? 0 : nl;
+    const int e = planes_from_lds<BITS, false>(cbs + rl * E, cb, cb);
+    rscale = ldexpf(1.0f, -e);
+  }
+
+  int64_t aoff[A_TASKS];
+  int alds[A_TASKS];
+#pragma unroll
+  for (int i = 0; i < A_TASKS; ++i) {
+    const int task = tid + 256 * i;
+    const int m = task >> 2, kg = task & 3;
+    const int64_t row = (m0 + m < p.M) ? m0 + m : p.M - 1;
+    aoff[i] = row * p.ldx + 16 * kg;
+    alds[i] = m * kBigLDA + 16 * kg;
+  }
+  // weight loads: chunk c = tid + 256 * d of the stage -> row c / (RB / DSZ)
+  const uint8_t* bsrc[DPT];
+#pragma unroll
+  for (int d = 0; d < DPT; ++d) {
+    const int c = tid + 256 * d;
+    const int r = c / (RB / DSZ);
+    const int64_t n = n0 + r < p.N ? n0 + r : p.N - 1;
+    bsrc[d] = p.w + ((n * p.K * BITS) >> 3) + (c - r * (RB / DSZ)) * DSZ;
+  }
+
+  floatx16g acc[MBLK];
+#pragma unroll
+  for (int mb = 0; mb < MBLK; ++mb)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[mb][i] = 0.0f;
+
+  const int64_t nk = p.K / kBigKS;
+  RawA<XT> ra0[A_TASKS], ra1[A_TASKS];
+
+  auto issue_a = [&](int64_t kt, RawA<XT> (&dst)[A_TASKS]) {
+    const int64_t k = (kt < nk ? kt : nk - 1) * kBigKS;
+#pragma unroll
+    for (int i = 0; i < A_TASKS; ++i) issue_a16<XT>(p.x, aoff[i] + k, dst[i]);
+  };
+  auto commit_a = [&](int buf, const RawA<XT> (&src)[A_TASKS]) {
+#pragma unroll
+    for (int i = 0; i < A_TASKS; ++i) {
+      uint32_t o[8];
+      convert_a16_big<BITS, XT>(src[i], o);
+      uint4* dst = reinterpret_cast<uint4*>(&As[buf][alds[i]]);
+      dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
+      dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+    }
+  };
+  auto dma_b = [&](int64_t kt, int slot) {
+    const int64_t kb = (((kt < nk ? kt : nk - 1) * kBigKS) * BITS) >> 3;
+#pragma unroll
+    for (int d = 0; d < DPT; ++d) {
+      const void* src = reinterpret_cast<const void*>(bsrc[d] + kb);
+      lds_void_g* dst = (lds_void_g*)(&Bs[slot][(wave * 64 + 256 * d) * DSZ]);
+      if constexpr (DSZ == 16) __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+      else __builtin_amdgcn_global_load_lds(src, dst, 4, 0, 0);
+    }
+  };
+  auto compute = [&](int buf, int slot) {
+    uint32_t bq[2 * BITS];
+    const uint32_t* brow = reinterpret_cast<const uint32_t*>(&Bs[slot][nl * RB]);
+#pragma unroll
+    for (int w = 0; w < 2 * BITS; ++w) bq[w] = brow[w];
+    const uint16_t* arow = &As[buf][col * kBigLDA + 8 * g];
+    half8 xf[2][MBLK];
+#pragma unroll
+    for (int mb = 0; mb < MBLK; ++mb) xf[0][mb] = *reinterpret_cast<const half8*>(arow + mb * 32 * kBigLDA);
+#pragma unroll
+    for (int s = 0; s < kBigKS / 16; ++s) {
+      if (s + 1 < kBigKS / 16) {
+#pragma unroll
+        for (int mb = 0; mb < MBLK; ++mb)
+          xf[(s + 1) & 1][mb] = *reinterpret_cast<const half8*>(arow + mb * 32 * kBigLDA + 16 * (s + 1));
+      }
+      const half8 wf = decode_word<BITS>(stage_word<BITS>(bq, s, g), cb);
+#pragma unroll
+      for (int mb = 0; mb < MBLK; ++mb) acc[mb] = mfma32(wf, xf[s & 1][mb], acc[mb]);
+    }
+  };
+
+  // prologue: weight stages 0..2 and activation stages 0, 1 in flight
+  dma_b(0, 0);
+  dma_b(1, 1);
+  dma_b(2, 2);
+  issue_a(0, ra0);
+  issue_a(1, ra1);
+  commit_a(0, ra0);  // waits for stage 0 (and the weight stages before it)
+  issue_a(2, ra0);
+  __syncthreads();
+  // steady state, two stages per trip (register sets alternate):
+  //   compute kt | commit kt+1 (loaded two phases ago) | barrier |
+  //   weight stage kt+3 into the freed ring slot, activations of kt+3
+  int64_t kt = 0;
+  int slot = 0;
+  for (; kt + 2 <= nk; kt += 2) {
+    compute(0, slot);
+    __builtin_amdgcn_sched_barrier(0);
+    commit_a(1, ra1);
+    __syncthreads();
+    dma_b(kt + 3, slot);
+    issue_a(kt + 3, ra1);
+    __builtin_amdgcn_sched_barrier(0);
+    slot = slot == RING - 1 ? 0 : slot + 1;
+    compute(1, slot);
+    __builtin_amdgcn_sched_barrier(0);
+    if (kt + 2 < nk) commit_a(0, ra0);
+    __syncthreads();
+    dma_b(kt + 4, slot);
+    issue_a(kt + 4, ra0);
+    __builtin_amdgcn_sched_barrier(0);
+    slot = slot == RING - 1 ? 0 : slot + 1;
+  }
+  if (kt < nk) compute(0, slot);
+
+  // epilogue: acc[mb][4j + i] = y[m][n], m = m0 + mb*32 + col, n = n0 + 32*wave + 8j + 4g + i
+  const bool vec = p.ldy % 4 == 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int nlo = 8 * j + 4 * g;
+    const int64_t n = n0 + wave * 32 + nlo;
+    float sc[4], bv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sc[i] = __shfl(rscale, nlo + i, 32);
+      bv[i] = (p.bias && n + i < p.N) ? load_as_float(p.bias, p.bias_dt, n + i) : 0.0f;
+    }
+#pragma unroll
+    for (int mb = 0; mb < MBLK; ++mb) {
+      const int64_t m = m0 + mb * 32 + col;
+      if (m >= p.M) continue;
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = acc[mb][4 * j + i] * sc[i] + bv[i];
+      const int64_t off = m * p.ldy + n;
+      if (vec && n + 4 <= p.N) {
+        if (p.y_dt == DIMQ_F32) {
+          *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.y) + off) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+          uint32_t h[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) h[i] = p.y_dt == DIMQ_F16 ? float_to_f16_bits(v[i]) : float_to_bf16_bits(v[i]);
+          *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.y) + off) =
+              make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (n + i < p.N) store_from_float(p.y, p.y_dt, off + i, v[i]);
+      }
+    }
+  }
+}
+
+template <int BITS, int XT, int MBLK>
+int launch_deep(const GemmArgs& p, hipStream_t s) {
+  constexpr int BM = MBLK * 32, BN = 128;
+  const int64_t tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+  hipLaunchKernelGGL((gemm_deep_kernel<BITS, XT, MBLK>), dim3(static_cast<unsigned>(tiles)), dim3(256), 0, s, p);
+  return check_launch("linear_codebook (large tiles, deep pipeline)");
+}
+
+template <int BITS, int XT, int WGM, int WGN, int MBLK, int NBLK>
+int launch_big(const GemmArgs& p, hipStream_t s) {
+  constexpr int BM = WGM * MBLK * 32, BN = WGN * NBLK * 32;
+  const int64_t tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+  hipLaunchKernelGGL((gemm_big_kernel<BITS, XT, WGM, WGN, MBLK, NBLK>), dim3(static_cast<unsigned>(tiles)),
+                     dim3(64 * WGM * WGN), 0, s, p);
+  return check_launch("linear_codebook (large tiles)");
+}
+
+// Tile ids (WGM x WGN waves of (MBLK*32) x (NBLK*32)):
+//   0: 256x128 (1x4, 256x32)   1: 256x128 (2x2, 128x64)   2: 128x128 (2x2, 64x64)
+//   3: 256x256 (1x4, 256x64)   4: 192x256 (1x4, 192x64)   5: 128x256 (1x4, 128x64)
+//   6: 256x128 deep pipeline   7: 128x128 deep pipeline
+template <int BITS>
+int launch_big_bits(const GemmArgs& p, int xt, int tile, hipStream_t s) {
+#define DIMQ_BIG_TILES(XT)                                               \
+  switch (tile) {                                                        \
+    case 0: return launch_big<BITS, XT, 1, 4, 8, 1>(p, s);               \
+    case 1: return launch_big<BITS, XT, 2, 2, 4, 2>(p, s);               \
+    case 3: return launch_big<BITS, XT, 1, 4, 8, 2>(p, s);               \
+    case 4: return launch_big<BITS, XT, 1, 4, 6, 2>(p, s);               \
+    case 5: return launch_big<BITS, XT, 1, 4, 4, 2>(p, s);               \
+    case 6: return launch_deep<BITS, XT, 8>(p, s);                       \
+    case 7: return launch_deep<BITS, XT, 4>(p, s);                       \
+    default: return launch_big<BITS, XT, 2, 2, 2, 2>(p, s);              \
+  }
+  switch (xt) {
+    case DIMQ_F32: DIMQ_BIG_TILES(DIMQ_F32)
+    case DIMQ_F16: DIMQ_BIG_TILES(DIMQ_F16)
+    default: DIMQ_BIG_TILES(DIMQ_BF16)
+  }
+#undef DIMQ_BIG_TILES
+}
+
+}  // namespace
+
+int launch_big_b2(const GemmArgs& p, int xt, int tile, hipStream_t s);
+int launch_big_b3(const GemmArgs& p, int xt, int tile, hipStream_t s);
+int launch_big_b4(const GemmArgs& p, int xt, int tile, hipStream_t s);
+
+}  // namespace dimq

@@ -290,6 +290,40 @@ def test_linear_codebook_dtypes(gpu, xdt, odt):
         assert oracle.rel_err(y.float(), ref) <= tol, (xdt, odt, variant, oracle.rel_err(y.float(), ref))
 
 
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("tile", ["0", "2", "6", "7"])
+@pytest.mark.parametrize("M,N,K,xdt", [(257, 130, 128, torch.float32), (520, 384, 192, torch.bfloat16),
+                                       (65, 256, 64, torch.float16)])
+def test_linear_codebook_large_tiles(gpu, monkeypatch, bits, tile, M, N, K, xdt):
+    """The 32x32x16 large-tile kernels (256x128 / 128x128 tiles, deep-pipeline variants), M / N tails."""
+    monkeypatch.setenv("DIMQ_GEMM_BIG", tile)
+    ops = _ops()
+    for per_channel in (True, False):
+        announce(f"linear_codebook large tile={tile} bits={bits} M={M} N={N} K={K} {xdt} pc={per_channel}")
+        g = _gen(bits * 7 + M + N + K)
+        cb, idx, packed = _codebook_case(N, K, bits, per_channel, g)
+        x = torch.randn(M, K, generator=g).to(xdt)
+        bias = torch.randn(N, generator=g) * 0.1
+        y = ops.dimq_linear_codebook(x.to(gpu), packed.to(gpu), cb.to(gpu), bits, bias.to(gpu), N, K,
+                                     out_dtype=torch.float32)
+        ref = oracle.linear_dequant_reference(x.float(), packed, bits, cb, N, K, bias)
+        assert oracle.rel_err(y, ref) <= TOL, (bits, tile, M, N, K, per_channel, oracle.rel_err(y, ref))
+
+
+def test_linear_codebook_cfg1_shape(gpu):
+    """BASELINE cfg1: X fp32 [1576,768], 4-bit per-channel W [3072,768], bias, y fp32."""
+    ops = _ops()
+    announce("linear_codebook cfg1 shape")
+    g = _gen(0)
+    cb, idx, packed = _codebook_case(3072, 768, 4, True, g)
+    x = torch.randn(1576, 768, generator=g)
+    bias = torch.randn(3072, generator=g) * 0.02
+    y = ops.dimq_linear_codebook(x.to(gpu), packed.to(gpu), cb.to(gpu), 4, bias.to(gpu), 3072, 768,
+                                 out_dtype=torch.float32)
+    ref = oracle.linear_dequant_reference(x, packed, 4, cb, 3072, 768, bias)
+    assert oracle.rel_err(y, ref) <= TOL
+
+
 def test_linear_codebook_small_codebook_and_errors(gpu):
     ops = _ops()
     g = _gen(5)

@@ -123,7 +123,7 @@ __device__ __forceinline__ void stage_halo(const HaloArgs& p, int b, int ih0, ui
   } else {
     // NHWC: task = (halo pixel, 8 channels) -> one 16-byte load, one 16-byte LDS store
     const int tasks = p.IH_t * p.IW_t * (C / 8);
-    constexpr int TPT = 4;
+    constexpr int TPT = 8;
     for (int t0 = 0; t0 < tasks; t0 += 256 * TPT) {
       uint4 v[TPT];
 #pragma unroll
@@ -323,6 +323,118 @@ __global__ __launch_bounds__(256) void conv_halo_kernel(const HaloArgs p) {
   }
 }
 
+// Resident-weight variant of the halo kernel for T = KH*KW*C/16 <= 36
+// sub-steps (3x3 at C = 64, 1x1 at C <= 128): every lane decodes its output
+// channel's T weight fragments once (4*T VGPRs) and keeps them for the tile,
+// so the MFMA loop is one ds_read_b128 and one v_mfma_f32_32x32x16_f16 per
+// sub-step and block, with no decode work.  A wave runs two m-blocks at a
+// time (two independent accumulator chains: one dependent 32x32x16 chain
+// leaves the matrix core idle most of the time), and stores each finished
+// pair straight from registers while the next pair computes.  Launch bounds
+// give two work-groups (8 waves) per CU.
+template <int BITS, int CC16, int STRIDE, int KHW, bool PXROWS>
+__global__ __launch_bounds__(256, 2) void conv_resident_kernel(const HaloArgs p) {
+  constexpr int T = KHW * CC16;
+  static_assert(T <= 36, "resident weights are limited to 36 sub-steps");
+  constexpr int CHUNKS = (T + 3) / 4;
+  constexpr int WPL = CHUNKS * BITS;
+  constexpr int CP = CC16 * 16 + 8;
+  extern __shared__ __attribute__((aligned(16))) uint16_t halo[];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 31;
+  const int g = lane >> 5;
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int b = tile / p.tiles_h;
+  const int oh0 = (tile - b * p.tiles_h) * p.TH;
+  const int oc0 = blockIdx.y * 64;
+  const int wn = wave & 1;
+  const int wm = wave >> 1;
+  const int ocl = oc0 + 32 * wn + col;
+
+  constexpr int E = 1 << BITS;
+  __shared__ float cbs[64 * E];
+  stage_codebook<E>(p.cb, p.cb_dt, p.cb_rows, p.cb_size, oc0, 64, p.OC, cbs, tid, 256);
+
+  uint32_t wreg[WPL];
+  {
+    const int oc = min(ocl, p.OC - 1);
+    const uint32_t* src = p.kw + ((int64_t)oc * 2 + g) * WPL;
+#pragma unroll
+    for (int w = 0; w < WPL; ++w) wreg[w] = src[w];
+  }
+
+  stage_halo<CC16>(p, b, oh0 * STRIDE - p.pad_h, halo, tid);
+  __syncthreads();
+
+  CodebookRegs<BITS> cbr;
+  float scale;
+  {
+    const int rl = (p.cb_rows == 1) ? 0 : 32 * wn + col;
+    const int e = planes_from_lds<BITS, false>(cbs + rl * E, cbr, cbr);
+    scale = ldexpf(1.0f, -e);
+  }
+  const float bv = (p.bias && ocl < p.OC) ? load_as_float(p.bias, p.bias_dt, ocl) : 0.0f;
+
+  half8 wf[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    uint32_t chunk[BITS];
+#pragma unroll
+    for (int w = 0; w < BITS; ++w) chunk[w] = wreg[(t >> 2) * BITS + w];
+    wf[t] = decode_sub<BITS>(chunk, t & 3, cbr);
+  }
+
+  const int P = min(p.TH, p.OH - oh0) * p.OW;
+  const int nblk = (P + 31) / 32;
+  const int row_step = p.IW_t * CP;
+  // this wave's blocks wm, wm + 2, ... in pairs (q = 0, 1 -> blocks mb, mb + 2)
+  for (int mb = wm; mb < nblk; mb += 4) {
+    int base[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      int pix = (mb + 2 * q) * 32 + col;
+      if (pix >= P) pix = 0;  // rows past the tile read pixel 0 and are not stored
+      const int r = pix / p.OW;
+      const int c = pix - r * p.OW;
+      base[q] = ((r * STRIDE) * p.IW_t + c * STRIDE) * CP + 8 * g;
+    }
+    auto frag = [&](int u) {
+      const int t = u >> 1, q = u & 1;
+      const int khw = t / CC16;
+      const int cc = t - khw * CC16;
+      const int kh = (KHW == 9) ? khw / 3 : 0;
+      const int kw = (KHW == 9) ? khw - 3 * kh : 0;
+      return *reinterpret_cast<const half8*>(halo + base[q] + kh * row_step + kw * CP + 16 * cc);
+    };
+    constexpr int U = 2 * T;
+    constexpr int DEPTH = 4;
+    half8 xr[DEPTH];
+#pragma unroll
+    for (int u = 0; u < DEPTH; ++u) xr[u] = frag(u);
+    floatx16 acc[2];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[0][i] = acc[1][i] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int t = u >> 1, q = u & 1;
+      acc[q] = PXROWS ? mfma32x32x16(xr[u % DEPTH], wf[t], acc[q]) : mfma32x32x16(wf[t], xr[u % DEPTH], acc[q]);
+      if (u + DEPTH < U) xr[u % DEPTH] = frag(u + DEPTH);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, DEPTH, 0);
+#pragma unroll
+    for (int u = 0; u < U - DEPTH; ++u) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, DEPTH, 0);
+    store_block<PXROWS>(p, acc[0], b, oh0, P, mb, col, g, ocl, oc0 + 32 * wn, scale, bv);
+    if (mb + 2 < nblk) store_block<PXROWS>(p, acc[1], b, oh0, P, mb + 2, col, g, ocl, oc0 + 32 * wn, scale, bv);
+  }
+}
+
 // ---- weight preparation: conv_kcrs b-bit stream -> kernel layout
 // out[((n*2 + g)*CHUNKS + chunk)*BITS + w]: sub-steps t = 4*chunk + s, slot j
 // holds channel c = 16*(t % CC16) + 8*g + j at (kh, kw) = divmod(t / CC16, KW),
@@ -377,6 +489,17 @@ __global__ void prepare_kernel(const uint8_t* __restrict__ src, int OC, int C, i
 
 template <int BITS, int CC, int STRIDE, int KHW>
 int launch_halo_k(const HaloArgs& p, dim3 grid, size_t lds, hipStream_t s) {
+  if constexpr (KHW * CC <= 36) {
+    auto k = p.y_layout == DIMQ_NCHW ? conv_resident_kernel<BITS, CC, STRIDE, KHW, true>
+                                     : conv_resident_kernel<BITS, CC, STRIDE, KHW, false>;
+    if (lds > 64 * 1024) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return set_error(DIMQ_ERR_HIP, "conv2d_codebook (halo): %s", hipGetErrorString(e));
+    }
+    hipLaunchKernelGGL(k, grid, dim3(256), lds, s, p);
+    return check_launch("conv2d_codebook (halo, resident weights)");
+  }
   if (p.y_layout == DIMQ_NCHW)
     hipLaunchKernelGGL((conv_halo_kernel<BITS, CC, STRIDE, KHW, true>), grid, dim3(256), lds, s, p);
   else
@@ -452,6 +575,11 @@ int launch_conv_halo(const void* x, int x_dtype, int x_layout, int64_t B, int64_
   p.pad_h = (int)ph;
   p.pad_w = (int)pw;
   p.TH = (int)halo_tile_rows(C, KH, KW, stride, OH, OW);
+  if (const char* rows = getenv("DIMQ_HALO_ROWS")) {  // A/B runs on the resident kernel
+    const int64_t th = atoi(rows);
+    const int64_t lds = ((th - 1) * stride + KH) * ((OW - 1) * stride + KW) * (C + 8) * 2;
+    if (th >= 1 && th <= OH && KH * KW * (C / 16) <= 36 && lds <= 150 * 1024) p.TH = (int)th;
+  }
   p.IH_t = (p.TH - 1) * (int)stride + (int)KH;
   p.IW_t = ((int)OW - 1) * (int)stride + (int)KW;
   p.CP = (int)C + 8;
@@ -468,8 +596,8 @@ int launch_conv_halo(const void* x, int x_dtype, int x_layout, int64_t B, int64_
   p.y = y;
   p.y_dt = y_dtype;
   p.y_layout = y_layout;
-  const char* force = getenv("DIMQ_CONV_KERNEL");  // A/B runs: 0 = one-shot halo kernel
-  if (stream_supported(p, (int)stride, bits) && !(force && atoi(force) == 0))
+  const char* force = getenv("DIMQ_CONV_KERNEL");  // A/B runs: 1 = row-streaming kernel
+  if (stream_supported(p, (int)stride, bits) && force && atoi(force) == 1)
     return launch_conv_stream(p, (int)stride, bits, s);
   const int CC = (int)(C / 16);
   switch (bits) {

@@ -5,6 +5,7 @@
 
 #include "gemm_big.h"
 #include "gemm_kernel.h"
+#include "gemv_fast.h"
 
 namespace dimq {
 namespace {
@@ -117,6 +118,13 @@ int linear_codebook_impl(const void* x, int x_dtype, int64_t M, int64_t K, int64
   if (tile < 0 || tile >= kTileCount) tile = gemm_pick_tile(M, N, variant);
   if (tile >= kTileFast128x64 && gemm_fast_tile(kTile64x32, p, bits) == kTile64x32) tile = gemm_pick_tile(M, N, variant);
   if (tile == kTileGemv && (M > 16 || bits == 8)) tile = gemm_pick_tile(M, N, DIMQ_VARIANT_MFMA);
+  if (tile == kTileGemv && gemv_fast_supported(p, bits) && !getenv("DIMQ_GEMV_OLD")) {
+    switch (bits) {
+      case 2: return launch_gemv_fast<2>(p, x_dtype, s);
+      case 3: return launch_gemv_fast<3>(p, x_dtype, s);
+      default: return launch_gemv_fast<4>(p, x_dtype, s);
+    }
+  }
   return dispatch<false>(p, bits, x_dtype, tile, s);
 }
 

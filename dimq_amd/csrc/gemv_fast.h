@@ -1,0 +1,141 @@
+// Decode-shape codebook GEMV (M <= 16): y[M,N] = x[M,K] W_hat^T + b, the
+// HBM-bound case of BASELINE cfg5 (W 4096x4096 3-bit: 6.3 MB of indices).
+//
+// Work-group = 16 waves on 16 output columns; wave w owns k-range
+// [w*K/16, (w+1)*K/16) and lane group g = lane / 16 a contiguous quarter of
+// it, so each lane's weight indices and activations are contiguous in memory.
+// Every load of the wave (the lane's K/64 packed indices: 24 bytes at 3 bits;
+// its activation row slice: 128 bytes at bf16) is issued before any compute,
+// so the whole weight stream is in flight at once.  The 16x16x32 MFMA's k
+// dimension takes 8 consecutive k from each lane group (any k order works as
+// long as the activation and weight lanes agree); rows m >= M are zero.  The
+// 16 partial sums are reduced through LDS.
+#pragma once
+
+#include "gemm_big.h"
+
+namespace dimq {
+namespace {
+
+template <int BITS, int XT>
+__global__ __launch_bounds__(1024) void gemv_fast_kernel(const GemmArgs p) {
+  static_assert(BITS >= 2 && BITS <= 4, "register codebooks hold at most 16 entries");
+  constexpr int WAVES = 16;
+  constexpr int KL = 64;  // k per lane and round; a round covers 16 waves x 4 lane groups x 64 = 4096 k
+  constexpr int E = 1 << BITS;
+  __shared__ floatx4 red[WAVES][64];
+  __shared__ float cbs[16 * E];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 15;
+  const int g = lane >> 4;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
+  const int64_t n = n0 + col < p.N ? n0 + col : p.N - 1;
+  const int rounds = static_cast<int>(p.K / (KL * WAVES * 4));  // k-ranges of KL per lane
+
+  stage_codebook<E>(p.cb, p.cb_dt, p.cb_rows, p.cb_size, n0, 16, p.N, cbs, tid, WAVES * 64);
+
+  floatx4 acc = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  const bool arow = col < p.M;
+  CodebookRegs<BITS> cb;
+  float colscale = 1.0f;
+  for (int r = 0; r < rounds; ++r) {
+    const int64_t k0 = ((int64_t)(r * WAVES + wave) * 4 + g) * KL;
+    // ---- all loads of the round first
+    uint32_t bw[KL * BITS / 32];
+    {
+      const uint8_t* src = p.w + (((n * p.K + k0) * BITS) >> 3);
+      if constexpr (BITS == 3) {
+#pragma unroll
+        for (int q = 0; q < 3; ++q) {
+          const uint2 t = reinterpret_cast<const uint2*>(src)[q];
+          bw[2 * q] = t.x;
+          bw[2 * q + 1] = t.y;
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < BITS / 2; ++q) {
+          const uint4 t = reinterpret_cast<const uint4*>(src)[q];
+          bw[4 * q] = t.x;
+          bw[4 * q + 1] = t.y;
+          bw[4 * q + 2] = t.z;
+          bw[4 * q + 3] = t.w;
+        }
+      }
+    }
+    RawA<XT> ra[KL / 16];
+    {
+#pragma unroll
+      for (int h = 0; h < KL / 16; ++h) {
+        if (arow) {
+          issue_a16<XT>(p.x, (int64_t)col * p.ldx + k0 + 16 * h, ra[h]);
+        } else {
+#pragma unroll
+          for (int w = 0; w < RawA<XT>::kWords; ++w) ra[h].w[w] = 0u;
+        }
+      }
+    }
+    if (r == 0) {
+      __syncthreads();  // codebook staged
+      const int e = planes_from_lds<BITS, false>(cbs + ((p.cb_rows == 1) ? 0 : col * E), cb, cb);
+      colscale = ldexpf(1.0f, -e);
+    }
+    // ---- decode + MFMA, 8 k per step
+#pragma unroll
+    for (int h = 0; h < KL / 16; ++h) {
+      uint32_t a8[8];
+      convert_a16_big<BITS, XT>(ra[h], a8);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int s = 2 * h + t;  // step: indices 8s .. 8s+7 of the lane's range
+        uint32_t chunk[BITS];
+#pragma unroll
+        for (int w = 0; w < BITS; ++w) chunk[w] = bw[(s >> 2) * BITS + w];
+        const half8 bf = decode_sub<BITS>(chunk, s & 3, cb);
+        const u32x4 a4 = {a8[4 * t], a8[4 * t + 1], a8[4 * t + 2], a8[4 * t + 3]};
+        acc = mfma16x16x32(__builtin_bit_cast(half8, a4), bf, acc);
+      }
+    }
+  }
+  if (rounds == 0) __syncthreads();
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0) {
+    floatx4 t = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) t += red[w][lane];
+    if (n0 + col < p.N) {
+      const float b = p.bias ? load_as_float(p.bias, p.bias_dt, n0 + col) : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t m = 4 * g + i;
+        if (m < p.M) store_from_float(p.y, p.y_dt, m * p.ldy + n0 + col, t[i] * colscale + b);
+      }
+    }
+  }
+}
+
+}  // namespace
+
+// Shapes it runs: M <= 4 (measured: at M = 16 the split-K kernel is faster,
+// the activation conversion of 16 rows per lane costing more than the
+// up-front loads save), K a multiple of 4096, 16-byte aligned rows/streams.
+inline bool gemv_fast_supported(const GemmArgs& p, int bits) {
+  return p.M >= 1 && p.M <= 4 && !p.conv && (bits == 2 || bits == 3 || bits == 4) && p.K % 4096 == 0 &&
+         p.fast_b && p.vec_a;
+}
+
+template <int BITS>
+int launch_gemv_fast(const GemmArgs& p, int xt, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((p.N + 15) / 16));
+  switch (xt) {
+    case DIMQ_F32: hipLaunchKernelGGL((gemv_fast_kernel<BITS, DIMQ_F32>), grid, dim3(1024), 0, s, p); break;
+    case DIMQ_F16: hipLaunchKernelGGL((gemv_fast_kernel<BITS, DIMQ_F16>), grid, dim3(1024), 0, s, p); break;
+    default: hipLaunchKernelGGL((gemv_fast_kernel<BITS, DIMQ_BF16>), grid, dim3(1024), 0, s, p); break;
+  }
+  return check_launch("linear_codebook (gemv)");
+}
+
+}  // namespace dimq

@@ -310,6 +310,24 @@ def test_linear_codebook_large_tiles(gpu, monkeypatch, bits, tile, M, N, K, xdt)
         assert oracle.rel_err(y, ref) <= TOL, (bits, tile, M, N, K, per_channel, oracle.rel_err(y, ref))
 
 
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("M,N,K,xdt", [(1, 300, 4096, torch.bfloat16), (4, 64, 8192, torch.float16),
+                                       (3, 130, 4096, torch.float32), (16, 130, 4096, torch.bfloat16)])
+def test_linear_codebook_gemv_fast(gpu, bits, M, N, K, xdt):
+    """Decode-shape GEMV (all loads issued up front), N tails, per-layer and per-channel codebooks."""
+    ops = _ops()
+    for per_channel in (True, False):
+        announce(f"linear_codebook gemv bits={bits} M={M} N={N} K={K} {xdt} pc={per_channel}")
+        g = _gen(bits * 13 + M + N)
+        cb, idx, packed = _codebook_case(N, K, bits, per_channel, g)
+        x = torch.randn(M, K, generator=g).to(xdt)
+        bias = torch.randn(N, generator=g) * 0.1
+        y = ops.dimq_linear_codebook(x.to(gpu), packed.to(gpu), cb.to(gpu), bits, bias.to(gpu), N, K,
+                                     out_dtype=torch.float32)
+        ref = oracle.linear_dequant_reference(x.float(), packed, bits, cb, N, K, bias)
+        assert oracle.rel_err(y, ref) <= TOL, (bits, M, N, K, per_channel, oracle.rel_err(y, ref))
+
+
 def test_linear_codebook_cfg1_shape(gpu):
     """BASELINE cfg1: X fp32 [1576,768], 4-bit per-channel W [3072,768], bias, y fp32."""
     ops = _ops()

@@ -171,6 +171,12 @@ extern "C" int dimq_conv2d_codebook(const void* x, int x_dtype, int x_layout, in
                             cb_size, bias, bias_dtype, s.OC, s.KH, s.KW, s.sh, s.ph, s.pw, s.OH, s.OW, y, y_dtype,
                             y_layout, as_stream(stream));
   }
+  if (variant != DIMQ_VARIANT_SMALL_M &&
+      stem_eligible(s.C, s.OC, s.KH, s.KW, s.sh, s.sw, s.pw, s.dh, s.dw, s.groups, s.OH, s.OW, bits, y_dtype, x, y)) {
+    return launch_conv_stem(x, x_dtype, x_layout, s.B, s.C, s.H, s.W, packed_w, packed_numel, bits, codebook,
+                            cb_dtype, cb_rows, cb_size, bias, bias_dtype, s.OC, s.KH, s.KW, s.ph, s.pw, s.OH, s.OW,
+                            y, y_dtype, y_layout, as_stream(stream));
+  }
   GemmArgs p = conv_args(s, x, x_layout, packed_w, codebook, cb_dtype, cb_rows, cb_size, bias, bias_dtype, y,
                          y_dtype, y_layout);
   int tile = gemm_pick_tile(p.M, p.N, variant);

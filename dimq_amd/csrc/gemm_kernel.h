@@ -873,6 +873,16 @@ int launch_conv_halo(const void* x, int x_dtype, int x_layout, int64_t B, int64_
 int launch_prepare(const uint8_t* src, int64_t OC, int64_t C, int64_t KH, int64_t KW, int bits, uint32_t* out,
                    hipStream_t s);
 
+// conv_stem.hip
+bool stem_eligible(int64_t C, int64_t OC, int64_t KH, int64_t KW, int64_t sh, int64_t sw, int64_t pw,
+                   int64_t dh, int64_t dw, int64_t groups, int64_t OH, int64_t OW, int bits, int y_dtype,
+                   const void* x, const void* y);
+int launch_conv_stem(const void* x, int x_dtype, int x_layout, int64_t B, int64_t C, int64_t H, int64_t W,
+                     const uint8_t* w, int64_t w_bytes, int bits, const void* cb, int cb_dtype, int64_t cb_rows,
+                     int64_t cb_size, const void* bias, int bias_dtype, int64_t OC, int64_t KH, int64_t KW,
+                     int64_t ph, int64_t pw, int64_t OH, int64_t OW, void* y, int y_dtype, int y_layout,
+                     hipStream_t s);
+
 // gemm.hip
 int gemm_pick_tile(int64_t M, int64_t N, int variant);
 int gemm_dispatch(const GemmArgs& p, int bits, int xt, bool a4, int tile, hipStream_t s);

@@ -386,6 +386,44 @@ def test_conv2d_codebook_vs_oracle(gpu, case, layout):
     assert oracle.rel_err(y.float(), ref) <= TOL, oracle.rel_err(y.float(), ref)
 
 
+# ---------------------------------------------------------------- small-channel stride-2 stem conv
+@pytest.mark.parametrize("case", [
+    dict(B=2, C=3, H=224, W=224, OC=64, K=7, p=3, bits=8, dt=torch.float16, out=torch.float16, pc=True),  # ResNet stem
+    dict(B=1, C=3, H=230, W=226, OC=64, K=7, p=3, bits=8, dt=torch.float16, out=torch.float32, pc=False),  # partial band
+    dict(B=3, C=3, H=37, W=37, OC=32, K=7, p=3, bits=4, dt=torch.bfloat16, out=torch.float32, pc=True),   # W*C odd
+    dict(B=2, C=4, H=40, W=34, OC=64, K=7, p=2, bits=3, dt=torch.float16, out=torch.bfloat16, pc=True),   # even pad
+    dict(B=2, C=3, H=50, W=50, OC=24, K=3, p=1, bits=2, dt=torch.float16, out=torch.float16, pc=True),    # 3x3/2 stem
+    dict(B=1, C=1, H=31, W=29, OC=16, K=3, p=0, bits=8, dt=torch.float32, out=torch.float32, pc=True),    # fp32 input
+    dict(B=2, C=2, H=20, W=18, OC=40, K=7, p=3, bits=8, dt=torch.float16, out=torch.float16, pc=True, cbn=200),
+])
+@pytest.mark.parametrize("layout", ["nchw", "nhwc"])
+def test_conv2d_stem_vs_oracle(gpu, case, layout):
+    """C <= 4, stride-2 convs take the stem kernel; checked against the CPU reference and the generic path."""
+    ops = _ops()
+    announce(f"conv stem {case} {layout}")
+    g = _gen(case["C"] * 7 + case["OC"] + case["bits"] + case["H"])
+    K, pad = case["K"], case["p"]
+    shape = (case["OC"], case["C"], K, K)
+    x = torch.randn(case["B"], case["C"], case["H"], case["W"], generator=g).to(case["dt"])
+    cb, idx, packed = _codebook_case(case["OC"], case["C"] * K * K, case["bits"], case["pc"], g,
+                                     cb_entries=case.get("cbn"))
+    bias = torch.randn(case["OC"], generator=g) * 0.1
+    xd = x.to(gpu)
+    if layout == "nhwc":
+        xd = xd.to(memory_format=torch.channels_last)
+    args = (xd, packed.to(gpu), cb.to(gpu), case["bits"], bias.to(gpu), shape, (2, 2), (pad, pad), (1, 1), 1)
+    y = ops.dimq_conv2d_codebook(*args, out_dtype=case["out"])
+    assert y.dtype == case["out"]
+    if layout == "nhwc" and case["C"] > 1:  # a 1-channel input is NCHW- and NHWC-contiguous at once
+        assert y.is_contiguous(memory_format=torch.channels_last)
+    ref = oracle.conv2d_dequant_reference(x.float(), packed, case["bits"], cb, shape, bias, 2, pad, 1, 1)
+    assert y.shape == ref.shape
+    tol = TOL if case["out"] != torch.bfloat16 else 8e-3  # bf16 output rounding alone is 2^-9 relative
+    assert oracle.rel_err(y.float(), ref) <= tol, oracle.rel_err(y.float(), ref)
+    y2 = ops.dimq_conv2d_codebook(*args, out_dtype=torch.float32, variant="small_m")  # generic implicit GEMM
+    assert oracle.rel_err(y.float(), y2) <= max(tol, 2e-3)
+
+
 # ---------------------------------------------------------------- HIP graph replay
 def test_graph_replay_matches_eager(gpu):
     """Kernels captured in a HIP graph give the eager result on every replay (bench.py times graphs)."""

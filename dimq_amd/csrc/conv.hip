@@ -1,7 +1,7 @@
 // Host side of the codebook Conv2d ops: argument checks (reference messages
 // from csrc/dimq_conv2d_lut.cu:105-134) and launch of the implicit-GEMM
 // kernels (im2col gathered on the fly, never materialised).
-#include "gemm_kernel.h"
+#include "gemm_big.h"
 
 namespace dimq {
 namespace {
@@ -69,6 +69,84 @@ GemmArgs conv_args(const ConvShape& s, const void* x, int x_layout, const uint8_
   return p;
 }
 
+// ---- implicit-GEMM conv on the large-tile GEMM kernels (C % 64 == 0)
+// Weight layout: the conv_kcrs stream re-packed tap-major, index (oc, kh, kw, c)
+// at k = (kh*KW + kw)*C + c, same bits (no expansion).
+bool gemm_conv_weight_supported(int64_t C, int64_t KH, int64_t KW, int bits) {
+  if (halo_weight_supported(C, KH, KW, bits)) return false;  // those have the LDS-halo layout
+  return (bits == 2 || bits == 3 || bits == 4) && C > 0 && C % 64 == 0 && KH > 0 && KW > 0;
+}
+
+int64_t gemm_conv_prepared_words(int64_t OC, int64_t C, int64_t KH, int64_t KW, int bits) {
+  return OC * C * KH * KW * bits / 32;  // C % 64 == 0: whole words
+}
+
+template <int BITS>
+__global__ void prepare_tapmajor_kernel(const uint8_t* __restrict__ src, int64_t src_bytes, int C, int KH, int KW,
+                                        int64_t groups32, uint32_t* __restrict__ out) {
+  const int64_t gi = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (gi >= groups32) return;
+  const int64_t K = static_cast<int64_t>(C) * KH * KW;
+  uint32_t words[BITS];
+#pragma unroll
+  for (int w = 0; w < BITS; ++w) words[w] = 0u;
+  for (int j = 0; j < 32; ++j) {
+    const int64_t f = gi * 32 + j;
+    const int64_t oc = f / K;
+    const int r = static_cast<int>(f - oc * K);
+    const int tap = r / C;
+    const int c = r - tap * C;
+    const int kh = tap / KW;
+    const int kw = tap - kh * KW;
+    const int64_t bit = (((oc * C + c) * KH + kh) * KW + kw) * BITS;
+    const int64_t byte = bit >> 3;
+    const int sh = static_cast<int>(bit & 7);
+    uint32_t v = static_cast<uint32_t>(src[byte]) >> sh;
+    if (sh + BITS > 8 && byte + 1 < src_bytes) v |= static_cast<uint32_t>(src[byte + 1]) << (8 - sh);
+    v &= (1u << BITS) - 1u;
+    const int fb = j * BITS;
+    words[fb >> 5] |= v << (fb & 31);
+    if ((fb & 31) + BITS > 32) words[(fb >> 5) + 1] |= v >> (32 - (fb & 31));
+  }
+#pragma unroll
+  for (int w = 0; w < BITS; ++w) out[gi * BITS + w] = words[w];
+}
+
+int launch_prepare_tapmajor(const uint8_t* src, int64_t src_bytes, int64_t OC, int64_t C, int64_t KH, int64_t KW,
+                            int bits, uint32_t* out, hipStream_t s) {
+  const int64_t groups32 = OC * C * KH * KW / 32;
+  const unsigned blocks = static_cast<unsigned>((groups32 + 255) / 256);
+  switch (bits) {
+    case 2: hipLaunchKernelGGL(prepare_tapmajor_kernel<2>, dim3(blocks), dim3(256), 0, s, src, src_bytes, (int)C,
+                               (int)KH, (int)KW, groups32, out); break;
+    case 3: hipLaunchKernelGGL(prepare_tapmajor_kernel<3>, dim3(blocks), dim3(256), 0, s, src, src_bytes, (int)C,
+                               (int)KH, (int)KW, groups32, out); break;
+    default: hipLaunchKernelGGL(prepare_tapmajor_kernel<4>, dim3(blocks), dim3(256), 0, s, src, src_bytes, (int)C,
+                                (int)KH, (int)KW, groups32, out); break;
+  }
+  return check_launch("prepare_conv_weight (tap-major)");
+}
+
+int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+// Tile of the implicit-GEMM conv: 128x128 when that fills every CU, else 64x128.
+int gemm_conv_tile(int64_t M, int64_t N) {
+  const char* force = getenv("DIMQ_CONV_BIG");  // A/B runs: 0..2
+  if (force && atoi(force) >= 0 && atoi(force) <= 2) return atoi(force);
+  const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
+  return t128 >= device_cus() ? 0 : 1;
+}
+
 ConvShape make_shape(int64_t B, int64_t C, int64_t H, int64_t W, int64_t OC, int64_t ICg, int64_t KH, int64_t KW,
                      int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw, int64_t groups) {
   ConvShape s{B, C, H, W, OC, ICg, KH, KW, sh, sw, ph, pw, dh, dw, groups, 0, 0};
@@ -114,22 +192,31 @@ extern "C" int dimq_conv2d_lut(const void* x, int x_dtype, int64_t B, int64_t C,
 
 extern "C" int64_t dimq_conv2d_prepared_words(int64_t out_channels, int64_t in_channels, int64_t kernel_h,
                                               int64_t kernel_w, int bits) {
-  if (!halo_weight_supported(in_channels, kernel_h, kernel_w, bits) || out_channels <= 0) return 0;
-  return halo_prepared_words(out_channels, in_channels, kernel_h, kernel_w, bits);
+  if (out_channels <= 0) return 0;
+  if (halo_weight_supported(in_channels, kernel_h, kernel_w, bits))
+    return halo_prepared_words(out_channels, in_channels, kernel_h, kernel_w, bits);
+  if (gemm_conv_weight_supported(in_channels, kernel_h, kernel_w, bits))
+    return gemm_conv_prepared_words(out_channels, in_channels, kernel_h, kernel_w, bits);
+  return 0;
 }
 
 extern "C" int dimq_conv2d_prepare_weight(const uint8_t* packed_w, int64_t packed_numel, int bits,
                                           int64_t out_channels, int64_t in_channels, int64_t kernel_h,
                                           int64_t kernel_w, uint32_t* prepared_w, int64_t prepared_words,
                                           void* stream) {
-  if (!halo_weight_supported(in_channels, kernel_h, kernel_w, bits))
+  const bool halo = halo_weight_supported(in_channels, kernel_h, kernel_w, bits);
+  if (!halo && !gemm_conv_weight_supported(in_channels, kernel_h, kernel_w, bits))
     return set_error(DIMQ_ERR_UNSUPPORTED, "no kernel layout for C=%lld KH=%lld KW=%lld bits=%d",
                      (long long)in_channels, (long long)kernel_h, (long long)kernel_w, bits);
   DIMQ_CHECK(out_channels > 0, "channel counts must be positive");
   const int64_t wnumel = out_channels * in_channels * kernel_h * kernel_w;
   DIMQ_CHECK(packed_numel >= (wnumel * bits + 7) / 8, "packed_weight is too small for requested conv weight shape");
-  DIMQ_CHECK(prepared_words >= halo_prepared_words(out_channels, in_channels, kernel_h, kernel_w, bits),
-             "prepared weight buffer is too small");
+  const int64_t need = halo ? halo_prepared_words(out_channels, in_channels, kernel_h, kernel_w, bits)
+                            : gemm_conv_prepared_words(out_channels, in_channels, kernel_h, kernel_w, bits);
+  DIMQ_CHECK(prepared_words >= need, "prepared weight buffer is too small");
+  if (!halo)
+    return launch_prepare_tapmajor(packed_w, packed_numel, out_channels, in_channels, kernel_h, kernel_w, bits,
+                                   prepared_w, as_stream(stream));
   return launch_prepare(packed_w, out_channels, in_channels, kernel_h, kernel_w, bits, prepared_w,
                         as_stream(stream));
 }
@@ -170,6 +257,21 @@ extern "C" int dimq_conv2d_codebook(const void* x, int x_dtype, int x_layout, in
     return launch_conv_halo(x, x_dtype, x_layout, s.B, s.C, s.H, s.W, prepared_w, bits, codebook, cb_dtype, cb_rows,
                             cb_size, bias, bias_dtype, s.OC, s.KH, s.KW, s.sh, s.ph, s.pw, s.OH, s.OW, y, y_dtype,
                             y_layout, as_stream(stream));
+  }
+  if (prepared_w != nullptr && variant != DIMQ_VARIANT_SMALL_M && s.groups == 1 &&
+      gemm_conv_weight_supported(s.C, s.KH, s.KW, bits) && x_layout == DIMQ_NHWC && y_layout == DIMQ_NHWC &&
+      (x_dtype == DIMQ_F16 || x_dtype == DIMQ_BF16) && aligned(x, 16) && aligned(prepared_w, 16)) {
+    DIMQ_CHECK(prepared_words >= gemm_conv_prepared_words(s.OC, s.C, s.KH, s.KW, bits),
+               "prepared weight buffer is too small");
+    GemmArgs p = conv_args(s, x, x_layout, reinterpret_cast<const uint8_t*>(prepared_w), codebook, cb_dtype, cb_rows,
+                           cb_size, bias, bias_dtype, y, y_dtype, y_layout);
+    p.ldy = s.OC;
+    const int tile = gemm_conv_tile(p.M, p.N);
+    switch (bits) {
+      case 2: return launch_big_conv_b2(p, x_dtype, tile, as_stream(stream));
+      case 3: return launch_big_conv_b3(p, x_dtype, tile, as_stream(stream));
+      default: return launch_big_conv_b4(p, x_dtype, tile, as_stream(stream));
+    }
   }
   if (variant != DIMQ_VARIANT_SMALL_M &&
       stem_eligible(s.C, s.OC, s.KH, s.KW, s.sh, s.sw, s.pw, s.dh, s.dw, s.groups, s.OH, s.OW, bits, y_dtype, x, y)) {

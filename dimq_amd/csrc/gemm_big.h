@@ -111,7 +111,12 @@ __device__ __forceinline__ void convert_a16_big(const RawA<XT>& r, uint32_t out[
   }
 }
 
-template <int BITS, int XT, int WGM, int WGN, int MBLK, int NBLK>
+// CONV: implicit-GEMM convolution on NHWC activations with a tap-major
+// weight stream (k = (kh*KW + kw)*C + c, C % 64 == 0): row m is output pixel
+// (b, oh, ow), and a 64-wide k stage is 64 consecutive channels of one input
+// pixel (one tap), or zeros where the tap falls into the padding.  y is the
+// NHWC output, row-major [M, OC].
+template <int BITS, int XT, int WGM, int WGN, int MBLK, int NBLK, bool CONV = false>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_big_kernel(const GemmArgs p) {
   static_assert(BITS >= 2 && BITS <= 4, "register codebooks hold at most 16 entries");
   constexpr int NT = 64 * WGM * WGN;
@@ -152,13 +157,31 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_big_kernel(const GemmArgs
   // activation tasks: (row m, 16-wide group kg) per thread, 4 groups per row
   int64_t aoff[A_TASKS];
   int alds[A_TASKS];
+  int aih[A_TASKS], aiw[A_TASKS];  // CONV: input row/column of tap (0, 0)
 #pragma unroll
   for (int i = 0; i < A_TASKS; ++i) {
     const int task = tid + NT * i;
     const int m = task >> 2, kg = task & 3;
-    const int64_t row = (m0 + m < p.M) ? m0 + m : p.M - 1;
-    aoff[i] = row * p.ldx + 16 * kg;
     alds[i] = m * kBigLDA + 16 * kg;
+    if constexpr (CONV) {
+      const int64_t mg = m0 + m;
+      const int64_t hw = p.cOH * p.cOW;
+      aoff[i] = 16 * kg;
+      aih[i] = -(1 << 30);  // rows past M read zeros
+      aiw[i] = 0;
+      if (mg < p.M) {
+        const int64_t b = mg / hw;
+        const int r = static_cast<int>(mg - b * hw);
+        const int oh = r / static_cast<int>(p.cOW);
+        const int ow = r - oh * static_cast<int>(p.cOW);
+        aoff[i] += b * p.cH * p.cW * p.cC;
+        aih[i] = oh * p.csh - p.cph;
+        aiw[i] = ow * p.csw - p.cpw;
+      }
+    } else {
+      const int64_t row = (m0 + m < p.M) ? m0 + m : p.M - 1;
+      aoff[i] = row * p.ldx + 16 * kg;
+    }
   }
 
   floatx16g acc[MBLK][NBLK];
@@ -175,8 +198,27 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_big_kernel(const GemmArgs
 
   auto issue_a = [&](int64_t kt) {
     const int64_t k = (kt < nk ? kt : nk - 1) * kBigKS;
+    if constexpr (CONV) {
+      const int tap = static_cast<int>(k / p.cC);
+      const int64_t c0 = k - tap * p.cC;
+      const int kh = tap / p.cKW;
+      const int kw = tap - kh * p.cKW;
 #pragma unroll
-    for (int i = 0; i < A_TASKS; ++i) issue_a16<XT>(p.x, aoff[i] + k, ra[i]);
+      for (int i = 0; i < A_TASKS; ++i) {
+        const int ih = aih[i] + kh * p.cdh;
+        const int iw = aiw[i] + kw * p.cdw;
+        if (static_cast<unsigned>(ih) < static_cast<unsigned>(p.cH) &&
+            static_cast<unsigned>(iw) < static_cast<unsigned>(p.cW)) {
+          issue_a16<XT>(p.x, aoff[i] + (static_cast<int64_t>(ih) * p.cW + iw) * p.cC + c0, ra[i]);
+        } else {
+#pragma unroll
+          for (int w = 0; w < RawA<XT>::kWords; ++w) ra[i].w[w] = 0u;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < A_TASKS; ++i) issue_a16<XT>(p.x, aoff[i] + k, ra[i]);
+    }
   };
   auto commit_a = [&](int buf) {
 #pragma unroll
@@ -514,13 +556,30 @@ int launch_deep(const GemmArgs& p, hipStream_t s) {
   return check_launch("linear_codebook (large tiles, deep pipeline)");
 }
 
-template <int BITS, int XT, int WGM, int WGN, int MBLK, int NBLK>
+template <int BITS, int XT, int WGM, int WGN, int MBLK, int NBLK, bool CONV = false>
 int launch_big(const GemmArgs& p, hipStream_t s) {
   constexpr int BM = WGM * MBLK * 32, BN = WGN * NBLK * 32;
   const int64_t tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-  hipLaunchKernelGGL((gemm_big_kernel<BITS, XT, WGM, WGN, MBLK, NBLK>), dim3(static_cast<unsigned>(tiles)),
+  hipLaunchKernelGGL((gemm_big_kernel<BITS, XT, WGM, WGN, MBLK, NBLK, CONV>), dim3(static_cast<unsigned>(tiles)),
                      dim3(64 * WGM * WGN), 0, s, p);
-  return check_launch("linear_codebook (large tiles)");
+  return check_launch(CONV ? "conv2d_codebook (implicit GEMM, large tiles)" : "linear_codebook (large tiles)");
+}
+
+// Implicit-GEMM conv tiles: 0 = 128x128 (2x2 waves of 64x64), 1 = 64x128
+// (1x4 waves of 64x32), 2 = 256x128 (2x2 waves of 128x64).
+template <int BITS>
+int launch_big_conv_bits(const GemmArgs& p, int xt, int tile, hipStream_t s) {
+#define DIMQ_CONV_TILES(XT)                                            \
+  switch (tile) {                                                      \
+    case 1: return launch_big<BITS, XT, 1, 4, 2, 1, true>(p, s);       \
+    case 2: return launch_big<BITS, XT, 2, 2, 4, 2, true>(p, s);       \
+    default: return launch_big<BITS, XT, 2, 2, 2, 2, true>(p, s);      \
+  }
+  if (xt == DIMQ_F16) {
+    DIMQ_CONV_TILES(DIMQ_F16)
+  }
+  DIMQ_CONV_TILES(DIMQ_BF16)
+#undef DIMQ_CONV_TILES
 }
 
 // Tile ids (WGM x WGN waves of (MBLK*32) x (NBLK*32)):
@@ -553,5 +612,8 @@ int launch_big_bits(const GemmArgs& p, int xt, int tile, hipStream_t s) {
 int launch_big_b2(const GemmArgs& p, int xt, int tile, hipStream_t s);
 int launch_big_b3(const GemmArgs& p, int xt, int tile, hipStream_t s);
 int launch_big_b4(const GemmArgs& p, int xt, int tile, hipStream_t s);
+int launch_big_conv_b2(const GemmArgs& p, int xt, int tile, hipStream_t s);
+int launch_big_conv_b3(const GemmArgs& p, int xt, int tile, hipStream_t s);
+int launch_big_conv_b4(const GemmArgs& p, int xt, int tile, hipStream_t s);
 
 }  // namespace dimq

@@ -499,6 +499,59 @@ def test_conv2d_halo_prepared_vs_oracle(gpu, case, layout):
     assert oracle.rel_err(y, y2) <= 1e-5  # prepared (halo) and generic implicit-GEMM paths agree
 
 
+# ---------------------------------------------------------------- implicit-GEMM conv on large tiles (C % 64 == 0)
+@pytest.mark.parametrize("case", [
+    dict(B=2, C=256, H=14, W=14, OC=256, K=3, s=1, p=1, d=1, bits=2, dt=torch.float16, out=torch.float32),  # layer3
+    dict(B=3, C=256, H=14, W=14, OC=512, K=3, s=2, p=1, d=1, bits=2, dt=torch.bfloat16, out=torch.float32),
+    dict(B=2, C=512, H=7, W=7, OC=512, K=3, s=1, p=1, d=1, bits=2, dt=torch.float16, out=torch.float16),  # layer4
+    dict(B=4, C=256, H=14, W=14, OC=512, K=1, s=2, p=0, d=1, bits=4, dt=torch.float16, out=torch.float16),
+    dict(B=1, C=192, H=11, W=9, OC=96, K=5, s=1, p=3, d=2, bits=3, dt=torch.float16, out=torch.float32, pc=False),
+    dict(B=1, C=64, H=9, W=9, OC=200, K=5, s=1, p=2, d=1, bits=4, dt=torch.bfloat16, out=torch.bfloat16, cbn=11),
+])
+@pytest.mark.parametrize("layout", ["nhwc", "nchw"])
+def test_conv2d_gemm_prepared_vs_oracle(gpu, case, layout):
+    """Tap-major prepared weights: NHWC takes the large-tile implicit GEMM, NCHW the generic kernel."""
+    ops = _ops()
+    announce(f"conv gemm {case} {layout}")
+    g = _gen(case["C"] + case["OC"] + case["bits"] * 5 + case["K"])
+    K = case["K"]
+    shape = (case["OC"], case["C"], K, K)
+    x = torch.relu(torch.randn(case["B"], case["C"], case["H"], case["W"], generator=g)).to(case["dt"])
+    cb, idx, packed = _codebook_case(case["OC"], case["C"] * K * K, case["bits"], case.get("pc", True), g,
+                                     cb_entries=case.get("cbn"))
+    bias = torch.randn(case["OC"], generator=g) * 0.1
+    xd = x.to(gpu)
+    if layout == "nhwc":
+        xd = xd.to(memory_format=torch.channels_last)
+    pd = packed.to(gpu)
+    prep = ops.prepare_conv_weight(pd, case["bits"], shape)
+    assert prep is not None and prep.numel() == case["OC"] * case["C"] * K * K * case["bits"] // 32
+    conv = (case["s"],) * 2, (case["p"],) * 2, (case["d"],) * 2, 1
+    y = ops.dimq_conv2d_codebook(xd, pd, cb.to(gpu), case["bits"], bias.to(gpu), shape, *conv,
+                                 out_dtype=case["out"], prepared_weight=prep)
+    ref = oracle.conv2d_dequant_reference(x.float(), packed, case["bits"], cb, shape, bias, case["s"], case["p"],
+                                          case["d"], 1)
+    assert y.shape == ref.shape and y.dtype == case["out"]
+    tol = TOL if case["out"] != torch.bfloat16 else 8e-3  # bf16 output rounding alone is 2^-9 relative
+    assert oracle.rel_err(y.float(), ref) <= tol, oracle.rel_err(y.float(), ref)
+    y2 = ops.dimq_conv2d_codebook(xd, pd, cb.to(gpu), case["bits"], bias.to(gpu), shape, *conv,
+                                  out_dtype=torch.float32, variant="small_m")
+    assert oracle.rel_err(y.float(), y2) <= tol
+
+
+def test_conv2d_prepare_tapmajor_layout(gpu):
+    """The tap-major stream holds index (oc, kh, kw, c) at k = (kh*KW + kw)*C + c, LSB-first, same bits."""
+    ops = _ops()
+    g = _gen(77)
+    for bits in (2, 3, 4):
+        OC, C, KH, KW = 5, 128, 3, 2
+        idx = torch.randint(0, 1 << bits, (OC, C, KH, KW), generator=g, dtype=torch.uint8)
+        packed = torch.from_numpy(oracle.pack_bits(idx.reshape(-1), bits)).to(gpu)
+        prep = ops.prepare_conv_weight(packed, bits, (OC, C, KH, KW))
+        want = oracle.pack_bits(idx.permute(0, 2, 3, 1).reshape(-1), bits)
+        assert np.array_equal(prep.cpu().view(torch.uint8).numpy()[:want.size], want), bits
+
+
 def test_conv2d_prepare_unsupported_returns_none(gpu):
     ops = _ops()
     assert ops.prepare_conv_weight(torch.zeros(100, dtype=torch.uint8, device=gpu), 2, (16, 48, 3, 3)) is None

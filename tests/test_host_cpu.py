@@ -52,7 +52,9 @@ def test_host_only_entry_points(capi):
     assert lib.dimq_conv2d_prepared_words(128, 128, 1, 1, 4) == 128 * 2 * 2 * 4
     assert lib.dimq_conv2d_prepared_words(64, 64, 3, 3, 8) == 0      # bits without a kernel layout
     assert lib.dimq_conv2d_prepared_words(64, 48, 3, 3, 2) == 0      # channels without a kernel layout
-    assert lib.dimq_conv2d_prepared_words(64, 64, 5, 5, 2) == 0
+    assert lib.dimq_conv2d_prepared_words(64, 64, 5, 5, 2) == 64 * 64 * 25 * 2 // 32   # tap-major GEMM layout
+    assert lib.dimq_conv2d_prepared_words(512, 256, 3, 3, 2) == 512 * 256 * 9 * 2 // 32
+    assert lib.dimq_conv2d_prepared_words(512, 256, 1, 1, 4) == 512 * 256 * 4 // 32
 
 
 def test_argument_errors_return_codes_without_touching_the_gpu(capi):

@@ -73,12 +73,31 @@ GemmArgs conv_args(const ConvShape& s, const void* x, int x_layout, const uint8_
 // Weight layout: the conv_kcrs stream re-packed tap-major, index (oc, kh, kw, c)
 // at k = (kh*KW + kw)*C + c, same bits (no expansion).
 bool gemm_conv_weight_supported(int64_t C, int64_t KH, int64_t KW, int bits) {
-  if (halo_weight_supported(C, KH, KW, bits)) return false;  // those have the LDS-halo layout
   return (bits == 2 || bits == 3 || bits == 4) && C > 0 && C % 64 == 0 && KH > 0 && KW > 0;
 }
 
-int64_t gemm_conv_prepared_words(int64_t OC, int64_t C, int64_t KH, int64_t KW, int bits) {
+// The prepared weight holds every kernel layout the shape has, one after the
+// other: [LDS-halo layout, padded to 16 bytes][tap-major layout].
+int64_t halo_part_words(int64_t OC, int64_t C, int64_t KH, int64_t KW, int bits) {
+  if (!halo_weight_supported(C, KH, KW, bits)) return 0;
+  return (halo_prepared_words(OC, C, KH, KW, bits) + 3) / 4 * 4;
+}
+
+int64_t gemm_part_words(int64_t OC, int64_t C, int64_t KH, int64_t KW, int bits) {
+  if (!gemm_conv_weight_supported(C, KH, KW, bits)) return 0;
   return OC * C * KH * KW * bits / 32;  // C % 64 == 0: whole words
+}
+
+// Which kernel a conv with both layouts takes (measured on ResNet-18's layers
+// at batch 128): the LDS-halo kernel only for stride-1 KxK convs of fewer
+// than 128 channels (64 vs 110 us at C = 64, 56x56), where its halo reuse
+// beats the GEMM's 64-wide k stages; the implicit GEMM for the rest (stride 2
+// C = 128: 38 vs 115 us; 1x1: 20-30 vs 35-39 us; C >= 128 stride 1: equal).
+bool prefer_gemm_conv(int64_t C, int64_t KH, int64_t KW, int64_t stride) {
+  const char* force = getenv("DIMQ_CONV_PATH");  // A/B runs: "halo" or "gemm"
+  if (force && force[0] == 'h') return false;
+  if (force && force[0] == 'g') return true;
+  return !(C < 128 && stride == 1 && KH * KW > 1);
 }
 
 template <int BITS>
@@ -193,32 +212,32 @@ extern "C" int dimq_conv2d_lut(const void* x, int x_dtype, int64_t B, int64_t C,
 extern "C" int64_t dimq_conv2d_prepared_words(int64_t out_channels, int64_t in_channels, int64_t kernel_h,
                                               int64_t kernel_w, int bits) {
   if (out_channels <= 0) return 0;
-  if (halo_weight_supported(in_channels, kernel_h, kernel_w, bits))
-    return halo_prepared_words(out_channels, in_channels, kernel_h, kernel_w, bits);
-  if (gemm_conv_weight_supported(in_channels, kernel_h, kernel_w, bits))
-    return gemm_conv_prepared_words(out_channels, in_channels, kernel_h, kernel_w, bits);
-  return 0;
+  return halo_part_words(out_channels, in_channels, kernel_h, kernel_w, bits) +
+         gemm_part_words(out_channels, in_channels, kernel_h, kernel_w, bits);
 }
 
 extern "C" int dimq_conv2d_prepare_weight(const uint8_t* packed_w, int64_t packed_numel, int bits,
                                           int64_t out_channels, int64_t in_channels, int64_t kernel_h,
                                           int64_t kernel_w, uint32_t* prepared_w, int64_t prepared_words,
                                           void* stream) {
-  const bool halo = halo_weight_supported(in_channels, kernel_h, kernel_w, bits);
-  if (!halo && !gemm_conv_weight_supported(in_channels, kernel_h, kernel_w, bits))
+  const int64_t hw = halo_part_words(out_channels, in_channels, kernel_h, kernel_w, bits);
+  const int64_t gw = gemm_part_words(out_channels, in_channels, kernel_h, kernel_w, bits);
+  if (hw + gw == 0)
     return set_error(DIMQ_ERR_UNSUPPORTED, "no kernel layout for C=%lld KH=%lld KW=%lld bits=%d",
                      (long long)in_channels, (long long)kernel_h, (long long)kernel_w, bits);
   DIMQ_CHECK(out_channels > 0, "channel counts must be positive");
   const int64_t wnumel = out_channels * in_channels * kernel_h * kernel_w;
   DIMQ_CHECK(packed_numel >= (wnumel * bits + 7) / 8, "packed_weight is too small for requested conv weight shape");
-  const int64_t need = halo ? halo_prepared_words(out_channels, in_channels, kernel_h, kernel_w, bits)
-                            : gemm_conv_prepared_words(out_channels, in_channels, kernel_h, kernel_w, bits);
-  DIMQ_CHECK(prepared_words >= need, "prepared weight buffer is too small");
-  if (!halo)
+  DIMQ_CHECK(prepared_words >= hw + gw, "prepared weight buffer is too small");
+  if (hw) {
+    const int rc = launch_prepare(packed_w, out_channels, in_channels, kernel_h, kernel_w, bits, prepared_w,
+                                  as_stream(stream));
+    if (rc != DIMQ_OK) return rc;
+  }
+  if (gw)
     return launch_prepare_tapmajor(packed_w, packed_numel, out_channels, in_channels, kernel_h, kernel_w, bits,
-                                   prepared_w, as_stream(stream));
-  return launch_prepare(packed_w, out_channels, in_channels, kernel_h, kernel_w, bits, prepared_w,
-                        as_stream(stream));
+                                   prepared_w + hw, as_stream(stream));
+  return DIMQ_OK;
 }
 
 extern "C" int dimq_conv2d_codebook(const void* x, int x_dtype, int x_layout, int64_t B, int64_t C, int64_t H,
@@ -250,21 +269,17 @@ extern "C" int dimq_conv2d_codebook(const void* x, int x_dtype, int x_layout, in
   DIMQ_CHECK(packed_numel >= (wnumel * bits + 7) / 8, "packed_weight is too small for requested conv weight shape");
   DIMQ_CHECK(variant >= DIMQ_VARIANT_AUTO && variant <= DIMQ_VARIANT_MFMA, "unknown kernel variant %d", variant);
   if (s.B * s.OC * s.OH * s.OW == 0) return DIMQ_OK;
-  if (prepared_w != nullptr && variant != DIMQ_VARIANT_SMALL_M && aligned(x, 16) &&
-      halo_eligible(s.C, s.KH, s.KW, s.sh, s.sw, s.dh, s.dw, s.groups, s.OH, s.OW, bits, x_dtype)) {
-    DIMQ_CHECK(prepared_words >= halo_prepared_words(s.OC, s.C, s.KH, s.KW, bits),
-               "prepared weight buffer is too small");
-    return launch_conv_halo(x, x_dtype, x_layout, s.B, s.C, s.H, s.W, prepared_w, bits, codebook, cb_dtype, cb_rows,
-                            cb_size, bias, bias_dtype, s.OC, s.KH, s.KW, s.sh, s.ph, s.pw, s.OH, s.OW, y, y_dtype,
-                            y_layout, as_stream(stream));
-  }
-  if (prepared_w != nullptr && variant != DIMQ_VARIANT_SMALL_M && s.groups == 1 &&
-      gemm_conv_weight_supported(s.C, s.KH, s.KW, bits) && x_layout == DIMQ_NHWC && y_layout == DIMQ_NHWC &&
-      (x_dtype == DIMQ_F16 || x_dtype == DIMQ_BF16) && aligned(x, 16) && aligned(prepared_w, 16)) {
-    DIMQ_CHECK(prepared_words >= gemm_conv_prepared_words(s.OC, s.C, s.KH, s.KW, bits),
-               "prepared weight buffer is too small");
-    GemmArgs p = conv_args(s, x, x_layout, reinterpret_cast<const uint8_t*>(prepared_w), codebook, cb_dtype, cb_rows,
-                           cb_size, bias, bias_dtype, y, y_dtype, y_layout);
+  const int64_t hw = prepared_w ? halo_part_words(s.OC, s.C, s.KH, s.KW, bits) : 0;
+  const int64_t gw = prepared_w ? gemm_part_words(s.OC, s.C, s.KH, s.KW, bits) : 0;
+  if (prepared_w != nullptr) DIMQ_CHECK(prepared_words >= hw + gw, "prepared weight buffer is too small");
+  const bool gemm_ok = gw > 0 && variant != DIMQ_VARIANT_SMALL_M && s.groups == 1 && x_layout == DIMQ_NHWC &&
+                       y_layout == DIMQ_NHWC && (x_dtype == DIMQ_F16 || x_dtype == DIMQ_BF16) && aligned(x, 16) &&
+                       aligned(y, 16) && aligned(prepared_w + hw, 16);
+  const bool halo_ok = hw > 0 && variant != DIMQ_VARIANT_SMALL_M && aligned(x, 16) &&
+                       halo_eligible(s.C, s.KH, s.KW, s.sh, s.sw, s.dh, s.dw, s.groups, s.OH, s.OW, bits, x_dtype);
+  if (gemm_ok && (!halo_ok || prefer_gemm_conv(s.C, s.KH, s.KW, s.sh))) {
+    GemmArgs p = conv_args(s, x, x_layout, reinterpret_cast<const uint8_t*>(prepared_w + hw), codebook, cb_dtype,
+                           cb_rows, cb_size, bias, bias_dtype, y, y_dtype, y_layout);
     p.ldy = s.OC;
     const int tile = gemm_conv_tile(p.M, p.N);
     switch (bits) {
@@ -272,6 +287,11 @@ extern "C" int dimq_conv2d_codebook(const void* x, int x_dtype, int x_layout, in
       case 3: return launch_big_conv_b3(p, x_dtype, tile, as_stream(stream));
       default: return launch_big_conv_b4(p, x_dtype, tile, as_stream(stream));
     }
+  }
+  if (halo_ok) {
+    return launch_conv_halo(x, x_dtype, x_layout, s.B, s.C, s.H, s.W, prepared_w, bits, codebook, cb_dtype, cb_rows,
+                            cb_size, bias, bias_dtype, s.OC, s.KH, s.KW, s.sh, s.ph, s.pw, s.OH, s.OW, y, y_dtype,
+                            y_layout, as_stream(stream));
   }
   if (variant != DIMQ_VARIANT_SMALL_M &&
       stem_eligible(s.C, s.OC, s.KH, s.KW, s.sh, s.sw, s.pw, s.dh, s.dw, s.groups, s.OH, s.OW, bits, y_dtype, x, y)) {

@@ -473,9 +473,13 @@ def test_graph_replay_matches_eager(gpu):
     dict(B=3, C=64, H=20, W=12, OC=192, K=3, s=1, bits=4, dt=torch.float16),   # 3 channel blocks, odd bands
 ])
 @pytest.mark.parametrize("layout", ["nchw", "nhwc"])
-def test_conv2d_halo_prepared_vs_oracle(gpu, case, layout):
+@pytest.mark.parametrize("path", ["auto", "halo"])
+def test_conv2d_halo_prepared_vs_oracle(gpu, case, layout, path, monkeypatch):
+    """path "halo" keeps NHWC calls of C >= 128 / 1x1 layers on the LDS-halo kernel (auto: implicit GEMM)."""
+    if path == "halo":
+        monkeypatch.setenv("DIMQ_CONV_PATH", "halo")
     ops = _ops()
-    announce(f"conv halo {case} {layout}")
+    announce(f"conv halo {case} {layout} {path}")
     g = _gen(case["C"] + case["OC"] * 3 + case["bits"] + case["s"])
     K = case["K"]
     pad = K // 2

@@ -47,9 +47,11 @@ def test_library_exports_every_declared_symbol(capi):
 def test_host_only_entry_points(capi):
     lib = capi.lib
     assert lib.dimq_abi_version() == 1
-    # kernel-layout words: OC * 2 lane groups * ceil(T/4) words-groups * bits, T = KH*KW*C/16
-    assert lib.dimq_conv2d_prepared_words(64, 64, 3, 3, 2) == 64 * 2 * 9 * 2
-    assert lib.dimq_conv2d_prepared_words(128, 128, 1, 1, 4) == 128 * 2 * 2 * 4
+    # LDS-halo layout words: OC * 2 lane groups * ceil(T/4) words-groups * bits, T = KH*KW*C/16,
+    # followed by the tap-major layout: OC * C * KH * KW * bits / 32
+    assert lib.dimq_conv2d_prepared_words(64, 64, 3, 3, 2) == 64 * 2 * 9 * 2 + 64 * 64 * 9 * 2 // 32
+    assert lib.dimq_conv2d_prepared_words(128, 128, 1, 1, 4) == 128 * 2 * 2 * 4 + 128 * 128 * 4 // 32
+    assert lib.dimq_conv2d_prepared_words(3, 64, 1, 1, 3) == 20 + 3 * 64 * 3 // 32  # halo part 18 -> 20 words
     assert lib.dimq_conv2d_prepared_words(64, 64, 3, 3, 8) == 0      # bits without a kernel layout
     assert lib.dimq_conv2d_prepared_words(64, 48, 3, 3, 2) == 0      # channels without a kernel layout
     assert lib.dimq_conv2d_prepared_words(64, 64, 5, 5, 2) == 64 * 64 * 25 * 2 // 32   # tap-major GEMM layout

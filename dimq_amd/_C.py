@@ -67,6 +67,11 @@ _SIGS = {
     "dimq_conv2d_prepare_weight": (_int, [_vp, _i64, _int, _i64, _i64, _i64, _i64, _vp, _i64, _vp]),
     "dimq_conv2d_codebook": (_int, [_vp, _int, _int, _i64, _i64, _i64, _i64, _vp, _i64, _int, _vp, _i64, _vp, _int,
                                     _i64, _i64, _vp, _int] + [_i64] * 10 + [_vp, _int, _int, _int, _vp]),
+    "dimq_linear_codebook_ex": (_int, [_vp, _int, _i64, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _vp, _int,
+                                       _i64, _vp, _int, _vp, _int, _int, _int, _vp]),
+    "dimq_conv2d_codebook_ex": (_int, [_vp, _int, _int, _i64, _i64, _i64, _i64, _vp, _i64, _int, _vp, _i64, _vp,
+                                       _int, _i64, _i64, _vp, _int] + [_i64] * 10 +
+                                [_vp, _int, _int, _vp, _int, _int, _int, _vp]),
 }
 
 for _name, (_res, _args) in _SIGS.items():
@@ -300,7 +305,21 @@ def _cb_shape(codebook: torch.Tensor, n: int):
     raise RuntimeError("codebook must be [K] (per layer) or [out_features, K] (per channel)")
 
 
-def linear_codebook_impl(x, packed_w, codebook, bits, bias, out_features, in_features, out_dtype=None, variant=0):
+def _residual_args(residual: torch.Tensor | None, y: torch.Tensor, mf=torch.contiguous_format):
+    """Residual of the fused epilogue: y's shape, moved into y's memory order."""
+    if residual is None:
+        return None, None, F32
+    _require_cuda(residual, "residual must be CUDA when provided")
+    if tuple(residual.shape) != tuple(y.shape):
+        raise RuntimeError(f"residual shape {tuple(residual.shape)} must equal the output shape {tuple(y.shape)}")
+    if not residual.is_floating_point():
+        raise RuntimeError("residual must be floating point")
+    r = residual.contiguous(memory_format=mf)
+    return r, _ptr(r), _dtype(r)
+
+
+def linear_codebook_impl(x, packed_w, codebook, bits, bias, out_features, in_features, out_dtype=None, variant=0,
+                         residual=None, activation=0):
     _require_cuda(x, "linear_codebook expects CUDA input")
     _require_cuda(packed_w, "linear_codebook expects CUDA packed_weight")
     _require_cuda(codebook, "linear_codebook expects CUDA codebook")
@@ -316,10 +335,14 @@ def linear_codebook_impl(x, packed_w, codebook, bits, bias, out_features, in_fea
     odt = x.dtype if out_dtype is None else out_dtype
     M = xc.numel() // in_features if in_features else 0
     y = torch.empty((M, out_features), dtype=odt, device=xc.device)
+    if residual is not None and tuple(residual.shape) != (*x.shape[:-1], out_features):
+        raise RuntimeError(f"residual shape {tuple(residual.shape)} must equal the output shape "
+                           f"{(*x.shape[:-1], out_features)}")
+    r, rp, rdt = _residual_args(None if residual is None else residual.reshape(M, out_features), y)
     with torch.cuda.device(xc.device):
-        _check(lib.dimq_linear_codebook(_ptr(xc), _dtype(xc), M, in_features, _ptr(pw), pw.numel(), int(bits),
-                                        _ptr(cb), _dtype(cb), rows, size, bp, bdt, out_features, _ptr(y), _dtype(y),
-                                        int(variant), _stream(xc.device)))
+        _check(lib.dimq_linear_codebook_ex(_ptr(xc), _dtype(xc), M, in_features, _ptr(pw), pw.numel(), int(bits),
+                                           _ptr(cb), _dtype(cb), rows, size, bp, bdt, out_features, _ptr(y),
+                                           _dtype(y), rp, rdt, int(activation), int(variant), _stream(xc.device)))
     return y.view(*x.shape[:-1], out_features)
 
 
@@ -344,7 +367,7 @@ def prepared_conv_words(out_channels, in_channels, kernel_h, kernel_w, bits) -> 
 
 def conv2d_codebook_impl(x, packed_w, codebook, bits, bias, out_channels, in_channels_per_group, kernel_h, kernel_w,
                          stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w, groups, out_dtype=None, variant=0,
-                         prepared_w=None):
+                         prepared_w=None, residual=None, activation=0):
     _require_cuda(x, "conv2d_codebook expects CUDA input")
     if x.dim() != 4:
         raise RuntimeError("conv2d_codebook expects a 4-D input")
@@ -375,11 +398,13 @@ def conv2d_codebook_impl(x, packed_w, codebook, bits, bias, out_channels, in_cha
         prep_ptr, prep_words = _ptr(prep), prep.numel()
     else:
         prep_ptr, prep_words = None, 0
+    r, rp, rdt = _residual_args(residual, y, mf)
     with torch.cuda.device(xc.device):
-        _check(lib.dimq_conv2d_codebook(_ptr(xc), _dtype(xc), layout, B, C, H, W, _ptr(pw), pw.numel(), int(bits),
-                                        prep_ptr, prep_words, _ptr(cb), _dtype(cb), rows, size, bp, bdt, out_channels, kernel_h, kernel_w,
-                                        stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w, groups, _ptr(y),
-                                        _dtype(y), layout, int(variant), _stream(xc.device)))
+        _check(lib.dimq_conv2d_codebook_ex(_ptr(xc), _dtype(xc), layout, B, C, H, W, _ptr(pw), pw.numel(), int(bits),
+                                           prep_ptr, prep_words, _ptr(cb), _dtype(cb), rows, size, bp, bdt,
+                                           out_channels, kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w,
+                                           dilation_h, dilation_w, groups, _ptr(y), _dtype(y), layout, rp, rdt,
+                                           int(activation), int(variant), _stream(xc.device)))
     return y
 
 
@@ -409,12 +434,14 @@ _SCHEMAS = {
     "build_product_table_grouped": ("build_product_table_grouped(Tensor codebook, float act_scale, int act_zp) "
                                     "-> Tensor", build_product_table_grouped_impl),
     "linear_codebook": ("linear_codebook(Tensor x, Tensor packed_w, Tensor codebook, int bits, Tensor? bias, "
-                        "int out_features, int in_features, ScalarType? out_dtype=None, int variant=0) -> Tensor",
+                        "int out_features, int in_features, ScalarType? out_dtype=None, int variant=0, "
+                        "Tensor? residual=None, int activation=0) -> Tensor",
                         linear_codebook_impl),
     "conv2d_codebook": ("conv2d_codebook(Tensor x, Tensor packed_w, Tensor codebook, int bits, Tensor? bias, "
                         "int out_channels, int in_channels_per_group, int kernel_h, int kernel_w, int stride_h, "
                         "int stride_w, int pad_h, int pad_w, int dilation_h, int dilation_w, int groups, "
-                        "ScalarType? out_dtype=None, int variant=0, Tensor? prepared_w=None) -> Tensor",
+                        "ScalarType? out_dtype=None, int variant=0, Tensor? prepared_w=None, Tensor? residual=None, "
+                        "int activation=0) -> Tensor",
                         conv2d_codebook_impl),
     "prepare_conv_weight": ("prepare_conv_weight(Tensor packed_w, int bits, int out_channels, int in_channels, "
                             "int kernel_h, int kernel_w) -> Tensor", prepare_conv_weight_impl),

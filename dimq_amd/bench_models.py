@@ -42,8 +42,11 @@ class _Attention(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         b, n, d = x.shape
         h = self.heads
-        qkv = self.qkv(x).reshape(b, n, 3, h, d // h).permute(2, 0, 3, 1, 4)
-        q, k, v = (t.contiguous() for t in qkv.unbind(0))
+        # q, k, v stay strided views of the qkv output (head dim contiguous): the
+        # attention kernel takes them as they are and returns o in (b, n, h, d)
+        # memory order, so neither side needs a copy
+        qkv = self.qkv(x).view(b, n, 3, h, d // h)
+        q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
         o = F.scaled_dot_product_attention(q, k, v)
         return self.proj(o.transpose(1, 2).reshape(b, n, d))
 

@@ -87,6 +87,57 @@ __device__ __forceinline__ void store_from_float(void* p, int dt, int64_t i, flo
   }
 }
 
+// ---------------------------------------------------------------- fused epilogue
+// Weight-only ops: y = act(v + residual[off]) with the residual in y's shape
+// and memory order; a zero-initialised Epi is no residual, no activation.
+struct Epi {
+  const void* res;
+  int res_dt;
+  int act;      // enum dimq_activation
+  int res_vec;  // residual 16-byte aligned: vector loads where y's stores are
+};
+
+__device__ __forceinline__ float act_apply(float v, int act) {
+  if (act == DIMQ_ACT_RELU) return v < 0.0f ? 0.0f : v;  // NaN passes, as torch.relu
+  if (act == DIMQ_ACT_GELU) return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+  return v;
+}
+
+__device__ __forceinline__ float epi1(const Epi& e, int64_t off, float v) {
+  if (e.res) v += load_as_float(e.res, e.res_dt, off);
+  return act_apply(v, e.act);
+}
+
+// N (a multiple of 4) consecutive outputs starting at off; vec: off % 4 == 0.
+template <int N>
+__device__ __forceinline__ void epiN(const Epi& e, int64_t off, float (&v)[N], bool vec) {
+  if (e.res) {
+    if (vec && e.res_vec && e.res_dt == DIMQ_F32) {
+#pragma unroll
+      for (int q = 0; q < N / 4; ++q) {
+        const float4 r = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(e.res) + off + 4 * q);
+        v[4 * q] += r.x; v[4 * q + 1] += r.y; v[4 * q + 2] += r.z; v[4 * q + 3] += r.w;
+      }
+    } else if (vec && e.res_vec && (e.res_dt == DIMQ_F16 || e.res_dt == DIMQ_BF16)) {
+#pragma unroll
+      for (int q = 0; q < N / 4; ++q) {
+        const uint2 r = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(e.res) + off + 4 * q);
+        const uint32_t h[4] = {r.x & 0xffffu, r.x >> 16, r.y & 0xffffu, r.y >> 16};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          v[4 * q + i] += e.res_dt == DIMQ_F16 ? f16_bits_to_float(h[i]) : bf16_bits_to_float(h[i]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; ++i) v[i] += load_as_float(e.res, e.res_dt, off + i);
+    }
+  }
+  if (e.act) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = act_apply(v[i], e.act);
+  }
+}
+
 // u4 activation code: clamp(rint(x / s) + zp, 0, 15), IEEE divide
 // (dimq_backend/reference.py:11-21).
 __device__ __forceinline__ int quantize_u4(float x, float s, int zp) {

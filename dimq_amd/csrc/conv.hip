@@ -242,11 +242,28 @@ extern "C" int dimq_conv2d_prepare_weight(const uint8_t* packed_w, int64_t packe
 
 extern "C" int dimq_conv2d_codebook(const void* x, int x_dtype, int x_layout, int64_t B, int64_t C, int64_t H,
                                     int64_t W, const uint8_t* packed_w, int64_t packed_numel, int bits,
-                                    const uint32_t* prepared_w, int64_t prepared_words, const void* codebook, int cb_dtype, int64_t cb_rows, int64_t cb_size,
-                                    const void* bias, int bias_dtype, int64_t out_channels, int64_t kernel_h,
-                                    int64_t kernel_w, int64_t stride_h, int64_t stride_w, int64_t pad_h,
-                                    int64_t pad_w, int64_t dilation_h, int64_t dilation_w, int64_t groups, void* y,
-                                    int y_dtype, int y_layout, int variant, void* stream) {
+                                    const uint32_t* prepared_w, int64_t prepared_words, const void* codebook,
+                                    int cb_dtype, int64_t cb_rows, int64_t cb_size, const void* bias, int bias_dtype,
+                                    int64_t out_channels, int64_t kernel_h, int64_t kernel_w, int64_t stride_h,
+                                    int64_t stride_w, int64_t pad_h, int64_t pad_w, int64_t dilation_h,
+                                    int64_t dilation_w, int64_t groups, void* y, int y_dtype, int y_layout,
+                                    int variant, void* stream) {
+  return dimq_conv2d_codebook_ex(x, x_dtype, x_layout, B, C, H, W, packed_w, packed_numel, bits, prepared_w,
+                                 prepared_words, codebook, cb_dtype, cb_rows, cb_size, bias, bias_dtype,
+                                 out_channels, kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w, dilation_h,
+                                 dilation_w, groups, y, y_dtype, y_layout, nullptr, 0, DIMQ_ACT_NONE, variant,
+                                 stream);
+}
+
+extern "C" int dimq_conv2d_codebook_ex(const void* x, int x_dtype, int x_layout, int64_t B, int64_t C, int64_t H,
+                                       int64_t W, const uint8_t* packed_w, int64_t packed_numel, int bits,
+                                       const uint32_t* prepared_w, int64_t prepared_words, const void* codebook,
+                                       int cb_dtype, int64_t cb_rows, int64_t cb_size, const void* bias,
+                                       int bias_dtype, int64_t out_channels, int64_t kernel_h, int64_t kernel_w,
+                                       int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                                       int64_t dilation_h, int64_t dilation_w, int64_t groups, void* y, int y_dtype,
+                                       int y_layout, const void* residual, int residual_dtype, int activation,
+                                       int variant, void* stream) {
   if (!(bits == 2 || bits == 3 || bits == 4 || bits == 8))
     return set_error(DIMQ_ERR_UNSUPPORTED, "bits must be one of 2, 3, 4, 8 (got %d)", bits);
   DIMQ_CHECK(x_dtype == DIMQ_F32 || x_dtype == DIMQ_F16 || x_dtype == DIMQ_BF16,
@@ -268,6 +285,9 @@ extern "C" int dimq_conv2d_codebook(const void* x, int x_dtype, int x_layout, in
   const int64_t wnumel = s.OC * s.ICg * s.KH * s.KW;
   DIMQ_CHECK(packed_numel >= (wnumel * bits + 7) / 8, "packed_weight is too small for requested conv weight shape");
   DIMQ_CHECK(variant >= DIMQ_VARIANT_AUTO && variant <= DIMQ_VARIANT_MFMA, "unknown kernel variant %d", variant);
+  DIMQ_CHECK(residual == nullptr || is_float_dtype(residual_dtype), "residual must be floating point");
+  DIMQ_CHECK(activation >= DIMQ_ACT_NONE && activation <= DIMQ_ACT_GELU, "unknown activation %d", activation);
+  const Epi epi{residual, residual_dtype, activation, residual != nullptr && aligned(residual, 16)};
   if (s.B * s.OC * s.OH * s.OW == 0) return DIMQ_OK;
   const int64_t hw = prepared_w ? halo_part_words(s.OC, s.C, s.KH, s.KW, bits) : 0;
   const int64_t gw = prepared_w ? gemm_part_words(s.OC, s.C, s.KH, s.KW, bits) : 0;
@@ -281,6 +301,7 @@ extern "C" int dimq_conv2d_codebook(const void* x, int x_dtype, int x_layout, in
     GemmArgs p = conv_args(s, x, x_layout, reinterpret_cast<const uint8_t*>(prepared_w + hw), codebook, cb_dtype,
                            cb_rows, cb_size, bias, bias_dtype, y, y_dtype, y_layout);
     p.ldy = s.OC;
+    p.epi = epi;
     const int tile = gemm_conv_tile(p.M, p.N);
     switch (bits) {
       case 2: return launch_big_conv_b2(p, x_dtype, tile, as_stream(stream));
@@ -291,16 +312,17 @@ extern "C" int dimq_conv2d_codebook(const void* x, int x_dtype, int x_layout, in
   if (halo_ok) {
     return launch_conv_halo(x, x_dtype, x_layout, s.B, s.C, s.H, s.W, prepared_w, bits, codebook, cb_dtype, cb_rows,
                             cb_size, bias, bias_dtype, s.OC, s.KH, s.KW, s.sh, s.ph, s.pw, s.OH, s.OW, y, y_dtype,
-                            y_layout, as_stream(stream));
+                            y_layout, epi, as_stream(stream));
   }
   if (variant != DIMQ_VARIANT_SMALL_M &&
       stem_eligible(s.C, s.OC, s.KH, s.KW, s.sh, s.sw, s.pw, s.dh, s.dw, s.groups, s.OH, s.OW, bits, y_dtype, x, y)) {
     return launch_conv_stem(x, x_dtype, x_layout, s.B, s.C, s.H, s.W, packed_w, packed_numel, bits, codebook,
                             cb_dtype, cb_rows, cb_size, bias, bias_dtype, s.OC, s.KH, s.KW, s.ph, s.pw, s.OH, s.OW,
-                            y, y_dtype, y_layout, as_stream(stream));
+                            y, y_dtype, y_layout, epi, as_stream(stream));
   }
   GemmArgs p = conv_args(s, x, x_layout, packed_w, codebook, cb_dtype, cb_rows, cb_size, bias, bias_dtype, y,
                          y_dtype, y_layout);
+  p.epi = epi;
   int tile = gemm_pick_tile(p.M, p.N, variant);
   if (tile == kTileGemv) tile = kTile16x16;  // the GEMV kernel has no im2col/group support
   return gemm_dispatch(p, bits, x_dtype, false, tile, as_stream(stream));

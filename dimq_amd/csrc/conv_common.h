@@ -25,6 +25,7 @@ struct HaloArgs {
   int bias_dt;
   void* y;
   int y_dt, y_layout;
+  Epi epi;  // fused residual / activation
 };
 
 // Streaming kernel (conv_stream.hip): shapes it runs, LDS bytes, launch.
@@ -37,9 +38,11 @@ __device__ __forceinline__ uint32_t to_f16_bits(uint32_t raw, int dt) {
   return dt == DIMQ_F16 ? raw : float_to_f16_bits(bf16_bits_to_float(raw));
 }
 
-// Four consecutive outputs of one lane: one 16-byte (fp32) or 8-byte (16-bit)
-// store when `vec`, element stores otherwise.
-__device__ __forceinline__ void store4(void* y, int dt, int64_t off, const float v[4], bool vec) {
+// Four consecutive outputs of one lane, after the fused epilogue: one 16-byte
+// (fp32) or 8-byte (16-bit) store when `vec`, element stores otherwise.
+__device__ __forceinline__ void store4(void* y, int dt, int64_t off, const float vin[4], bool vec, const Epi& e) {
+  float v[4] = {vin[0], vin[1], vin[2], vin[3]};
+  epiN<4>(e, off, v, vec);
   if (vec && dt == DIMQ_F32) {
     *reinterpret_cast<float4*>(reinterpret_cast<float*>(y) + off) = make_float4(v[0], v[1], v[2], v[3]);
   } else if (vec) {
@@ -85,7 +88,7 @@ __device__ __forceinline__ void store_block(const HaloArgs& p, const floatx16& a
 #pragma unroll
       for (int i = 0; i < 4; ++i) v[i] = acc[4 * j + i] * scale + bv;
       if (p.y_layout == DIMQ_NCHW && pix0 + 4 <= P) {
-        store4(p.y, p.y_dt, chan + pix0, v, vec);
+        store4(p.y, p.y_dt, chan + pix0, v, vec, p.epi);
       } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -93,7 +96,7 @@ __device__ __forceinline__ void store_block(const HaloArgs& p, const floatx16& a
             const int64_t off = p.y_layout == DIMQ_NCHW
                                     ? chan + pix0 + i
                                     : ((int64_t)b * ohw + (int64_t)oh0 * p.OW + pix0 + i) * p.OC + ocl;
-            store_from_float(p.y, p.y_dt, off, v[i]);
+            store_from_float(p.y, p.y_dt, off, epi1(p.epi, off, v[i]));
           }
         }
       }
@@ -114,14 +117,14 @@ __device__ __forceinline__ void store_block(const HaloArgs& p, const floatx16& a
       }
       if (pix >= P) continue;
       if (p.y_layout == DIMQ_NHWC && ocb + 4 <= p.OC) {
-        store4(p.y, p.y_dt, pbase * p.OC + ocb, v, vec);
+        store4(p.y, p.y_dt, pbase * p.OC + ocb, v, vec, p.epi);
       } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           if (ocb + i < p.OC) {
             const int64_t off = p.y_layout == DIMQ_NHWC ? pbase * p.OC + ocb + i
                                                         : ((int64_t)b * p.OC + ocb + i) * ohw + (int64_t)oh0 * p.OW + pix;
-            store_from_float(p.y, p.y_dt, off, v[i]);
+            store_from_float(p.y, p.y_dt, off, epi1(p.epi, off, v[i]));
           }
         }
       }

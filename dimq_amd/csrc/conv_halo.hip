@@ -270,7 +270,7 @@ __global__ __launch_bounds__(256) void conv_halo_kernel(const HaloArgs p) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) v[i] = acc[q][4 * j + i] * scale + bv;
           if (p.y_layout == DIMQ_NCHW && pix0 + 4 <= P) {
-            store4(p.y, p.y_dt, chan + pix0, v, vec);
+            store4(p.y, p.y_dt, chan + pix0, v, vec, p.epi);
           } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -278,7 +278,7 @@ __global__ __launch_bounds__(256) void conv_halo_kernel(const HaloArgs p) {
                 const int64_t off = p.y_layout == DIMQ_NCHW
                                         ? chan + pix0 + i
                                         : ((int64_t)b * ohw + (int64_t)oh0 * p.OW + pix0 + i) * p.OC + ocl;
-                store_from_float(p.y, p.y_dt, off, v[i]);
+                store_from_float(p.y, p.y_dt, off, epi1(p.epi, off, v[i]));
               }
             }
           }
@@ -307,14 +307,14 @@ __global__ __launch_bounds__(256) void conv_halo_kernel(const HaloArgs p) {
         for (int i = 0; i < 4; ++i) v[i] = acc[q][4 * j + i] * sc[i] + bv[i];
         const int64_t pbase = (int64_t)b * ohw + (int64_t)oh0 * p.OW + pix;
         if (p.y_layout == DIMQ_NHWC && ocb + 4 <= p.OC) {
-          store4(p.y, p.y_dt, pbase * p.OC + ocb, v, vec);
+          store4(p.y, p.y_dt, pbase * p.OC + ocb, v, vec, p.epi);
         } else {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             if (ocb + i < p.OC) {
               const int64_t off = p.y_layout == DIMQ_NHWC ? pbase * p.OC + ocb + i
                                                           : ((int64_t)b * p.OC + ocb + i) * ohw + (int64_t)oh0 * p.OW + pix;
-              store_from_float(p.y, p.y_dt, off, v[i]);
+              store_from_float(p.y, p.y_dt, off, epi1(p.epi, off, v[i]));
             }
           }
         }
@@ -558,8 +558,9 @@ int launch_conv_halo(const void* x, int x_dtype, int x_layout, int64_t B, int64_
                      const uint32_t* kw, int bits, const void* cb, int cb_dtype, int64_t cb_rows, int64_t cb_size,
                      const void* bias, int bias_dtype, int64_t OC, int64_t KH, int64_t KW, int64_t stride,
                      int64_t ph, int64_t pw, int64_t OH, int64_t OW, void* y, int y_dtype, int y_layout,
-                     hipStream_t s) {
+                     const Epi& epi, hipStream_t s) {
   HaloArgs p{};
+  p.epi = epi;
   p.x = x;
   p.x_dt = x_dtype;
   p.x_layout = x_layout;

@@ -56,6 +56,7 @@ struct StemArgs {
   int bias_dt;
   void* y;
   int y_dt, y_layout;
+  Epi epi;  // fused residual / activation
 };
 
 namespace {
@@ -324,6 +325,7 @@ __global__ __launch_bounds__(kStemThreads, 2) void conv_stem_kernel(const StemAr
             for (int u = 0; u < 8; ++u) v[u] = v[u] * rsc[u] + rbs[u];
             if (pb + px >= P || ch * 8 >= p.OC) continue;
             const int64_t off = (gp0 + px) * p.OC + ch * 8;
+            epiN<8>(p.epi, off, v, true);
             if (p.y_dt == DIMQ_F32) {
               float* yp = reinterpret_cast<float*>(p.y) + off;
               *reinterpret_cast<float4*>(yp) = make_float4(v[0], v[1], v[2], v[3]);
@@ -348,6 +350,7 @@ __global__ __launch_bounds__(kStemThreads, 2) void conv_stem_kernel(const StemAr
             if (lane >= p.OC) continue;
             const int px0 = 8 * it;
             if (vec_nchw && pb + px0 + 8 <= P) {
+              epiN<8>(p.epi, cbase + px0, v, true);
               if (p.y_dt == DIMQ_F32) {
                 float* yp = reinterpret_cast<float*>(p.y) + cbase + px0;
                 *reinterpret_cast<float4*>(yp) = make_float4(v[0], v[1], v[2], v[3]);
@@ -363,7 +366,7 @@ __global__ __launch_bounds__(kStemThreads, 2) void conv_stem_kernel(const StemAr
             } else {
 #pragma unroll
               for (int u = 0; u < 8; ++u)
-                if (pb + px0 + u < P) store_from_float(p.y, p.y_dt, cbase + px0 + u, v[u]);
+                if (pb + px0 + u < P) store_from_float(p.y, p.y_dt, cbase + px0 + u, epi1(p.epi, cbase + px0 + u, v[u]));
             }
           }
         }
@@ -420,7 +423,7 @@ int launch_conv_stem(const void* x, int x_dtype, int x_layout, int64_t B, int64_
                      const uint8_t* w, int64_t w_bytes, int bits, const void* cb, int cb_dtype, int64_t cb_rows,
                      int64_t cb_size, const void* bias, int bias_dtype, int64_t OC, int64_t KH, int64_t KW,
                      int64_t ph, int64_t pw, int64_t OH, int64_t OW, void* y, int y_dtype, int y_layout,
-                     hipStream_t s) {
+                     const Epi& epi, hipStream_t s) {
   const int np = stem_np(KW, pw);
   StemArgs p{};
   p.x = x;
@@ -452,6 +455,7 @@ int launch_conv_stem(const void* x, int x_dtype, int x_layout, int64_t B, int64_
   p.y = y;
   p.y_dt = y_dtype;
   p.y_layout = y_layout;
+  p.epi = epi;
 
   // two work-groups per CU, as many rounds as needed, whole multiple of 8 work-groups
   const int64_t slots = 2LL * device_cu_count();

@@ -81,8 +81,9 @@ int gemm_dispatch(const GemmArgs& p, int bits, int xt, bool a4, int tile, hipStr
 int linear_codebook_impl(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed_w,
                          int bits, const void* codebook, int cb_dtype, int64_t cb_rows, int64_t cb_size,
                          const void* bias, int bias_dtype, int64_t N, void* y, int y_dtype, int64_t ldy,
-                         int variant, hipStream_t s) {
+                         const Epi& epi, int variant, hipStream_t s) {
   GemmArgs p{};
+  p.epi = epi;
   p.x = x;
   p.M = M;
   p.K = K;
@@ -136,6 +137,15 @@ extern "C" int dimq_linear_codebook(const void* x, int x_dtype, int64_t M, int64
                                     int64_t packed_numel, int bits, const void* codebook, int cb_dtype,
                                     int64_t cb_rows, int64_t cb_size, const void* bias, int bias_dtype, int64_t N,
                                     void* y, int y_dtype, int variant, void* stream) {
+  return dimq_linear_codebook_ex(x, x_dtype, M, K, packed_w, packed_numel, bits, codebook, cb_dtype, cb_rows, cb_size,
+                                 bias, bias_dtype, N, y, y_dtype, nullptr, 0, DIMQ_ACT_NONE, variant, stream);
+}
+
+extern "C" int dimq_linear_codebook_ex(const void* x, int x_dtype, int64_t M, int64_t K, const uint8_t* packed_w,
+                                       int64_t packed_numel, int bits, const void* codebook, int cb_dtype,
+                                       int64_t cb_rows, int64_t cb_size, const void* bias, int bias_dtype, int64_t N,
+                                       void* y, int y_dtype, const void* residual, int residual_dtype,
+                                       int activation, int variant, void* stream) {
   if (!(bits == 2 || bits == 3 || bits == 4 || bits == 8))
     return set_error(DIMQ_ERR_UNSUPPORTED, "bits must be one of 2, 3, 4, 8 (got %d)", bits);
   DIMQ_CHECK(x_dtype == DIMQ_F32 || x_dtype == DIMQ_F16 || x_dtype == DIMQ_BF16,
@@ -149,8 +159,11 @@ extern "C" int dimq_linear_codebook(const void* x, int x_dtype, int64_t M, int64
   DIMQ_CHECK(cb_size >= 1 && cb_size <= (1 << bits), "codebook rows must hold between 1 and 2^bits entries");
   DIMQ_CHECK(packed_numel >= (N * K * bits + 7) / 8, "packed_weight is too small for out_features * in_features");
   DIMQ_CHECK(variant >= DIMQ_VARIANT_AUTO && variant <= DIMQ_VARIANT_MFMA, "unknown kernel variant %d", variant);
+  DIMQ_CHECK(residual == nullptr || is_float_dtype(residual_dtype), "residual must be floating point");
+  DIMQ_CHECK(activation >= DIMQ_ACT_NONE && activation <= DIMQ_ACT_GELU, "unknown activation %d", activation);
+  const Epi epi{residual, residual_dtype, activation, residual != nullptr && aligned(residual, 16)};
   return linear_codebook_impl(x, x_dtype, M, K, K, packed_w, bits, codebook, cb_dtype, cb_rows, cb_size, bias,
-                              bias_dtype, N, y, y_dtype, N, variant, as_stream(stream));
+                              bias_dtype, N, y, y_dtype, N, epi, variant, as_stream(stream));
 }
 
 extern "C" int dimq_linear_lut(const void* x, int x_dtype, int64_t M, const uint8_t* packed_w, int64_t packed_numel,

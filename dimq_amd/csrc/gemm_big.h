@@ -336,6 +336,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_big_kernel(const GemmArgs
         for (int i = 0; i < 4; ++i) v[i] = acc[mb][nb][4 * j + i] * sc[i] + bv[i];
         const int64_t off = m * p.ldy + n;
         if (vec && n + 4 <= p.N) {
+          epiN<4>(p.epi, off, v, true);
           if (p.y_dt == DIMQ_F32) {
             *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.y) + off) = make_float4(v[0], v[1], v[2], v[3]);
           } else {
@@ -348,7 +349,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_big_kernel(const GemmArgs
         } else {
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            if (n + i < p.N) store_from_float(p.y, p.y_dt, off + i, v[i]);
+            if (n + i < p.N) store_from_float(p.y, p.y_dt, off + i, epi1(p.epi, off + i, v[i]));
         }
       }
     }
@@ -530,6 +531,7 @@ __global__ __launch_bounds__(256) void gemm_deep_kernel(const GemmArgs p) {
       for (int i = 0; i < 4; ++i) v[i] = acc[mb][4 * j + i] * sc[i] + bv[i];
       const int64_t off = m * p.ldy + n;
       if (vec && n + 4 <= p.N) {
+        epiN<4>(p.epi, off, v, true);
         if (p.y_dt == DIMQ_F32) {
           *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.y) + off) = make_float4(v[0], v[1], v[2], v[3]);
         } else {
@@ -542,7 +544,7 @@ __global__ __launch_bounds__(256) void gemm_deep_kernel(const GemmArgs p) {
       } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (n + i < p.N) store_from_float(p.y, p.y_dt, off + i, v[i]);
+          if (n + i < p.N) store_from_float(p.y, p.y_dt, off + i, epi1(p.epi, off + i, v[i]));
       }
     }
   }

@@ -50,6 +50,7 @@ struct GemmArgs {
   int64_t cB, cC, cH, cW, cOH, cOW, cOC, cICg;
   int cKH, cKW, csh, csw, cph, cpw, cdh, cdw;
   int groups;  // grid z (1 for Linear)
+  Epi epi;     // fused residual / activation (weight-only ops)
 };
 
 // Output element offset of (row m, global column n).
@@ -400,7 +401,10 @@ __global__ __launch_bounds__(256) void gemm_cb_kernel(const GemmArgs p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int64_t m = m0 + mb * 16 + 4 * g + i;
-        if (m < p.M) store_from_float(p.y, p.y_dt, out_offset(p, m, nz + n), acc[mb][nb][i] * colscale[nb] + b);
+        if (m < p.M) {
+          const int64_t o = out_offset(p, m, nz + n);
+          store_from_float(p.y, p.y_dt, o, epi1(p.epi, o, acc[mb][nb][i] * colscale[nb] + b));
+        }
       }
     }
   }
@@ -552,7 +556,10 @@ __global__ __launch_bounds__(256) void gemm_cb8_kernel(const GemmArgs p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int64_t m = m0 + mb * 16 + 4 * g + i;
-        if (m < p.M) store_from_float(p.y, p.y_dt, out_offset(p, m, nz + n), acc[mb][nb][i] * sc + b);
+        if (m < p.M) {
+          const int64_t o = out_offset(p, m, nz + n);
+          store_from_float(p.y, p.y_dt, o, epi1(p.epi, o, acc[mb][nb][i] * sc + b));
+        }
       }
     }
   }
@@ -619,7 +626,7 @@ __global__ __launch_bounds__(WPW * 64) void gemv_cb_kernel(const GemmArgs p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int64_t m = 4 * g + i;
-        if (m < p.M) store_from_float(p.y, p.y_dt, m * p.ldy + n, t[i] * colscale + b);
+        if (m < p.M) store_from_float(p.y, p.y_dt, m * p.ldy + n, epi1(p.epi, m * p.ldy + n, t[i] * colscale + b));
       }
     }
   }
@@ -837,7 +844,7 @@ __global__ __launch_bounds__(256) void gemm_fast_kernel(const GemmArgs p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int64_t m = m0 + mb * 16 + 4 * g + i;
-        if (m < p.M) store_from_float(p.y, p.y_dt, m * p.ldy + n, acc[mb][nb][i] * colscale[nb] + b);
+        if (m < p.M) store_from_float(p.y, p.y_dt, m * p.ldy + n, epi1(p.epi, m * p.ldy + n, acc[mb][nb][i] * colscale[nb] + b));
       }
     }
   }
@@ -869,7 +876,7 @@ int launch_conv_halo(const void* x, int x_dtype, int x_layout, int64_t B, int64_
                      const uint32_t* kw, int bits, const void* cb, int cb_dtype, int64_t cb_rows, int64_t cb_size,
                      const void* bias, int bias_dtype, int64_t OC, int64_t KH, int64_t KW, int64_t stride,
                      int64_t ph, int64_t pw, int64_t OH, int64_t OW, void* y, int y_dtype, int y_layout,
-                     hipStream_t s);
+                     const Epi& epi, hipStream_t s);
 int launch_prepare(const uint8_t* src, int64_t OC, int64_t C, int64_t KH, int64_t KW, int bits, uint32_t* out,
                    hipStream_t s);
 
@@ -881,7 +888,7 @@ int launch_conv_stem(const void* x, int x_dtype, int x_layout, int64_t B, int64_
                      const uint8_t* w, int64_t w_bytes, int bits, const void* cb, int cb_dtype, int64_t cb_rows,
                      int64_t cb_size, const void* bias, int bias_dtype, int64_t OC, int64_t KH, int64_t KW,
                      int64_t ph, int64_t pw, int64_t OH, int64_t OW, void* y, int y_dtype, int y_layout,
-                     hipStream_t s);
+                     const Epi& epi, hipStream_t s);
 
 // gemm.hip
 int gemm_pick_tile(int64_t M, int64_t N, int variant);

@@ -111,7 +111,7 @@ __global__ __launch_bounds__(1024) void gemv_fast_kernel(const GemmArgs p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int64_t m = 4 * g + i;
-        if (m < p.M) store_from_float(p.y, p.y_dt, m * p.ldy + n0 + col, t[i] * colscale + b);
+        if (m < p.M) store_from_float(p.y, p.y_dt, m * p.ldy + n0 + col, epi1(p.epi, m * p.ldy + n0 + col, t[i] * colscale + b));
       }
     }
   }

@@ -106,11 +106,13 @@ class DIMQCodebookLinear(nn.Module):
         self.out_dtype = out_dtype
         self.variant = variant
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None,
+                activation: str | None = None) -> torch.Tensor:
+        """act(linear(x) + residual); residual and activation ("relu", "gelu") are fused into the kernel."""
         _require_gpu(x, self.packed_weight, True, "DIMQCodebookLinear")
         return ops.dimq_linear_codebook(x, self.packed_weight, self.codebook, self.bits, self.bias,
                                         self.out_features, self.in_features, out_dtype=self.out_dtype,
-                                        variant=self.variant)
+                                        variant=self.variant, residual=residual, activation=activation)
 
     @classmethod
     @torch.no_grad()
@@ -155,7 +157,7 @@ class DIMQCodebookConv2d(nn.Module):
         self._prepared_key = None
 
     def prepared_weight(self) -> torch.Tensor | None:
-        """Kernel-layout copy of packed_weight (conv_halo kernel), built on first use."""
+        """Kernel-layout copies of packed_weight (LDS-halo and tap-major layouts), built on first use."""
         if self.groups != 1:
             return None
         key = (self.packed_weight.data_ptr(), self.packed_weight.device)
@@ -164,12 +166,15 @@ class DIMQCodebookConv2d(nn.Module):
             self._prepared_key = key
         return self._prepared
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None,
+                activation: str | None = None) -> torch.Tensor:
+        """act(conv(x) + residual); residual and activation ("relu", "gelu") are fused into the kernel."""
         _require_gpu(x, self.packed_weight, True, "DIMQCodebookConv2d")
         return ops.dimq_conv2d_codebook(x, self.packed_weight, self.codebook, self.bits, self.bias,
                                         self.weight_shape, self.stride, self.padding, self.dilation, self.groups,
                                         out_dtype=self.out_dtype, variant=self.variant,
-                                        prepared_weight=self.prepared_weight())
+                                        prepared_weight=self.prepared_weight(), residual=residual,
+                                        activation=activation)
 
     @classmethod
     @torch.no_grad()

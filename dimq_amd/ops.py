@@ -103,6 +103,7 @@ def dimq_conv2d_lut(
 # ---------------------------------------------------------------------------
 
 VARIANTS = {"auto": 0, "small_m": 1, "mfma": 2}
+ACTIVATIONS = {None: 0, "none": 0, "relu": 1, "gelu": 2}
 
 
 def pack_bits(indices: torch.Tensor, bits: int) -> torch.Tensor:
@@ -137,12 +138,18 @@ def dimq_linear_codebook(
     *,
     out_dtype: torch.dtype | None = None,
     variant: str = "auto",
+    residual: torch.Tensor | None = None,
+    activation: str | None = None,
 ) -> torch.Tensor:
-    """y = x @ W_hat^T + bias with W_hat[n, k] = codebook[n or 0, idx[n, k]]."""
+    """y = act(x @ W_hat^T + bias + residual) with W_hat[n, k] = codebook[n or 0, idx[n, k]].
+
+    ``residual`` (output shape) and ``activation`` ("relu" or "gelu", exact erf
+    form) are fused into the kernel's store; without them this is the plain
+    weight-only Linear."""
     require_extension()
     return torch.ops.dimq.linear_codebook(
         x, packed_weight, codebook, int(bits), bias, int(out_features), int(in_features), out_dtype,
-        VARIANTS[variant],
+        VARIANTS[variant], residual, ACTIVATIONS[activation],
     )
 
 
@@ -161,11 +168,15 @@ def dimq_conv2d_codebook(
     out_dtype: torch.dtype | None = None,
     variant: str = "auto",
     prepared_weight: torch.Tensor | None = None,
+    residual: torch.Tensor | None = None,
+    activation: str | None = None,
 ) -> torch.Tensor:
     """Weight-only codebook conv2d; NCHW or channels_last input, output in the same memory format.
 
     ``prepared_weight`` (from :func:`prepare_conv_weight`) enables the LDS-halo
-    kernel for the shapes it supports."""
+    and large-tile implicit-GEMM kernels for the shapes they support.
+    ``residual`` (output shape) and ``activation`` ("relu" / "gelu") are fused
+    into the kernel's store: y = act(conv + bias + residual)."""
     require_extension()
     out_channels, cin_per_group, kernel_h, kernel_w = [int(v) for v in weight_shape]
     stride_h, stride_w = _pair(stride)
@@ -173,7 +184,8 @@ def dimq_conv2d_codebook(
     dil_h, dil_w = _pair(dilation)
     return torch.ops.dimq.conv2d_codebook(
         x, packed_weight, codebook, int(bits), bias, out_channels, cin_per_group, kernel_h, kernel_w, stride_h,
-        stride_w, pad_h, pad_w, dil_h, dil_w, int(groups), out_dtype, VARIANTS[variant], prepared_weight,
+        stride_w, pad_h, pad_w, dil_h, dil_w, int(groups), out_dtype, VARIANTS[variant], prepared_weight, residual,
+        ACTIVATIONS[activation],
     )
 
 

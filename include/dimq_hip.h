@@ -44,6 +44,13 @@ enum dimq_status {
 enum dimq_layout { DIMQ_NCHW = 0, DIMQ_NHWC = 1 };
 
 /* Kernel variant selector for the weight-only ops. */
+/* Activation of the fused epilogue of the *_ex weight-only ops. */
+enum dimq_activation {
+  DIMQ_ACT_NONE = 0,
+  DIMQ_ACT_RELU = 1, /* max(v, 0); NaN stays NaN as in torch.relu */
+  DIMQ_ACT_GELU = 2  /* exact: 0.5 v (1 + erf(v / sqrt 2)), torch's F.gelu default */
+};
+
 enum dimq_variant {
   DIMQ_VARIANT_AUTO = 0,
   DIMQ_VARIANT_SMALL_M = 1, /* register-codebook gather, 16-row tiles (decode / GEMV) */
@@ -142,14 +149,19 @@ int dimq_linear_codebook(const void* x, int x_dtype, int64_t M, int64_t K, const
                          int variant, void* stream);
 
 /* Words of the kernel-layout weight of a conv (0 when the shape has no
- * kernel layout: supported are C in {64, 128}, 3x3 or 1x1, bits in {2,3,4}). */
+ * kernel layout).  The prepared weight holds, one after the other, the
+ * LDS-halo layout (C in {64, 128}, 3x3 or 1x1, bits in {2,3,4}; padded to a
+ * multiple of 4 words) and the tap-major layout (C % 64 == 0, bits in
+ * {2,3,4}), each when the shape has it. */
 int64_t dimq_conv2d_prepared_words(int64_t out_channels, int64_t in_channels, int64_t kernel_h, int64_t kernel_w,
                                    int bits);
 
-/* One-time repack of a conv_kcrs b-bit index stream into the kernel layout
- * read by the LDS-halo conv kernel (per output channel and lane group, the
- * indices of each (kh, kw, 32-channel) step in decode order).  Same bytes
- * of information; done when a layer is loaded, not per call. */
+/* One-time repack of a conv_kcrs b-bit index stream into the kernel
+ * layouts: the LDS-halo layout (per output channel and lane group, the
+ * indices of each (kh, kw, 32-channel) step in decode order) and the
+ * tap-major layout read by the implicit-GEMM kernel (index (oc, kh, kw, c)
+ * at k = (kh*KW + kw)*C + c, LSB-first).  Same bits, no expansion; done when
+ * a layer is loaded, not per call. */
 int dimq_conv2d_prepare_weight(const uint8_t* packed_w, int64_t packed_numel, int bits, int64_t out_channels,
                                int64_t in_channels, int64_t kernel_h, int64_t kernel_w, uint32_t* prepared_w,
                                int64_t prepared_words, void* stream);
@@ -158,8 +170,10 @@ int dimq_conv2d_prepare_weight(const uint8_t* packed_w, int64_t packed_numel, in
  * x [B,C,H,W] in x_layout (NCHW or NHWC memory order); y [B,OC,OH,OW] in
  * y_layout; packed_w: b-bit stream of the conv_kcrs index tensor
  * [OC, C/groups, KH, KW] (dimq_backend/export.py:232).  prepared_w
- * (nullable): the same weights in kernel layout; when given and the shape
- * fits, the LDS-halo kernel runs, otherwise the implicit-GEMM kernel. */
+ * (nullable): the same weights in kernel layouts (dimq_conv2d_prepare_weight);
+ * with it, NHWC 16-bit calls take the large-tile implicit GEMM or the LDS-halo
+ * kernel by shape.  Stride-2 convs of C <= 4 channels (network stems) take a
+ * dedicated kernel; everything else the generic implicit-GEMM kernel. */
 int dimq_conv2d_codebook(const void* x, int x_dtype, int x_layout, int64_t B, int64_t C, int64_t H, int64_t W,
                          const uint8_t* packed_w, int64_t packed_numel, int bits, const uint32_t* prepared_w,
                          int64_t prepared_words, const void* codebook,
@@ -167,6 +181,30 @@ int dimq_conv2d_codebook(const void* x, int x_dtype, int x_layout, int64_t B, in
                          int64_t out_channels, int64_t kernel_h, int64_t kernel_w, int64_t stride_h,
                          int64_t stride_w, int64_t pad_h, int64_t pad_w, int64_t dilation_h, int64_t dilation_w,
                          int64_t groups, void* y, int y_dtype, int y_layout, int variant, void* stream);
+
+/* Fused-epilogue forms of the two weight-only ops (no counterpart in the
+ * reference, whose models run bias, residual add and activation as separate
+ * torch ops after the DIMQ layer: modules.py:36-47,104-122 feed F.relu / the
+ * residual sum of the calling model).  Each output element becomes
+ *   y = act(acc * scale + bias + residual)
+ * in fp32 before the one rounding to y_dtype.  residual (nullable, any float
+ * dtype in residual_dtype) has y's shape and memory order ([M, N] row-major
+ * for Linear; y_layout for Conv2d) and may alias y.  activation: enum
+ * dimq_activation.  The plain entry points above are these with residual
+ * NULL and DIMQ_ACT_NONE. */
+int dimq_linear_codebook_ex(const void* x, int x_dtype, int64_t M, int64_t K, const uint8_t* packed_w,
+                            int64_t packed_numel, int bits, const void* codebook, int cb_dtype, int64_t cb_rows,
+                            int64_t cb_size, const void* bias, int bias_dtype, int64_t N, void* y, int y_dtype,
+                            const void* residual, int residual_dtype, int activation, int variant, void* stream);
+
+int dimq_conv2d_codebook_ex(const void* x, int x_dtype, int x_layout, int64_t B, int64_t C, int64_t H, int64_t W,
+                            const uint8_t* packed_w, int64_t packed_numel, int bits, const uint32_t* prepared_w,
+                            int64_t prepared_words, const void* codebook, int cb_dtype, int64_t cb_rows,
+                            int64_t cb_size, const void* bias, int bias_dtype, int64_t out_channels,
+                            int64_t kernel_h, int64_t kernel_w, int64_t stride_h, int64_t stride_w, int64_t pad_h,
+                            int64_t pad_w, int64_t dilation_h, int64_t dilation_w, int64_t groups, void* y,
+                            int y_dtype, int y_layout, const void* residual, int residual_dtype, int activation,
+                            int variant, void* stream);
 
 #ifdef __cplusplus
 }

@@ -342,6 +342,84 @@ def test_linear_codebook_cfg1_shape(gpu):
     assert oracle.rel_err(y, ref) <= TOL
 
 
+# ---------------------------------------------------------------- fused epilogue (residual + activation)
+_ACTS = {None: lambda t: t, "relu": torch.relu, "gelu": torch.nn.functional.gelu}
+
+
+@pytest.mark.parametrize("case", [
+    dict(M=300, N=256, K=512, bits=4, xdt=torch.bfloat16, out=torch.bfloat16, rdt=torch.bfloat16, act="gelu"),  # deep
+    dict(M=200, N=256, K=2048, bits=2, xdt=torch.float16, out=torch.float32, rdt=torch.float32, act="relu"),  # big
+    dict(M=2, N=64, K=4096, bits=3, xdt=torch.bfloat16, out=torch.float32, rdt=torch.float16, act=None),  # gemv fast
+    dict(M=9, N=100, K=256, bits=4, xdt=torch.float32, out=torch.float16, rdt=torch.float32, act="gelu"),  # gemv
+    dict(M=70, N=50, K=96, bits=3, xdt=torch.float16, out=torch.float32, rdt=torch.bfloat16, act="relu"),  # generic
+    dict(M=40, N=72, K=128, bits=8, xdt=torch.float16, out=torch.float32, rdt=torch.float32, act="gelu"),  # 8-bit
+])
+def test_linear_codebook_fused_epilogue(gpu, case):
+    """y = act(x W_hat^T + b + residual) on every Linear kernel family, against the fp32 CPU reference."""
+    ops = _ops()
+    announce(f"linear fused {case}")
+    M, N, K, bits = case["M"], case["N"], case["K"], case["bits"]
+    g = _gen(M + N + K + bits)
+    cb, idx, packed = _codebook_case(N, K, bits, True, g)
+    x = torch.randn(M, K, generator=g).to(case["xdt"])
+    bias = torch.randn(N, generator=g) * 0.05
+    res = (torch.randn(M, N, generator=g) * 0.3).to(case["rdt"])
+    y = ops.dimq_linear_codebook(x.to(gpu), packed.to(gpu), cb.to(gpu), bits, bias.to(gpu), N, K,
+                                 out_dtype=case["out"], residual=res.to(gpu), activation=case["act"])
+    ref = _ACTS[case["act"]](oracle.linear_dequant_reference(x.float(), packed, bits, cb, N, K, bias) + res.float())
+    tol = TOL if case["out"] != torch.bfloat16 else 8e-3
+    assert oracle.rel_err(y.float(), ref) <= tol, oracle.rel_err(y.float(), ref)
+
+
+@pytest.mark.parametrize("case", [
+    dict(B=2, C=64, H=20, W=18, OC=64, K=3, s=1, bits=2, prep=True, path="auto", g=1),    # resident halo
+    dict(B=2, C=128, H=12, W=12, OC=64, K=3, s=1, bits=3, prep=True, path="halo", g=1),   # decode-per-step halo
+    dict(B=2, C=256, H=9, W=9, OC=128, K=3, s=2, bits=2, prep=True, path="auto", g=1),    # implicit GEMM
+    dict(B=2, C=3, H=40, W=40, OC=64, K=7, s=2, bits=8, prep=False, path="auto", g=1),    # stem
+    dict(B=2, C=16, H=9, W=9, OC=24, K=3, s=1, bits=4, prep=False, path="auto", g=2),     # generic
+])
+@pytest.mark.parametrize("layout", ["nchw", "nhwc"])
+@pytest.mark.parametrize("act", ["relu", "gelu"])
+def test_conv2d_codebook_fused_epilogue(gpu, case, layout, act, monkeypatch):
+    """y = act(conv + b + residual) on every Conv2d kernel family; the residual comes in the other memory order."""
+    if case["path"] == "halo":
+        monkeypatch.setenv("DIMQ_CONV_PATH", "halo")
+    ops = _ops()
+    announce(f"conv fused {case} {layout} {act}")
+    g = _gen(case["C"] + case["OC"] + case["K"] + case["bits"])
+    K, pad, s = case["K"], case["K"] // 2, case["s"]
+    shape = (case["OC"], case["C"] // case["g"], K, K)
+    x = torch.relu(torch.randn(case["B"], case["C"], case["H"], case["W"], generator=g)).half()
+    cb, idx, packed = _codebook_case(case["OC"], int(np.prod(shape[1:])), case["bits"], True, g)
+    bias = torch.randn(case["OC"], generator=g) * 0.1
+    ref0 = oracle.conv2d_dequant_reference(x.float(), packed, case["bits"], cb, shape, bias, s, pad, 1, case["g"])
+    res = torch.randn(ref0.shape, generator=g) * 0.3
+    xd = x.to(gpu)
+    rd = res.half().to(gpu)
+    if layout == "nhwc":
+        xd = xd.to(memory_format=torch.channels_last)
+    else:
+        rd = rd.to(memory_format=torch.channels_last)
+    pd = packed.to(gpu)
+    prep = ops.prepare_conv_weight(pd, case["bits"], shape) if case["prep"] else None
+    y = ops.dimq_conv2d_codebook(xd, pd, cb.to(gpu), case["bits"], bias.to(gpu), shape, (s, s), (pad, pad), (1, 1),
+                                 case["g"], out_dtype=torch.float32, prepared_weight=prep, residual=rd, activation=act)
+    ref = _ACTS[act](ref0 + res.half().float())
+    assert oracle.rel_err(y.float(), ref) <= TOL, oracle.rel_err(y.float(), ref)
+
+
+def test_fused_epilogue_errors(gpu):
+    ops = _ops()
+    g = _gen(9)
+    cb, idx, packed = _codebook_case(16, 64, 4, True, g)
+    x = torch.randn(5, 64, generator=g).to(gpu)
+    with pytest.raises(RuntimeError, match="residual shape"):
+        ops.dimq_linear_codebook(x, packed.to(gpu), cb.to(gpu), 4, None, 16, 64,
+                                 residual=torch.zeros(5, 15, device=gpu))
+    with pytest.raises(KeyError):
+        ops.dimq_linear_codebook(x, packed.to(gpu), cb.to(gpu), 4, None, 16, 64, activation="tanh")
+
+
 def test_linear_codebook_small_codebook_and_errors(gpu):
     ops = _ops()
     g = _gen(5)

@@ -25,7 +25,22 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .modules import quantize_model_weight_only
+from .modules import DIMQCodebookConv2d, DIMQCodebookLinear, quantize_model_weight_only
+
+
+def _fused(mod: nn.Module, x: torch.Tensor, residual: torch.Tensor | None = None,
+           act: str | None = None) -> torch.Tensor:
+    """act(mod(x) + residual): fused into the kernel's store for codebook layers, torch ops otherwise."""
+    if isinstance(mod, (DIMQCodebookConv2d, DIMQCodebookLinear)):
+        return mod(x, residual=residual, activation=act)
+    y = mod(x)
+    if residual is not None:
+        y = y + residual
+    if act == "relu":
+        y = F.relu(y)
+    elif act == "gelu":
+        y = F.gelu(y)
+    return y
 
 
 # ---------------------------------------------------------------------------
@@ -39,7 +54,7 @@ class _Attention(nn.Module):
         self.qkv = nn.Linear(dim, 3 * dim)
         self.proj = nn.Linear(dim, dim)
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None) -> torch.Tensor:
         b, n, d = x.shape
         h = self.heads
         # q, k, v stay strided views of the qkv output (head dim contiguous): the
@@ -48,7 +63,7 @@ class _Attention(nn.Module):
         qkv = self.qkv(x).view(b, n, 3, h, d // h)
         q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
         o = F.scaled_dot_product_attention(q, k, v)
-        return self.proj(o.transpose(1, 2).reshape(b, n, d))
+        return _fused(self.proj, o.transpose(1, 2).reshape(b, n, d), residual=residual)
 
 
 class _Block(nn.Module):
@@ -61,8 +76,10 @@ class _Block(nn.Module):
         self.fc2 = nn.Linear(mlp, dim)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        x = x + self.attn(self.ln_1(x))
-        return x + self.fc2(F.gelu(self.fc1(self.ln_2(x))))
+        # x + attn(ln_1(x)), then x + fc2(gelu(fc1(ln_2(x)))); the residual adds and
+        # the GELU run in the projections' epilogues
+        x = self.attn(self.ln_1(x), residual=x)
+        return _fused(self.fc2, _fused(self.fc1, self.ln_2(x), act="gelu"), residual=x)
 
 
 class ViT(nn.Module):
@@ -138,10 +155,10 @@ class _BasicBlock(nn.Module):
         self.downsample = nn.Conv2d(cin, cout, 1, stride) if (stride != 1 or cin != cout) else None
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        out = F.relu(self.conv1(x), inplace=True)
-        out = self.conv2(out)
+        # relu(conv2(relu(conv1(x))) + identity), ReLUs and the residual add in the conv epilogues
+        out = _fused(self.conv1, x, act="relu")
         idn = x if self.downsample is None else self.downsample(x)
-        return F.relu(out + idn, inplace=True)
+        return _fused(self.conv2, out, residual=idn, act="relu")
 
 
 class ResNet18(nn.Module):
@@ -158,7 +175,7 @@ class ResNet18(nn.Module):
         self.fc = nn.Linear(512, classes)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        x = F.relu(self.conv1(x), inplace=True)
+        x = _fused(self.conv1, x, act="relu")
         x = F.max_pool2d(x, 3, 2, 1)
         x = self.layer4(self.layer3(self.layer2(self.layer1(x))))
         x = torch.flatten(F.adaptive_avg_pool2d(x, 1), 1)

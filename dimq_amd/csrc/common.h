@@ -97,9 +97,21 @@ struct Epi {
   int res_vec;  // residual 16-byte aligned: vector loads where y's stores are
 };
 
+// GELU(v) = 0.5 v (1 + erf(v / sqrt 2)) with erf from Abramowitz & Stegun
+// 7.1.26 (|error| <= 1.5e-7): branch-free and short, so it can sit in every
+// unrolled store of an epilogue without blowing up the kernel's code.
+__device__ __forceinline__ float gelu_erf(float v) {
+  const float z = v * 0.70710678118654752f;
+  const float a = fabsf(z);
+  const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * a);
+  const float poly = t * (0.254829592f + t * (-0.284496736f + t * (1.421413741f + t * (-1.453152027f + t * 1.061405429f))));
+  const float erf_a = 1.0f - poly * __expf(-a * a);
+  return 0.5f * v * (1.0f + copysignf(erf_a, z));
+}
+
 __device__ __forceinline__ float act_apply(float v, int act) {
   if (act == DIMQ_ACT_RELU) return v < 0.0f ? 0.0f : v;  // NaN passes, as torch.relu
-  if (act == DIMQ_ACT_GELU) return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+  if (act == DIMQ_ACT_GELU) return gelu_erf(v);
   return v;
 }
 
@@ -108,34 +120,99 @@ __device__ __forceinline__ float epi1(const Epi& e, int64_t off, float v) {
   return act_apply(v, e.act);
 }
 
-// N (a multiple of 4) consecutive outputs starting at off; vec: off % 4 == 0.
+// Residual of N (a multiple of 4) consecutive outputs.  For 16-bit residuals
+// on the vector path (the model case) the hot epilogues load them with
+// res_issue ahead of their stores -- a load placed after an earlier store of
+// the same tile cannot be hoisted over it, since the residual may alias y --
+// and fold them in with epi_apply; other residuals are loaded at the store.
 template <int N>
-__device__ __forceinline__ void epiN(const Epi& e, int64_t off, float (&v)[N], bool vec) {
-  if (e.res) {
-    if (vec && e.res_vec && e.res_dt == DIMQ_F32) {
+struct ResPairs {
+  uint32_t w[N / 2];
+};
+
+__device__ __forceinline__ bool res_pairs(const Epi& e, bool vec) {
+  return e.res && vec && e.res_vec && (e.res_dt == DIMQ_F16 || e.res_dt == DIMQ_BF16);
+}
+
+template <int N>
+__device__ __forceinline__ void res_issue(const Epi& e, int64_t off, ResPairs<N>& r) {
 #pragma unroll
-      for (int q = 0; q < N / 4; ++q) {
-        const float4 r = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(e.res) + off + 4 * q);
-        v[4 * q] += r.x; v[4 * q + 1] += r.y; v[4 * q + 2] += r.z; v[4 * q + 3] += r.w;
-      }
-    } else if (vec && e.res_vec && (e.res_dt == DIMQ_F16 || e.res_dt == DIMQ_BF16)) {
-#pragma unroll
-      for (int q = 0; q < N / 4; ++q) {
-        const uint2 r = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(e.res) + off + 4 * q);
-        const uint32_t h[4] = {r.x & 0xffffu, r.x >> 16, r.y & 0xffffu, r.y >> 16};
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          v[4 * q + i] += e.res_dt == DIMQ_F16 ? f16_bits_to_float(h[i]) : bf16_bits_to_float(h[i]);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < N; ++i) v[i] += load_as_float(e.res, e.res_dt, off + i);
-    }
+  for (int q = 0; q < N / 4; ++q) {
+    const uint2 t = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(e.res) + off + 4 * q);
+    r.w[2 * q] = t.x;
+    r.w[2 * q + 1] = t.y;
   }
+}
+
+// v += residual: from r when given and 16-bit, else loaded here.
+template <int N>
+__device__ __forceinline__ void res_add(const Epi& e, const ResPairs<N>* r, int64_t off, bool vec, float (&v)[N]) {
+  if (res_pairs(e, vec)) {
+    ResPairs<N> t;
+    if (r) {
+      t = *r;
+    } else {
+      res_issue<N>(e, off, t);
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const uint32_t h = (t.w[i >> 1] >> (16 * (i & 1))) & 0xffffu;
+      v[i] += e.res_dt == DIMQ_F16 ? f16_bits_to_float(h) : bf16_bits_to_float(h);
+    }
+  } else if (vec && e.res_vec && e.res_dt == DIMQ_F32) {
+#pragma unroll
+    for (int q = 0; q < N / 4; ++q) {
+      const float4 t = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(e.res) + off + 4 * q);
+      v[4 * q] += t.x; v[4 * q + 1] += t.y; v[4 * q + 2] += t.z; v[4 * q + 3] += t.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += load_as_float(e.res, e.res_dt, off + i);
+  }
+}
+
+// Runtime epilogue (generic kernels): residual and activation read from e.
+template <int N>
+__device__ __forceinline__ void epi_apply(const Epi& e, const ResPairs<N>* r, int64_t off, bool vec,
+                                          float (&v)[N]) {
+  if (e.res) res_add<N>(e, r, off, vec, v);
   if (e.act) {
 #pragma unroll
     for (int i = 0; i < N; ++i) v[i] = act_apply(v[i], e.act);
   }
+}
+
+template <int N>
+__device__ __forceinline__ void epiN(const Epi& e, int64_t off, float (&v)[N], bool vec) {
+  epi_apply<N>(e, nullptr, off, vec, v);
+}
+
+// Compile-time epilogue modes of the fast kernels (a template parameter, so
+// a kernel without epilogue carries none of its code): residual flag | act.
+// Combinations a kernel is not instantiated for run on the generic kernels,
+// whose epilogue is the runtime one above.
+constexpr int kEpiNone = 0, kEpiRelu = 1, kEpiGelu = 2, kEpiRes = 4, kEpiResRelu = 5;
+
+inline int epi_mode(const Epi& e) { return (e.res ? kEpiRes : 0) | e.act; }
+
+template <int MODE, int N>
+__device__ __forceinline__ void epi_m(const Epi& e, const ResPairs<N>* r, int64_t off, bool vec, float (&v)[N]) {
+  if constexpr ((MODE & kEpiRes) != 0) res_add<N>(e, r, off, vec, v);
+  if constexpr ((MODE & 3) == kEpiRelu) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = v[i] < 0.0f ? 0.0f : v[i];
+  } else if constexpr ((MODE & 3) == kEpiGelu) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = gelu_erf(v[i]);
+  }
+}
+
+template <int MODE>
+__device__ __forceinline__ float epi1_m(const Epi& e, int64_t off, float v) {
+  if constexpr ((MODE & kEpiRes) != 0) v += load_as_float(e.res, e.res_dt, off);
+  if constexpr ((MODE & 3) == kEpiRelu) v = v < 0.0f ? 0.0f : v;
+  if constexpr ((MODE & 3) == kEpiGelu) v = gelu_erf(v);
+  return v;
 }
 
 // u4 activation code: clamp(rint(x / s) + zp, 0, 15), IEEE divide

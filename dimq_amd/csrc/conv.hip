@@ -292,11 +292,14 @@ extern "C" int dimq_conv2d_codebook_ex(const void* x, int x_dtype, int x_layout,
   const int64_t hw = prepared_w ? halo_part_words(s.OC, s.C, s.KH, s.KW, bits) : 0;
   const int64_t gw = prepared_w ? gemm_part_words(s.OC, s.C, s.KH, s.KW, bits) : 0;
   if (prepared_w != nullptr) DIMQ_CHECK(prepared_words >= hw + gw, "prepared weight buffer is too small");
+  const int mode = epi_mode(epi);
   const bool gemm_ok = gw > 0 && variant != DIMQ_VARIANT_SMALL_M && s.groups == 1 && x_layout == DIMQ_NHWC &&
+                       (mode == kEpiNone || mode == kEpiRelu || mode == kEpiRes || mode == kEpiResRelu) &&
                        y_layout == DIMQ_NHWC && (x_dtype == DIMQ_F16 || x_dtype == DIMQ_BF16) && aligned(x, 16) &&
                        aligned(y, 16) && aligned(prepared_w + hw, 16);
   const bool halo_ok = hw > 0 && variant != DIMQ_VARIANT_SMALL_M && aligned(x, 16) &&
-                       halo_eligible(s.C, s.KH, s.KW, s.sh, s.sw, s.dh, s.dw, s.groups, s.OH, s.OW, bits, x_dtype);
+                       halo_eligible(s.C, s.KH, s.KW, s.sh, s.sw, s.dh, s.dw, s.groups, s.OH, s.OW, bits, x_dtype,
+                                     epi_mode(epi), y_layout);
   if (gemm_ok && (!halo_ok || prefer_gemm_conv(s.C, s.KH, s.KW, s.sh))) {
     GemmArgs p = conv_args(s, x, x_layout, reinterpret_cast<const uint8_t*>(prepared_w + hw), codebook, cb_dtype,
                            cb_rows, cb_size, bias, bias_dtype, y, y_dtype, y_layout);
@@ -315,7 +318,8 @@ extern "C" int dimq_conv2d_codebook_ex(const void* x, int x_dtype, int x_layout,
                             y_layout, epi, as_stream(stream));
   }
   if (variant != DIMQ_VARIANT_SMALL_M &&
-      stem_eligible(s.C, s.OC, s.KH, s.KW, s.sh, s.sw, s.pw, s.dh, s.dw, s.groups, s.OH, s.OW, bits, y_dtype, x, y)) {
+      stem_eligible(s.C, s.OC, s.KH, s.KW, s.sh, s.sw, s.pw, s.dh, s.dw, s.groups, s.OH, s.OW, bits, y_dtype, x, y,
+                    epi_mode(epi))) {
     return launch_conv_stem(x, x_dtype, x_layout, s.B, s.C, s.H, s.W, packed_w, packed_numel, bits, codebook,
                             cb_dtype, cb_rows, cb_size, bias, bias_dtype, s.OC, s.KH, s.KW, s.ph, s.pw, s.OH, s.OW,
                             y, y_dtype, y_layout, epi, as_stream(stream));

@@ -40,9 +40,11 @@ __device__ __forceinline__ uint32_t to_f16_bits(uint32_t raw, int dt) {
 
 // Four consecutive outputs of one lane, after the fused epilogue: one 16-byte
 // (fp32) or 8-byte (16-bit) store when `vec`, element stores otherwise.
-__device__ __forceinline__ void store4(void* y, int dt, int64_t off, const float vin[4], bool vec, const Epi& e) {
+template <int MODE>
+__device__ __forceinline__ void store4(void* y, int dt, int64_t off, const float vin[4], bool vec, const Epi& e,
+                                      const ResPairs<4>* r = nullptr) {
   float v[4] = {vin[0], vin[1], vin[2], vin[3]};
-  epiN<4>(e, off, v, vec);
+  epi_m<MODE, 4>(e, r, off, vec, v);
   if (vec && dt == DIMQ_F32) {
     *reinterpret_cast<float4*>(reinterpret_cast<float*>(y) + off) = make_float4(v[0], v[1], v[2], v[3]);
   } else if (vec) {
@@ -72,7 +74,7 @@ __device__ __forceinline__ int xcd_tile(int bid, int n) {
 // Epilogue of one 32x32 MFMA block.  PXROWS: rows = pixels pix0 + 8j + 4g + i
 // of output channel ocl (lane column); else rows = output channels
 // ocr + 8j + 4g + i of pixel pix (lane column).
-template <bool PXROWS>
+template <bool PXROWS, int MODE>
 __device__ __forceinline__ void store_block(const HaloArgs& p, const floatx16& acc, int b, int oh0, int P, int mb,
                                             int col, int g, int ocl, int ocr, float scale, float bv) {
   const int64_t ohw = (int64_t)p.OH * p.OW;
@@ -80,6 +82,14 @@ __device__ __forceinline__ void store_block(const HaloArgs& p, const floatx16& a
     if (ocl >= p.OC) return;
     const bool vec = (ohw % 4 == 0) && (p.OW % 4 == 0) && (p.y_layout == DIMQ_NCHW);
     const int64_t chan = ((int64_t)b * p.OC + ocl) * ohw + (int64_t)oh0 * p.OW;
+    ResPairs<4> rr[4];  // 16-bit residuals of the block, loaded before its first store
+    if ((MODE & kEpiRes) && res_pairs(p.epi, vec)) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int pix0 = mb * 32 + 8 * j + 4 * g;
+        if (p.y_layout == DIMQ_NCHW && pix0 + 4 <= P) res_issue<4>(p.epi, chan + pix0, rr[j]);
+      }
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int pix0 = mb * 32 + 8 * j + 4 * g;
@@ -88,7 +98,7 @@ __device__ __forceinline__ void store_block(const HaloArgs& p, const floatx16& a
 #pragma unroll
       for (int i = 0; i < 4; ++i) v[i] = acc[4 * j + i] * scale + bv;
       if (p.y_layout == DIMQ_NCHW && pix0 + 4 <= P) {
-        store4(p.y, p.y_dt, chan + pix0, v, vec, p.epi);
+        store4<MODE>(p.y, p.y_dt, chan + pix0, v, vec, p.epi, &rr[j]);
       } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -96,7 +106,7 @@ __device__ __forceinline__ void store_block(const HaloArgs& p, const floatx16& a
             const int64_t off = p.y_layout == DIMQ_NCHW
                                     ? chan + pix0 + i
                                     : ((int64_t)b * ohw + (int64_t)oh0 * p.OW + pix0 + i) * p.OC + ocl;
-            store_from_float(p.y, p.y_dt, off, epi1(p.epi, off, v[i]));
+            store_from_float(p.y, p.y_dt, off, epi1_m<MODE>(p.epi, off, v[i]));
           }
         }
       }
@@ -105,6 +115,14 @@ __device__ __forceinline__ void store_block(const HaloArgs& p, const floatx16& a
     const int pix = mb * 32 + col;
     const bool vec = (p.OC % 4 == 0) && (p.y_layout == DIMQ_NHWC);
     const int64_t pbase = (int64_t)b * ohw + (int64_t)oh0 * p.OW + pix;
+    ResPairs<4> rr[4];  // 16-bit residuals of the block, loaded before its first store
+    if ((MODE & kEpiRes) && res_pairs(p.epi, vec) && pix < P && p.y_layout == DIMQ_NHWC) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int ocb = ocr + 8 * j + 4 * g;
+        if (ocb + 4 <= p.OC) res_issue<4>(p.epi, pbase * p.OC + ocb, rr[j]);
+      }
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int ocb = ocr + 8 * j + 4 * g;
@@ -117,14 +135,14 @@ __device__ __forceinline__ void store_block(const HaloArgs& p, const floatx16& a
       }
       if (pix >= P) continue;
       if (p.y_layout == DIMQ_NHWC && ocb + 4 <= p.OC) {
-        store4(p.y, p.y_dt, pbase * p.OC + ocb, v, vec, p.epi);
+        store4<MODE>(p.y, p.y_dt, pbase * p.OC + ocb, v, vec, p.epi, &rr[j]);
       } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           if (ocb + i < p.OC) {
             const int64_t off = p.y_layout == DIMQ_NHWC ? pbase * p.OC + ocb + i
                                                         : ((int64_t)b * p.OC + ocb + i) * ohw + (int64_t)oh0 * p.OW + pix;
-            store_from_float(p.y, p.y_dt, off, epi1(p.epi, off, v[i]));
+            store_from_float(p.y, p.y_dt, off, epi1_m<MODE>(p.epi, off, v[i]));
           }
         }
       }

@@ -135,7 +135,7 @@ __device__ __forceinline__ int stem_index(const StemArgs& p, int64_t flat) {
   return static_cast<int>((v >> sh) & ((1u << p.bits) - 1u));
 }
 
-template <int KH, int NP>
+template <int KH, int NP, int MODE>
 __global__ __launch_bounds__(kStemThreads, 2) void conv_stem_kernel(const StemArgs p) {
   constexpr int SPK = NP / 2;  // k16 steps per kh
   constexpr int T = KH * SPK;  // k16 steps in all
@@ -325,7 +325,7 @@ __global__ __launch_bounds__(kStemThreads, 2) void conv_stem_kernel(const StemAr
             for (int u = 0; u < 8; ++u) v[u] = v[u] * rsc[u] + rbs[u];
             if (pb + px >= P || ch * 8 >= p.OC) continue;
             const int64_t off = (gp0 + px) * p.OC + ch * 8;
-            epiN<8>(p.epi, off, v, true);
+            epi_m<MODE, 8>(p.epi, nullptr, off, true, v);
             if (p.y_dt == DIMQ_F32) {
               float* yp = reinterpret_cast<float*>(p.y) + off;
               *reinterpret_cast<float4*>(yp) = make_float4(v[0], v[1], v[2], v[3]);
@@ -350,7 +350,7 @@ __global__ __launch_bounds__(kStemThreads, 2) void conv_stem_kernel(const StemAr
             if (lane >= p.OC) continue;
             const int px0 = 8 * it;
             if (vec_nchw && pb + px0 + 8 <= P) {
-              epiN<8>(p.epi, cbase + px0, v, true);
+              epi_m<MODE, 8>(p.epi, nullptr, cbase + px0, true, v);
               if (p.y_dt == DIMQ_F32) {
                 float* yp = reinterpret_cast<float*>(p.y) + cbase + px0;
                 *reinterpret_cast<float4*>(yp) = make_float4(v[0], v[1], v[2], v[3]);
@@ -366,7 +366,7 @@ __global__ __launch_bounds__(kStemThreads, 2) void conv_stem_kernel(const StemAr
             } else {
 #pragma unroll
               for (int u = 0; u < 8; ++u)
-                if (pb + px0 + u < P) store_from_float(p.y, p.y_dt, cbase + px0 + u, epi1(p.epi, cbase + px0 + u, v[u]));
+                if (pb + px0 + u < P) store_from_float(p.y, p.y_dt, cbase + px0 + u, epi1_m<MODE>(p.epi, cbase + px0 + u, v[u]));
             }
           }
         }
@@ -408,7 +408,8 @@ int64_t stem_rows(int64_t KH, int64_t OH, int64_t OW, int np) {
 
 bool stem_eligible(int64_t C, int64_t OC, int64_t KH, int64_t KW, int64_t sh, int64_t sw, int64_t pw,
                    int64_t dh, int64_t dw, int64_t groups, int64_t OH, int64_t OW, int bits, int y_dtype,
-                   const void* x, const void* y) {
+                   const void* x, const void* y, int epi_mode_) {
+  if (epi_mode_ != kEpiNone && epi_mode_ != kEpiRelu) return false;  // other epilogues: generic kernel
   if (groups != 1 || C < 1 || C > 4 || OC < 1 || OC > 64 || OC % 8 != 0) return false;
   if (sh != 2 || sw != 2 || dh != 1 || dw != 1) return false;
   if (bits < 2 || bits > 8) return false;
@@ -467,16 +468,15 @@ int launch_conv_stem(const void* x, int x_dtype, int x_layout, int64_t B, int64_
   const int T = (int)KH * np / 2;
   const int64_t units = std::max<int64_t>((int64_t)p.IR * p.npairs, 2LL * T * 64);
   const size_t lds = (size_t)units * 16 + 4 * kStemOutFloats * sizeof(float);
-  const void* k = KH == 7 ? reinterpret_cast<const void*>(conv_stem_kernel<7, 4>)
-                          : reinterpret_cast<const void*>(conv_stem_kernel<3, 2>);
+  const bool relu = epi_mode(epi) == kEpiRelu;
+  auto k = KH == 7 ? (relu ? conv_stem_kernel<7, 4, kEpiRelu> : conv_stem_kernel<7, 4, kEpiNone>)
+                   : (relu ? conv_stem_kernel<3, 2, kEpiRelu> : conv_stem_kernel<3, 2, kEpiNone>);
   if (lds > 64 * 1024) {
-    const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return set_error(DIMQ_ERR_HIP, "conv2d_codebook (stem): %s", hipGetErrorString(e));
   }
-  if (KH == 7)
-    hipLaunchKernelGGL((conv_stem_kernel<7, 4>), dim3((unsigned)G), dim3(kStemThreads), lds, s, p);
-  else
-    hipLaunchKernelGGL((conv_stem_kernel<3, 2>), dim3((unsigned)G), dim3(kStemThreads), lds, s, p);
+  hipLaunchKernelGGL(k, dim3((unsigned)G), dim3(kStemThreads), lds, s, p);
   return check_launch("conv2d_codebook (stem)");
 }
 

@@ -201,13 +201,13 @@ __device__ __forceinline__ void store_tile(const HaloArgs& p, const float* tile,
       const float v[4] = {v4.x, v4.y, v4.z, v4.w};
       const int64_t base = ((int64_t)b * p.OC + oc0 + oc) * ohw + (int64_t)oh0 * p.OW + px0 + q;
       if (p.y_layout == DIMQ_NCHW && q + 4 <= npx) {
-        store4(p.y, p.y_dt, base, v, vec, p.epi);
+        store4<kEpiNone>(p.y, p.y_dt, base, v, vec, p.epi);
       } else {
         for (int k = 0; k < 4 && q + k < npx; ++k) {
           const int64_t off = p.y_layout == DIMQ_NCHW
                                   ? base + k
                                   : ((int64_t)b * ohw + (int64_t)oh0 * p.OW + px0 + q + k) * p.OC + oc0 + oc;
-          store_from_float(p.y, p.y_dt, off, epi1(p.epi, off, v[k]));
+          store_from_float(p.y, p.y_dt, off, v[k]);
         }
       }
     }
@@ -221,13 +221,13 @@ __device__ __forceinline__ void store_tile(const HaloArgs& p, const float* tile,
       const float v[4] = {v4.x, v4.y, v4.z, v4.w};
       const int64_t pix = (int64_t)b * ohw + (int64_t)oh0 * p.OW + px0 + px;
       if (p.y_layout == DIMQ_NHWC && oc0 + o4 + 4 <= p.OC) {
-        store4(p.y, p.y_dt, pix * p.OC + oc0 + o4, v, vec, p.epi);
+        store4<kEpiNone>(p.y, p.y_dt, pix * p.OC + oc0 + o4, v, vec, p.epi);
       } else {
         for (int k = 0; k < 4 && oc0 + o4 + k < p.OC; ++k) {
           const int64_t off = p.y_layout == DIMQ_NHWC
                                   ? pix * p.OC + oc0 + o4 + k
                                   : ((int64_t)b * p.OC + oc0 + o4 + k) * ohw + (int64_t)oh0 * p.OW + px0 + px;
-          store_from_float(p.y, p.y_dt, off, epi1(p.epi, off, v[k]));
+          store_from_float(p.y, p.y_dt, off, v[k]);
         }
       }
     }
@@ -262,7 +262,7 @@ __device__ __forceinline__ void store_tile_full(const HaloArgs& p, const float* 
       v[0] = v4.x; v[1] = v4.y; v[2] = v4.z; v[3] = v4.w;
       off = ((int64_t)b * ohw + (int64_t)oh0 * p.OW + px0 + px) * p.OC + oc0 + o4;
     }
-    store4(p.y, p.y_dt, off, v, true, p.epi);
+    store4<kEpiNone>(p.y, p.y_dt, off, v, true, p.epi);
   }
 }
 

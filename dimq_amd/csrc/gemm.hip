@@ -28,6 +28,8 @@ int gemm_fast_tile(int tile, const GemmArgs& p, int bits) {
 // 128x128 tile (2) for K >= 2048.  Returns -1 when the shape does not qualify.
 int gemm_big_tile(const GemmArgs& p, int bits, int variant) {
   if (variant == DIMQ_VARIANT_SMALL_M || p.conv || !(bits == 2 || bits == 3 || bits == 4)) return -1;
+  const int mode = epi_mode(p.epi);  // epilogues the large tiles are instantiated for
+  if (!(mode == kEpiNone || mode == kEpiRelu || mode == kEpiGelu || mode == kEpiRes)) return -1;
   if (p.M <= 64 || p.K % 64 != 0 || !p.fast_b || !p.vec_a) return -1;
   const char* force = getenv("DIMQ_GEMM_BIG");  // A/B runs: -1 = off, 0..7 = tile
   if (force) return (atoi(force) >= 0 && atoi(force) <= 7) ? atoi(force) : -1;

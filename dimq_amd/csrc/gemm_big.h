@@ -116,8 +116,16 @@ __device__ __forceinline__ void convert_a16_big(const RawA<XT>& r, uint32_t out[
 // (b, oh, ow), and a 64-wide k stage is 64 consecutive channels of one input
 // pixel (one tap), or zeros where the tap falls into the padding.  y is the
 // NHWC output, row-major [M, OC].
-template <int BITS, int XT, int WGM, int WGN, int MBLK, int NBLK, bool CONV = false>
-__global__ __launch_bounds__(64 * WGM * WGN) void gemm_big_kernel(const GemmArgs p) {
+// Occupancy hint: the 2-bit implicit-GEMM conv with 64x64 wave tiles fits
+// three waves per SIMD without spilling (measured faster than two); the other
+// instantiations keep the compiler's choice.
+constexpr int big_min_waves(int bits, int mblk, int nblk, bool conv) {
+  return (conv && bits == 2 && mblk * nblk <= 4) ? 3 : 1;
+}
+
+template <int BITS, int XT, int WGM, int WGN, int MBLK, int NBLK, bool CONV = false, int MODE = kEpiNone>
+__global__ __launch_bounds__(64 * WGM * WGN, big_min_waves(BITS, MBLK, NBLK, CONV)) void gemm_big_kernel(
+    const GemmArgs p) {
   static_assert(BITS >= 2 && BITS <= 4, "register codebooks hold at most 16 entries");
   constexpr int NT = 64 * WGM * WGN;
   constexpr int BM = WGM * MBLK * 32;
@@ -317,10 +325,21 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_big_kernel(const GemmArgs
   const bool vec = p.ldy % 4 == 0 && p.y_dt != DIMQ_F64;
 #pragma unroll
   for (int nb = 0; nb < NBLK; ++nb) {
+    // residuals of this column block: all loads out before the first store
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int nl = 8 * j + 4 * g;
       const int64_t n = n0 + wn * NBLK * 32 + nb * 32 + nl;
+      // 16-bit residuals of this row group: loads out before its stores (a
+      // whole-tile prefetch would cost this kernel an occupancy step)
+      ResPairs<4> rr[MBLK];
+      if ((MODE & kEpiRes) && res_pairs(p.epi, vec)) {
+#pragma unroll
+        for (int mb = 0; mb < MBLK; ++mb) {
+          const int64_t m = m0 + wm * MBLK * 32 + mb * 32 + col;
+          if (m < p.M && n + 4 <= p.N) res_issue<4>(p.epi, m * p.ldy + n, rr[mb]);
+        }
+      }
       float sc[4], bv[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -336,7 +355,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_big_kernel(const GemmArgs
         for (int i = 0; i < 4; ++i) v[i] = acc[mb][nb][4 * j + i] * sc[i] + bv[i];
         const int64_t off = m * p.ldy + n;
         if (vec && n + 4 <= p.N) {
-          epiN<4>(p.epi, off, v, true);
+          epi_m<MODE, 4>(p.epi, &rr[mb], off, true, v);
           if (p.y_dt == DIMQ_F32) {
             *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.y) + off) = make_float4(v[0], v[1], v[2], v[3]);
           } else {
@@ -349,7 +368,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_big_kernel(const GemmArgs
         } else {
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            if (n + i < p.N) store_from_float(p.y, p.y_dt, off + i, epi1(p.epi, off + i, v[i]));
+            if (n + i < p.N) store_from_float(p.y, p.y_dt, off + i, epi1_m<MODE>(p.epi, off + i, v[i]));
         }
       }
     }
@@ -362,7 +381,7 @@ typedef __attribute__((address_space(3))) void lds_void_g;
 // (wave tile (MBLK*32) x 32), activations two stages ahead in registers,
 // packed weights through a 3-stage LDS ring filled with global_load_lds
 // (no registers held by the weight loads).
-template <int BITS, int XT, int MBLK>
+template <int BITS, int XT, int MBLK, int MODE = kEpiNone>
 __global__ __launch_bounds__(256) void gemm_deep_kernel(const GemmArgs p) {
   static_assert(BITS >= 2 && BITS <= 4, "register codebooks hold at most 16 entries");
   constexpr int BM = MBLK * 32;
@@ -512,6 +531,21 @@ __global__ __launch_bounds__(256) void gemm_deep_kernel(const GemmArgs p) {
 
   // epilogue: acc[mb][4j + i] = y[m][n], m = m0 + mb*32 + col, n = n0 + 32*wave + 8j + 4g + i
   const bool vec = p.ldy % 4 == 0;
+  constexpr bool RES = (MODE & kEpiRes) != 0;
+  ResPairs<4> rr[RES ? 4 : 1][RES ? MBLK : 1];  // 16-bit residuals: all loads out before the first store
+  if constexpr ((MODE & kEpiRes) != 0) {
+    if (res_pairs(p.epi, vec)) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t n = n0 + wave * 32 + 8 * j + 4 * g;
+#pragma unroll
+      for (int mb = 0; mb < MBLK; ++mb) {
+        const int64_t m = m0 + mb * 32 + col;
+        if (m < p.M && n + 4 <= p.N) res_issue<4>(p.epi, m * p.ldy + n, rr[j][mb]);
+      }
+    }
+    }
+  }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int nlo = 8 * j + 4 * g;
@@ -531,7 +565,9 @@ __global__ __launch_bounds__(256) void gemm_deep_kernel(const GemmArgs p) {
       for (int i = 0; i < 4; ++i) v[i] = acc[mb][4 * j + i] * sc[i] + bv[i];
       const int64_t off = m * p.ldy + n;
       if (vec && n + 4 <= p.N) {
-        epiN<4>(p.epi, off, v, true);
+        const ResPairs<4>* rp = nullptr;
+        if constexpr (RES) rp = &rr[j][mb];
+        epi_m<MODE, 4>(p.epi, rp, off, true, v);
         if (p.y_dt == DIMQ_F32) {
           *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.y) + off) = make_float4(v[0], v[1], v[2], v[3]);
         } else {
@@ -544,38 +580,53 @@ __global__ __launch_bounds__(256) void gemm_deep_kernel(const GemmArgs p) {
       } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (n + i < p.N) store_from_float(p.y, p.y_dt, off + i, epi1(p.epi, off + i, v[i]));
+          if (n + i < p.N) store_from_float(p.y, p.y_dt, off + i, epi1_m<MODE>(p.epi, off + i, v[i]));
       }
     }
   }
 }
 
-template <int BITS, int XT, int MBLK>
+template <int BITS, int XT, int MBLK, int MODE = kEpiNone>
 int launch_deep(const GemmArgs& p, hipStream_t s) {
   constexpr int BM = MBLK * 32, BN = 128;
   const int64_t tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-  hipLaunchKernelGGL((gemm_deep_kernel<BITS, XT, MBLK>), dim3(static_cast<unsigned>(tiles)), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((gemm_deep_kernel<BITS, XT, MBLK, MODE>), dim3(static_cast<unsigned>(tiles)), dim3(256), 0, s,
+                     p);
   return check_launch("linear_codebook (large tiles, deep pipeline)");
 }
 
-template <int BITS, int XT, int WGM, int WGN, int MBLK, int NBLK, bool CONV = false>
+template <int BITS, int XT, int WGM, int WGN, int MBLK, int NBLK, bool CONV = false, int MODE = kEpiNone>
 int launch_big(const GemmArgs& p, hipStream_t s) {
   constexpr int BM = WGM * MBLK * 32, BN = WGN * NBLK * 32;
   const int64_t tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-  hipLaunchKernelGGL((gemm_big_kernel<BITS, XT, WGM, WGN, MBLK, NBLK, CONV>), dim3(static_cast<unsigned>(tiles)),
-                     dim3(64 * WGM * WGN), 0, s, p);
+  hipLaunchKernelGGL((gemm_big_kernel<BITS, XT, WGM, WGN, MBLK, NBLK, CONV, MODE>),
+                     dim3(static_cast<unsigned>(tiles)), dim3(64 * WGM * WGN), 0, s, p);
   return check_launch(CONV ? "conv2d_codebook (implicit GEMM, large tiles)" : "linear_codebook (large tiles)");
 }
 
 // Implicit-GEMM conv tiles: 0 = 128x128 (2x2 waves of 64x64), 1 = 64x128
 // (1x4 waves of 64x32), 2 = 256x128 (2x2 waves of 128x64).
+// Epilogue modes: none / relu / residual / residual + relu on tiles 0 and 1
+// (tile 2, an A/B option, only none; callers check gemm_conv_mode_ok).
+template <int BITS, int XT, int WGM, int WGN, int MBLK, int NBLK>
+int launch_big_conv_modes(const GemmArgs& p, int mode, hipStream_t s) {
+  switch (mode) {
+    case kEpiRelu: return launch_big<BITS, XT, WGM, WGN, MBLK, NBLK, true, kEpiRelu>(p, s);
+    case kEpiRes: return launch_big<BITS, XT, WGM, WGN, MBLK, NBLK, true, kEpiRes>(p, s);
+    case kEpiResRelu: return launch_big<BITS, XT, WGM, WGN, MBLK, NBLK, true, kEpiResRelu>(p, s);
+    default: return launch_big<BITS, XT, WGM, WGN, MBLK, NBLK, true, kEpiNone>(p, s);
+  }
+}
+
 template <int BITS>
 int launch_big_conv_bits(const GemmArgs& p, int xt, int tile, hipStream_t s) {
-#define DIMQ_CONV_TILES(XT)                                            \
-  switch (tile) {                                                      \
-    case 1: return launch_big<BITS, XT, 1, 4, 2, 1, true>(p, s);       \
-    case 2: return launch_big<BITS, XT, 2, 2, 4, 2, true>(p, s);       \
-    default: return launch_big<BITS, XT, 2, 2, 2, 2, true>(p, s);      \
+  const int mode = epi_mode(p.epi);
+  if (mode != kEpiNone && tile == 2) tile = 0;
+#define DIMQ_CONV_TILES(XT)                                                 \
+  switch (tile) {                                                           \
+    case 1: return launch_big_conv_modes<BITS, XT, 1, 4, 2, 1>(p, mode, s); \
+    case 2: return launch_big<BITS, XT, 2, 2, 4, 2, true>(p, s);            \
+    default: return launch_big_conv_modes<BITS, XT, 2, 2, 2, 2>(p, mode, s); \
   }
   if (xt == DIMQ_F16) {
     DIMQ_CONV_TILES(DIMQ_F16)
@@ -588,8 +639,30 @@ int launch_big_conv_bits(const GemmArgs& p, int xt, int tile, hipStream_t s) {
 //   0: 256x128 (1x4, 256x32)   1: 256x128 (2x2, 128x64)   2: 128x128 (2x2, 64x64)
 //   3: 256x256 (1x4, 256x64)   4: 192x256 (1x4, 192x64)   5: 128x256 (1x4, 128x64)
 //   6: 256x128 deep pipeline   7: 128x128 deep pipeline
+// Epilogue modes: none / relu / gelu / residual on the default tiles 2 and 7;
+// the other tiles (A/B options) only without epilogue.
+template <int BITS, int XT>
+int launch_big_linear_modes(const GemmArgs& p, int tile, int mode, hipStream_t s) {
+  if (tile == 7) {
+    switch (mode) {
+      case kEpiRelu: return launch_deep<BITS, XT, 4, kEpiRelu>(p, s);
+      case kEpiGelu: return launch_deep<BITS, XT, 4, kEpiGelu>(p, s);
+      case kEpiRes: return launch_deep<BITS, XT, 4, kEpiRes>(p, s);
+      default: return launch_deep<BITS, XT, 4, kEpiNone>(p, s);
+    }
+  }
+  switch (mode) {
+    case kEpiRelu: return launch_big<BITS, XT, 2, 2, 2, 2, false, kEpiRelu>(p, s);
+    case kEpiGelu: return launch_big<BITS, XT, 2, 2, 2, 2, false, kEpiGelu>(p, s);
+    case kEpiRes: return launch_big<BITS, XT, 2, 2, 2, 2, false, kEpiRes>(p, s);
+    default: return launch_big<BITS, XT, 2, 2, 2, 2, false, kEpiNone>(p, s);
+  }
+}
+
 template <int BITS>
 int launch_big_bits(const GemmArgs& p, int xt, int tile, hipStream_t s) {
+  const int mode = epi_mode(p.epi);
+  if (mode != kEpiNone && tile != 2 && tile != 7) tile = p.K >= 2048 ? 2 : 7;
 #define DIMQ_BIG_TILES(XT)                                               \
   switch (tile) {                                                        \
     case 0: return launch_big<BITS, XT, 1, 4, 8, 1>(p, s);               \
@@ -598,8 +671,7 @@ int launch_big_bits(const GemmArgs& p, int xt, int tile, hipStream_t s) {
     case 4: return launch_big<BITS, XT, 1, 4, 6, 2>(p, s);               \
     case 5: return launch_big<BITS, XT, 1, 4, 4, 2>(p, s);               \
     case 6: return launch_deep<BITS, XT, 8>(p, s);                       \
-    case 7: return launch_deep<BITS, XT, 4>(p, s);                       \
-    default: return launch_big<BITS, XT, 2, 2, 2, 2>(p, s);              \
+    default: return launch_big_linear_modes<BITS, XT>(p, tile, mode, s); \
   }
   switch (xt) {
     case DIMQ_F32: DIMQ_BIG_TILES(DIMQ_F32)

@@ -3,7 +3,4 @@
 
 namespace dimq {
 int launch_big_b3(const GemmArgs& p, int xt, int tile, hipStream_t s) { return launch_big_bits<3>(p, xt, tile, s); }
-int launch_big_conv_b3(const GemmArgs& p, int xt, int tile, hipStream_t s) {
-  return launch_big_conv_bits<3>(p, xt, tile, s);
-}
 }  // namespace dimq

@@ -3,7 +3,4 @@
 
 namespace dimq {
 int launch_big_b4(const GemmArgs& p, int xt, int tile, hipStream_t s) { return launch_big_bits<4>(p, xt, tile, s); }
-int launch_big_conv_b4(const GemmArgs& p, int xt, int tile, hipStream_t s) {
-  return launch_big_conv_bits<4>(p, xt, tile, s);
-}
 }  // namespace dimq

@@ -1,0 +1,8 @@
+// Instantiations of the large-tile implicit-GEMM conv for 2-bit weights.
+#include "gemm_big.h"
+
+namespace dimq {
+int launch_big_conv_b2(const GemmArgs& p, int xt, int tile, hipStream_t s) {
+  return launch_big_conv_bits<2>(p, xt, tile, s);
+}
+}  // namespace dimq

@@ -871,7 +871,7 @@ int64_t halo_prepared_words(int64_t OC, int64_t C, int64_t KH, int64_t KW, int b
 int64_t halo_tile_rows(int64_t C, int64_t KH, int64_t KW, int64_t stride, int64_t OH, int64_t OW);
 bool halo_weight_supported(int64_t C, int64_t KH, int64_t KW, int bits);
 bool halo_eligible(int64_t C, int64_t KH, int64_t KW, int64_t sh, int64_t sw, int64_t dh, int64_t dw,
-                   int64_t groups, int64_t OH, int64_t OW, int bits, int x_dtype);
+                   int64_t groups, int64_t OH, int64_t OW, int bits, int x_dtype, int epi_mode, int y_layout);
 int launch_conv_halo(const void* x, int x_dtype, int x_layout, int64_t B, int64_t C, int64_t H, int64_t W,
                      const uint32_t* kw, int bits, const void* cb, int cb_dtype, int64_t cb_rows, int64_t cb_size,
                      const void* bias, int bias_dtype, int64_t OC, int64_t KH, int64_t KW, int64_t stride,
@@ -883,7 +883,7 @@ int launch_prepare(const uint8_t* src, int64_t OC, int64_t C, int64_t KH, int64_
 // conv_stem.hip
 bool stem_eligible(int64_t C, int64_t OC, int64_t KH, int64_t KW, int64_t sh, int64_t sw, int64_t pw,
                    int64_t dh, int64_t dw, int64_t groups, int64_t OH, int64_t OW, int bits, int y_dtype,
-                   const void* x, const void* y);
+                   const void* x, const void* y, int epi_mode);
 int launch_conv_stem(const void* x, int x_dtype, int x_layout, int64_t B, int64_t C, int64_t H, int64_t W,
                      const uint8_t* w, int64_t w_bytes, int bits, const void* cb, int cb_dtype, int64_t cb_rows,
                      int64_t cb_size, const void* bias, int bias_dtype, int64_t OC, int64_t KH, int64_t KW,

@@ -26,6 +26,8 @@
 
 #include "gemm_kernel.h"
 
+#include <utility>
+
 namespace dimq {
 namespace {
 
@@ -36,6 +38,18 @@ constexpr int kBigLDA = kBigKS + 8;  // LDS row pitch (halves)
 
 __device__ __forceinline__ floatx16g mfma32(half8 a, half8 b, floatx16g c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>): a loop body
+// instantiated per index, for bodies too large for the unroller whose register
+// arrays must stay statically indexed.
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
 // 64 indices of row n from column k0 (K % 64 == 0): 8*BITS bytes, 16-byte
@@ -323,8 +337,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, big_min_waves(BITS, MBLK, NBLK, CON
   // epilogue: acc[mb][nb][4j + i] = y[m][n], m = block row m0 + wm*MBLK*32 +
   // mb*32 + col, n = n0 + wn*NBLK*32 + nb*32 + 8j + 4g + i
   const bool vec = p.ldy % 4 == 0 && p.y_dt != DIMQ_F64;
-#pragma unroll
-  for (int nb = 0; nb < NBLK; ++nb) {
+  static_for<NBLK>([&](auto nbc) {
+    constexpr int nb = decltype(nbc)::value;
     // residuals of this column block: all loads out before the first store
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -372,7 +386,206 @@ __global__ __launch_bounds__(64 * WGM * WGN, big_min_waves(BITS, MBLK, NBLK, CON
         }
       }
     }
+  });
+}
+
+// Shared-decode variant: the work-group decodes each 64-wide k stage of its
+// BN weight rows once, cooperatively, into LDS as fp16 (row pitch 72 halves,
+// the layout the activations use), and every wave reads its weight fragments
+// from there.  With per-lane decoding (gemm_big_kernel) every wave row of the
+// tile decodes the same columns again; here a weight is decoded once per
+// work-group, so the tile can be tall (BM = 256) and the decode and
+// activation-conversion work per MFMA drops.  Thread t decodes B_TASKS of the
+// 8 words (k16 step s, lane group g) of weight row t / (8 / B_TASKS).
+template <int BITS, int XT, int WGM, int WGN, int MBLK, int NBLK, int MODE = kEpiNone, int INTERLEAVE = 0>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_lds_kernel(const GemmArgs p) {
+  static_assert(BITS >= 2 && BITS <= 4, "register codebooks hold at most 16 entries");
+  constexpr int NT = 64 * WGM * WGN;
+  constexpr int BM = WGM * MBLK * 32;
+  constexpr int BN = WGN * NBLK * 32;
+  constexpr int E = 1 << BITS;
+  constexpr int A_TASKS = BM * (kBigKS / 16) / NT;
+  constexpr int B_TASKS = BN * 8 / NT;  // decode words per thread and stage
+  static_assert(A_TASKS * NT == BM * (kBigKS / 16), "activation groups split evenly over the threads");
+  static_assert(B_TASKS * NT == BN * 8 && 8 % B_TASKS == 0, "weight words split evenly over the threads");
+  constexpr int TPR = 8 / B_TASKS;  // threads per weight row
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kBigLDA];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * kBigLDA];
+  __shared__ float escale[BN];
+  // the codebook rows are staged in the second weight buffer, which is first
+  // written after the barrier that follows the codebook planes' setup
+  static_assert(BN * E * 4 <= BN * kBigLDA * 2, "codebook staging fits in one weight stage buffer");
+  float* cbs = reinterpret_cast<float*>(&Bs[1][0]);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 31;
+  const int g = lane >> 5;
+  const int wm = wave / WGN;
+  const int wn = wave - wm * WGN;
+  int64_t mt, nt;
+  tile_coords((p.N + BN - 1) / BN, mt, nt);
+  const int64_t m0 = mt * BM;
+  const int64_t n0 = nt * BN;
+
+  stage_codebook<E>(p.cb, p.cb_dt, p.cb_rows, p.cb_size, n0, BN, p.N, cbs, tid, NT);
+  __syncthreads();
+  // this thread's weight row and words
+  const int brl = tid / TPR;
+  const int bw0 = (tid - brl * TPR) * B_TASKS;
+  const int64_t brow = n0 + brl < p.N ? n0 + brl : p.N - 1;
+  CodebookRegs<BITS> cb;
+  {
+    const int e = planes_from_lds<BITS, false>(cbs + ((p.cb_rows == 1) ? 0 : brl * E), cb, cb);
+    if (bw0 == 0) escale[brl] = ldexpf(1.0f, -e);
   }
+
+  int64_t aoff[A_TASKS];
+  int alds[A_TASKS];
+#pragma unroll
+  for (int i = 0; i < A_TASKS; ++i) {
+    const int task = tid + NT * i;
+    const int m = task >> 2, kg = task & 3;
+    alds[i] = m * kBigLDA + 16 * kg;
+    const int64_t row = (m0 + m < p.M) ? m0 + m : p.M - 1;
+    aoff[i] = row * p.ldx + 16 * kg;
+  }
+
+  floatx16g acc[MBLK][NBLK];
+#pragma unroll
+  for (int mb = 0; mb < MBLK; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NBLK; ++nb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[mb][nb][i] = 0.0f;
+
+  const int64_t nk = p.K / kBigKS;
+  RawA<XT> ra0[A_TASKS], ra1[A_TASKS];
+  uint32_t bq0[2 * BITS], bq1[2 * BITS];
+  auto issue = [&](int64_t kt, RawA<XT> (&ra)[A_TASKS], uint32_t (&bq)[2 * BITS]) {
+    const int64_t k = (kt < nk ? kt : nk - 1) * kBigKS;
+#pragma unroll
+    for (int i = 0; i < A_TASKS; ++i) issue_a16<XT>(p.x, aoff[i] + k, ra[i]);
+    issue_b_stage<BITS>(p.w, brow, p.K, k, bq);
+  };
+  auto commit = [&](int buf, const RawA<XT> (&ra)[A_TASKS], const uint32_t (&bq)[2 * BITS]) {
+#pragma unroll
+    for (int i = 0; i < A_TASKS; ++i) {
+      uint32_t o[8];
+      convert_a16_big<BITS, XT>(ra[i], o);
+      uint4* dst = reinterpret_cast<uint4*>(&As[buf][alds[i]]);
+      dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
+      dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+    }
+#pragma unroll
+    for (int j = 0; j < B_TASKS; ++j) {
+      const int w = bw0 + j;  // word w: k16 step w >> 1, lane group w & 1
+      const half8 h = decode_word<BITS>(stage_word<BITS>(bq, w >> 1, w & 1), cb);
+      *reinterpret_cast<half8*>(&Bs[buf][brl * kBigLDA + 8 * w]) = h;
+    }
+  };
+  auto compute = [&](int buf) {
+    const uint16_t* arow = &As[buf][(wm * MBLK * 32 + col) * kBigLDA + 8 * g];
+    const uint16_t* bro = &Bs[buf][(wn * NBLK * 32 + col) * kBigLDA + 8 * g];
+#pragma unroll
+    for (int s = 0; s < kBigKS / 16; ++s) {
+      half8 xf[MBLK], wf[NBLK];
+#pragma unroll
+      for (int mb = 0; mb < MBLK; ++mb) xf[mb] = *reinterpret_cast<const half8*>(arow + mb * 32 * kBigLDA + 16 * s);
+#pragma unroll
+      for (int nb = 0; nb < NBLK; ++nb) wf[nb] = *reinterpret_cast<const half8*>(bro + nb * 32 * kBigLDA + 16 * s);
+#pragma unroll
+      for (int nb = 0; nb < NBLK; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < MBLK; ++mb) acc[mb][nb] = mfma32(wf[nb], xf[mb], acc[mb][nb]);
+    }
+  };
+  // One stage's MFMAs with the next stage's conversion and decode woven in
+  // between them (its loads were issued a full stage earlier), so the matrix
+  // cores and the VALU work at the same time within each wave; the weave
+  // writes the other LDS buffer, which every wave finished reading before the
+  // previous barrier.
+  auto step = [&](int buf, bool next, const RawA<XT> (&ra)[A_TASKS], const uint32_t (&bq)[2 * BITS]) {
+    compute(buf);
+    if (next) commit(buf ^ 1, ra, bq);
+    if constexpr (INTERLEAVE) {
+      constexpr int NMFMA = MBLK * NBLK * (kBigKS / 16);
+#pragma unroll
+      for (int i = 0; i < NMFMA; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, INTERLEAVE, 0);  // then VALU
+      }
+    }
+  };
+
+  // prologue: stages 0 and 1 loading, stage 0 committed, stage 2 loading
+  issue(0, ra0, bq0);
+  issue(1, ra1, bq1);
+  commit(0, ra0, bq0);
+  __syncthreads();
+  issue(2, ra0, bq0);
+  int64_t kt = 0;
+  for (; kt + 2 <= nk; kt += 2) {
+    step(0, true, ra1, bq1);  // compute stage kt, commit stage kt+1 (set 1)
+    __syncthreads();
+    issue(kt + 3, ra1, bq1);
+    step(1, kt + 2 < nk, ra0, bq0);  // compute stage kt+1, commit stage kt+2 (set 0)
+    __syncthreads();
+    issue(kt + 4, ra0, bq0);
+  }
+  if (kt < nk) compute(0);
+
+  // epilogue: acc[mb][nb][4j + i] = y[m][n], m = m0 + wm*MBLK*32 + mb*32 + col,
+  // n = n0 + wn*NBLK*32 + nb*32 + 8j + 4g + i
+  const bool vec = p.ldy % 4 == 0 && p.y_dt != DIMQ_F64;
+  static_for<NBLK>([&](auto nbc) {
+    constexpr int nb = decltype(nbc)::value;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int nl = wn * NBLK * 32 + nb * 32 + 8 * j + 4 * g;
+      const int64_t n = n0 + nl;
+      float sc[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sc[i] = escale[nl + i < BN ? nl + i : BN - 1];
+        bv[i] = (p.bias && n + i < p.N) ? load_as_float(p.bias, p.bias_dt, n + i) : 0.0f;
+      }
+      ResPairs<4> rr[MBLK];
+      if ((MODE & kEpiRes) && res_pairs(p.epi, vec)) {
+#pragma unroll
+        for (int mb = 0; mb < MBLK; ++mb) {
+          const int64_t m = m0 + wm * MBLK * 32 + mb * 32 + col;
+          if (m < p.M && n + 4 <= p.N) res_issue<4>(p.epi, m * p.ldy + n, rr[mb]);
+        }
+      }
+#pragma unroll
+      for (int mb = 0; mb < MBLK; ++mb) {
+        const int64_t m = m0 + wm * MBLK * 32 + mb * 32 + col;
+        if (m >= p.M) continue;
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = acc[mb][nb][4 * j + i] * sc[i] + bv[i];
+        const int64_t off = m * p.ldy + n;
+        if (vec && n + 4 <= p.N) {
+          epi_m<MODE, 4>(p.epi, &rr[mb], off, true, v);
+          if (p.y_dt == DIMQ_F32) {
+            *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.y) + off) = make_float4(v[0], v[1], v[2], v[3]);
+          } else {
+            uint32_t h[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) h[i] = p.y_dt == DIMQ_F16 ? float_to_f16_bits(v[i]) : float_to_bf16_bits(v[i]);
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.y) + off) =
+                make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (n + i < p.N) store_from_float(p.y, p.y_dt, off + i, epi1_m<MODE>(p.epi, off + i, v[i]));
+        }
+      }
+    }
+  });
 }
 
 typedef __attribute__((address_space(3))) void lds_void_g;
@@ -586,6 +799,15 @@ __global__ __launch_bounds__(256) void gemm_deep_kernel(const GemmArgs p) {
   }
 }
 
+template <int BITS, int XT, int WGM, int WGN, int MBLK, int NBLK, int MODE = kEpiNone, int INTERLEAVE = 0>
+int launch_lds(const GemmArgs& p, hipStream_t s) {
+  constexpr int BM = WGM * MBLK * 32, BN = WGN * NBLK * 32;
+  const int64_t tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+  hipLaunchKernelGGL((gemm_lds_kernel<BITS, XT, WGM, WGN, MBLK, NBLK, MODE, INTERLEAVE>),
+                     dim3(static_cast<unsigned>(tiles)), dim3(64 * WGM * WGN), 0, s, p);
+  return check_launch("linear_codebook (shared-decode tiles)");
+}
+
 template <int BITS, int XT, int MBLK, int MODE = kEpiNone>
 int launch_deep(const GemmArgs& p, hipStream_t s) {
   constexpr int BM = MBLK * 32, BN = 128;
@@ -639,10 +861,20 @@ int launch_big_conv_bits(const GemmArgs& p, int xt, int tile, hipStream_t s) {
 //   0: 256x128 (1x4, 256x32)   1: 256x128 (2x2, 128x64)   2: 128x128 (2x2, 64x64)
 //   3: 256x256 (1x4, 256x64)   4: 192x256 (1x4, 192x64)   5: 128x256 (1x4, 128x64)
 //   6: 256x128 deep pipeline   7: 128x128 deep pipeline
+//   8: 256x256 shared decode (4x2, 64x128), phases not interleaved
+//  10: 256x256 shared decode, next stage's decode woven between the MFMAs
 // Epilogue modes: none / relu / gelu / residual on the default tiles 2 and 7;
 // the other tiles (A/B options) only without epilogue.
 template <int BITS, int XT>
 int launch_big_linear_modes(const GemmArgs& p, int tile, int mode, hipStream_t s) {
+  if (tile == 10) {
+    switch (mode) {
+      case kEpiRelu: return launch_lds<BITS, XT, 4, 2, 2, 4, kEpiRelu, 8>(p, s);
+      case kEpiGelu: return launch_lds<BITS, XT, 4, 2, 2, 4, kEpiGelu, 8>(p, s);
+      case kEpiRes: return launch_lds<BITS, XT, 4, 2, 2, 4, kEpiRes, 8>(p, s);
+      default: return launch_lds<BITS, XT, 4, 2, 2, 4, kEpiNone, 8>(p, s);
+    }
+  }
   if (tile == 7) {
     switch (mode) {
       case kEpiRelu: return launch_deep<BITS, XT, 4, kEpiRelu>(p, s);
@@ -662,9 +894,10 @@ int launch_big_linear_modes(const GemmArgs& p, int tile, int mode, hipStream_t s
 template <int BITS>
 int launch_big_bits(const GemmArgs& p, int xt, int tile, hipStream_t s) {
   const int mode = epi_mode(p.epi);
-  if (mode != kEpiNone && tile != 2 && tile != 7) tile = p.K >= 2048 ? 2 : 7;
+  if (mode != kEpiNone && tile != 2 && tile != 7 && tile != 10) tile = p.K >= 2048 ? 2 : 7;
 #define DIMQ_BIG_TILES(XT)                                               \
   switch (tile) {                                                        \
+    case 8: return launch_lds<BITS, XT, 4, 2, 2, 4, kEpiNone, 0>(p, s);  \
     case 0: return launch_big<BITS, XT, 1, 4, 8, 1>(p, s);               \
     case 1: return launch_big<BITS, XT, 2, 2, 4, 2>(p, s);               \
     case 3: return launch_big<BITS, XT, 1, 4, 8, 2>(p, s);               \

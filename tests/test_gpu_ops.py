@@ -291,11 +291,12 @@ def test_linear_codebook_dtypes(gpu, xdt, odt):
 
 
 @pytest.mark.parametrize("bits", [2, 3, 4])
-@pytest.mark.parametrize("tile", ["0", "2", "6", "7"])
+@pytest.mark.parametrize("tile", ["0", "2", "6", "7", "8", "10"])
 @pytest.mark.parametrize("M,N,K,xdt", [(257, 130, 128, torch.float32), (520, 384, 192, torch.bfloat16),
                                        (65, 256, 64, torch.float16)])
 def test_linear_codebook_large_tiles(gpu, monkeypatch, bits, tile, M, N, K, xdt):
-    """The 32x32x16 large-tile kernels (256x128 / 128x128 tiles, deep-pipeline variants), M / N tails."""
+    """The 32x32x16 large-tile kernels (256x128 / 128x128 tiles, deep-pipeline and shared-decode
+    variants), M / N tails."""
     monkeypatch.setenv("DIMQ_GEMM_BIG", tile)
     ops = _ops()
     for per_channel in (True, False):
@@ -349,6 +350,8 @@ _ACTS = {None: lambda t: t, "relu": torch.relu, "gelu": torch.nn.functional.gelu
 @pytest.mark.parametrize("case", [
     dict(M=300, N=256, K=512, bits=4, xdt=torch.bfloat16, out=torch.bfloat16, rdt=torch.bfloat16, act="gelu"),  # deep
     dict(M=200, N=256, K=2048, bits=2, xdt=torch.float16, out=torch.float32, rdt=torch.float32, act="relu"),  # big
+    dict(M=2100, N=320, K=256, bits=4, xdt=torch.bfloat16, out=torch.bfloat16, rdt=torch.bfloat16, act=None),  # lds
+    dict(M=2050, N=264, K=2048, bits=3, xdt=torch.bfloat16, out=torch.float32, rdt=torch.float16, act="gelu"),
     dict(M=2, N=64, K=4096, bits=3, xdt=torch.bfloat16, out=torch.float32, rdt=torch.float16, act=None),  # gemv fast
     dict(M=9, N=100, K=256, bits=4, xdt=torch.float32, out=torch.float16, rdt=torch.float32, act="gelu"),  # gemv
     dict(M=70, N=50, K=96, bits=3, xdt=torch.float16, out=torch.float32, rdt=torch.bfloat16, act="relu"),  # generic

@@ -411,7 +411,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_lds_kernel(const GemmArgs
   constexpr int TPR = 8 / B_TASKS;  // threads per weight row
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kBigLDA];
   __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * kBigLDA];
-  __shared__ float escale[BN];
+  __shared__ float escale[BN], ebias[BN];  // per tile column: 2^-e and the bias
   // the codebook rows are staged in the second weight buffer, which is first
   // written after the barrier that follows the codebook planes' setup
   static_assert(BN * E * 4 <= BN * kBigLDA * 2, "codebook staging fits in one weight stage buffer");
@@ -429,17 +429,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_lds_kernel(const GemmArgs
   const int64_t m0 = mt * BM;
   const int64_t n0 = nt * BN;
 
-  stage_codebook<E>(p.cb, p.cb_dt, p.cb_rows, p.cb_size, n0, BN, p.N, cbs, tid, NT);
-  __syncthreads();
   // this thread's weight row and words
   const int brl = tid / TPR;
   const int bw0 = (tid - brl * TPR) * B_TASKS;
   const int64_t brow = n0 + brl < p.N ? n0 + brl : p.N - 1;
-  CodebookRegs<BITS> cb;
-  {
-    const int e = planes_from_lds<BITS, false>(cbs + ((p.cb_rows == 1) ? 0 : brl * E), cb, cb);
-    if (bw0 == 0) escale[brl] = ldexpf(1.0f, -e);
-  }
+  CodebookRegs<BITS> cb;  // set in the prologue, after the first stages' loads are out
 
   int64_t aoff[A_TASKS];
   int alds[A_TASKS];
@@ -519,9 +513,19 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_lds_kernel(const GemmArgs
     }
   };
 
-  // prologue: stages 0 and 1 loading, stage 0 committed, stage 2 loading
+  // prologue: stages 0 and 1 loading while the codebook rows are staged (the
+  // two latencies overlap), stage 0 committed, stage 2 loading
   issue(0, ra0, bq0);
   issue(1, ra1, bq1);
+  stage_codebook<E>(p.cb, p.cb_dt, p.cb_rows, p.cb_size, n0, BN, p.N, cbs, tid, NT);
+  __syncthreads();
+  {
+    const int e = planes_from_lds<BITS, false>(cbs + ((p.cb_rows == 1) ? 0 : brl * E), cb, cb);
+    if (bw0 == 0) {
+      escale[brl] = ldexpf(1.0f, -e);
+      ebias[brl] = (p.bias && n0 + brl < p.N) ? load_as_float(p.bias, p.bias_dt, n0 + brl) : 0.0f;
+    }
+  }
   commit(0, ra0, bq0);
   __syncthreads();
   issue(2, ra0, bq0);
@@ -536,56 +540,89 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_lds_kernel(const GemmArgs
   }
   if (kt < nk) compute(0);
 
-  // epilogue: acc[mb][nb][4j + i] = y[m][n], m = m0 + wm*MBLK*32 + mb*32 + col,
-  // n = n0 + wn*NBLK*32 + nb*32 + 8j + 4g + i
-  const bool vec = p.ldy % 4 == 0 && p.y_dt != DIMQ_F64;
-  static_for<NBLK>([&](auto nbc) {
-    constexpr int nb = decltype(nbc)::value;
+  // Epilogue through LDS, in NBLK passes: pass nb parks every wave's column
+  // block nb (acc[mb][nb][4j + i] = tile row wm*MBLK*32 + mb*32 + col, column
+  // wn*32 + 8j + 4g + i of the pass) as fp32 in the activation buffers, then
+  // the work-group stores the pass as 8-column chunks of rows: 16-byte stores
+  // of contiguous rows, residuals loaded before the stores, and one compact
+  // loop instead of an unrolled store per accumulator (the unrolled form made
+  // the kernel's once-per-tile tail the size of its instruction cache).
+  constexpr int PW = WGN * 32;          // columns per pass
+  constexpr int OTP = PW + 4;           // fp32 row pitch of the parked pass
+  static_assert(BM * OTP * 4 <= 2 * BM * kBigLDA * 2, "a parked pass fits in the activation buffers");
+  constexpr int CH = BM * PW / 8;       // 8-column chunks per pass
+  constexpr int CPT = (CH + NT - 1) / NT;  // chunks per thread
+  float* ot = reinterpret_cast<float*>(&As[0][0]);
+  __syncthreads();  // an odd-stage tail may still be reading the activation buffers
+  const bool vec8 = p.ldy % 8 == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0 && p.y_dt != DIMQ_F64;
+  for (int nb = 0; nb < NBLK; ++nb) {
+    static_for<NBLK>([&](auto nbc) {
+      constexpr int NB = decltype(nbc)::value;
+      if (NB != nb) return;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int nl = wn * NBLK * 32 + nb * 32 + 8 * j + 4 * g;
-      const int64_t n = n0 + nl;
-      float sc[4], bv[4];
+      for (int mb = 0; mb < MBLK; ++mb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sc[i] = escale[nl + i < BN ? nl + i : BN - 1];
-        bv[i] = (p.bias && n + i < p.N) ? load_as_float(p.bias, p.bias_dt, n + i) : 0.0f;
-      }
-      ResPairs<4> rr[MBLK];
-      if ((MODE & kEpiRes) && res_pairs(p.epi, vec)) {
+        for (int j = 0; j < 4; ++j)
+          *reinterpret_cast<float4*>(ot + (wm * MBLK * 32 + mb * 32 + col) * OTP + wn * 32 + 8 * j + 4 * g) =
+              make_float4(acc[mb][NB][4 * j], acc[mb][NB][4 * j + 1], acc[mb][NB][4 * j + 2], acc[mb][NB][4 * j + 3]);
+    });
+    __syncthreads();
+    // chunk c: tile row c / (PW/8), pass columns 8*(c % (PW/8)) .. +8, i.e. wave
+    // column block q / 4 (wn), its 8-column group q % 4
+    ResPairs<8> rr[CPT];
+    if ((MODE & kEpiRes) && res_pairs(p.epi, vec8)) {
 #pragma unroll
-        for (int mb = 0; mb < MBLK; ++mb) {
-          const int64_t m = m0 + wm * MBLK * 32 + mb * 32 + col;
-          if (m < p.M && n + 4 <= p.N) res_issue<4>(p.epi, m * p.ldy + n, rr[mb]);
-        }
-      }
-#pragma unroll
-      for (int mb = 0; mb < MBLK; ++mb) {
-        const int64_t m = m0 + wm * MBLK * 32 + mb * 32 + col;
-        if (m >= p.M) continue;
-        float v[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = acc[mb][nb][4 * j + i] * sc[i] + bv[i];
-        const int64_t off = m * p.ldy + n;
-        if (vec && n + 4 <= p.N) {
-          epi_m<MODE, 4>(p.epi, &rr[mb], off, true, v);
-          if (p.y_dt == DIMQ_F32) {
-            *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.y) + off) = make_float4(v[0], v[1], v[2], v[3]);
-          } else {
-            uint32_t h[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) h[i] = p.y_dt == DIMQ_F16 ? float_to_f16_bits(v[i]) : float_to_bf16_bits(v[i]);
-            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.y) + off) =
-                make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-          }
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (n + i < p.N) store_from_float(p.y, p.y_dt, off + i, epi1_m<MODE>(p.epi, off + i, v[i]));
-        }
+      for (int u = 0; u < CPT; ++u) {
+        const int c = tid + u * NT;
+        const int r = c / (PW / 8), q = c - r * (PW / 8);
+        const int64_t m = m0 + r;
+        const int64_t n = n0 + (q >> 2) * NBLK * 32 + nb * 32 + 8 * (q & 3);
+        if (c < CH && m < p.M && n + 8 <= p.N) res_issue<8>(p.epi, m * p.ldy + n, rr[u]);
       }
     }
-  });
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+      const int c = tid + u * NT;
+      if (c >= CH) break;
+      const int r = c / (PW / 8), q = c - r * (PW / 8);
+      const int64_t m = m0 + r;
+      const int nl = (q >> 2) * NBLK * 32 + nb * 32 + 8 * (q & 3);  // column within the tile
+      const int64_t n = n0 + nl;
+      if (m >= p.M) continue;
+      const float4 a0 = *reinterpret_cast<const float4*>(ot + r * OTP + 8 * q);
+      const float4 a1 = *reinterpret_cast<const float4*>(ot + r * OTP + 8 * q + 4);
+      float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int ni = nl + i < BN ? nl + i : BN - 1;
+        v[i] = v[i] * escale[ni] + ebias[ni];
+      }
+      const int64_t off = m * p.ldy + n;
+      if (vec8 && n + 8 <= p.N) {
+        epi_m<MODE, 8>(p.epi, &rr[u], off, true, v);
+        if (p.y_dt == DIMQ_F32) {
+          float* yp = reinterpret_cast<float*>(p.y) + off;
+          *reinterpret_cast<float4*>(yp) = make_float4(v[0], v[1], v[2], v[3]);
+          *reinterpret_cast<float4*>(yp + 4) = make_float4(v[4], v[5], v[6], v[7]);
+        } else {
+          uint32_t h[8];
+          if (p.y_dt == DIMQ_F16) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) h[i] = float_to_f16_bits(v[i]);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) h[i] = float_to_bf16_bits(v[i]);
+          }
+          *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p.y) + off) =
+              make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+        }
+      } else {
+        for (int i = 0; i < 8; ++i)
+          if (n + i < p.N) store_from_float(p.y, p.y_dt, off + i, epi1_m<MODE>(p.epi, off + i, v[i]));
+      }
+    }
+    __syncthreads();  // the next pass overwrites the parked values
+  }
 }
 
 typedef __attribute__((address_space(3))) void lds_void_g;

@@ -26,36 +26,18 @@ int gemm_fast_tile(int tile, const GemmArgs& p, int bits) {
 // and aligned rows/streams.  Measured on the ViT-B/16 shapes (M = 12,608) and
 // cfg1: the deep-pipeline 128x128 tile (7) is fastest for K < 2048, the 2x2
 // 128x128 tile (2) for K >= 2048.  Returns -1 when the shape does not qualify.
-int gemm_device_cus() {
-  static int cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] <= 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cache[dev] = n;
-  }
-  return cache[dev];
-}
-
 int gemm_big_tile(const GemmArgs& p, int bits, int x_dtype, int variant) {
   if (variant == DIMQ_VARIANT_SMALL_M || p.conv || !(bits == 2 || bits == 3 || bits == 4)) return -1;
   const int mode = epi_mode(p.epi);  // epilogues the large tiles are instantiated for
   if (!(mode == kEpiNone || mode == kEpiRelu || mode == kEpiGelu || mode == kEpiRes)) return -1;
   if (p.M <= 64 || p.K % 64 != 0 || !p.fast_b || !p.vec_a) return -1;
-  const char* force = getenv("DIMQ_GEMM_BIG");  // A/B runs: -1 = off, 0..7 = tile
+  const char* force = getenv("DIMQ_GEMM_BIG");  // A/B runs: -1 = off, 0..8 or 10 = tile
   if (force) return (atoi(force) >= 0 && atoi(force) <= 10 && atoi(force) != 9) ? atoi(force) : -1;
-  // 256x256 shared-decode tiles (one work-group per CU) when the K loop is long
-  // or their tiles fill the CUs' rounds well; else the 128x128 tiles (two work-
-  // groups per CU, finer rounds).  Measured on the ViT-B/16 shapes at M 12,608:
-  // fc2 (K 3072) 117 vs 150 us, qkv 108 vs 117, proj 51 vs 55; fc1 (600 tiles
-  // in 2.3 rounds) 157 vs 151 us with the deep 128x128 kernel.
-  if (p.M >= 2048 && x_dtype != DIMQ_F32) {  // fp32 activations spill the 256x256 tile's registers
-    const int64_t t256 = ((p.M + 255) / 256) * ((p.N + 255) / 256);
-    const int64_t cus = gemm_device_cus();
-    const double eff = static_cast<double>(t256) / (static_cast<double>((t256 + cus - 1) / cus) * cus);
-    if (p.K >= 2048 || p.N <= 1024 || eff >= 0.85) return 10;
-  }
+  // 256x256 shared-decode tiles for large M (measured on the ViT-B/16 shapes at
+  // M 12,608, bf16: qkv 84 vs 104 us, proj 40 vs 50, fc1 114 vs 134, fc2 104 vs
+  // 133 against the best 128x128 tile); below M 2048 the 128x128 tiles fill
+  // the CUs better (M 1000: 17 vs 30 us).
+  if (p.M >= 2048 && x_dtype != DIMQ_F32) return 10;  // fp32 activations spill its registers
   return p.K >= 2048 ? 2 : 7;
 }
 

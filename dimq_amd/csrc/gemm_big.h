@@ -149,6 +149,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, big_min_waves(BITS, MBLK, NBLK, CON
   static_assert(A_TASKS * NT == BM * (kBigKS / 16), "tile rows must split evenly over the threads");
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kBigLDA];
   __shared__ float cbs[BN * E];
+  __shared__ float ebias[BN];  // the tile's bias, staged once (the epilogue's loads would serialise)
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -163,6 +164,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, big_min_waves(BITS, MBLK, NBLK, CON
   const int64_t n0 = nt * BN;
 
   stage_codebook<E>(p.cb, p.cb_dt, p.cb_rows, p.cb_size, n0, BN, p.N, cbs, tid, NT);
+  for (int c = tid; c < BN; c += NT) ebias[c] = (p.bias && n0 + c < p.N) ? load_as_float(p.bias, p.bias_dt, n0 + c) : 0.0f;
   __syncthreads();
   CodebookRegs<BITS> cb[NBLK];
   float rscale[NBLK];
@@ -358,7 +360,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, big_min_waves(BITS, MBLK, NBLK, CON
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         sc[i] = __shfl(rscale[nb], nl + i, 32);
-        bv[i] = (p.bias && n + i < p.N) ? load_as_float(p.bias, p.bias_dt, n + i) : 0.0f;
+        bv[i] = ebias[wn * NBLK * 32 + nb * 32 + nl + i];
       }
 #pragma unroll
       for (int mb = 0; mb < MBLK; ++mb) {
@@ -647,6 +649,7 @@ __global__ __launch_bounds__(256) void gemm_deep_kernel(const GemmArgs p) {
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kBigLDA];
   __shared__ __attribute__((aligned(16))) uint8_t Bs[RING][BSTAGE];
   __shared__ float cbs[BN * E];
+  __shared__ float ebias[BN];  // the tile's bias, staged once (the epilogue's loads would serialise)
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -659,6 +662,7 @@ __global__ __launch_bounds__(256) void gemm_deep_kernel(const GemmArgs p) {
   const int64_t n0 = nt * BN;
 
   stage_codebook<E>(p.cb, p.cb_dt, p.cb_rows, p.cb_size, n0, BN, p.N, cbs, tid, 256);
+  if (tid < BN) ebias[tid] = (p.bias && n0 + tid < p.N) ? load_as_float(p.bias, p.bias_dt, n0 + tid) : 0.0f;
   __syncthreads();
   CodebookRegs<BITS> cb;
   float rscale;
@@ -804,7 +808,7 @@ __global__ __launch_bounds__(256) void gemm_deep_kernel(const GemmArgs p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       sc[i] = __shfl(rscale, nlo + i, 32);
-      bv[i] = (p.bias && n + i < p.N) ? load_as_float(p.bias, p.bias_dt, n + i) : 0.0f;
+      bv[i] = ebias[wave * 32 + nlo + i];
     }
 #pragma unroll
     for (int mb = 0; mb < MBLK; ++mb) {

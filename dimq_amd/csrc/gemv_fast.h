@@ -35,8 +35,6 @@ __global__ __launch_bounds__(1024) void gemv_fast_kernel(const GemmArgs p) {
   const int64_t n = n0 + col < p.N ? n0 + col : p.N - 1;
   const int rounds = static_cast<int>(p.K / (KL * WAVES * 4));  // k-ranges of KL per lane
 
-  stage_codebook<E>(p.cb, p.cb_dt, p.cb_rows, p.cb_size, n0, 16, p.N, cbs, tid, WAVES * 64);
-
   floatx4 acc = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
   const bool arow = col < p.M;
   CodebookRegs<BITS> cb;
@@ -78,6 +76,9 @@ __global__ __launch_bounds__(1024) void gemv_fast_kernel(const GemmArgs p) {
       }
     }
     if (r == 0) {
+      // the codebook loads go out after the round's weight and activation
+      // loads, so their latencies overlap instead of adding up
+      stage_codebook<E>(p.cb, p.cb_dt, p.cb_rows, p.cb_size, n0, 16, p.N, cbs, tid, WAVES * 64);
       __syncthreads();  // codebook staged
       const int e = planes_from_lds<BITS, false>(cbs + ((p.cb_rows == 1) ? 0 : col * E), cb, cb);
       colscale = ldexpf(1.0f, -e);

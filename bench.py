@@ -92,7 +92,7 @@ def make_cfg2(dev, rotations, layout="nchw"):
     )
 
 
-def make_cfg1(dev, rotations):
+def make_cfg1(dev, rotations, variant="auto"):
     from dimq_amd import ops
     from dimq_amd.codebook import assign_indices, init_centers_per_channel
     from dimq_amd.export import pack_indices
@@ -107,7 +107,8 @@ def make_cfg1(dev, rotations):
     xs = [torch.randn(1576, 768, generator=g).to(dev) for _ in range(rotations)]
 
     def step(i):
-        return ops.dimq_linear_codebook(xs[i], packed, cb, 4, bias, 3072, 768, out_dtype=torch.float32)
+        return ops.dimq_linear_codebook(xs[i], packed, cb, 4, bias, 3072, 768, out_dtype=torch.float32,
+                                        variant=variant)
 
     alg_bytes = 1576 * 768 * 4 + packed.numel() + cb.numel() * 4 + 3072 * 4 + 1576 * 3072 * 4
     flops = 2.0 * 1576 * 3072 * 768
@@ -132,7 +133,7 @@ def make_cfg1(dev, rotations):
     )
 
 
-def make_cfg5(dev, rotations, M=16):
+def make_cfg5(dev, rotations, M=16, variant="auto"):
     from dimq_amd import ops
     from dimq_amd.codebook import assign_indices, init_centers_per_channel
     from dimq_amd.export import pack_indices
@@ -148,7 +149,8 @@ def make_cfg5(dev, rotations, M=16):
     xs = [torch.randn(M, 4096, generator=g).bfloat16().to(dev) for _ in range(rotations)]
 
     def step(i):
-        return ops.dimq_linear_codebook(xs[i], packs[i], cb, 3, None, 4096, 4096, out_dtype=torch.float32)
+        return ops.dimq_linear_codebook(xs[i], packs[i], cb, 3, None, 4096, 4096, out_dtype=torch.float32,
+                                        variant=variant)
 
     alg_bytes = packs[0].numel() + cb.numel() * 4 + M * 4096 * 2 + M * 4096 * 4
     flops = 2.0 * M * 4096 * 4096
@@ -416,6 +418,8 @@ def main():
     ap.add_argument("--m", type=int, default=16, help="rows for cfg5")
     ap.add_argument("--direction", default="unpack", choices=["pack", "unpack"])
     ap.add_argument("--layout", default="nchw", choices=["nchw", "nhwc"], help="cfg2 activation layout")
+    ap.add_argument("--variant", default="auto", choices=["auto", "small_m", "mfma"],
+                    help="cfg1/cfg5: force the LUT-gather (small_m) or dequant+MFMA kernel family")
     ap.add_argument("--rotations", type=int, default=0,
                     help="buffer sets to rotate (0 = enough for > 512 MB; smaller values let the MALL serve repeats)")
     ap.add_argument("--no-cpu", action="store_true")
@@ -433,6 +437,8 @@ def main():
     kw = {}
     if args.config == "cfg5":
         kw["M"] = args.m
+    if args.config in ("cfg1", "cfg5"):
+        kw["variant"] = args.variant
     if args.config == "codec":
         kw["direction"] = args.direction
     if args.config == "cfg2":
@@ -450,6 +456,8 @@ def main():
     del probe
     torch.cuda.empty_cache()
     wl = make(dev, rotations, **kw)
+    if "variant" in kw:
+        wl["extra_config"]["variant"] = kw["variant"]
 
     err = None if args.no_check else wl["check"]()
     ms, steps = time_gpu(wl, rotations, args.steps, args.warmup)

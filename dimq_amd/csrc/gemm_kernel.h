@@ -444,6 +444,7 @@ __global__ __launch_bounds__(256) void gemm_cb8_kernel(const GemmArgs p) {
     const int64_t n = n0 + r;
     const int64_t row = (p.cb_rows == 1) ? 0 : nz + n;
     float mx = 0.0f;
+#pragma unroll 16  // independent loads back to back, not one latency per entry
     for (int j = part; j < 256; j += 4) {
       const float c = (n < p.N && j < p.cb_size) ? load_as_float(p.cb, p.cb_dt, row * p.cb_size + j) : 0.0f;
       mx = fmaxf(mx, fabsf(c));
@@ -457,6 +458,7 @@ __global__ __launch_bounds__(256) void gemm_cb8_kernel(const GemmArgs p) {
     const int64_t row = (p.cb_rows == 1) ? 0 : nz + n;
     const float mx = fmaxf(fmaxf(rmax[r][0], rmax[r][1]), fmaxf(rmax[r][2], rmax[r][3]));
     const int e = cb_exponent(mx);
+#pragma unroll 16
     for (int j = part; j < 256; j += 4) {
       const float c = (n < p.N && j < p.cb_size) ? load_as_float(p.cb, p.cb_dt, row * p.cb_size + j) : 0.0f;
       cbs[r * 256 + j] = (uint16_t)float_to_f16_bits(ldexpf(c, e));

@@ -423,6 +423,21 @@ def test_fused_epilogue_errors(gpu):
         ops.dimq_linear_codebook(x, packed.to(gpu), cb.to(gpu), 4, None, 16, 64, activation="tanh")
 
 
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_linear_codebook_cfg5_full_shape(gpu, M):
+    """BASELINE cfg5 at full size: X bf16 [M, 4096], W [4096, 4096] N(0, 0.02), 3-bit per-channel codebook
+    (8 centroids), indices packed across byte boundaries; the decode GEMV kernels."""
+    ops = _ops()
+    announce(f"linear_codebook cfg5 M={M}")
+    g = _gen(40 + M)
+    cb, idx, packed = _codebook_case(4096, 4096, 3, True, g)
+    x = torch.randn(M, 4096, generator=g).bfloat16()
+    y = ops.dimq_linear_codebook(x.to(gpu), packed.to(gpu), cb.to(gpu), 3, None, 4096, 4096,
+                                 out_dtype=torch.float32)
+    ref = oracle.linear_dequant_reference(x.float(), packed, 3, cb, 4096, 4096)
+    assert oracle.rel_err(y, ref) <= TOL, oracle.rel_err(y, ref)
+
+
 def test_linear_codebook_small_codebook_and_errors(gpu):
     ops = _ops()
     g = _gen(5)

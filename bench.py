@@ -323,9 +323,90 @@ def make_copy(dev, rotations):
     )
 
 
+def make_w4a4(dev, rotations, op="linear"):
+    """The reference's own W4A4 ops (dimq::linear_lut / dimq::conv2d_lut) at the cfg1 / cfg2 shapes.
+
+    One 16-entry per-layer fp16 codebook (the packed exporter's format,
+    dimq_backend/export.py:167,217), u4 activations with scale/zero point;
+    y fp32.  One step = one op call (activation quantization pass + GEMM/conv).
+    """
+    from dimq_amd import ops
+    from dimq_amd.codebook import assign_indices
+    from dimq_amd.export import pack_indices
+
+    g = torch.Generator().manual_seed(6)
+    cb16 = torch.linspace(-0.06, 0.06, 16).half()
+    cb_dev = cb16.to(dev)
+    scale, zp = 0.25, 8
+    if op == "linear":
+        N, K, M = 3072, 768, 1576
+        w = torch.randn(N, K, generator=g) * 0.02
+        b = torch.randn(N, generator=g) * 0.02
+        packed = pack_indices(assign_indices(w, cb16.float()), 4).to(dev)
+        bias = b.to(dev)
+        xs = [torch.randn(M, K, generator=g).to(dev) for _ in range(rotations)]
+
+        def step(i):
+            return ops.dimq_linear_lut(xs[i], packed, cb_dev, scale, zp, bias, N, K)
+
+        x_bytes, y_bytes = M * K * 4, M * N * 4
+        flops = 2.0 * M * N * K
+        full = M
+
+        def cpu_step(rows):
+            import oracle
+            return oracle.linear_lut(xs[0][:rows].cpu(), packed.cpu(), cb16.float(), scale, zp, b, N, K)
+
+        def check():
+            import oracle
+            ref = oracle.linear_lut(xs[0].cpu(), packed.cpu(), cb16.float(), scale, zp, b, N, K)
+            return oracle.rel_err(step(0), torch.from_numpy(ref))
+
+        workload = ("reference W4A4 linear_lut at the cfg1 shape: X fp32 [1576,768], W [3072,768] 4-bit, one 16-entry "
+                    "fp16 codebook, u4 activations (scale 0.25, zp 8), bias, Y fp32")
+        extra = {"M": M, "N": N, "K": K, "bits": 4, "codebook": "per_layer_fp16", "op": "linear_lut"}
+    else:
+        shape = (64, 64, 3, 3)
+        w = _conv_weight_cfg2(g)
+        packed = pack_indices(assign_indices(w.reshape(64, -1), cb16.float()), 4).to(dev)
+        xs = [torch.relu(torch.randn(32, 64, 56, 56, generator=g)).half().to(dev) for _ in range(rotations)]
+
+        def step(i):
+            return ops.dimq_conv2d_lut(xs[i], packed, cb_dev, scale, zp, None, shape, (1, 1), (1, 1), (1, 1), 1)
+
+        x_bytes, y_bytes = 32 * 64 * 56 * 56 * 2, 32 * 64 * 56 * 56 * 4
+        flops = 2.0 * 32 * 56 * 56 * 64 * 64 * 9
+        full = 32
+
+        def cpu_step(batch):
+            import oracle
+            return oracle.conv2d_lut(xs[0][:batch].cpu().float(), packed.cpu(), cb16.float(), scale, zp, None, shape,
+                                     1, 1, 1, 1)
+
+        def check():
+            import oracle
+            ref = oracle.conv2d_lut(xs[0].cpu().float(), packed.cpu(), cb16.float(), scale, zp, None, shape, 1, 1, 1,
+                                    1)
+            return oracle.rel_err(step(0), torch.from_numpy(ref))
+
+        workload = ("reference W4A4 conv2d_lut at the cfg2 shape: x fp16 [32,64,56,56] (ReLU N(0,1)), W [64,64,3,3] "
+                    "4-bit, one 16-entry fp16 codebook, u4 activations (scale 0.25, zp 8), stride 1, pad 1, y fp32 NCHW")
+        extra = {"global_batch": 32, "in_shape": [32, 64, 56, 56], "weight_shape": list(shape), "bits": 4,
+                 "codebook": "per_layer_fp16", "op": "conv2d_lut"}
+    alg_bytes = x_bytes + y_bytes + packed.numel() + 32
+    return dict(
+        name=f"w4a4_{op}", workload=workload, step=step, flops=flops, alg_bytes=alg_bytes, bound="hbm",
+        dtype="fp16", unit="TFLOP/s", per_step_units=flops / 1e12, cpu_step=cpu_step, cpu_full_batch=full,
+        check=check, extra_config=extra, per_set_bytes=x_bytes + y_bytes,
+        cpu_cores=1, cpu_desc="C oracle of the reference LUT loop (reference.py:59-88 / 147-205), one thread",
+    )
+
+
 FIXED_ROTATIONS = {"vit": 4, "resnet18": 4}
 WORKLOADS = {"cfg2": make_cfg2, "cfg1": make_cfg1, "cfg5": make_cfg5, "codec": make_codec, "copy": make_copy,
-             "vit": make_vit, "resnet18": make_resnet18}
+             "vit": make_vit, "resnet18": make_resnet18,
+             "w4a4_linear": lambda dev, r: make_w4a4(dev, r, "linear"),
+             "w4a4_conv": lambda dev, r: make_w4a4(dev, r, "conv")}
 
 
 # ---------------------------------------------------------------------------
@@ -404,9 +485,9 @@ def time_cpu(wl, budget_s=15.0):
         model = [l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name")][0]
     except Exception:
         model = "unknown"
-    return dict(value=value, unit=wl["unit"], cores=threads, kind="port",
+    return dict(value=value, unit=wl["unit"], cores=wl.get("cpu_cores", threads), kind="port",
                 sample=f"{sample}/{full} of one step ({wl['name']}), median of {len(times)} runs after 3 warm-ups; "
-                       f"oracle dequantize + torch CPU fp32; {model}")
+                       f"{wl.get('cpu_desc', 'oracle dequantize + torch CPU fp32')}; {model}")
 
 
 def main():

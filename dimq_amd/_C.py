@@ -57,6 +57,12 @@ _SIGS = {
                                _vp, _vp]),
     "dimq_conv2d_lut": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _int, _i64, _dbl, _i64, _vp, _int,
                                _i64] + [_i64] * 11 + [_vp, _vp]),
+    "dimq_linear_lut_workspace_bytes": (_i64, [_i64, _i64, _int]),
+    "dimq_linear_lut_ws": (_int, [_vp, _int, _i64, _vp, _i64, _vp, _int, _i64, _dbl, _i64, _vp, _int, _i64, _i64,
+                                  _i64, _vp, _vp, _i64, _vp]),
+    "dimq_conv2d_lut_workspace_bytes": (_i64, [_i64] * 9 + [_int]),
+    "dimq_conv2d_lut_ws": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _int, _i64, _dbl, _i64, _vp,
+                                  _int, _i64] + [_i64] * 11 + [_vp, _vp, _i64, _vp]),
     "dimq_pack_bits": (_int, [_vp, _i64, _int, _vp, _vp]),
     "dimq_unpack_bits": (_int, [_vp, _i64, _i64, _int, _vp, _vp]),
     "dimq_hard_quantize": (_int, [_vp, _int, _i64, _i64, _vp, _i64, _int, _vp, _vp, _vp]),
@@ -174,6 +180,17 @@ def _bias_args(bias: torch.Tensor | None, n: int, what: str):
     return b, _ptr(b), _dtype(b), b.numel()
 
 
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor | None:
+    """Device workspace of the W4A4 fast path (None when the call needs none).
+
+    Allocated from torch's caching allocator on the current stream, so
+    back-to-back calls reuse the same block without a hipMalloc.
+    """
+    if nbytes <= 0:
+        return None
+    return torch.empty(int(nbytes), dtype=torch.uint8, device=device)
+
+
 def linear_lut_impl(x, packed_w, codebook, act_scale, act_zp, bias, out_features, in_features):
     _require_cuda(x, "linear_lut expects CUDA input")
     _require_cuda(packed_w, "linear_lut expects CUDA packed_weight")
@@ -198,10 +215,11 @@ def linear_lut_impl(x, packed_w, codebook, act_scale, act_zp, bias, out_features
     b, bp, bdt, bn = _bias_args(bias, out_features, "out_features")
     M = xc.numel() // in_features
     y = torch.empty((M, out_features), dtype=torch.float32, device=xc.device)
+    ws = _workspace(lib.dimq_linear_lut_workspace_bytes(M, in_features, _dtype(cb)), xc.device)
     with torch.cuda.device(xc.device):
-        _check(lib.dimq_linear_lut(_ptr(xc), _dtype(xc), M, _ptr(pw), pw.numel(), _ptr(cb), _dtype(cb), cb.numel(),
-                                   float(act_scale), int(act_zp), bp, bdt, bn, out_features, in_features, _ptr(y),
-                                   _stream(xc.device)))
+        _check(lib.dimq_linear_lut_ws(_ptr(xc), _dtype(xc), M, _ptr(pw), pw.numel(), _ptr(cb), _dtype(cb), cb.numel(),
+                                      float(act_scale), int(act_zp), bp, bdt, bn, out_features, in_features, _ptr(y),
+                                      _ptr(ws), 0 if ws is None else ws.numel(), _stream(xc.device)))
     return y.view(*x.shape[:-1], out_features)
 
 
@@ -226,11 +244,16 @@ def conv2d_lut_impl(x, packed_w, codebook, act_scale, act_zp, bias, out_channels
     oh = (H + 2 * pad_h - dilation_h * (kernel_h - 1) - 1) // stride_h + 1 if stride_h > 0 else 0
     ow = (W + 2 * pad_w - dilation_w * (kernel_w - 1) - 1) // stride_w + 1 if stride_w > 0 else 0
     y = torch.empty((B, out_channels, max(oh, 0), max(ow, 0)), dtype=torch.float32, device=xc.device)
+    ws = None
+    if y.numel() > 0:
+        ws = _workspace(lib.dimq_conv2d_lut_workspace_bytes(B, C, H, W, out_channels, in_channels_per_group, kernel_h,
+                                                            kernel_w, groups, _dtype(cb)), xc.device)
     with torch.cuda.device(xc.device):
-        _check(lib.dimq_conv2d_lut(_ptr(xc), _dtype(xc), B, C, H, W, _ptr(pw), pw.numel(), _ptr(cb), _dtype(cb),
-                                   cb.numel(), float(act_scale), int(act_zp), bp, bdt, bn, out_channels,
-                                   in_channels_per_group, kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w,
-                                   dilation_h, dilation_w, groups, _ptr(y), _stream(xc.device)))
+        _check(lib.dimq_conv2d_lut_ws(_ptr(xc), _dtype(xc), B, C, H, W, _ptr(pw), pw.numel(), _ptr(cb), _dtype(cb),
+                                      cb.numel(), float(act_scale), int(act_zp), bp, bdt, bn, out_channels,
+                                      in_channels_per_group, kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w,
+                                      dilation_h, dilation_w, groups, _ptr(y), _ptr(ws),
+                                      0 if ws is None else ws.numel(), _stream(xc.device)))
     return y
 
 

@@ -181,6 +181,20 @@ ConvShape make_shape(int64_t B, int64_t C, int64_t H, int64_t W, int64_t OC, int
 
 using namespace dimq;
 
+// Device workspace of the W4A4 fast path: the activations as fp16 a - zp
+// (NCHW) and, for shapes the LDS-halo kernel runs, its 4-bit weight layout.
+// 0 = no fast path (the codebook is not fp16).
+static int64_t lut_act_bytes(int64_t B, int64_t C, int64_t H, int64_t W) { return (B * C * H * W * 2 + 255) / 256 * 256; }
+
+extern "C" int64_t dimq_conv2d_lut_workspace_bytes(int64_t B, int64_t C, int64_t H, int64_t W, int64_t out_channels,
+                                                   int64_t in_channels_per_group, int64_t kernel_h,
+                                                   int64_t kernel_w, int64_t groups, int cb_dtype) {
+  if (cb_dtype != DIMQ_F16 || B <= 0 || C <= 0 || H <= 0 || W <= 0 || out_channels <= 0) return 0;
+  const int64_t hw = (groups == 1 && in_channels_per_group == C)
+                         ? halo_part_words(out_channels, C, kernel_h, kernel_w, 4) : 0;
+  return lut_act_bytes(B, C, H, W) + hw * 4;
+}
+
 extern "C" int dimq_conv2d_lut(const void* x, int x_dtype, int64_t B, int64_t C, int64_t H, int64_t W,
                                const uint8_t* packed_w, int64_t packed_numel, const void* codebook, int cb_dtype,
                                int64_t cb_numel, double act_scale, int64_t act_zp, const void* bias, int bias_dtype,
@@ -188,6 +202,25 @@ extern "C" int dimq_conv2d_lut(const void* x, int x_dtype, int64_t B, int64_t C,
                                int64_t kernel_h, int64_t kernel_w, int64_t stride_h, int64_t stride_w, int64_t pad_h,
                                int64_t pad_w, int64_t dilation_h, int64_t dilation_w, int64_t groups, float* y,
                                void* stream) {
+  return dimq_conv2d_lut_ws(x, x_dtype, B, C, H, W, packed_w, packed_numel, codebook, cb_dtype, cb_numel, act_scale,
+                            act_zp, bias, bias_dtype, bias_numel, out_channels, in_channels_per_group, kernel_h,
+                            kernel_w, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w, groups, y, nullptr, 0,
+                            stream);
+}
+
+// With an fp16 codebook and the workspace above: activations quantized once
+// to the exact fp16 integers a - zp, then the weight-only conv kernels with
+// act_scale on the accumulator (the LDS-halo kernel where the shape allows,
+// its weight layout built into the workspace; else the generic implicit GEMM).
+// Otherwise the generic A4 kernel (hi + lo fp16 codebook planes).
+extern "C" int dimq_conv2d_lut_ws(const void* x, int x_dtype, int64_t B, int64_t C, int64_t H, int64_t W,
+                                  const uint8_t* packed_w, int64_t packed_numel, const void* codebook, int cb_dtype,
+                                  int64_t cb_numel, double act_scale, int64_t act_zp, const void* bias,
+                                  int bias_dtype, int64_t bias_numel, int64_t out_channels,
+                                  int64_t in_channels_per_group, int64_t kernel_h, int64_t kernel_w, int64_t stride_h,
+                                  int64_t stride_w, int64_t pad_h, int64_t pad_w, int64_t dilation_h,
+                                  int64_t dilation_w, int64_t groups, float* y, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
   DIMQ_CHECK(is_float_dtype(x_dtype), "conv2d_lut expects floating input");
   DIMQ_CHECK(is_float_dtype(cb_dtype), "codebook must be floating point");
   DIMQ_CHECK(cb_numel == 16, "codebook must have 16 entries for W4");
@@ -201,12 +234,38 @@ extern "C" int dimq_conv2d_lut(const void* x, int x_dtype, int64_t B, int64_t C,
   DIMQ_CHECK(packed_numel >= (wnumel + 1) / 2, "packed_weight is too small for requested conv weight shape");
   if (bias) DIMQ_CHECK(bias_numel == out_channels, "bias numel must equal out_channels");
   DIMQ_CHECK(bias == nullptr || is_float_dtype(bias_dtype), "bias must be floating point");
+  DIMQ_CHECK(workspace_bytes >= 0, "workspace_bytes must be non-negative");
   if (s.B * s.OC * s.OH * s.OW == 0) return DIMQ_OK;
+  const hipStream_t st = as_stream(stream);
+  const int64_t need = dimq_conv2d_lut_workspace_bytes(s.B, s.C, s.H, s.W, s.OC, s.ICg, s.KH, s.KW, s.groups,
+                                                       cb_dtype);
+  if (workspace != nullptr && need > 0 && workspace_bytes >= need && aligned(workspace, 16)) {
+    const float sc = static_cast<float>(act_scale);
+    uint16_t* q = static_cast<uint16_t*>(workspace);
+    int r = launch_quantize_a4_f16(x, x_dtype, s.B * s.C * s.H * s.W, sc, static_cast<int>(act_zp), q, st);
+    if (r != DIMQ_OK) return r;
+    const int64_t hw = (s.groups == 1) ? halo_part_words(s.OC, s.C, s.KH, s.KW, 4) : 0;
+    if (hw > 0 && halo_eligible(s.C, s.KH, s.KW, s.sh, s.sw, s.dh, s.dw, s.groups, s.OH, s.OW, 4, DIMQ_F16,
+                                kEpiNone, DIMQ_NCHW)) {
+      uint32_t* kw = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(workspace) + lut_act_bytes(s.B, s.C, s.H, s.W));
+      r = launch_prepare(packed_w, s.OC, s.C, s.KH, s.KW, 4, kw, st);
+      if (r != DIMQ_OK) return r;
+      return launch_conv_halo(q, DIMQ_F16, DIMQ_NCHW, s.B, s.C, s.H, s.W, kw, 4, codebook, cb_dtype, 1, 16, bias,
+                              bias_dtype, s.OC, s.KH, s.KW, s.sh, s.ph, s.pw, s.OH, s.OW, y, DIMQ_F32, DIMQ_NCHW,
+                              Epi{}, st, sc);
+    }
+    GemmArgs p = conv_args(s, q, DIMQ_NCHW, packed_w, codebook, cb_dtype, 1, 16, bias, bias_dtype, y, DIMQ_F32,
+                           DIMQ_NCHW);
+    p.acc_scale = sc;
+    int tile = gemm_pick_tile(p.M, p.N, DIMQ_VARIANT_AUTO);
+    if (tile == kTileGemv) tile = kTile16x16;  // the GEMV kernel has no im2col/group support
+    return gemm_dispatch(p, 4, DIMQ_F16, false, tile, st);
+  }
   GemmArgs p = conv_args(s, x, DIMQ_NCHW, packed_w, codebook, cb_dtype, 1, 16, bias, bias_dtype, y, DIMQ_F32,
                          DIMQ_NCHW);
   p.act_scale = static_cast<float>(act_scale);
   p.act_zp = static_cast<int>(act_zp);
-  return gemm_dispatch(p, 4, x_dtype, true, kTile64x32, as_stream(stream));
+  return gemm_dispatch(p, 4, x_dtype, true, kTile64x32, st);
 }
 
 extern "C" int64_t dimq_conv2d_prepared_words(int64_t out_channels, int64_t in_channels, int64_t kernel_h,

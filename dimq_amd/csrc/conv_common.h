@@ -26,6 +26,7 @@ struct HaloArgs {
   void* y;
   int y_dt, y_layout;
   Epi epi;  // fused residual / activation
+  float acc_scale = 1.0f;  // factor on every accumulator (W4A4 calls: the activation scale)
 };
 
 // Streaming kernel (conv_stream.hip): shapes it runs, LDS bytes, launch.

@@ -214,7 +214,7 @@ __global__ __launch_bounds__(256) void conv_halo_kernel(const HaloArgs p) {
   {
     const int rl = (p.cb_rows == 1) ? 0 : 32 * wn + col;
     const int e = planes_from_lds<BITS, false>(cbs + rl * E, cbr, cbr);
-    scale = ldexpf(1.0f, -e);
+    scale = ldexpf(p.acc_scale, -e);
   }
 
   // ---- this lane's pixels: m-blocks mb = wm + 2*q (pixels past the tile read
@@ -377,7 +377,7 @@ __global__ __launch_bounds__(256, 2) void conv_resident_kernel(const HaloArgs p)
   {
     const int rl = (p.cb_rows == 1) ? 0 : 32 * wn + col;
     const int e = planes_from_lds<BITS, false>(cbs + rl * E, cbr, cbr);
-    scale = ldexpf(1.0f, -e);
+    scale = ldexpf(p.acc_scale, -e);
   }
   const float bv = (p.bias && ocl < p.OC) ? load_as_float(p.bias, p.bias_dt, ocl) : 0.0f;
 

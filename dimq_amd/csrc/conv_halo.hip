@@ -95,9 +95,10 @@ int launch_conv_halo(const void* x, int x_dtype, int x_layout, int64_t B, int64_
                      const uint32_t* kw, int bits, const void* cb, int cb_dtype, int64_t cb_rows, int64_t cb_size,
                      const void* bias, int bias_dtype, int64_t OC, int64_t KH, int64_t KW, int64_t stride,
                      int64_t ph, int64_t pw, int64_t OH, int64_t OW, void* y, int y_dtype, int y_layout,
-                     const Epi& epi, hipStream_t s) {
+                     const Epi& epi, hipStream_t s, float acc_scale) {
   HaloArgs p{};
   p.epi = epi;
+  p.acc_scale = acc_scale;
   p.x = x;
   p.x_dt = x_dtype;
   p.x_layout = x_layout;

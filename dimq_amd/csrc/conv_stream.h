@@ -344,7 +344,7 @@ __global__ __launch_bounds__(kStreamThreads) void conv_stream_kernel(const HaloA
   {
     const int rl = (p.cb_rows == 1) ? 0 : 32 * wn + col;
     const int e = planes_from_lds<BITS, false>(cbs + rl * E, cbr, cbr);
-    scale = ldexpf(1.0f, -e);
+    scale = ldexpf(p.acc_scale, -e);
   }
   const float bv = (p.bias && ocl < p.OC) ? load_as_float(p.bias, p.bias_dt, ocl) : 0.0f;
 

@@ -88,9 +88,10 @@ int gemm_dispatch(const GemmArgs& p, int bits, int xt, bool a4, int tile, hipStr
 int linear_codebook_impl(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed_w,
                          int bits, const void* codebook, int cb_dtype, int64_t cb_rows, int64_t cb_size,
                          const void* bias, int bias_dtype, int64_t N, void* y, int y_dtype, int64_t ldy,
-                         const Epi& epi, int variant, hipStream_t s) {
+                         const Epi& epi, int variant, hipStream_t s, float acc_scale = 1.0f) {
   GemmArgs p{};
   p.epi = epi;
+  p.acc_scale = acc_scale;
   p.x = x;
   p.M = M;
   p.K = K;
@@ -173,10 +174,30 @@ extern "C" int dimq_linear_codebook_ex(const void* x, int x_dtype, int64_t M, in
                               bias_dtype, N, y, y_dtype, N, epi, variant, as_stream(stream));
 }
 
+extern "C" int64_t dimq_linear_lut_workspace_bytes(int64_t M, int64_t in_features, int cb_dtype) {
+  if (cb_dtype != DIMQ_F16 || M <= 0 || in_features <= 0) return 0;
+  return (M * in_features * 2 + 255) / 256 * 256;
+}
+
 extern "C" int dimq_linear_lut(const void* x, int x_dtype, int64_t M, const uint8_t* packed_w, int64_t packed_numel,
                                const void* codebook, int cb_dtype, int64_t cb_numel, double act_scale,
                                int64_t act_zp, const void* bias, int bias_dtype, int64_t bias_numel,
                                int64_t out_features, int64_t in_features, float* y, void* stream) {
+  return dimq_linear_lut_ws(x, x_dtype, M, packed_w, packed_numel, codebook, cb_dtype, cb_numel, act_scale, act_zp,
+                            bias, bias_dtype, bias_numel, out_features, in_features, y, nullptr, 0, stream);
+}
+
+// With an fp16 codebook (the reference exporter's default, export.py
+// codebook_dtype) and a workspace of M*K fp16: the activations become the
+// exact fp16 integers a - zp (one element-wise pass), then the weight-only
+// kernels run on them with the 16-entry codebook and act_scale on the
+// accumulator, so the call takes the same fast tiles as linear_codebook.
+// Otherwise the generic A4 tiles (hi + lo fp16 codebook planes).
+extern "C" int dimq_linear_lut_ws(const void* x, int x_dtype, int64_t M, const uint8_t* packed_w,
+                                  int64_t packed_numel, const void* codebook, int cb_dtype, int64_t cb_numel,
+                                  double act_scale, int64_t act_zp, const void* bias, int bias_dtype,
+                                  int64_t bias_numel, int64_t out_features, int64_t in_features, float* y,
+                                  void* workspace, int64_t workspace_bytes, void* stream) {
   DIMQ_CHECK(is_float_dtype(x_dtype), "linear_lut expects floating input");
   DIMQ_CHECK(is_float_dtype(cb_dtype), "codebook must be floating point");
   DIMQ_CHECK(cb_numel == 16, "codebook must have 16 entries for W4");
@@ -188,7 +209,19 @@ extern "C" int dimq_linear_lut(const void* x, int x_dtype, int64_t M, const uint
              "packed_weight is too small for out_features * in_features");
   if (bias) DIMQ_CHECK(bias_numel == out_features, "bias numel must equal out_features");
   DIMQ_CHECK(bias == nullptr || is_float_dtype(bias_dtype), "bias must be floating point");
+  DIMQ_CHECK(workspace_bytes >= 0, "workspace_bytes must be non-negative");
   if (M == 0) return DIMQ_OK;
+  const int64_t need = dimq_linear_lut_workspace_bytes(M, in_features, cb_dtype);
+  if (workspace != nullptr && need > 0 && workspace_bytes >= need && aligned(workspace, 16)) {
+    uint16_t* q = static_cast<uint16_t*>(workspace);
+    const hipStream_t st = as_stream(stream);
+    const int rc = launch_quantize_a4_f16(x, x_dtype, M * in_features, static_cast<float>(act_scale),
+                                          static_cast<int>(act_zp), q, st);
+    if (rc != DIMQ_OK) return rc;
+    return linear_codebook_impl(q, DIMQ_F16, M, in_features, in_features, packed_w, 4, codebook, cb_dtype, 1, 16,
+                                bias, bias_dtype, out_features, y, DIMQ_F32, out_features, Epi{}, DIMQ_VARIANT_AUTO,
+                                st, static_cast<float>(act_scale));
+  }
   GemmArgs p{};
   p.x = x;
   p.M = M;

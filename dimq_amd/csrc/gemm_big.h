@@ -175,7 +175,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, big_min_waves(BITS, MBLK, NBLK, CON
     brow[nb] = n0 + nl < p.N ? n0 + nl : p.N - 1;
     const int rl = (p.cb_rows == 1) ? 0 : nl;
     const int e = planes_from_lds<BITS, false>(cbs + rl * E, cb[nb], cb[nb]);
-    rscale[nb] = ldexpf(1.0f, -e);
+    rscale[nb] = ldexpf(p.acc_scale, -e);
   }
 
   // activation tasks: (row m, 16-wide group kg) per thread, 4 groups per row
@@ -524,7 +524,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_lds_kernel(const GemmArgs
   {
     const int e = planes_from_lds<BITS, false>(cbs + ((p.cb_rows == 1) ? 0 : brl * E), cb, cb);
     if (bw0 == 0) {
-      escale[brl] = ldexpf(1.0f, -e);
+      escale[brl] = ldexpf(p.acc_scale, -e);
       ebias[brl] = (p.bias && n0 + brl < p.N) ? load_as_float(p.bias, p.bias_dt, n0 + brl) : 0.0f;
     }
   }
@@ -670,7 +670,7 @@ __global__ __launch_bounds__(256) void gemm_deep_kernel(const GemmArgs p) {
   {
     const int rl = (p.cb_rows == 1) ? 0 : nl;
     const int e = planes_from_lds<BITS, false>(cbs + rl * E, cb, cb);
-    rscale = ldexpf(1.0f, -e);
+    rscale = ldexpf(p.acc_scale, -e);
   }
 
   int64_t aoff[A_TASKS];

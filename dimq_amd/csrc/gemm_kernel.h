@@ -51,6 +51,10 @@ struct GemmArgs {
   int cKH, cKW, csh, csw, cph, cpw, cdh, cdw;
   int groups;  // grid z (1 for Linear)
   Epi epi;     // fused residual / activation (weight-only ops)
+  // factor on every accumulator before bias/epilogue (weight-only kernels):
+  // the activation scale of a W4A4 call whose activations were pre-quantized
+  // to the exact fp16 integers a - zp
+  float acc_scale = 1.0f;
 };
 
 // Output element offset of (row m, global column n).
@@ -310,7 +314,7 @@ __global__ __launch_bounds__(256) void gemm_cb_kernel(const GemmArgs p) {
       const int64_t row = (p.cb_rows == 1) ? 0 : nz + n;
       e = load_codebook_row<BITS, A4>(p, row, n < p.N, cb[nb][0], cb[nb][NCB - 1]);
     }
-    colscale[nb] = ldexpf(A4 ? p.act_scale : 1.0f, -e);
+    colscale[nb] = ldexpf(A4 ? p.act_scale : p.acc_scale, -e);
   }
   __syncthreads();
 
@@ -463,7 +467,7 @@ __global__ __launch_bounds__(256) void gemm_cb8_kernel(const GemmArgs p) {
       const float c = (n < p.N && j < p.cb_size) ? load_as_float(p.cb, p.cb_dt, row * p.cb_size + j) : 0.0f;
       cbs[r * 256 + j] = (uint16_t)float_to_f16_bits(ldexpf(c, e));
     }
-    if (part == 0) rscale[r] = ldexpf(1.0f, -e);
+    if (part == 0) rscale[r] = ldexpf(p.acc_scale, -e);
   }
 
   floatx4 acc[MB][NB];
@@ -591,7 +595,7 @@ __global__ __launch_bounds__(WPW * 64) void gemv_cb_kernel(const GemmArgs p) {
   __syncthreads();
   CodebookRegs<BITS> cb;
   const int e = planes_from_lds<BITS, false>(cbs + ((p.cb_rows == 1) ? 0 : col * E), cb, cb);
-  const float colscale = ldexpf(1.0f, -e);
+  const float colscale = ldexpf(p.acc_scale, -e);
   const int64_t nk = (p.K + kKM - 1) / kKM;
   const bool arow = col < p.M;
   floatx4 acc = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -744,7 +748,7 @@ __global__ __launch_bounds__(256) void gemm_fast_kernel(const GemmArgs p) {
     brow[nb] = n < p.N ? n : p.N - 1;
     const int rl = (p.cb_rows == 1) ? 0 : wave * WN + nb * 16 + col;
     const int e = planes_from_lds<BITS, A4>(cbs + rl * E, cb[nb][0], cb[nb][NCB - 1]);
-    colscale[nb] = ldexpf(A4 ? p.act_scale : 1.0f, -e);
+    colscale[nb] = ldexpf(A4 ? p.act_scale : p.acc_scale, -e);
   }
   // activation tasks: (row m, 16-wide group kg) per thread
   int64_t aoff[A_PER_T];
@@ -878,7 +882,7 @@ int launch_conv_halo(const void* x, int x_dtype, int x_layout, int64_t B, int64_
                      const uint32_t* kw, int bits, const void* cb, int cb_dtype, int64_t cb_rows, int64_t cb_size,
                      const void* bias, int bias_dtype, int64_t OC, int64_t KH, int64_t KW, int64_t stride,
                      int64_t ph, int64_t pw, int64_t OH, int64_t OW, void* y, int y_dtype, int y_layout,
-                     const Epi& epi, hipStream_t s);
+                     const Epi& epi, hipStream_t s, float acc_scale = 1.0f);
 int launch_prepare(const uint8_t* src, int64_t OC, int64_t C, int64_t KH, int64_t KW, int bits, uint32_t* out,
                    hipStream_t s);
 
@@ -891,6 +895,9 @@ int launch_conv_stem(const void* x, int x_dtype, int x_layout, int64_t B, int64_
                      int64_t cb_size, const void* bias, int bias_dtype, int64_t OC, int64_t KH, int64_t KW,
                      int64_t ph, int64_t pw, int64_t OH, int64_t OW, void* y, int y_dtype, int y_layout,
                      const Epi& epi, hipStream_t s);
+
+// quant.hip: W4A4 activations as the fp16 integers a - zp (out 16-byte aligned)
+int launch_quantize_a4_f16(const void* x, int x_dtype, int64_t n, float s, int zp, uint16_t* out, hipStream_t st);
 
 // gemm.hip
 int gemm_pick_tile(int64_t M, int64_t N, int variant);

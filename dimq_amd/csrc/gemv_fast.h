@@ -81,7 +81,7 @@ __global__ __launch_bounds__(1024) void gemv_fast_kernel(const GemmArgs p) {
       stage_codebook<E>(p.cb, p.cb_dt, p.cb_rows, p.cb_size, n0, 16, p.N, cbs, tid, WAVES * 64);
       __syncthreads();  // codebook staged
       const int e = planes_from_lds<BITS, false>(cbs + ((p.cb_rows == 1) ? 0 : col * E), cb, cb);
-      colscale = ldexpf(1.0f, -e);
+      colscale = ldexpf(p.acc_scale, -e);
     }
     // ---- decode + MFMA, 8 k per step
 #pragma unroll

@@ -103,6 +103,36 @@ int dimq_conv2d_lut(const void* x, int x_dtype, int64_t B, int64_t C, int64_t H,
                     int64_t kernel_w, int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
                     int64_t dilation_h, int64_t dilation_w, int64_t groups, float* y, void* stream);
 
+/* Workspace forms of linear_lut / conv2d_lut (same reference ops, same
+ * arguments, checks and messages as the two entry points above, plus a
+ * caller-owned device workspace; the library allocates nothing).  With an
+ * fp16 codebook — the reference exporter's default
+ * (dimq_backend/export.py:167,217, codebook_dtype=torch.float16) — and a
+ * workspace of at least the *_workspace_bytes size, 16-byte aligned, the
+ * activations are quantized once to the exact fp16 integers a - zp and the
+ * weight-only kernels run on them with act_scale applied to the fp32
+ * accumulator: y = s * sum_k C[w] * (a - zp) + bias, equal to the reference's
+ * sum_k C[w] * (s * (a - zp)) up to fp32 rounding and summation order.
+ * Otherwise (workspace NULL or short, codebook not fp16) they run the same
+ * kernels as dimq_linear_lut / dimq_conv2d_lut.  The workspace is read and
+ * written on `stream`: calls that share one must be ordered on that stream.
+ * *_workspace_bytes returns 0 when no workspace is used for the shape. */
+int64_t dimq_linear_lut_workspace_bytes(int64_t M, int64_t in_features, int cb_dtype);
+int dimq_linear_lut_ws(const void* x, int x_dtype, int64_t M, const uint8_t* packed_w, int64_t packed_numel,
+                       const void* codebook, int cb_dtype, int64_t cb_numel, double act_scale, int64_t act_zp,
+                       const void* bias, int bias_dtype, int64_t bias_numel, int64_t out_features,
+                       int64_t in_features, float* y, void* workspace, int64_t workspace_bytes, void* stream);
+int64_t dimq_conv2d_lut_workspace_bytes(int64_t B, int64_t C, int64_t H, int64_t W, int64_t out_channels,
+                                        int64_t in_channels_per_group, int64_t kernel_h, int64_t kernel_w,
+                                        int64_t groups, int cb_dtype);
+int dimq_conv2d_lut_ws(const void* x, int x_dtype, int64_t B, int64_t C, int64_t H, int64_t W,
+                       const uint8_t* packed_w, int64_t packed_numel, const void* codebook, int cb_dtype,
+                       int64_t cb_numel, double act_scale, int64_t act_zp, const void* bias, int bias_dtype,
+                       int64_t bias_numel, int64_t out_channels, int64_t in_channels_per_group, int64_t kernel_h,
+                       int64_t kernel_w, int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                       int64_t dilation_h, int64_t dilation_w, int64_t groups, float* y, void* workspace,
+                       int64_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------------
  * 2. Generalised ops for the BASELINE configurations: b in {2,3,4,8} bits,
  *    per-layer or per-output-channel codebooks, weight-only GEMM/conv.

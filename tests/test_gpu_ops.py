@@ -245,6 +245,106 @@ def test_conv2d_lut_vs_oracle(gpu, case):
     torch.testing.assert_close(y.cpu(), torch.from_numpy(ref), rtol=1e-5, atol=1e-5)
 
 
+# W4A4 ops with an fp16 codebook (the reference exporter's default): the
+# workspace path, activations as fp16 a - zp into the weight-only kernels.
+# Shapes reach the GEMV kernels (M <= 16), the 128x128 tiles (cfg1), the
+# shared-decode 256x256 tile (M >= 2048) and the generic tiles (odd K).
+def _a4_exact_check(y, ref32, exact, K):
+    """W4A4 accuracy bar: at the reference's test sizes (K = 11 and 27 there;
+    here K <= 128) its own tolerance against the oracle's fp32 LUT loop
+    (rtol = atol = 1e-5, test_cuda_ops.py:64,93); at every size, the
+    deviation from the exact (float64) value of s * sum_k C[w] (a - zp) + b is
+    at most twice the deviation of that fp32 LUT loop (the reference's
+    arithmetic) plus 1e-6 max|exact|: over K in the hundreds and millions of
+    outputs, fp32 summation order alone moves some sums by more than 1e-5, in
+    the reference as here."""
+    y = y.detach().cpu().double()
+    ref32 = torch.as_tensor(ref32).double()
+    if K <= 128:
+        torch.testing.assert_close(y.float(), ref32.float(), rtol=1e-5, atol=1e-5)
+    err = (y - exact).abs().max().item()
+    err_ref = (ref32 - exact).abs().max().item()
+    assert err <= 2 * err_ref + 1e-6 * exact.abs().max().item(), (err, err_ref)
+
+
+def _a4_levels(x, scale, zp):
+    """s * (a - zp) in float64, a = the reference's u4 activation code (oracle)."""
+    a = torch.from_numpy(oracle.quantize_act_u4(x.float(), scale, zp).astype(np.int64))
+    return scale * (a - zp).double()
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (4, 256, 4096), (16, 300, 768), (1576, 1024, 768),
+                                   (2304, 512, 768), (37, 130, 96), (5, 11, 6)])
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+def test_linear_lut_fp16_codebook_fast_path(gpu, M, N, K, xdt):
+    ops = _ops()
+    from dimq_amd import _C
+    announce(f"linear_lut fp16 codebook M={M} N={N} K={K} {xdt}")
+    assert _C.lib.dimq_linear_lut_workspace_bytes(M, K, _C.F16) >= M * K * 2
+    g = _gen(M * 5 + N + K)
+    x = torch.randn(M, K, generator=g).to(xdt)
+    idx = torch.randint(0, 16, (N, K), generator=g, dtype=torch.uint8)
+    cb = (torch.linspace(-0.5, 0.5, 16) + 0.01 * torch.randn(16, generator=g)).half()
+    bias = torch.randn(N, generator=g)
+    packed = torch.from_numpy(oracle.pack_bits(idx, 4))
+    y = ops.dimq_linear_lut(x.to(gpu), packed.to(gpu), cb.to(gpu), 0.2, 7, bias.to(gpu), N, K)
+    ref = oracle.linear_lut(x.float(), packed, cb.float(), 0.2, 7, bias, N, K)
+    exact = _a4_levels(x, 0.2, 7) @ cb.double()[idx.long()].T + bias.double()
+    _a4_exact_check(y, ref, exact, K)
+
+
+def test_linear_lut_fp16_codebook_matches_generic_path(gpu):
+    # the workspace path and the no-workspace entry point (generic A4 tiles)
+    # agree on the same inputs, and a short workspace falls back
+    from dimq_amd import _C
+    M, N, K = 64, 96, 256
+    g = _gen(77)
+    x = torch.randn(M, K, generator=g).to(gpu)
+    idx = torch.randint(0, 16, (N, K), generator=g, dtype=torch.uint8)
+    cb = torch.linspace(-1, 1, 16).half().to(gpu)
+    packed = torch.from_numpy(oracle.pack_bits(idx, 4)).to(gpu)
+    s = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for ws_bytes in (M * K * 2, M * K * 2 - 2, 0):
+        y = torch.empty(M, N, device=gpu)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=gpu)
+        rc = _C.lib.dimq_linear_lut_ws(x.data_ptr(), _C.F32, M, packed.data_ptr(), packed.numel(), cb.data_ptr(),
+                                       _C.F16, 16, 0.125, 8, None, 0, 0, N, K, y.data_ptr(),
+                                       ws.data_ptr() if ws_bytes else None, ws_bytes, s)
+        assert rc == 0, _C.lib.dimq_last_error()
+        outs.append(y)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(outs[0], outs[2], rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(outs[1], outs[2], rtol=0, atol=0)  # short workspace: the generic path itself
+
+
+@pytest.mark.parametrize("case", [
+    dict(B=2, C=64, H=56, W=56, OC=64, KH=3, KW=3, s=(1, 1), p=(1, 1), d=(1, 1), g=1),    # cfg2 shape, halo kernel
+    dict(B=2, C=128, H=28, W=28, OC=128, KH=3, KW=3, s=(1, 1), p=(1, 1), d=(1, 1), g=1),  # C 128, decode per step
+    dict(B=3, C=64, H=30, W=30, OC=128, KH=1, KW=1, s=(2, 2), p=(0, 0), d=(1, 1), g=1),   # 1x1 stride 2
+    dict(B=2, C=4, H=9, W=8, OC=6, KH=3, KW=3, s=(1, 1), p=(1, 1), d=(1, 1), g=1),        # generic implicit GEMM
+    dict(B=1, C=6, H=11, W=7, OC=4, KH=3, KW=2, s=(2, 1), p=(1, 0), d=(1, 2), g=2),       # groups + dilation
+])
+@pytest.mark.parametrize("xdt", [torch.float32, torch.float16])
+def test_conv2d_lut_fp16_codebook_fast_path(gpu, case, xdt):
+    ops = _ops()
+    announce(f"conv2d_lut fp16 codebook {case} {xdt}")
+    g = _gen(case["C"] * 11 + case["OC"] + case["H"])
+    x = torch.randn(case["B"], case["C"], case["H"], case["W"], generator=g).to(xdt)
+    shape = (case["OC"], case["C"] // case["g"], case["KH"], case["KW"])
+    idx = torch.randint(0, 16, shape, generator=g, dtype=torch.uint8)
+    cb = torch.linspace(-0.7, 0.6, 16).half()
+    bias = torch.randn(case["OC"], generator=g)
+    packed = torch.from_numpy(oracle.pack_bits(idx, 4))
+    y = ops.dimq_conv2d_lut(x.to(gpu), packed.to(gpu), cb.to(gpu), 0.25, 7, bias.to(gpu), shape, case["s"], case["p"],
+                            case["d"], case["g"])
+    ref = oracle.conv2d_lut(x.float(), packed, cb.float(), 0.25, 7, bias, shape, case["s"], case["p"], case["d"],
+                            case["g"])
+    exact = torch.nn.functional.conv2d(_a4_levels(x, 0.25, 7), cb.double()[idx.long()], bias.double(), case["s"],
+                                       case["p"], case["d"], case["g"])
+    _a4_exact_check(y, ref, exact, shape[1] * shape[2] * shape[3])
+
+
 # ---------------------------------------------------------------- weight-only codebook Linear
 def _codebook_case(N, K, bits, per_channel, g, cb_entries=None):
     Kc = cb_entries or (1 << bits)

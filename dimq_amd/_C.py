@@ -63,6 +63,7 @@ _SIGS = {
     "dimq_conv2d_lut_workspace_bytes": (_i64, [_i64] * 9 + [_int]),
     "dimq_conv2d_lut_ws": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _int, _i64, _dbl, _i64, _vp,
                                   _int, _i64] + [_i64] * 11 + [_vp, _vp, _i64, _vp]),
+    "dimq_layer_norm": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp, _int, _dbl, _vp, _vp]),
     "dimq_pack_bits": (_int, [_vp, _i64, _int, _vp, _vp]),
     "dimq_unpack_bits": (_int, [_vp, _i64, _i64, _int, _vp, _vp]),
     "dimq_hard_quantize": (_int, [_vp, _int, _i64, _i64, _vp, _i64, _int, _vp, _vp, _vp]),
@@ -431,6 +432,36 @@ def conv2d_codebook_impl(x, packed_w, codebook, bits, bias, out_channels, in_cha
     return y
 
 
+def layer_norm_impl(x, normalized_size, weight, bias, eps):
+    """LayerNorm over the last dimension (support op of the ViT workload)."""
+    _require_cuda(x, "layer_norm expects CUDA input")
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise RuntimeError("layer_norm expects fp16 or bf16 input")
+    D = int(normalized_size)
+    if x.dim() == 0 or x.size(-1) != D:
+        raise RuntimeError("layer_norm: last input dimension must equal the normalized size")
+    xv = x.reshape(-1, D) if x.dim() != 2 else x
+    if xv.stride(-1) != 1 or xv.stride(0) % 8 != 0 or xv.data_ptr() % 16 != 0:
+        xv = xv.contiguous()
+    wdt = F32
+    for t in (weight, bias):
+        if t is not None:
+            _require_cuda(t, "layer_norm weight and bias must be CUDA tensors")
+            if t.numel() != D:
+                raise RuntimeError("layer_norm weight and bias must have the normalized size")
+    if weight is not None and bias is not None and weight.dtype != bias.dtype:
+        bias = bias.to(weight.dtype)
+    w = weight.contiguous() if weight is not None else None
+    b = bias.contiguous() if bias is not None else None
+    if w is not None or b is not None:
+        wdt = _dtype(w if w is not None else b)
+    y = torch.empty(xv.shape, dtype=x.dtype, device=x.device)
+    with torch.cuda.device(x.device):
+        _check(lib.dimq_layer_norm(_ptr(xv), _dtype(xv), xv.shape[0], D, xv.stride(0), _ptr(w), _ptr(b), wdt,
+                                   float(eps), _ptr(y), _stream(x.device)))
+    return y.view(x.shape)
+
+
 # ---------------------------------------------------------------------------
 # torch.library registration
 # ---------------------------------------------------------------------------
@@ -468,6 +499,9 @@ _SCHEMAS = {
                         conv2d_codebook_impl),
     "prepare_conv_weight": ("prepare_conv_weight(Tensor packed_w, int bits, int out_channels, int in_channels, "
                             "int kernel_h, int kernel_w) -> Tensor", prepare_conv_weight_impl),
+    # support op of the end-to-end ViT workload
+    "layer_norm": ("layer_norm(Tensor x, int normalized_size, Tensor? weight, Tensor? bias, float eps) -> Tensor",
+                   layer_norm_impl),
 }
 
 

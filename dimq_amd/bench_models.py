@@ -25,7 +25,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .modules import DIMQCodebookConv2d, DIMQCodebookLinear, quantize_model_weight_only
+from .modules import DIMQCodebookConv2d, DIMQCodebookLinear, DIMQLayerNorm, quantize_model_weight_only
 
 
 def _fused(mod: nn.Module, x: torch.Tensor, residual: torch.Tensor | None = None,
@@ -128,11 +128,20 @@ def vit_b16(seed: int = 3) -> ViT:
 
 
 def quantize_vit(model: ViT, bits: int = 4, out_dtype: torch.dtype = torch.bfloat16) -> ViT:
-    """cfg4: qkv / proj / fc1 / fc2 -> weight-only codebook layers (per-output-channel codebooks)."""
+    """cfg4: qkv / proj / fc1 / fc2 -> weight-only codebook layers (per-output-channel codebooks);
+    the LayerNorms -> DIMQLayerNorm (the HIP LayerNorm kernel, same parameters)."""
     def pick(name, module):
         leaf = name.rsplit(".", 1)[-1]
         return bits if leaf in ("qkv", "proj", "fc1", "fc2") else None
-    return quantize_model_weight_only(model, pick, out_dtype=out_dtype)
+    model = quantize_model_weight_only(model, pick, out_dtype=out_dtype)
+    for name, mod in list(model.named_modules()):
+        if type(mod) is nn.LayerNorm:
+            parent = model
+            parts = name.split(".")
+            for part in parts[:-1]:
+                parent = parent._modules[part]
+            parent._modules[parts[-1]] = DIMQLayerNorm.from_layer_norm(mod)
+    return model
 
 
 def vit_flops(batch: int, model: ViT | None = None) -> float:

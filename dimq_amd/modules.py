@@ -201,6 +201,31 @@ class DIMQCodebookConv2d(nn.Module):
                    dilation=layer.get("dilation", (1, 1)), groups=layer.get("groups", 1))
 
 
+class DIMQLayerNorm(nn.LayerNorm):
+    """nn.LayerNorm whose forward runs the HIP LayerNorm kernel (fp16/bf16 CUDA
+    inputs, normalized over the last dimension).  Same parameters and state
+    dict as nn.LayerNorm; other inputs raise: the CPU reference model converts
+    it back to nn.LayerNorm (torch's own op)."""
+
+    @classmethod
+    def from_layer_norm(cls, ln: nn.LayerNorm) -> "DIMQLayerNorm":
+        if len(ln.normalized_shape) != 1:
+            raise ValueError("DIMQLayerNorm normalizes over the last dimension only")
+        new = cls(ln.normalized_shape[0], eps=ln.eps, elementwise_affine=ln.elementwise_affine,
+                  bias=ln.bias is not None, device=ln.weight.device if ln.weight is not None else None,
+                  dtype=ln.weight.dtype if ln.weight is not None else None)
+        if ln.weight is not None:
+            new.weight.data.copy_(ln.weight.data)
+        if ln.bias is not None:
+            new.bias.data.copy_(ln.bias.data)
+        return new
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if not x.is_cuda:
+            raise RuntimeError("DIMQLayerNorm runs on CUDA (HIP) tensors only")
+        return ops.layer_norm(x, self.weight, self.bias, self.eps)
+
+
 def make_packed_layer(layer: Mapping[str, Any], *, use_cuda_kernel: bool = True) -> nn.Module:
     """modules.py:153-158, extended with weight-only (format v2) layers."""
     weight_only = layer.get("activation_quantization") == "none" or layer.get("bit_a", 4) is None

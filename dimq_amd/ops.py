@@ -200,6 +200,13 @@ def prepare_conv_weight(packed_weight: torch.Tensor, bits: int, weight_shape: Se
     return torch.ops.dimq.prepare_conv_weight(packed_weight, int(bits), out_channels, cin, kernel_h, kernel_w)
 
 
+def layer_norm(x: torch.Tensor, weight: torch.Tensor | None, bias: torch.Tensor | None,
+               eps: float = 1e-5) -> torch.Tensor:
+    """LayerNorm over the last dimension on the HIP kernel (fp16/bf16 x; the ViT workload's LayerNorms)."""
+    require_extension()
+    return torch.ops.dimq.layer_norm(x, int(x.shape[-1]), weight, bias, float(eps))
+
+
 def _pair(value: Sequence[int] | int) -> tuple[int, int]:
     if isinstance(value, int):
         return int(value), int(value)

@@ -236,6 +236,20 @@ int dimq_conv2d_codebook_ex(const void* x, int x_dtype, int x_layout, int64_t B,
                             int y_dtype, int y_layout, const void* residual, int residual_dtype, int activation,
                             int variant, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * 3. Support op of the end-to-end ViT-B/16 workload (not a DIMQ op: the
+ *    reference runs torch.nn.LayerNorm between its quantized layers,
+ *    train_dimq_vit.py via torchvision's vit_b_16).
+ * ------------------------------------------------------------------------- */
+
+/* LayerNorm over the last dimension: y = (x - mean) * rstd * weight + bias,
+ * mean and biased variance in fp32 per row, as torch.nn.functional.layer_norm.
+ * x [rows, dim] fp16/bf16 with row stride ldx (elements), y [rows, dim]
+ * contiguous in x's dtype; weight/bias [dim] (nullable) in wb_dtype.
+ * dim % 8 == 0, dim <= 2048, 16-byte aligned x and y. */
+int dimq_layer_norm(const void* x, int x_dtype, int64_t rows, int64_t dim, int64_t ldx, const void* weight,
+                    const void* bias, int wb_dtype, double eps, void* y, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -292,10 +292,20 @@ def dequantized_model(qmodel):
     import torch
     import torch.nn as nn
 
-    from dimq_amd.modules import DIMQCodebookConv2d, DIMQCodebookLinear
+    from dimq_amd.modules import DIMQCodebookConv2d, DIMQCodebookLinear, DIMQLayerNorm
 
     m = copy.deepcopy(qmodel).cpu().float()
     for name, mod in list(m.named_modules()):
+        if isinstance(mod, DIMQLayerNorm):  # HIP LayerNorm -> torch's own op, same parameters
+            new = nn.LayerNorm(mod.normalized_shape, eps=mod.eps, elementwise_affine=mod.elementwise_affine,
+                               bias=mod.bias is not None)
+            new.load_state_dict(mod.state_dict())
+            parent = m
+            parts = name.split(".")
+            for part in parts[:-1]:
+                parent = parent._modules[part]
+            parent._modules[parts[-1]] = new
+            continue
         if isinstance(mod, DIMQCodebookLinear):
             new = nn.Linear(mod.in_features, mod.out_features, bias=mod.bias is not None)
             w = dequantize(mod.packed_weight, mod.bits, mod.codebook.float(), mod.out_features, mod.in_features)

@@ -756,3 +756,42 @@ def test_conv2d_prepare_unsupported_returns_none(gpu):
     ops = _ops()
     assert ops.prepare_conv_weight(torch.zeros(100, dtype=torch.uint8, device=gpu), 2, (16, 48, 3, 3)) is None
     assert ops.prepare_conv_weight(torch.zeros(100, dtype=torch.uint8, device=gpu), 8, (16, 64, 3, 3)) is None
+
+
+# ---------------------------------------------------------------- LayerNorm (ViT workload support op)
+@pytest.mark.parametrize("rows,D,dt", [(12608, 768, torch.bfloat16), (300, 768, torch.float16), (5, 8, torch.bfloat16),
+                                       (33, 1024, torch.bfloat16), (7, 2048, torch.float16), (130, 520, torch.bfloat16)])
+def test_layer_norm_vs_torch_fp32(gpu, rows, D, dt):
+    """HIP LayerNorm against torch's fp32 CPU layer_norm of the same 16-bit inputs: the only
+    difference allowed is the one rounding of the output to fp16/bf16 (plus fp32 noise)."""
+    ops = _ops()
+    announce(f"layer_norm rows={rows} D={D} {dt}")
+    g = _gen(rows + D)
+    x = (torch.randn(rows, D, generator=g) * 3 + 0.5).to(dt)
+    w = (1 + 0.1 * torch.randn(D, generator=g)).to(dt)
+    b = (0.1 * torch.randn(D, generator=g)).to(dt)
+    y = ops.layer_norm(x.to(gpu), w.to(gpu), b.to(gpu), 1e-6).cpu()
+    ref = torch.nn.functional.layer_norm(x.float(), (D,), w.float(), b.float(), 1e-6)
+    ulp = 2.0 ** -8 if dt == torch.bfloat16 else 2.0 ** -11  # half an output ulp is the rounding bound
+    assert y.dtype == dt and y.shape == x.shape
+    assert ((y.float() - ref).abs() <= ulp * ref.abs() + 1e-4).all()
+
+
+def test_layer_norm_strided_rows_and_module(gpu):
+    # x[:, 0] of a [B, N, D] activation (the ViT head's LayerNorm) is a strided row view
+    from dimq_amd.modules import DIMQLayerNorm
+    g = _gen(9)
+    x = torch.randn(6, 197, 768, generator=g).bfloat16()
+    ln = torch.nn.LayerNorm(768, eps=1e-6)
+    with torch.no_grad():
+        ln.weight.copy_(1 + 0.1 * torch.randn(768, generator=g))
+        ln.bias.copy_(0.1 * torch.randn(768, generator=g))
+    mod = DIMQLayerNorm.from_layer_norm(ln).to(gpu).bfloat16()
+    xd = x.to(gpu)
+    y = mod(xd[:, 0]).cpu()
+    ref = torch.nn.functional.layer_norm(x[:, 0].float(), (768,), ln.weight.bfloat16().float(),
+                                         ln.bias.bfloat16().float(), 1e-6)
+    assert ((y.float() - ref).abs() <= 2.0 ** -8 * ref.abs() + 1e-4).all()
+    torch.testing.assert_close(mod(xd).cpu()[:, 0], y, rtol=0, atol=0)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        mod(x)

@@ -325,7 +325,7 @@ def test_linear_lut_fp16_codebook_matches_generic_path(gpu):
     dict(B=2, C=4, H=9, W=8, OC=6, KH=3, KW=3, s=(1, 1), p=(1, 1), d=(1, 1), g=1),        # generic implicit GEMM
     dict(B=1, C=6, H=11, W=7, OC=4, KH=3, KW=2, s=(2, 1), p=(1, 0), d=(1, 2), g=2),       # groups + dilation
 ])
-@pytest.mark.parametrize("xdt", [torch.float32, torch.float16])
+@pytest.mark.parametrize("xdt", [torch.float32, torch.float16, torch.bfloat16])
 def test_conv2d_lut_fp16_codebook_fast_path(gpu, case, xdt):
     ops = _ops()
     announce(f"conv2d_lut fp16 codebook {case} {xdt}")

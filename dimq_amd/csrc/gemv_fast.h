@@ -6,7 +6,12 @@
 // it, so each lane's weight indices and activations are contiguous in memory.
 // Every load of the wave (the lane's K/64 packed indices: 24 bytes at 3 bits;
 // its activation row slice: 128 bytes at bf16) is issued before any compute,
-// so the whole weight stream is in flight at once.  The 16x16x32 MFMA's k
+// so the whole weight stream is in flight at once.  Loads retire in order,
+// so the codebook values and the activations are loaded *before* the weight
+// stream: the waits for them (codebook planes, activation conversion) do not
+// wait for the weights, and that VALU work runs while the weights stream in
+// (measured at cfg5 M = 1: the codebook and activations issued after the
+// weights left every VALU phase serial behind the last weight byte).  The 16x16x32 MFMA's k
 // dimension takes 8 consecutive k from each lane group (any k order works as
 // long as the activation and weight lanes agree); rows m >= M are zero.  The
 // 16 partial sums are reduced through LDS.
@@ -39,9 +44,29 @@ __global__ __launch_bounds__(1024) void gemv_fast_kernel(const GemmArgs p) {
   const bool arow = col < p.M;
   CodebookRegs<BITS> cb;
   float colscale = 1.0f;
+  // codebook value tid of the 16 rows (as stage_codebook: 0 past cb_size or N)
+  const int cb_total = ((p.cb_rows == 1) ? 1 : 16) * E;
+  float cbv = 0.0f;
+  if (tid < cb_total) {
+    const int rr = tid / E, j = tid - (tid / E) * E;
+    const int64_t row = (p.cb_rows == 1) ? 0 : n0 + rr;
+    if (j < p.cb_size && (p.cb_rows == 1 || row < p.N)) cbv = load_as_float(p.cb, p.cb_dt, row * p.cb_size + j);
+  }
   for (int r = 0; r < rounds; ++r) {
     const int64_t k0 = ((int64_t)(r * WAVES + wave) * 4 + g) * KL;
-    // ---- all loads of the round first
+    // ---- all loads of the round first: activations, then the weight stream
+    RawA<XT> ra[KL / 16];
+    {
+#pragma unroll
+      for (int h = 0; h < KL / 16; ++h) {
+        if (arow) {
+          issue_a16<XT>(p.x, (int64_t)col * p.ldx + k0 + 16 * h, ra[h]);
+        } else {
+#pragma unroll
+          for (int w = 0; w < RawA<XT>::kWords; ++w) ra[h].w[w] = 0u;
+        }
+      }
+    }
     uint32_t bw[KL * BITS / 32];
     {
       const uint8_t* src = p.w + (((n * p.K + k0) * BITS) >> 3);
@@ -63,31 +88,20 @@ __global__ __launch_bounds__(1024) void gemv_fast_kernel(const GemmArgs p) {
         }
       }
     }
-    RawA<XT> ra[KL / 16];
-    {
-#pragma unroll
-      for (int h = 0; h < KL / 16; ++h) {
-        if (arow) {
-          issue_a16<XT>(p.x, (int64_t)col * p.ldx + k0 + 16 * h, ra[h]);
-        } else {
-#pragma unroll
-          for (int w = 0; w < RawA<XT>::kWords; ++w) ra[h].w[w] = 0u;
-        }
-      }
-    }
     if (r == 0) {
-      // the codebook loads go out after the round's weight and activation
-      // loads, so their latencies overlap instead of adding up
-      stage_codebook<E>(p.cb, p.cb_dt, p.cb_rows, p.cb_size, n0, 16, p.N, cbs, tid, WAVES * 64);
+      if (tid < cb_total) cbs[tid] = cbv;
       __syncthreads();  // codebook staged
       const int e = planes_from_lds<BITS, false>(cbs + ((p.cb_rows == 1) ? 0 : col * E), cb, cb);
       colscale = ldexpf(p.acc_scale, -e);
     }
+    // ---- activations to fp16 (their loads went out before the weights')
+    uint32_t a8s[KL / 16][8];
+#pragma unroll
+    for (int h = 0; h < KL / 16; ++h) convert_a16_big<BITS, XT>(ra[h], a8s[h]);
     // ---- decode + MFMA, 8 k per step
 #pragma unroll
     for (int h = 0; h < KL / 16; ++h) {
-      uint32_t a8[8];
-      convert_a16_big<BITS, XT>(ra[h], a8);
+      const uint32_t* a8 = a8s[h];
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const int s = 2 * h + t;  // step: indices 8s .. 8s+7 of the lane's range
@@ -124,7 +138,10 @@ __global__ __launch_bounds__(1024) void gemv_fast_kernel(const GemmArgs p) {
 // the activation conversion of 16 rows per lane costing more than the
 // up-front loads save), K a multiple of 4096, 16-byte aligned rows/streams.
 inline bool gemv_fast_supported(const GemmArgs& p, int bits) {
-  return p.M >= 1 && p.M <= 4 && !p.conv && (bits == 2 || bits == 3 || bits == 4) && p.K % 4096 == 0 &&
+  int max_m = 4;
+  if (const char* f = getenv("DIMQ_GEMV_FAST_M")) max_m = atoi(f);  // A/B runs: largest M it takes (<= 16)
+  max_m = max_m < 1 ? 1 : (max_m > 16 ? 16 : max_m);
+  return p.M >= 1 && p.M <= max_m && !p.conv && (bits == 2 || bits == 3 || bits == 4) && p.K % 4096 == 0 &&
          p.fast_b && p.vec_a;
 }
 

@@ -134,6 +134,13 @@ int linear_codebook_impl(const void* x, int x_dtype, int64_t M, int64_t K, int64
       default: return launch_gemv_fast<4>(p, x_dtype, s);
     }
   }
+  if (tile == kTileGemv && gemv_split_supported(p, bits) && !getenv("DIMQ_GEMV_OLD")) {
+    switch (bits) {
+      case 2: return launch_gemv_split<2>(p, x_dtype, s);
+      case 3: return launch_gemv_split<3>(p, x_dtype, s);
+      default: return launch_gemv_split<4>(p, x_dtype, s);
+    }
+  }
   return dispatch<false>(p, bits, x_dtype, tile, s);
 }
 

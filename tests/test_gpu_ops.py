@@ -413,9 +413,12 @@ def test_linear_codebook_large_tiles(gpu, monkeypatch, bits, tile, M, N, K, xdt)
 
 @pytest.mark.parametrize("bits", [2, 3, 4])
 @pytest.mark.parametrize("M,N,K,xdt", [(1, 300, 4096, torch.bfloat16), (4, 64, 8192, torch.float16),
-                                       (3, 130, 4096, torch.float32), (16, 130, 4096, torch.bfloat16)])
+                                       (3, 130, 4096, torch.float32), (16, 130, 4096, torch.bfloat16),
+                                       (5, 77, 4096, torch.float16), (9, 200, 8192, torch.bfloat16),
+                                       (16, 48, 12288, torch.float32)])
 def test_linear_codebook_gemv_fast(gpu, bits, M, N, K, xdt):
-    """Decode-shape GEMV (all loads issued up front), N tails, per-layer and per-channel codebooks."""
+    """Decode-shape GEMVs (all loads issued up front: M <= 4 one k range per lane, 4 < M <= 16 split-K
+    rounds), N tails, per-layer and per-channel codebooks."""
     ops = _ops()
     for per_channel in (True, False):
         announce(f"linear_codebook gemv bits={bits} M={M} N={N} K={K} {xdt} pc={per_channel}")

@@ -59,6 +59,32 @@ def test_host_only_entry_points(capi):
     assert lib.dimq_conv2d_prepared_words(512, 256, 1, 1, 4) == 512 * 256 * 4 // 32
 
 
+def test_w4a4_workspace_sizes(capi):
+    lib = capi.lib
+    F16, F32 = capi.F16, capi.F32
+    up = lambda b: (b + 255) // 256 * 256
+    # linear_lut: the activations as fp16 a - zp, only for fp16 codebooks
+    assert lib.dimq_linear_lut_workspace_bytes(1576, 768, F16) == up(1576 * 768 * 2)
+    assert lib.dimq_linear_lut_workspace_bytes(1576, 768, F32) == 0
+    assert lib.dimq_linear_lut_workspace_bytes(0, 768, F16) == 0
+    # conv2d_lut: the activations + the 4-bit LDS-halo weight layout where the shape has one
+    halo_words = 64 * 2 * 9 * 4  # OC * 2 lane groups * ceil(T/4) * bits, T = 9 * 64 / 16
+    assert lib.dimq_conv2d_lut_workspace_bytes(32, 64, 56, 56, 64, 64, 3, 3, 1, F16) == \
+        up(32 * 64 * 56 * 56 * 2) + halo_words * 4
+    assert lib.dimq_conv2d_lut_workspace_bytes(2, 6, 11, 7, 4, 3, 3, 2, 2, F16) == up(2 * 6 * 11 * 7 * 2)
+    assert lib.dimq_conv2d_lut_workspace_bytes(32, 64, 56, 56, 64, 64, 3, 3, 1, F32) == 0
+
+
+def test_layer_norm_argument_errors(capi):
+    lib = capi.lib
+    assert lib.dimq_layer_norm(None, capi.F32, 4, 768, 768, None, None, capi.F32, 1e-6, None, None) == 1
+    assert lib.dimq_last_error() == b"layer_norm expects fp16 or bf16 input"
+    assert lib.dimq_layer_norm(None, capi.BF16, 4, 100, 100, None, None, capi.F32, 1e-6, None, None) == 1
+    assert b"multiple of 8" in lib.dimq_last_error()
+    assert lib.dimq_layer_norm(None, capi.BF16, 4, 768, 512, None, None, capi.F32, 1e-6, None, None) == 1
+    assert b"row stride" in lib.dimq_last_error()
+
+
 def test_argument_errors_return_codes_without_touching_the_gpu(capi):
     lib = capi.lib
     assert lib.dimq_pack_bits(None, 0, 5, None, None) == 2                 # DIMQ_ERR_UNSUPPORTED

@@ -64,6 +64,7 @@ _SIGS = {
     "dimq_conv2d_lut_ws": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _int, _i64, _dbl, _i64, _vp,
                                   _int, _i64] + [_i64] * 11 + [_vp, _vp, _i64, _vp]),
     "dimq_layer_norm": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp, _int, _dbl, _vp, _vp]),
+    "dimq_max_pool2d_nhwc": (_int, [_vp, _int] + [_i64] * 10 + [_vp, _vp]),
     "dimq_pack_bits": (_int, [_vp, _i64, _int, _vp, _vp]),
     "dimq_unpack_bits": (_int, [_vp, _i64, _i64, _int, _vp, _vp]),
     "dimq_hard_quantize": (_int, [_vp, _int, _i64, _i64, _vp, _i64, _int, _vp, _vp, _vp]),
@@ -462,6 +463,24 @@ def layer_norm_impl(x, normalized_size, weight, bias, eps):
     return y.view(x.shape)
 
 
+def max_pool2d_impl(x, kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w):
+    """2-D max pooling of a channels-last fp16/bf16 tensor (support op of the ResNet workload)."""
+    _require_cuda(x, "max_pool2d expects CUDA input")
+    if x.dim() != 4 or not x.is_contiguous(memory_format=torch.channels_last):
+        raise RuntimeError("max_pool2d expects a channels-last 4-D input")
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise RuntimeError("max_pool2d expects fp16 or bf16 input")
+    B, C, H, W = x.shape
+    oh = (H + 2 * pad_h - kernel_h) // stride_h + 1 if stride_h > 0 else 0
+    ow = (W + 2 * pad_w - kernel_w) // stride_w + 1 if stride_w > 0 else 0
+    y = torch.empty((B, C, max(oh, 0), max(ow, 0)), dtype=x.dtype, device=x.device,
+                    memory_format=torch.channels_last)
+    with torch.cuda.device(x.device):
+        _check(lib.dimq_max_pool2d_nhwc(_ptr(x), _dtype(x), B, C, H, W, kernel_h, kernel_w, stride_h, stride_w, pad_h,
+                                        pad_w, _ptr(y), _stream(x.device)))
+    return y
+
+
 # ---------------------------------------------------------------------------
 # torch.library registration
 # ---------------------------------------------------------------------------
@@ -502,6 +521,8 @@ _SCHEMAS = {
     # support op of the end-to-end ViT workload
     "layer_norm": ("layer_norm(Tensor x, int normalized_size, Tensor? weight, Tensor? bias, float eps) -> Tensor",
                    layer_norm_impl),
+    "max_pool2d_nhwc": ("max_pool2d_nhwc(Tensor x, int kernel_h, int kernel_w, int stride_h, int stride_w, int pad_h, "
+                        "int pad_w) -> Tensor", max_pool2d_impl),
 }
 
 

@@ -25,7 +25,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .modules import DIMQCodebookConv2d, DIMQCodebookLinear, DIMQLayerNorm, quantize_model_weight_only
+from .modules import DIMQCodebookConv2d, DIMQCodebookLinear, DIMQLayerNorm, DIMQMaxPool2d, quantize_model_weight_only
 
 
 def _fused(mod: nn.Module, x: torch.Tensor, residual: torch.Tensor | None = None,
@@ -174,6 +174,7 @@ class ResNet18(nn.Module):
     def __init__(self, classes: int = 1000) -> None:
         super().__init__()
         self.conv1 = nn.Conv2d(3, 64, 7, 2, 3)
+        self.maxpool = nn.MaxPool2d(3, 2, 1)
         layers = []
         cin = 64
         for i, cout in enumerate((64, 128, 256, 512)):
@@ -185,7 +186,7 @@ class ResNet18(nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         x = _fused(self.conv1, x, act="relu")
-        x = F.max_pool2d(x, 3, 2, 1)
+        x = self.maxpool(x)
         x = self.layer4(self.layer3(self.layer2(self.layer1(x))))
         x = torch.flatten(F.adaptive_avg_pool2d(x, 1), 1)
         return self.fc(x)
@@ -216,12 +217,14 @@ def resnet18(seed: int = 2) -> ResNet18:
 
 
 def quantize_resnet18(model: ResNet18, out_dtype: torch.dtype = torch.float16) -> ResNet18:
-    """cfg3: 8-bit stem and fc, 2-bit 3x3 convs, 4-bit 1x1 downsample convs."""
+    """cfg3: 8-bit stem and fc, 2-bit 3x3 convs, 4-bit 1x1 downsample convs; the stem pool -> DIMQMaxPool2d."""
     def pick(name, module):
         if isinstance(module, nn.Linear) or name == "conv1":
             return 8
         return 2 if module.kernel_size == (3, 3) else 4
-    return quantize_model_weight_only(model, pick, out_dtype=out_dtype)
+    model = quantize_model_weight_only(model, pick, out_dtype=out_dtype)
+    model.maxpool = DIMQMaxPool2d.from_max_pool(model.maxpool)  # the HIP max-pool kernel
+    return model
 
 
 def resnet18_flops(batch: int) -> float:

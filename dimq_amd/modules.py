@@ -226,6 +226,23 @@ class DIMQLayerNorm(nn.LayerNorm):
         return ops.layer_norm(x, self.weight, self.bias, self.eps)
 
 
+class DIMQMaxPool2d(nn.MaxPool2d):
+    """nn.MaxPool2d whose forward runs the HIP max-pool kernel (channels-last
+    fp16/bf16 CUDA inputs, dilation 1, floor mode).  Other inputs raise: the
+    CPU reference model converts it back to nn.MaxPool2d (torch's own op)."""
+
+    @classmethod
+    def from_max_pool(cls, mp: nn.MaxPool2d) -> "DIMQMaxPool2d":
+        if mp.dilation not in (1, (1, 1)) or mp.ceil_mode or mp.return_indices:
+            raise ValueError("DIMQMaxPool2d supports dilation 1, floor mode and no indices")
+        return cls(mp.kernel_size, mp.stride, mp.padding)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if not x.is_cuda:
+            raise RuntimeError("DIMQMaxPool2d runs on CUDA (HIP) tensors only")
+        return ops.max_pool2d_nhwc(x, self.kernel_size, self.stride, self.padding)
+
+
 def make_packed_layer(layer: Mapping[str, Any], *, use_cuda_kernel: bool = True) -> nn.Module:
     """modules.py:153-158, extended with weight-only (format v2) layers."""
     weight_only = layer.get("activation_quantization") == "none" or layer.get("bit_a", 4) is None

@@ -207,6 +207,15 @@ def layer_norm(x: torch.Tensor, weight: torch.Tensor | None, bias: torch.Tensor 
     return torch.ops.dimq.layer_norm(x, int(x.shape[-1]), weight, bias, float(eps))
 
 
+def max_pool2d_nhwc(x: torch.Tensor, kernel_size, stride=None, padding=0) -> torch.Tensor:
+    """2-D max pooling of a channels-last fp16/bf16 tensor on the HIP kernel (the ResNet workload's stem pool)."""
+    require_extension()
+    kh, kw = _pair(kernel_size)
+    sh, sw = _pair(stride if stride is not None else kernel_size)
+    ph, pw = _pair(padding)
+    return torch.ops.dimq.max_pool2d_nhwc(x, kh, kw, sh, sw, ph, pw)
+
+
 def _pair(value: Sequence[int] | int) -> tuple[int, int]:
     if isinstance(value, int):
         return int(value), int(value)

@@ -237,9 +237,9 @@ int dimq_conv2d_codebook_ex(const void* x, int x_dtype, int x_layout, int64_t B,
                             int variant, void* stream);
 
 /* ---------------------------------------------------------------------------
- * 3. Support op of the end-to-end ViT-B/16 workload (not a DIMQ op: the
- *    reference runs torch.nn.LayerNorm between its quantized layers,
- *    train_dimq_vit.py via torchvision's vit_b_16).
+ * 3. Support ops of the end-to-end workloads (not DIMQ ops: the reference
+ *    runs torch's LayerNorm and max pooling between its quantized layers,
+ *    train_dimq_vit.py / train_dimq_resnet.py via torchvision's models).
  * ------------------------------------------------------------------------- */
 
 /* LayerNorm over the last dimension: y = (x - mean) * rstd * weight + bias,
@@ -249,6 +249,16 @@ int dimq_conv2d_codebook_ex(const void* x, int x_dtype, int x_layout, int64_t B,
  * dim % 8 == 0, dim <= 2048, 16-byte aligned x and y. */
 int dimq_layer_norm(const void* x, int x_dtype, int64_t rows, int64_t dim, int64_t ldx, const void* weight,
                     const void* bias, int wb_dtype, double eps, void* y, void* stream);
+
+/* 2-D max pooling over channels-last activations (the ResNet-18 workload's
+ * stem pool; the reference's ResNet runs torch's max_pool2d, torchvision
+ * resnet18): y[b,oh,ow,c] = max over the window's in-image taps, NaN
+ * propagating, as torch.nn.functional.max_pool2d (dilation 1, floor mode).
+ * x [B,H,W,C] and y [B,OH,OW,C] contiguous NHWC in fp16/bf16, C % 8 == 0,
+ * 16-byte aligned; OH = (H + 2 pad_h - kernel_h) / stride_h + 1. */
+int dimq_max_pool2d_nhwc(const void* x, int x_dtype, int64_t B, int64_t C, int64_t H, int64_t W, int64_t kernel_h,
+                         int64_t kernel_w, int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                         void* y, void* stream);
 
 #ifdef __cplusplus
 }

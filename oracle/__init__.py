@@ -292,14 +292,17 @@ def dequantized_model(qmodel):
     import torch
     import torch.nn as nn
 
-    from dimq_amd.modules import DIMQCodebookConv2d, DIMQCodebookLinear, DIMQLayerNorm
+    from dimq_amd.modules import DIMQCodebookConv2d, DIMQCodebookLinear, DIMQLayerNorm, DIMQMaxPool2d
 
     m = copy.deepcopy(qmodel).cpu().float()
     for name, mod in list(m.named_modules()):
-        if isinstance(mod, DIMQLayerNorm):  # HIP LayerNorm -> torch's own op, same parameters
-            new = nn.LayerNorm(mod.normalized_shape, eps=mod.eps, elementwise_affine=mod.elementwise_affine,
-                               bias=mod.bias is not None)
-            new.load_state_dict(mod.state_dict())
+        if isinstance(mod, (DIMQLayerNorm, DIMQMaxPool2d)):  # HIP support ops -> torch's own ops
+            if isinstance(mod, DIMQLayerNorm):
+                new = nn.LayerNorm(mod.normalized_shape, eps=mod.eps, elementwise_affine=mod.elementwise_affine,
+                                   bias=mod.bias is not None)
+                new.load_state_dict(mod.state_dict())
+            else:
+                new = nn.MaxPool2d(mod.kernel_size, mod.stride, mod.padding)
             parent = m
             parts = name.split(".")
             for part in parts[:-1]:

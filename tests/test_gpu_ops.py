@@ -798,3 +798,23 @@ def test_layer_norm_strided_rows_and_module(gpu):
     torch.testing.assert_close(mod(xd).cpu()[:, 0], y, rtol=0, atol=0)
     with pytest.raises(RuntimeError, match="CUDA"):
         mod(x)
+
+
+# ---------------------------------------------------------------- max pooling (ResNet workload support op)
+@pytest.mark.parametrize("shape,k,s,p,dt", [((2, 64, 112, 112), 3, 2, 1, torch.float16),
+                                            ((3, 16, 9, 10), 3, 2, 1, torch.bfloat16),
+                                            ((2, 8, 7, 7), 2, 2, 0, torch.float16),
+                                            ((1, 24, 5, 6), 3, 1, 1, torch.bfloat16)])
+def test_max_pool2d_nhwc_vs_torch(gpu, shape, k, s, p, dt):
+    """Channels-last HIP max pool against torch's CPU max_pool2d of the same values: exact, NaN included."""
+    ops = _ops()
+    announce(f"max_pool2d {shape} k={k} s={s} p={p} {dt}")
+    x = torch.randn(shape, generator=_gen(sum(shape) + k)).to(dt)
+    x[0, 1, 2, 3] = float("nan")
+    x = x.contiguous(memory_format=torch.channels_last)
+    y = ops.max_pool2d_nhwc(x.to(gpu), k, s, p)
+    ref = torch.nn.functional.max_pool2d(x.float(), k, s, p)
+    assert y.shape == ref.shape and y.dtype == dt and y.is_contiguous(memory_format=torch.channels_last)
+    torch.testing.assert_close(y.cpu().float(), ref, rtol=0, atol=0, equal_nan=True)
+    with pytest.raises(RuntimeError, match="channels-last"):
+        ops.max_pool2d_nhwc(x.contiguous().to(gpu), k, s, p)

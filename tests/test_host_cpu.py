@@ -75,7 +75,7 @@ def test_w4a4_workspace_sizes(capi):
     assert lib.dimq_conv2d_lut_workspace_bytes(32, 64, 56, 56, 64, 64, 3, 3, 1, F32) == 0
 
 
-def test_layer_norm_argument_errors(capi):
+def test_support_op_argument_errors(capi):
     lib = capi.lib
     assert lib.dimq_layer_norm(None, capi.F32, 4, 768, 768, None, None, capi.F32, 1e-6, None, None) == 1
     assert lib.dimq_last_error() == b"layer_norm expects fp16 or bf16 input"
@@ -83,6 +83,10 @@ def test_layer_norm_argument_errors(capi):
     assert b"multiple of 8" in lib.dimq_last_error()
     assert lib.dimq_layer_norm(None, capi.BF16, 4, 768, 512, None, None, capi.F32, 1e-6, None, None) == 1
     assert b"row stride" in lib.dimq_last_error()
+    assert lib.dimq_max_pool2d_nhwc(None, capi.F16, 1, 12, 4, 4, 3, 3, 2, 2, 1, 1, None, None) == 1
+    assert b"multiple of 8" in lib.dimq_last_error()
+    assert lib.dimq_max_pool2d_nhwc(None, capi.F16, 1, 16, 4, 4, 3, 3, 2, 2, 2, 2, None, None) == 1
+    assert lib.dimq_last_error() == b"pad should be at most half of effective kernel size"
 
 
 def test_argument_errors_return_codes_without_touching_the_gpu(capi):

@@ -442,31 +442,30 @@ __global__ __launch_bounds__(256) void gemm_cb8_kernel(const GemmArgs p) {
   const int64_t nz = static_cast<int64_t>(blockIdx.z) * p.N;
   const int64_t cbase = static_cast<int64_t>(blockIdx.z) * p.cICg;
 
-  // codebook rows -> LDS (fp16, scaled by a per-row power of two)
-  for (int r = tid / 4; r < ROWS; r += 64) {
-    const int part = tid & 3;
+  // codebook rows -> LDS (fp16, scaled by a per-row power of two).  One
+  // pass: thread (row r = tid / 4, quarter part) loads its 64 entries back to
+  // back into registers (every load in flight at once), the row maxima meet
+  // in LDS, and the scaled entries go out from the registers.
+  static_assert(ROWS == 64, "one codebook row per 4 threads");
+  {
+    const int r = tid >> 2, part = tid & 3;
     const int64_t n = n0 + r;
     const int64_t row = (p.cb_rows == 1) ? 0 : nz + n;
+    float cv[64];
+#pragma unroll
+    for (int i = 0; i < 64; ++i) {
+      const int j = part + 4 * i;
+      cv[i] = (n < p.N && j < p.cb_size) ? load_as_float(p.cb, p.cb_dt, row * p.cb_size + j) : 0.0f;
+    }
     float mx = 0.0f;
-#pragma unroll 16  // independent loads back to back, not one latency per entry
-    for (int j = part; j < 256; j += 4) {
-      const float c = (n < p.N && j < p.cb_size) ? load_as_float(p.cb, p.cb_dt, row * p.cb_size + j) : 0.0f;
-      mx = fmaxf(mx, fabsf(c));
-    }
+#pragma unroll
+    for (int i = 0; i < 64; ++i) mx = fmaxf(mx, fabsf(cv[i]));
     rmax[r][part] = mx;
-  }
-  __syncthreads();
-  for (int r = tid / 4; r < ROWS; r += 64) {
-    const int part = tid & 3;
-    const int64_t n = n0 + r;
-    const int64_t row = (p.cb_rows == 1) ? 0 : nz + n;
-    const float mx = fmaxf(fmaxf(rmax[r][0], rmax[r][1]), fmaxf(rmax[r][2], rmax[r][3]));
+    __syncthreads();
+    mx = fmaxf(fmaxf(rmax[r][0], rmax[r][1]), fmaxf(rmax[r][2], rmax[r][3]));
     const int e = cb_exponent(mx);
-#pragma unroll 16
-    for (int j = part; j < 256; j += 4) {
-      const float c = (n < p.N && j < p.cb_size) ? load_as_float(p.cb, p.cb_dt, row * p.cb_size + j) : 0.0f;
-      cbs[r * 256 + j] = (uint16_t)float_to_f16_bits(ldexpf(c, e));
-    }
+#pragma unroll
+    for (int i = 0; i < 64; ++i) cbs[r * 256 + part + 4 * i] = (uint16_t)float_to_f16_bits(ldexpf(cv[i], e));
     if (part == 0) rscale[r] = ldexpf(p.acc_scale, -e);
   }
 

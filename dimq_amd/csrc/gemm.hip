@@ -160,6 +160,52 @@ extern "C" int dimq_linear_codebook(const void* x, int x_dtype, int64_t M, int64
                                  bias, bias_dtype, N, y, y_dtype, nullptr, 0, DIMQ_ACT_NONE, variant, stream);
 }
 
+// fp32 activations on the large tiles: the tiles' fp16 form after one
+// conversion pass (the same round-to-nearest conversion the fp32 tiles apply
+// as they stage, so the results are the same bits; measured at cfg1, 1576 x
+// 768 fp32: 32.6 us for the fp32 tile against 25.2 us for the fp16 one).
+extern "C" int64_t dimq_linear_codebook_workspace_bytes(int64_t M, int64_t K, int bits, int x_dtype) {
+  if (x_dtype != DIMQ_F32 || M <= 64 || K <= 0 || K % 64 != 0 || !(bits == 2 || bits == 3 || bits == 4)) return 0;
+  return (M * K * 2 + 255) / 256 * 256;
+}
+
+extern "C" int dimq_linear_codebook_ex_ws(const void* x, int x_dtype, int64_t M, int64_t K, const uint8_t* packed_w,
+                                          int64_t packed_numel, int bits, const void* codebook, int cb_dtype,
+                                          int64_t cb_rows, int64_t cb_size, const void* bias, int bias_dtype,
+                                          int64_t N, void* y, int y_dtype, const void* residual, int residual_dtype,
+                                          int activation, int variant, void* workspace, int64_t workspace_bytes,
+                                          void* stream) {
+  DIMQ_CHECK(workspace_bytes >= 0, "workspace_bytes must be non-negative");
+  const int64_t need = dimq_linear_codebook_workspace_bytes(M, K, bits, x_dtype);
+  const int mode = epi_mode(Epi{residual, residual_dtype, activation, 0});
+  if (workspace != nullptr && need > 0 && workspace_bytes >= need && aligned(workspace, 16) &&
+      variant != DIMQ_VARIANT_SMALL_M && aligned(packed_w, 16) && aligned(x, 16) &&
+      (mode == kEpiNone || mode == kEpiRelu || mode == kEpiGelu || mode == kEpiRes) && !getenv("DIMQ_NO_F16_PASS")) {
+    // argument checks first, as the plain entry point does them
+    DIMQ_CHECK(y_dtype == DIMQ_F32 || y_dtype == DIMQ_F16 || y_dtype == DIMQ_BF16,
+               "linear_codebook output dtype must be fp32, fp16 or bf16");
+    DIMQ_CHECK(is_float_dtype(cb_dtype), "codebook must be floating point");
+    DIMQ_CHECK(bias == nullptr || is_float_dtype(bias_dtype), "bias must be floating point");
+    DIMQ_CHECK(N > 0, "linear dimensions must be positive");
+    DIMQ_CHECK(cb_rows == 1 || cb_rows == N, "codebook must have 1 (per layer) or out_features (per channel) rows");
+    DIMQ_CHECK(cb_size >= 1 && cb_size <= (1 << bits), "codebook rows must hold between 1 and 2^bits entries");
+    DIMQ_CHECK(packed_numel >= (N * K * bits + 7) / 8, "packed_weight is too small for out_features * in_features");
+    DIMQ_CHECK(variant >= DIMQ_VARIANT_AUTO && variant <= DIMQ_VARIANT_MFMA, "unknown kernel variant %d", variant);
+    DIMQ_CHECK(residual == nullptr || is_float_dtype(residual_dtype), "residual must be floating point");
+    DIMQ_CHECK(activation >= DIMQ_ACT_NONE && activation <= DIMQ_ACT_GELU, "unknown activation %d", activation);
+    uint16_t* q = static_cast<uint16_t*>(workspace);
+    const hipStream_t st = as_stream(stream);
+    const int rc = launch_to_f16(x, x_dtype, M * K, q, st);
+    if (rc != DIMQ_OK) return rc;
+    return dimq_linear_codebook_ex(q, DIMQ_F16, M, K, packed_w, packed_numel, bits, codebook, cb_dtype, cb_rows,
+                                   cb_size, bias, bias_dtype, N, y, y_dtype, residual, residual_dtype, activation,
+                                   variant, stream);
+  }
+  return dimq_linear_codebook_ex(x, x_dtype, M, K, packed_w, packed_numel, bits, codebook, cb_dtype, cb_rows, cb_size,
+                                 bias, bias_dtype, N, y, y_dtype, residual, residual_dtype, activation, variant,
+                                 stream);
+}
+
 extern "C" int dimq_linear_codebook_ex(const void* x, int x_dtype, int64_t M, int64_t K, const uint8_t* packed_w,
                                        int64_t packed_numel, int bits, const void* codebook, int cb_dtype,
                                        int64_t cb_rows, int64_t cb_size, const void* bias, int bias_dtype, int64_t N,

@@ -432,6 +432,24 @@ def test_linear_codebook_gemv_fast(gpu, bits, M, N, K, xdt):
         assert oracle.rel_err(y, ref) <= TOL, (bits, M, N, K, per_channel, oracle.rel_err(y, ref))
 
 
+@pytest.mark.parametrize("act", [None, "gelu"])
+def test_linear_codebook_fp32_pass_same_bits(gpu, monkeypatch, act):
+    """fp32 activations on the large tiles go through one fp32 -> fp16 pass (round to nearest even, the
+    rounding the fp32 tiles apply while staging): the output must be bit-identical to the fp32 tiles'."""
+    ops = _ops()
+    g = _gen(91)
+    cb, idx, packed = _codebook_case(384, 768, 4, True, g)
+    x = torch.randn(1576, 768, generator=g).to(gpu)
+    bias = (torch.randn(384, generator=g) * 0.1).to(gpu)
+    run = lambda: ops.dimq_linear_codebook(x, packed.to(gpu), cb.to(gpu), 4, bias, 384, 768,
+                                           out_dtype=torch.float32, activation=act)
+    y_pass = run()
+    monkeypatch.setenv("DIMQ_NO_F16_PASS", "1")
+    y_direct = run()
+    torch.cuda.synchronize()
+    assert torch.equal(y_pass, y_direct)
+
+
 def test_linear_codebook_cfg1_shape(gpu):
     """BASELINE cfg1: X fp32 [1576,768], 4-bit per-channel W [3072,768], bias, y fp32."""
     ops = _ops()

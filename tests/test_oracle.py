@@ -215,3 +215,26 @@ def test_conv_dequant_reference_matches_direct_sum():
             for ow in range(4):
                 ref[0, co, oh, ow] = (xp[0, :, oh:oh + 3, ow:ow + 3] * w[co]).sum()
     np.testing.assert_allclose(y, ref, rtol=1e-5, atol=1e-5)
+
+
+def test_a4_exact_bar_accepts_summation_order_and_rejects_planted_zero_point():
+    """The W4A4 fast-path bar (float64-exact deviation at most twice the fp32 LUT loop's): an fp32 sum in
+    another order passes at K = 4096; the oracle's own LUT with a wrong zero point fails."""
+    import torch
+    from tests.a4_check import a4_exact_check, a4_levels
+
+    g = torch.Generator().manual_seed(4096)
+    M, N, K = 2, 512, 4096
+    x = torch.randn(M, K, generator=g)
+    idx = torch.randint(0, 16, (N, K), generator=g, dtype=torch.uint8)
+    cb = (torch.linspace(-0.5, 0.5, 16) + 0.01 * torch.randn(16, generator=g)).half()
+    bias = torch.randn(N, generator=g)
+    packed = torch.from_numpy(oracle.pack_bits(idx, 4))
+    ref = oracle.linear_lut(x, packed, cb.float(), 0.2, 7, bias, N, K)
+    lv = a4_levels(x, 0.2, 7)
+    exact = lv @ cb.double()[idx.long()].T + bias.double()
+    other_order = (lv.float() / 0.2) @ cb.float()[idx.long()].T * 0.2 + bias  # blocked fp32, scale last
+    a4_exact_check(other_order, ref, exact, K)
+    planted = torch.from_numpy(oracle.linear_lut(x, packed, cb.float(), 0.2, 6, bias, N, K))
+    with pytest.raises(AssertionError):
+        a4_exact_check(planted, ref, exact, K)

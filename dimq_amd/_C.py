@@ -80,6 +80,9 @@ _SIGS = {
     "dimq_linear_codebook_workspace_bytes": (_i64, [_i64, _i64, _int, _int]),
     "dimq_linear_codebook_ex_ws": (_int, [_vp, _int, _i64, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _vp, _int,
                                           _i64, _vp, _int, _vp, _int, _int, _int, _vp, _i64, _vp]),
+    "dimq_linear_codebook_act_workspace_bytes": (_i64, [_i64, _i64]),
+    "dimq_linear_codebook_act": (_int, [_vp, _int, _i64, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _vp, _i64, _vp,
+                                        _int, _i64, _vp, _int, _int, _vp, _i64, _vp]),
     "dimq_conv2d_codebook_ex": (_int, [_vp, _int, _int, _i64, _i64, _i64, _i64, _vp, _i64, _int, _vp, _i64, _vp,
                                        _int, _i64, _i64, _vp, _int] + [_i64] * 10 +
                                 [_vp, _int, _int, _vp, _int, _int, _int, _vp]),
@@ -376,6 +379,34 @@ def linear_codebook_impl(x, packed_w, codebook, bits, bias, out_features, in_fea
     return y.view(*x.shape[:-1], out_features)
 
 
+def linear_codebook_act_impl(x, packed_w, codebook, bits, act_centers, bias, out_features, in_features,
+                             out_dtype=None, variant=0):
+    _require_cuda(x, "linear_codebook_act expects CUDA input")
+    _require_cuda(packed_w, "linear_codebook_act expects CUDA packed_weight")
+    _require_cuda(codebook, "linear_codebook_act expects CUDA codebook")
+    _require_cuda(act_centers, "linear_codebook_act expects CUDA activation centres")
+    if x.dim() == 0 or x.size(-1) != in_features:
+        raise RuntimeError("input last dimension must equal in_features")
+    if packed_w.dtype != torch.uint8:
+        raise RuntimeError("packed_weight must be uint8")
+    xc = x.contiguous()
+    pw = packed_w.contiguous().view(-1)
+    cb = codebook.contiguous()
+    ac = act_centers.detach().reshape(-1).float().contiguous()
+    rows, size = _cb_shape(cb, out_features)
+    b, bp, bdt, _ = _bias_args(bias, out_features, "out_features")
+    odt = x.dtype if out_dtype is None else out_dtype
+    M = xc.numel() // in_features if in_features else 0
+    y = torch.empty((M, out_features), dtype=odt, device=xc.device)
+    ws = _workspace(lib.dimq_linear_codebook_act_workspace_bytes(M, in_features), xc.device)
+    with torch.cuda.device(xc.device):
+        _check(lib.dimq_linear_codebook_act(_ptr(xc), _dtype(xc), M, in_features, _ptr(pw), pw.numel(), int(bits),
+                                            _ptr(cb), _dtype(cb), rows, size, _ptr(ac), ac.numel(), bp, bdt,
+                                            out_features, _ptr(y), _dtype(y), int(variant), _ptr(ws),
+                                            0 if ws is None else ws.numel(), _stream(xc.device)))
+    return y.view(*x.shape[:-1], out_features)
+
+
 def prepare_conv_weight_impl(packed_w, bits, out_channels, in_channels, kernel_h, kernel_w):
     _require_cuda(packed_w, "prepare_conv_weight expects a CUDA tensor")
     if packed_w.dtype != torch.uint8:
@@ -523,6 +554,9 @@ _SCHEMAS = {
                         conv2d_codebook_impl),
     "prepare_conv_weight": ("prepare_conv_weight(Tensor packed_w, int bits, int out_channels, int in_channels, "
                             "int kernel_h, int kernel_w) -> Tensor", prepare_conv_weight_impl),
+    "linear_codebook_act": ("linear_codebook_act(Tensor x, Tensor packed_w, Tensor codebook, int bits, "
+                            "Tensor act_centers, Tensor? bias, int out_features, int in_features, "
+                            "ScalarType? out_dtype=None, int variant=0) -> Tensor", linear_codebook_act_impl),
     # support op of the end-to-end ViT workload
     "layer_norm": ("layer_norm(Tensor x, int normalized_size, Tensor? weight, Tensor? bias, float eps) -> Tensor",
                    layer_norm_impl),

@@ -206,6 +206,36 @@ extern "C" int dimq_linear_codebook_ex_ws(const void* x, int x_dtype, int64_t M,
                                  stream);
 }
 
+extern "C" int64_t dimq_linear_codebook_act_workspace_bytes(int64_t M, int64_t K) {
+  if (M <= 0 || K <= 0) return 0;
+  return (M * K * 2 + 255) / 256 * 256;
+}
+
+// Activations quantized to their nearest activation-codebook centre (as fp16
+// values, one element-wise pass into the workspace), then the weight-codebook
+// tiles on them: the dequantize-then-MFMA form of the weight x activation
+// codebook product.
+extern "C" int dimq_linear_codebook_act(const void* x, int x_dtype, int64_t M, int64_t K, const uint8_t* packed_w,
+                                        int64_t packed_numel, int bits, const void* codebook, int cb_dtype,
+                                        int64_t cb_rows, int64_t cb_size, const float* act_centers, int64_t n_act,
+                                        const void* bias, int bias_dtype, int64_t N, void* y, int y_dtype, int variant,
+                                        void* workspace, int64_t workspace_bytes, void* stream) {
+  DIMQ_CHECK(x_dtype == DIMQ_F32 || x_dtype == DIMQ_F16 || x_dtype == DIMQ_BF16,
+             "linear_codebook_act expects fp32, fp16 or bf16 input");
+  DIMQ_CHECK(n_act >= 1 && n_act <= 256, "activation codebook must hold between 1 and 256 centres");
+  DIMQ_CHECK(act_centers != nullptr, "activation codebook is required");
+  DIMQ_CHECK(M >= 0 && N > 0 && K > 0, "linear dimensions must be positive");
+  if (M == 0) return DIMQ_OK;
+  const int64_t need = dimq_linear_codebook_act_workspace_bytes(M, K);
+  DIMQ_CHECK(workspace != nullptr && workspace_bytes >= need && aligned(workspace, 16),
+             "workspace must be 16-byte aligned and hold dimq_linear_codebook_act_workspace_bytes bytes");
+  uint16_t* q = static_cast<uint16_t*>(workspace);
+  const int rc = launch_act_codebook_f16(x, x_dtype, M * K, act_centers, static_cast<int>(n_act), q, as_stream(stream));
+  if (rc != DIMQ_OK) return rc;
+  return dimq_linear_codebook_ex(q, DIMQ_F16, M, K, packed_w, packed_numel, bits, codebook, cb_dtype, cb_rows, cb_size,
+                                 bias, bias_dtype, N, y, y_dtype, nullptr, 0, DIMQ_ACT_NONE, variant, stream);
+}
+
 extern "C" int dimq_linear_codebook_ex(const void* x, int x_dtype, int64_t M, int64_t K, const uint8_t* packed_w,
                                        int64_t packed_numel, int bits, const void* codebook, int cb_dtype,
                                        int64_t cb_rows, int64_t cb_size, const void* bias, int bias_dtype, int64_t N,

@@ -897,6 +897,9 @@ int launch_conv_stem(const void* x, int x_dtype, int x_layout, int64_t B, int64_
 
 // quant.hip: W4A4 activations as the fp16 integers a - zp (out 16-byte aligned)
 int launch_quantize_a4_f16(const void* x, int x_dtype, int64_t n, float s, int zp, uint16_t* out, hipStream_t st);
+// quant.hip: activations -> fp16 values of their nearest activation-codebook centre
+int launch_act_codebook_f16(const void* x, int x_dtype, int64_t n, const float* centers, int K, uint16_t* out,
+                            hipStream_t st);
 // quant.hip: fp32 (fp64) activations -> fp16, round to nearest even (out 16-byte aligned)
 int launch_to_f16(const void* x, int x_dtype, int64_t n, uint16_t* out, hipStream_t st);
 

@@ -144,7 +144,57 @@ __global__ __launch_bounds__(kThreads) void hard_quantize_kernel(const void* __r
   }
 }
 
+// Activation codebook (the QAT wrapper's activation_centers,
+// quant/dimq_wrapper.py:80-85 via hard_quantize_weight, quant/dimq.py:197-221):
+// out = fp16(C_a[argmin_c (x - C_a[c])^2]) with hard_quantize_kernel's torch
+// argmin semantics (first minimum; a NaN distance wins, the first NaN kept).
+// 4 activations per thread, the K <= 256 centres in LDS.
+__global__ __launch_bounds__(kThreads) void act_codebook_f16_kernel(const void* __restrict__ x, int dt, int64_t n,
+                                                                    const float* __restrict__ centers, int K,
+                                                                    uint16_t* __restrict__ out) {
+  __shared__ float c_s[256];
+  for (int j = threadIdx.x; j < K; j += kThreads) c_s[j] = centers[j];
+  __syncthreads();
+  const int64_t start = static_cast<int64_t>(blockIdx.x) * (kThreads * 4);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int64_t e = start + r * kThreads + threadIdx.x;
+    if (e >= n) break;
+    const float v = load_as_float(x, dt, e);
+    int best = 0;
+    float best_d = __builtin_inff();
+    bool have = false;
+    bool have_nan = false;
+    for (int j = 0; j < K; ++j) {
+      const float diff = v - c_s[j];
+      const float d = __fmul_rn(diff, diff);
+      if (d != d) {
+        if (!have_nan) {
+          best = j;
+          have_nan = true;
+        }
+      } else if (!have_nan && (!have || d < best_d)) {
+        best = j;
+        best_d = d;
+        have = true;
+      }
+    }
+    out[e] = (uint16_t)float_to_f16_bits(c_s[best]);
+  }
+}
+
 }  // namespace
+
+// Launches act_codebook_f16_kernel (K in [1, 256]).
+int launch_act_codebook_f16(const void* x, int x_dtype, int64_t n, const float* centers, int K, uint16_t* out,
+                            hipStream_t st) {
+  if (n == 0) return DIMQ_OK;
+  const int64_t blocks = (n + kThreads * 4 - 1) / (kThreads * 4);
+  DIMQ_CHECK(blocks < (int64_t)1 << 31, "activations too large for one launch");
+  hipLaunchKernelGGL(act_codebook_f16_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, st, x, x_dtype,
+                     n, centers, K, out);
+  return check_launch("activation codebook");
+}
 
 // Launches quantize_a4_f16_kernel; out must be 16-byte aligned.
 int launch_quantize_a4_f16(const void* x, int x_dtype, int64_t n, float s, int zp, uint16_t* out, hipStream_t st) {

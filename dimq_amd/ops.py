@@ -200,6 +200,17 @@ def prepare_conv_weight(packed_weight: torch.Tensor, bits: int, weight_shape: Se
     return torch.ops.dimq.prepare_conv_weight(packed_weight, int(bits), out_channels, cin, kernel_h, kernel_w)
 
 
+def dimq_linear_codebook_act(x: torch.Tensor, packed_weight: torch.Tensor, codebook: torch.Tensor, bits: int,
+                             act_centers: torch.Tensor, bias: torch.Tensor | None, out_features: int,
+                             in_features: int, out_dtype: torch.dtype | None = None,
+                             variant: str = "auto") -> torch.Tensor:
+    """Weight x activation codebook Linear: x quantized to its nearest activation centre (the QAT wrapper's
+    activation_centers, quant/dimq_wrapper.py:80-85), then the weight-codebook GEMM."""
+    require_extension()
+    return torch.ops.dimq.linear_codebook_act(x, packed_weight, codebook, int(bits), act_centers, bias,
+                                              int(out_features), int(in_features), out_dtype, VARIANTS[variant])
+
+
 def layer_norm(x: torch.Tensor, weight: torch.Tensor | None, bias: torch.Tensor | None,
                eps: float = 1e-5) -> torch.Tensor:
     """LayerNorm over the last dimension on the HIP kernel (fp16/bf16 x; the ViT workload's LayerNorms)."""

@@ -243,6 +243,22 @@ int dimq_linear_codebook_ex_ws(const void* x, int x_dtype, int64_t M, int64_t K,
                                const void* residual, int residual_dtype, int activation, int variant, void* workspace,
                                int64_t workspace_bytes, void* stream);
 
+/* Weight x activation codebook Linear (no kernel counterpart in the
+ * reference: its QAT wrapper quantizes activations to activation_centers with
+ * hard_quantize_weight before F.linear, quant/dimq_wrapper.py:80-85,
+ * quant/dimq.py:197-221): y = Q(x) W_hat^T + b with
+ * Q(x) = C_a[argmin_c (x - C_a[c])^2] (torch argmin semantics: first minimum,
+ * NaN distances win).  act_centers: n_act <= 256 fp32 centres on the device.
+ * The quantized activations go to the caller's workspace as fp16 (at least
+ * dimq_linear_codebook_act_workspace_bytes, 16-byte aligned), then the
+ * weight-codebook tiles run on them. */
+int64_t dimq_linear_codebook_act_workspace_bytes(int64_t M, int64_t K);
+int dimq_linear_codebook_act(const void* x, int x_dtype, int64_t M, int64_t K, const uint8_t* packed_w,
+                             int64_t packed_numel, int bits, const void* codebook, int cb_dtype, int64_t cb_rows,
+                             int64_t cb_size, const float* act_centers, int64_t n_act, const void* bias, int bias_dtype,
+                             int64_t N, void* y, int y_dtype, int variant, void* workspace, int64_t workspace_bytes,
+                             void* stream);
+
 int dimq_conv2d_codebook_ex(const void* x, int x_dtype, int x_layout, int64_t B, int64_t C, int64_t H, int64_t W,
                             const uint8_t* packed_w, int64_t packed_numel, int bits, const uint32_t* prepared_w,
                             int64_t prepared_words, const void* codebook, int cb_dtype, int64_t cb_rows,

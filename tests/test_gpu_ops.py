@@ -441,6 +441,30 @@ def test_linear_codebook_cfg1_shape(gpu):
     assert oracle.rel_err(y, ref) <= TOL
 
 
+# ---------------------------------------------------------------- weight x activation codebook Linear
+@pytest.mark.parametrize("M,N,K,bits,xdt,n_act", [(1, 4096, 4096, 3, torch.bfloat16, 16),
+                                                 (300, 256, 768, 4, torch.float32, 16),
+                                                 (2100, 384, 256, 4, torch.bfloat16, 8),
+                                                 (37, 130, 96, 2, torch.float16, 256)])
+def test_linear_codebook_act_vs_reference(gpu, M, N, K, bits, xdt, n_act):
+    """y = Q(x) W_hat^T + b, Q(x) = C_a[argmin (x - C_a)^2] as in the QAT wrapper's activation fake-quant
+    (quant/dimq_wrapper.py:80-85 with quant/dimq.py:197-221), against torch CPU fp32."""
+    ops = _ops()
+    announce(f"linear_codebook_act M={M} N={N} K={K} bits={bits} {xdt} n_act={n_act}")
+    g = _gen(M + N + K + n_act)
+    cb, idx, packed = _codebook_case(N, K, bits, True, g)
+    x = torch.randn(M, K, generator=g).to(xdt)
+    x.view(-1)[7] = float("nan")  # a NaN activation takes the first centre (torch argmin of NaN distances)
+    ca = torch.randn(n_act, generator=g).sort().values
+    bias = torch.randn(N, generator=g) * 0.1
+    y = ops.dimq_linear_codebook_act(x.to(gpu), packed.to(gpu), cb.to(gpu), bits, ca.to(gpu), bias.to(gpu), N, K,
+                                     out_dtype=torch.float32)
+    xf = x.float()
+    q = ca[((xf.reshape(-1)[:, None] - ca[None, :]) ** 2).argmin(1)].reshape(M, K)
+    ref = oracle.linear_dequant_reference(q, packed, bits, cb, N, K, bias)
+    assert oracle.rel_err(y, ref) <= TOL, oracle.rel_err(y, ref)
+
+
 # ---------------------------------------------------------------- fused epilogue (residual + activation)
 _ACTS = {None: lambda t: t, "relu": torch.relu, "gelu": torch.nn.functional.gelu}
 

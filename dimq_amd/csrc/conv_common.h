@@ -27,6 +27,7 @@ struct HaloArgs {
   int y_dt, y_layout;
   Epi epi;  // fused residual / activation
   float acc_scale = 1.0f;  // factor on every accumulator (W4A4 calls: the activation scale)
+  int park_lds = 0;        // resident kernel: fp32 NCHW stores transposed through LDS (launch sized it)
 };
 
 // Streaming kernel (conv_stream.hip): shapes it runs, LDS bytes, launch.

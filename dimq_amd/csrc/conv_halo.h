@@ -326,6 +326,45 @@ __global__ __launch_bounds__(256) void conv_halo_kernel(const HaloArgs p) {
   }
 }
 
+// fp32 NCHW stores of one 32-pixel x 32-channel MFMA block (PXROWS layout:
+// lane (col, g) holds channel col's pixels 8j + 4g + i) through the wave's
+// private LDS area: the block is parked channel-major (row pitch 36 floats),
+// then lane l stores pixels 4(l % 8) .. +3 of channel l / 8 + 8 it, so each
+// store instruction writes 8 whole 128-byte channel runs instead of 32
+// quarter runs.  A wave's LDS operations execute in order, so the wave-local
+// park / read needs no work-group barrier.
+constexpr int kParkPitch = 36;
+constexpr int kParkFloats = 32 * kParkPitch;
+
+__device__ __forceinline__ void store_block_lds(const HaloArgs& p, const floatx16& acc, int b, int oh0, int P, int mb,
+                                                int col, int g, int ocr, int lane, float scale, float bv,
+                                                float* park) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    *reinterpret_cast<float4*>(park + col * kParkPitch + 8 * j + 4 * g) =
+        make_float4(acc[4 * j] * scale + bv, acc[4 * j + 1] * scale + bv, acc[4 * j + 2] * scale + bv,
+                    acc[4 * j + 3] * scale + bv);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int64_t ohw = (int64_t)p.OH * p.OW;
+  const int p4 = 4 * (lane & 7);
+  const int pix0 = mb * 32 + p4;
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int c = (lane >> 3) + 8 * it;
+    const float4 v = *reinterpret_cast<const float4*>(park + c * kParkPitch + p4);
+    const int oc = ocr + c;
+    if (oc < p.OC && pix0 < P)  // P % 4 == 0 (OW % 4 == 0): a chunk is all in or all out
+      *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.y) + ((int64_t)b * p.OC + oc) * ohw +
+                                 (int64_t)oh0 * p.OW + pix0) = v;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Resident-weight variant of the halo kernel for T = KH*KW*C/16 <= 36
 // sub-steps (3x3 at C = 64, 1x1 at C <= 128): every lane decodes its output
 // channel's T weight fragments once (4*T VGPRs) and keeps them for the tile,
@@ -356,6 +395,11 @@ __global__ __launch_bounds__(256, 2) void conv_resident_kernel(const HaloArgs p)
   const int wn = wave & 1;
   const int wm = wave >> 1;
   const int ocl = oc0 + 32 * wn + col;
+  // fp32 NCHW output without epilogue: each wave transposes its 32 x 32
+  // blocks through a private LDS area after the halo (launch adds it)
+  const bool lds_store = PXROWS && MODE == kEpiNone && p.y_dt == DIMQ_F32 && p.y_layout == DIMQ_NCHW &&
+                         (p.OW % 4) == 0 && p.park_lds;
+  float* park = reinterpret_cast<float*>(halo + (size_t)p.IH_t * p.IW_t * CP) + wave * kParkFloats;
 
   constexpr int E = 1 << BITS;
   __shared__ float cbs[64 * E];
@@ -433,6 +477,13 @@ __global__ __launch_bounds__(256, 2) void conv_resident_kernel(const HaloArgs p)
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
     __builtin_amdgcn_sched_group_barrier(0x008, DEPTH, 0);
+    if constexpr (PXROWS && MODE == kEpiNone) {
+      if (lds_store) {
+        store_block_lds(p, acc[0], b, oh0, P, mb, col, g, oc0 + 32 * wn, lane, scale, bv, park);
+        if (mb + 2 < nblk) store_block_lds(p, acc[1], b, oh0, P, mb + 2, col, g, oc0 + 32 * wn, lane, scale, bv, park);
+        continue;
+      }
+    }
     store_block<PXROWS, MODE>(p, acc[0], b, oh0, P, mb, col, g, ocl, oc0 + 32 * wn, scale, bv);
     if (mb + 2 < nblk) store_block<PXROWS, MODE>(p, acc[1], b, oh0, P, mb + 2, col, g, ocl, oc0 + 32 * wn, scale, bv);
   }
@@ -448,8 +499,15 @@ inline bool halo_mode_ok(int mode, bool resident, bool nchw) {
 }
 
 template <int BITS, int CC, int STRIDE, int KHW, bool PXROWS, int MODE>
-int launch_resident(const HaloArgs& p, dim3 grid, size_t lds, hipStream_t s) {
+int launch_resident(const HaloArgs& p0, dim3 grid, size_t lds, hipStream_t s) {
   auto k = conv_resident_kernel<BITS, CC, STRIDE, KHW, PXROWS, MODE>;
+  HaloArgs p = p0;
+  p.park_lds = 0;
+  if (PXROWS && MODE == kEpiNone && p.y_dt == DIMQ_F32 && p.y_layout == DIMQ_NCHW && p.OW % 4 == 0 &&
+      !getenv("DIMQ_CONV_DIRECT_STORE")) {  // A/B runs: stores straight from registers
+    p.park_lds = 1;
+    lds += (size_t)4 * kParkFloats * sizeof(float);
+  }
   if (lds > 64 * 1024) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);

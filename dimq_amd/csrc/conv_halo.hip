@@ -33,13 +33,17 @@ __global__ void prepare_kernel(const uint8_t* __restrict__ src, int OC, int C, i
   uint32_t words[BITS];
 #pragma unroll
   for (int w = 0; w < BITS; ++w) words[w] = 0;
+  // fully unrolled and predicated (no early exit), so all 32 index loads
+  // of the thread go out back to back instead of in four latency rounds
+#pragma unroll
   for (int s = 0; s < 4; ++s) {
     const int t = 4 * chunk + s;
-    if (t >= T) break;
+    if (t >= T) continue;
     const int khw = t / CC;
     const int cc = t - khw * CC;
     const int kh = khw / KW;
     const int kw = khw - kh * KW;
+#pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int c = 16 * cc + 8 * g + j;
       const int64_t i = (((int64_t)n * C + c) * KH + kh) * KW + kw;

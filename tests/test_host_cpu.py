@@ -75,6 +75,25 @@ def test_w4a4_workspace_sizes(capi):
     assert lib.dimq_conv2d_lut_workspace_bytes(32, 64, 56, 56, 64, 64, 3, 3, 1, F32) == 0
 
 
+def test_linear_workspace_sizes_and_act_codebook_errors(capi):
+    lib = capi.lib
+    up = lambda b: (b + 255) // 256 * 256
+    # fp32 activations on the large-tile shapes get an fp16 copy; nothing else does
+    assert lib.dimq_linear_codebook_workspace_bytes(1576, 768, 4, capi.F32) == up(1576 * 768 * 2)
+    assert lib.dimq_linear_codebook_workspace_bytes(1576, 768, 4, capi.BF16) == 0
+    assert lib.dimq_linear_codebook_workspace_bytes(64, 768, 4, capi.F32) == 0     # GEMV / small tiles
+    assert lib.dimq_linear_codebook_workspace_bytes(1576, 100, 4, capi.F32) == 0   # K % 64 != 0
+    assert lib.dimq_linear_codebook_workspace_bytes(1576, 768, 8, capi.F32) == 0   # 8-bit tiles
+    assert lib.dimq_linear_codebook_act_workspace_bytes(300, 768) == up(300 * 768 * 2)
+    assert lib.dimq_linear_codebook_act_workspace_bytes(0, 768) == 0
+    args = [None, capi.F32, 4, 64, None, 128, 4, None, capi.F32, 1, 16]
+    tail = [None, capi.F32, 8, None, capi.F32, 0, None, 0, None]
+    assert lib.dimq_linear_codebook_act(*args, None, 300, *tail) == 1
+    assert lib.dimq_last_error() == b"activation codebook must hold between 1 and 256 centres"
+    assert lib.dimq_linear_codebook_act(*args, None, 16, *tail) == 1
+    assert lib.dimq_last_error() == b"activation codebook is required"
+
+
 def test_support_op_argument_errors(capi):
     lib = capi.lib
     assert lib.dimq_layer_norm(None, capi.F32, 4, 768, 768, None, None, capi.F32, 1e-6, None, None) == 1

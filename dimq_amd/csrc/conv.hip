@@ -94,9 +94,6 @@ int64_t gemm_part_words(int64_t OC, int64_t C, int64_t KH, int64_t KW, int bits)
 // beats the GEMM's 64-wide k stages; the implicit GEMM for the rest (stride 2
 // C = 128: 38 vs 115 us; 1x1: 20-30 vs 35-39 us; C >= 128 stride 1: equal).
 bool prefer_gemm_conv(int64_t C, int64_t KH, int64_t KW, int64_t stride) {
-  const char* force = getenv("DIMQ_CONV_PATH");  // A/B runs: "halo" or "gemm"
-  if (force && force[0] == 'h') return false;
-  if (force && force[0] == 'g') return true;
   return !(C < 128 && stride == 1 && KH * KW > 1);
 }
 
@@ -146,22 +143,9 @@ int launch_prepare_tapmajor(const uint8_t* src, int64_t src_bytes, int64_t OC, i
   return check_launch("prepare_conv_weight (tap-major)");
 }
 
-int device_cus() {
-  static int cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] <= 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cache[dev] = n;
-  }
-  return cache[dev];
-}
 
 // Tile of the implicit-GEMM conv: 128x128 when that fills every CU, else 64x128.
 int gemm_conv_tile(int64_t M, int64_t N) {
-  const char* force = getenv("DIMQ_CONV_BIG");  // A/B runs: 0..2
-  if (force && atoi(force) >= 0 && atoi(force) <= 2) return atoi(force);
   const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
   return t128 >= device_cus() ? 0 : 1;
 }
@@ -177,6 +161,20 @@ ConvShape make_shape(int64_t B, int64_t C, int64_t H, int64_t W, int64_t OC, int
 }
 
 }  // namespace
+
+// CUs of the current device (cached per device).
+int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
 }  // namespace dimq
 
 using namespace dimq;

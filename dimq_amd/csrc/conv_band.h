@@ -1,0 +1,277 @@
+// Banded direct 3x3 convolution for NCHW activations with fp32 NCHW output
+// (the reference op's layout: BASELINE cfg2, the W4A4 conv2d_lut path).
+//
+// One 512-thread work-group (8 waves, two per SIMD) owns a contiguous run of
+// 32-pixel blocks of one image (the image's OH*OW output pixels, flattened
+// row-major, split into `parts` runs) x 64 output channels.  Blocks are
+// 128-byte aligned runs of every output channel plane, so no two work-groups
+// write the same cache line.
+//
+// Schedule of a work-group:
+//   1. each lane loads its output channel's packed weights and codebook row,
+//      and every thread issues the loads of its share of the input rows: stage
+//      A = the halo rows of the first round of blocks, stage B = the rest;
+//   2. while those loads are in flight, each lane decodes its 36 weight
+//      fragments into VGPRs (resident for the whole work-group);
+//   3. stage A is transposed NCHW -> [row][col][channel] fp16 into LDS
+//      (8x8 transposes in registers), barrier, round 0 runs (one block-half
+//      per wave) while the other waves commit stage B, barrier, the remaining
+//      blocks run two accumulator chains per wave;
+//   4. each finished 32x32 block goes through a wave-private LDS area and
+//      leaves as non-temporal 16-byte stores, 8 channels x 128 bytes per
+//      instruction: the output is written once and never re-read here, and
+//      streaming it past the L2 keeps the 25 MB fp32 output of a cfg2 call
+//      from evicting the input rows other work-groups still read.
+#pragma once
+
+#include "conv_common.h"
+
+namespace dimq {
+namespace {
+
+constexpr int kBandThreads = 512;
+constexpr int kBandBlocksPerRound = 4;
+
+// Geometry of one part (work-group) of an image.
+struct BandPart {
+  int px0, px1;     // output pixels [px0, px1) of the image
+  int blk0, blk1;   // 32-pixel blocks
+  int r_first;      // first output row
+  int IH;           // halo rows (input rows r_first - pad .. r_last + KH - 1 - pad)
+  int ra;           // halo rows of stage A (rows round 0 reads)
+};
+
+__host__ __device__ inline BandPart band_part(int nblk, int parts, int part, int OH, int OW) {
+  BandPart q;
+  q.blk0 = nblk * part / parts;
+  q.blk1 = nblk * (part + 1) / parts;
+  q.px0 = 32 * q.blk0;
+  q.px1 = 32 * q.blk1 < OH * OW ? 32 * q.blk1 : OH * OW;
+  q.r_first = q.px0 / OW;
+  const int r_last = (q.px1 - 1) / OW;
+  q.IH = r_last - q.r_first + 3;
+  const int last0 = (q.px0 + 32 * kBandBlocksPerRound < q.px1 ? q.px0 + 32 * kBandBlocksPerRound : q.px1) - 1;
+  const int ra = last0 / OW - q.r_first + 3;
+  q.ra = ra < q.IH ? ra : q.IH;
+  return q;
+}
+
+// Staging task: (channel octet co, input row r of the stage, 8 columns q):
+// eight 16-byte loads, one per channel of the octet.
+struct BandTask {
+  uint4 v[8];
+};
+
+__device__ __forceinline__ void band_issue(const HaloArgs& p, int b, int ih_first, int t, int tasks, BandTask& tk) {
+  const int qn = p.W >> 3;
+  const int tt = t < tasks ? t : 0;
+  const int co = tt & 7, rest = tt >> 3, q = rest % qn, r = rest / qn;
+  const int ih = ih_first + r;
+  const bool live = t < tasks && ih >= 0 && ih < p.H;
+  const int ihc = live ? ih : 0;
+  const uint16_t* src =
+      reinterpret_cast<const uint16_t*>(p.x) + (((int64_t)b * p.C + 8 * co) * p.H + ihc) * p.W + 8 * q;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) tk.v[c] = *reinterpret_cast<const uint4*>(src + (int64_t)c * p.H * p.W);
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+    if (!live) tk.v[c] = make_uint4(0, 0, 0, 0);
+}
+
+// Halo row r0 + r of task t: pixels 8q .. 8q + 7 (halo columns + 1 for the
+// left padding column), channels 8co .. 8co + 7, as fp16.
+__device__ __forceinline__ void band_commit(const HaloArgs& p, int r0, int t, int tasks, const BandTask& tk,
+                                            uint16_t* halo) {
+  if (t >= tasks) return;
+  constexpr int CP = 72;
+  const int qn = p.W >> 3;
+  const int co = t & 7, rest = t >> 3, q = rest % qn, r = r0 + rest / qn;
+  uint32_t in[8][4];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    uint32_t w4[4] = {tk.v[c].x, tk.v[c].y, tk.v[c].z, tk.v[c].w};
+    if (p.x_dt != DIMQ_F16) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        w4[k] = to_f16_bits(w4[k] & 0xffffu, p.x_dt) | (to_f16_bits(w4[k] >> 16, p.x_dt) << 16);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) in[c][k] = w4[k];
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    // pixel j: channels 2w, 2w+1 from half (j & 1) of word j / 2 of rows 2w, 2w+1
+    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+    const uint4 o = make_uint4(perm(in[1][j >> 1], in[0][j >> 1], sel), perm(in[3][j >> 1], in[2][j >> 1], sel),
+                               perm(in[5][j >> 1], in[4][j >> 1], sel), perm(in[7][j >> 1], in[6][j >> 1], sel));
+    *reinterpret_cast<uint4*>(&halo[(r * p.IW_t + 8 * q + j + 1) * CP + 8 * co]) = o;
+  }
+}
+
+// One 32-pixel x 32-channel fp32 block (lane (col, g) holds channel col's
+// pixels 8j + 4g + i) -> wave-private LDS, channel-major -> non-temporal
+// 16-byte stores of 8 whole 128-byte channel runs per instruction.
+template <int MODE>
+__device__ __forceinline__ void band_store(const HaloArgs& p, const floatx16& acc, int b, int px1, int mb, int col,
+                                           int g, int ocr, int lane, float scale, float bv, float* park) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = acc[4 * j + i] * scale + bv;
+      if constexpr (MODE == kEpiRelu) v[i] = v[i] < 0.0f ? 0.0f : v[i];
+    }
+    *reinterpret_cast<float4*>(park + col * kParkPitch + 8 * j + 4 * g) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  const int64_t ohw = (int64_t)p.OH * p.OW;
+  const int p4 = 4 * (lane & 7);
+  const int pix0 = mb * 32 + p4;
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int c = (lane >> 3) + 8 * it;
+    const f4v v = *reinterpret_cast<const f4v*>(park + c * kParkPitch + p4);
+    const int oc = ocr + c;
+    if (oc < p.OC && pix0 < px1)  // OH*OW % 4 == 0: a 4-pixel chunk is all in or all out
+      __builtin_nontemporal_store(v, reinterpret_cast<f4v*>(reinterpret_cast<float*>(p.y) +
+                                                            ((int64_t)b * p.OC + oc) * ohw + pix0));
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Waves: wn = wave & 1 owns output channels oc0 + [32 wn, 32 wn + 32), wq =
+// wave >> 1 the blocks blk0 + wq + 4i.  KH = KW = 3, stride 1, pad 1, C = 64.
+template <int BITS, int MODE>
+__global__ __launch_bounds__(kBandThreads, 1) void conv_band_kernel(const HaloArgs p) {
+  constexpr int T = 36, WPL = 9 * BITS, CP = 72, E = 1 << BITS;
+  extern __shared__ __attribute__((aligned(16))) uint16_t halo[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, col = lane & 31, g = lane >> 5;
+  const int wg = xcd_tile(blockIdx.x, gridDim.x);
+  const int b = wg / p.parts, part = wg - b * p.parts;
+  const BandPart bp = band_part(p.nblk, p.parts, part, p.OH, p.OW);
+  const int ih_first = bp.r_first - p.pad_h;
+  const int oc0 = blockIdx.y * 64;
+  const int wn = wave & 1, wq = wave >> 1;
+  const int ocl = oc0 + 32 * wn + col;
+  float* park = reinterpret_cast<float*>(halo + (size_t)p.IH_t * p.IW_t * CP) + wave * kParkFloats;
+
+  // this lane's codebook row and packed weights
+  float cbv[E];
+  {
+    const int64_t row = p.cb_rows == 1 ? 0 : min(ocl, p.OC - 1);
+#pragma unroll
+    for (int j = 0; j < E; ++j) cbv[j] = j < p.cb_size ? load_as_float(p.cb, p.cb_dt, row * p.cb_size + j) : 0.0f;
+  }
+  uint32_t wreg[WPL];
+  {
+    const uint32_t* src = p.kw + ((int64_t)min(ocl, p.OC - 1) * 2 + g) * WPL;
+#pragma unroll
+    for (int w = 0; w < WPL; ++w) wreg[w] = src[w];
+  }
+  const float bv = (p.bias && ocl < p.OC) ? load_as_float(p.bias, p.bias_dt, ocl) : 0.0f;
+
+  const int tA = bp.ra * p.W, tB = (bp.IH - bp.ra) * p.W;  // 8 * rows * W / 8
+  BandTask tka, tkb;
+  band_issue(p, b, ih_first, tid, tA, tka);
+  band_issue(p, b, ih_first + bp.ra, tid, tB, tkb);
+
+  CodebookRegs<BITS> cbr;
+  const int e = planes_from_lds<BITS, false>(cbv, cbr, cbr);
+  const float scale = ldexpf(p.acc_scale, -e);
+  half8 wf[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    uint32_t chunk[BITS];
+#pragma unroll
+    for (int w = 0; w < BITS; ++w) chunk[w] = wreg[(t >> 2) * BITS + w];
+    wf[t] = decode_sub<BITS>(chunk, t & 3, cbr);
+  }
+  band_commit(p, 0, tid, tA, tka, halo);
+  for (int t = tid; t < bp.IH * 16; t += kBandThreads) {  // left and right padding columns
+    const int co = t & 7, side = (t >> 3) & 1, r = t >> 4;
+    *reinterpret_cast<uint4*>(&halo[(r * p.IW_t + (side ? p.IW_t - 1 : 0)) * CP + 8 * co]) = make_uint4(0, 0, 0, 0);
+  }
+  __syncthreads();
+
+  const int row_step = p.IW_t * CP;
+  // nq = 1 or 2 blocks (independent accumulator chains) of this wave
+  auto compute = [&](int nq, const int (&mbs)[2], floatx16 (&acc)[2]) {
+    int base[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      int pix = mbs[q] * 32 + col;
+      if (pix >= bp.px1) pix = bp.px0;  // rows past the part read a valid pixel and are not stored
+      const int oh = pix / p.OW;
+      const int ow = pix - oh * p.OW;
+      base[q] = ((oh - bp.r_first) * p.IW_t + ow) * CP + 8 * g;
+    }
+    auto frag = [&](int t, int q) {
+      const int khw = t >> 2, cc = t & 3, kh = khw / 3, kw = khw - 3 * kh;
+      return *reinterpret_cast<const half8*>(halo + base[q] + kh * row_step + kw * CP + 16 * cc);
+    };
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[0][i] = acc[1][i] = 0.0f;
+    constexpr int DEPTH = 4;
+    half8 xr[DEPTH];
+    if (nq == 2) {
+      constexpr int U = 2 * T;
+#pragma unroll
+      for (int u = 0; u < DEPTH; ++u) xr[u] = frag(u >> 1, u & 1);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        acc[u & 1] = mfma32x32x16(xr[u % DEPTH], wf[u >> 1], acc[u & 1]);
+        if (u + DEPTH < U) xr[u % DEPTH] = frag((u + DEPTH) >> 1, (u + DEPTH) & 1);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < DEPTH; ++u) xr[u] = frag(u, 0);
+#pragma unroll
+      for (int u = 0; u < T; ++u) {
+        acc[0] = mfma32x32x16(xr[u % DEPTH], wf[u], acc[0]);
+        if (u + DEPTH < T) xr[u % DEPTH] = frag(u + DEPTH, 0);
+      }
+    }
+  };
+  // round 0: one block-half per wave, reading stage A only
+  {
+    const int mb = bp.blk0 + wq;
+    if (mb < bp.blk1) {
+      floatx16 acc[2];
+      const int mbs[2] = {mb, mb};
+      compute(1, mbs, acc);
+      band_store<MODE>(p, acc[0], b, bp.px1, mb, col, g, oc0 + 32 * wn, lane, scale, bv, park);
+    }
+  }
+  band_commit(p, bp.ra, tid, tB, tkb, halo);
+  __syncthreads();
+  for (int mb = bp.blk0 + wq + kBandBlocksPerRound; mb < bp.blk1; mb += 2 * kBandBlocksPerRound) {
+    const bool two = mb + kBandBlocksPerRound < bp.blk1;
+    const int mbs[2] = {mb, mb + kBandBlocksPerRound};
+    floatx16 acc[2];
+    compute(two ? 2 : 1, mbs, acc);
+    band_store<MODE>(p, acc[0], b, bp.px1, mb, col, g, oc0 + 32 * wn, lane, scale, bv, park);
+    if (two) band_store<MODE>(p, acc[1], b, bp.px1, mb + kBandBlocksPerRound, col, g, oc0 + 32 * wn, lane, scale, bv,
+                              park);
+  }
+}
+
+template <int BITS>
+int launch_band_bits(const HaloArgs& p, int mode, hipStream_t s) {
+  auto k = mode == kEpiRelu ? conv_band_kernel<BITS, kEpiRelu> : conv_band_kernel<BITS, kEpiNone>;
+  const size_t lds = (size_t)p.IH_t * p.IW_t * 72 * sizeof(uint16_t) + (size_t)8 * kParkFloats * sizeof(float);
+  const hipError_t e =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return set_error(DIMQ_ERR_HIP, "conv2d_codebook (band): %s", hipGetErrorString(e));
+  const dim3 grid(static_cast<unsigned>(p.B * p.parts), static_cast<unsigned>((p.OC + 63) / 64));
+  hipLaunchKernelGGL(k, grid, dim3(kBandThreads), lds, s, p);
+  return check_launch("conv2d_codebook (band)");
+}
+
+}  // namespace
+}  // namespace dimq

@@ -1,5 +1,5 @@
-// Pieces shared by the two LDS-halo conv kernels (conv_halo.hip,
-// conv_stream.hip): the argument block, the 32x32x16 MFMA, the epilogue of
+// Pieces shared by the LDS-halo conv kernels (conv_halo.h, conv_band.h):
+// the argument block, the 32x32x16 MFMA, the epilogue of
 // one 32x32 output block and the XCD-aware tile order.
 #pragma once
 
@@ -15,8 +15,8 @@ struct HaloArgs {
   int TH;              // output rows per tile (band)
   int IH_t, IW_t, CP;  // halo tile rows, cols, channel pitch (fp16 elements)
   int tiles_h;         // ceil(OH / TH): tiles (bands) per image
-  int NR;              // streaming kernel: input rows held in the LDS ring (power of two)
-  int SR;              // streaming kernel: input rows one step adds at most (LDS staging rows)
+  int parts;           // band kernel: runs of 32-pixel blocks per image (one work-group each)
+  int nblk;            // band kernel: 32-pixel blocks per image
   const uint32_t* kw;  // kernel-layout weights
   int words_per_lane;  // ceil(T/4) * BITS
   const void* cb;
@@ -29,10 +29,6 @@ struct HaloArgs {
   float acc_scale = 1.0f;  // factor on every accumulator (W4A4 calls: the activation scale)
   int park_lds = 0;        // resident kernel: fp32 NCHW stores transposed through LDS (launch sized it)
 };
-
-// Streaming kernel (conv_stream.hip): shapes it runs, LDS bytes, launch.
-bool stream_supported(const HaloArgs& p, int stride, int bits);
-int launch_conv_stream(HaloArgs p, int stride, int bits, hipStream_t s);
 
 namespace {
 
@@ -61,6 +57,11 @@ __device__ __forceinline__ void store4(void* y, int dt, int64_t off, const float
 }
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// Wave-private LDS area of the transposed fp32 NCHW stores: one 32 x 32
+// block parked channel-major with a 36-float row pitch.
+constexpr int kParkPitch = 36;
+constexpr int kParkFloats = 32 * kParkPitch;
 
 __device__ __forceinline__ floatx16 mfma32x32x16(half8 a, half8 b, floatx16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);

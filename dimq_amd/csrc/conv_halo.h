@@ -21,9 +21,7 @@
 // row's packed indices and codebook byte planes in VGPRs for the whole tile.
 #pragma once
 
-#include "conv_common.h"
-
-#include <stdlib.h>
+#include "conv_band.h"
 
 #include <algorithm>
 
@@ -331,11 +329,10 @@ __global__ __launch_bounds__(256) void conv_halo_kernel(const HaloArgs p) {
 // private LDS area: the block is parked channel-major (row pitch 36 floats),
 // then lane l stores pixels 4(l % 8) .. +3 of channel l / 8 + 8 it, so each
 // store instruction writes 8 whole 128-byte channel runs instead of 32
-// quarter runs.  A wave's LDS operations execute in order, so the wave-local
-// park / read needs no work-group barrier.
-constexpr int kParkPitch = 36;
-constexpr int kParkFloats = 32 * kParkPitch;
-
+// quarter runs.  The stores are non-temporal: the output is not re-read by
+// this kernel, and streaming it past the L2 leaves the L2 to the input rows
+// neighbouring tiles share.  A wave's LDS operations execute in order, so the
+// wave-local park / read needs no work-group barrier.
 __device__ __forceinline__ void store_block_lds(const HaloArgs& p, const floatx16& acc, int b, int oh0, int P, int mb,
                                                 int col, int g, int ocr, int lane, float scale, float bv,
                                                 float* park) {
@@ -354,11 +351,13 @@ __device__ __forceinline__ void store_block_lds(const HaloArgs& p, const floatx1
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     const int c = (lane >> 3) + 8 * it;
-    const float4 v = *reinterpret_cast<const float4*>(park + c * kParkPitch + p4);
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    const f4v v = *reinterpret_cast<const f4v*>(park + c * kParkPitch + p4);
     const int oc = ocr + c;
     if (oc < p.OC && pix0 < P)  // P % 4 == 0 (OW % 4 == 0): a chunk is all in or all out
-      *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.y) + ((int64_t)b * p.OC + oc) * ohw +
-                                 (int64_t)oh0 * p.OW + pix0) = v;
+      __builtin_nontemporal_store(v, reinterpret_cast<f4v*>(reinterpret_cast<float*>(p.y) +
+                                                            ((int64_t)b * p.OC + oc) * ohw + (int64_t)oh0 * p.OW +
+                                                            pix0));
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -503,8 +502,7 @@ int launch_resident(const HaloArgs& p0, dim3 grid, size_t lds, hipStream_t s) {
   auto k = conv_resident_kernel<BITS, CC, STRIDE, KHW, PXROWS, MODE>;
   HaloArgs p = p0;
   p.park_lds = 0;
-  if (PXROWS && MODE == kEpiNone && p.y_dt == DIMQ_F32 && p.y_layout == DIMQ_NCHW && p.OW % 4 == 0 &&
-      !getenv("DIMQ_CONV_DIRECT_STORE")) {  // A/B runs: stores straight from registers
+  if (PXROWS && MODE == kEpiNone && p.y_dt == DIMQ_F32 && p.y_layout == DIMQ_NCHW && p.OW % 4 == 0) {
     p.park_lds = 1;
     lds += (size_t)4 * kParkFloats * sizeof(float);
   }
@@ -558,5 +556,8 @@ int launch_halo_cc(const HaloArgs& p, int CC16, int stride, int mode, hipStream_
 int launch_halo_b2(const HaloArgs& p, int CC16, int stride, int mode, hipStream_t s);
 int launch_halo_b3(const HaloArgs& p, int CC16, int stride, int mode, hipStream_t s);
 int launch_halo_b4(const HaloArgs& p, int CC16, int stride, int mode, hipStream_t s);
+int launch_band_b2(const HaloArgs& p, int mode, hipStream_t s);
+int launch_band_b3(const HaloArgs& p, int mode, hipStream_t s);
+int launch_band_b4(const HaloArgs& p, int mode, hipStream_t s);
 
 }  // namespace dimq

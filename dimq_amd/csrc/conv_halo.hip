@@ -63,6 +63,40 @@ __global__ void prepare_kernel(const uint8_t* __restrict__ src, int OC, int C, i
 
 }  // namespace
 
+// Band kernel (conv_band.h) for a halo call: NCHW in and fp32 NCHW out, C =
+// 64, 3x3, stride 1, pad 1.  Picks the parts per image (about one work-group
+// per CU, at most 13 blocks of 32 pixels per part) and checks that every
+// part's stages fit one task per thread and its halo fits in LDS; fills
+// p.parts, p.nblk, p.IH_t, p.IW_t.  False: the call takes the tile kernels.
+static bool band_setup(HaloArgs& p, int stride, int mode) {
+  if (p.x_layout != DIMQ_NCHW || p.y_layout != DIMQ_NCHW || p.y_dt != DIMQ_F32) return false;
+  if (p.C != 64 || p.KH != 3 || p.KW != 3 || stride != 1 || p.pad_h != 1 || p.pad_w != 1) return false;
+  if (mode != kEpiNone && mode != kEpiRelu) return false;
+  if (p.W % 8 != 0 || p.OW != p.W || p.OH != p.H || ((int64_t)p.OH * p.OW) % 4 != 0) return false;
+  if (!aligned(p.y, 16)) return false;
+  const int64_t npx = (int64_t)p.OH * p.OW;
+  if (npx > (1 << 24)) return false;
+  const int nblk = (int)((npx + 31) / 32);
+  const int cus = device_cus();
+  int parts = std::max<int>((cus + p.B - 1) / p.B, (nblk + 12) / 13);
+  parts = std::min(parts, nblk);
+  if ((int64_t)p.B * parts >= (1ll << 31)) return false;
+  int ihmax = 0;
+  for (int part = 0; part < parts; ++part) {
+    const BandPart q = band_part(nblk, parts, part, p.OH, p.OW);
+    if (q.blk1 <= q.blk0) return false;
+    if (q.ra * p.W > kBandThreads || (q.IH - q.ra) * p.W > kBandThreads) return false;
+    ihmax = std::max(ihmax, q.IH);
+  }
+  const int64_t lds = (int64_t)ihmax * (p.W + 2) * 72 * 2 + 8 * kParkFloats * 4;
+  if (lds > 160 * 1024) return false;
+  p.parts = parts;
+  p.nblk = nblk;
+  p.IH_t = ihmax;
+  p.IW_t = p.W + 2;
+  return true;
+}
+
 int64_t halo_prepared_words(int64_t OC, int64_t C, int64_t KH, int64_t KW, int bits) {
   const int64_t T = KH * KW * (C / 16);
   return OC * 2 * ((T + 3) / 4) * bits;
@@ -118,11 +152,6 @@ int launch_conv_halo(const void* x, int x_dtype, int x_layout, int64_t B, int64_
   p.pad_h = (int)ph;
   p.pad_w = (int)pw;
   p.TH = (int)halo_tile_rows(C, KH, KW, stride, OH, OW);
-  if (const char* rows = getenv("DIMQ_HALO_ROWS")) {  // A/B runs on the resident kernel
-    const int64_t th = atoi(rows);
-    const int64_t lds = ((th - 1) * stride + KH) * ((OW - 1) * stride + KW) * (C + 8) * 2;
-    if (th >= 1 && th <= OH && KH * KW * (C / 16) <= 36 && lds <= 150 * 1024) p.TH = (int)th;
-  }
   p.IH_t = (p.TH - 1) * (int)stride + (int)KH;
   p.IW_t = ((int)OW - 1) * (int)stride + (int)KW;
   p.CP = (int)C + 8;
@@ -139,11 +168,15 @@ int launch_conv_halo(const void* x, int x_dtype, int x_layout, int64_t B, int64_
   p.y = y;
   p.y_dt = y_dtype;
   p.y_layout = y_layout;
-  const char* force = getenv("DIMQ_CONV_KERNEL");  // A/B runs: 1 = row-streaming kernel
-  if (stream_supported(p, (int)stride, bits) && force && atoi(force) == 1 && epi_mode(epi) == kEpiNone)
-    return launch_conv_stream(p, (int)stride, bits, s);
   const int CC = (int)(C / 16);
   const int mode = epi_mode(epi);
+  if (band_setup(p, (int)stride, mode)) {
+    switch (bits) {
+      case 2: return launch_band_b2(p, mode, s);
+      case 3: return launch_band_b3(p, mode, s);
+      default: return launch_band_b4(p, mode, s);
+    }
+  }
   switch (bits) {
     case 2: return launch_halo_b2(p, CC, (int)stride, mode, s);
     case 3: return launch_halo_b3(p, CC, (int)stride, mode, s);

@@ -31,8 +31,6 @@ int gemm_big_tile(const GemmArgs& p, int bits, int x_dtype, int variant) {
   const int mode = epi_mode(p.epi);  // epilogues the large tiles are instantiated for
   if (!(mode == kEpiNone || mode == kEpiRelu || mode == kEpiGelu || mode == kEpiRes)) return -1;
   if (p.M <= 64 || p.K % 64 != 0 || !p.fast_b || !p.vec_a) return -1;
-  const char* force = getenv("DIMQ_GEMM_BIG");  // A/B runs: -1 = off, 0..8 or 10 = tile
-  if (force) return (atoi(force) >= 0 && atoi(force) <= 10 && atoi(force) != 9) ? atoi(force) : -1;
   // 256x256 shared-decode tiles for large M (measured on the ViT-B/16 shapes at
   // M 12,608, bf16: qkv 84 vs 104 us, proj 40 vs 50, fc1 114 vs 134, fc2 104 vs
   // 133 against the best 128x128 tile); below M 2048 the 128x128 tiles fill
@@ -122,23 +120,22 @@ int linear_codebook_impl(const void* x, int x_dtype, int64_t M, int64_t K, int64
       default: return launch_big_b4(p, x_dtype, big, s);
     }
   }
-  const char* force = getenv("DIMQ_GEMM_TILE");  // A/B runs: force a tile id
-  int tile = force ? atoi(force) : gemm_fast_tile(gemm_pick_tile(M, N, variant), p, bits);
+  int tile = gemm_fast_tile(gemm_pick_tile(M, N, variant), p, bits);
   if (tile < 0 || tile >= kTileCount) tile = gemm_pick_tile(M, N, variant);
   if (tile >= kTileFast128x64 && gemm_fast_tile(kTile64x32, p, bits) == kTile64x32) tile = gemm_pick_tile(M, N, variant);
   if (tile == kTileGemv && (M > 16 || bits == 8)) tile = gemm_pick_tile(M, N, DIMQ_VARIANT_MFMA);
   // 8-bit: 16-row tiles when the 64-row ones would leave most CUs idle
   // (ResNet-18 fc, M 128 x N 1000: 32 work-groups on 64-row tiles, 128 on
   // 16-row tiles; measured 28.9 -> 23.4 us per call)
-  if (!force && bits == 8 && tile == kTile64x32 && ((M + 63) / 64) * ((N + 63) / 64) < kCUs / 2) tile = kTile16x16;
-  if (tile == kTileGemv && gemv_fast_supported(p, bits) && !getenv("DIMQ_GEMV_OLD")) {
+  if (bits == 8 && tile == kTile64x32 && ((M + 63) / 64) * ((N + 63) / 64) < kCUs / 2) tile = kTile16x16;
+  if (tile == kTileGemv && gemv_fast_supported(p, bits)) {
     switch (bits) {
       case 2: return launch_gemv_fast<2>(p, x_dtype, s);
       case 3: return launch_gemv_fast<3>(p, x_dtype, s);
       default: return launch_gemv_fast<4>(p, x_dtype, s);
     }
   }
-  if (tile == kTileGemv && gemv_split_supported(p, bits) && !getenv("DIMQ_GEMV_OLD")) {
+  if (tile == kTileGemv && gemv_split_supported(p, bits)) {
     switch (bits) {
       case 2: return launch_gemv_split<2>(p, x_dtype, s);
       case 3: return launch_gemv_split<3>(p, x_dtype, s);
@@ -180,7 +177,7 @@ extern "C" int dimq_linear_codebook_ex_ws(const void* x, int x_dtype, int64_t M,
   const int mode = epi_mode(Epi{residual, residual_dtype, activation, 0});
   if (workspace != nullptr && need > 0 && workspace_bytes >= need && aligned(workspace, 16) &&
       variant != DIMQ_VARIANT_SMALL_M && aligned(packed_w, 16) && aligned(x, 16) &&
-      (mode == kEpiNone || mode == kEpiRelu || mode == kEpiGelu || mode == kEpiRes) && !getenv("DIMQ_NO_F16_PASS")) {
+      (mode == kEpiNone || mode == kEpiRelu || mode == kEpiGelu || mode == kEpiRes)) {
     // argument checks first, as the plain entry point does them
     DIMQ_CHECK(y_dtype == DIMQ_F32 || y_dtype == DIMQ_F16 || y_dtype == DIMQ_BF16,
                "linear_codebook output dtype must be fp32, fp16 or bf16");

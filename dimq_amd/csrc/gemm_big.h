@@ -881,14 +881,14 @@ int launch_big_conv_modes(const GemmArgs& p, int mode, hipStream_t s) {
   }
 }
 
+// Implicit-GEMM conv tiles: 0 = 128x128 (2x2 waves of 64x64), 1 = 64x128
+// (1x4 waves of 64x32) when the 128x128 grid would leave CUs idle.
 template <int BITS>
 int launch_big_conv_bits(const GemmArgs& p, int xt, int tile, hipStream_t s) {
   const int mode = epi_mode(p.epi);
-  if (mode != kEpiNone && tile == 2) tile = 0;
 #define DIMQ_CONV_TILES(XT)                                                 \
   switch (tile) {                                                           \
     case 1: return launch_big_conv_modes<BITS, XT, 1, 4, 2, 1>(p, mode, s); \
-    case 2: return launch_big<BITS, XT, 2, 2, 4, 2, true>(p, s);            \
     default: return launch_big_conv_modes<BITS, XT, 2, 2, 2, 2>(p, mode, s); \
   }
   if (xt == DIMQ_F16) {
@@ -898,14 +898,10 @@ int launch_big_conv_bits(const GemmArgs& p, int xt, int tile, hipStream_t s) {
 #undef DIMQ_CONV_TILES
 }
 
-// Tile ids (WGM x WGN waves of (MBLK*32) x (NBLK*32)):
-//   0: 256x128 (1x4, 256x32)   1: 256x128 (2x2, 128x64)   2: 128x128 (2x2, 64x64)
-//   3: 256x256 (1x4, 256x64)   4: 192x256 (1x4, 192x64)   5: 128x256 (1x4, 128x64)
-//   6: 256x128 deep pipeline   7: 128x128 deep pipeline
-//   8: 256x256 shared decode (4x2, 64x128), phases not interleaved
-//  10: 256x256 shared decode, next stage's decode woven between the MFMAs
-// Epilogue modes: none / relu / gelu / residual on the default tiles 2 and 7;
-// the other tiles (A/B options) only without epilogue.
+// Linear tile ids (WGM x WGN waves of (MBLK*32) x (NBLK*32)):
+//   2: 128x128 (2x2, 64x64)   7: 128x128 deep pipeline
+//  10: 256x256 shared decode (4x2, 64x128), next stage's decode woven between the MFMAs
+// Epilogue modes: none / relu / gelu / residual on each.
 template <int BITS, int XT>
 int launch_big_linear_modes(const GemmArgs& p, int tile, int mode, hipStream_t s) {
   if (tile == 10) {
@@ -935,24 +931,11 @@ int launch_big_linear_modes(const GemmArgs& p, int tile, int mode, hipStream_t s
 template <int BITS>
 int launch_big_bits(const GemmArgs& p, int xt, int tile, hipStream_t s) {
   const int mode = epi_mode(p.epi);
-  if (mode != kEpiNone && tile != 2 && tile != 7 && tile != 10) tile = p.K >= 2048 ? 2 : 7;
-#define DIMQ_BIG_TILES(XT)                                               \
-  switch (tile) {                                                        \
-    case 8: return launch_lds<BITS, XT, 4, 2, 2, 4, kEpiNone, 0>(p, s);  \
-    case 0: return launch_big<BITS, XT, 1, 4, 8, 1>(p, s);               \
-    case 1: return launch_big<BITS, XT, 2, 2, 4, 2>(p, s);               \
-    case 3: return launch_big<BITS, XT, 1, 4, 8, 2>(p, s);               \
-    case 4: return launch_big<BITS, XT, 1, 4, 6, 2>(p, s);               \
-    case 5: return launch_big<BITS, XT, 1, 4, 4, 2>(p, s);               \
-    case 6: return launch_deep<BITS, XT, 8>(p, s);                       \
-    default: return launch_big_linear_modes<BITS, XT>(p, tile, mode, s); \
-  }
   switch (xt) {
-    case DIMQ_F32: DIMQ_BIG_TILES(DIMQ_F32)
-    case DIMQ_F16: DIMQ_BIG_TILES(DIMQ_F16)
-    default: DIMQ_BIG_TILES(DIMQ_BF16)
+    case DIMQ_F32: return launch_big_linear_modes<BITS, DIMQ_F32>(p, tile, mode, s);
+    case DIMQ_F16: return launch_big_linear_modes<BITS, DIMQ_F16>(p, tile, mode, s);
+    default: return launch_big_linear_modes<BITS, DIMQ_BF16>(p, tile, mode, s);
   }
-#undef DIMQ_BIG_TILES
 }
 
 }  // namespace

@@ -269,10 +269,7 @@ int launch_gemv_split(const GemmArgs& p, int xt, hipStream_t s) {
 // the activation conversion of 16 rows per lane costing more than the
 // up-front loads save), K a multiple of 4096, 16-byte aligned rows/streams.
 inline bool gemv_fast_supported(const GemmArgs& p, int bits) {
-  int max_m = 4;
-  if (const char* f = getenv("DIMQ_GEMV_FAST_M")) max_m = atoi(f);  // A/B runs: largest M it takes (<= 16)
-  max_m = max_m < 1 ? 1 : (max_m > 16 ? 16 : max_m);
-  return p.M >= 1 && p.M <= max_m && !p.conv && (bits == 2 || bits == 3 || bits == 4) && p.K % 4096 == 0 &&
+  return p.M >= 1 && p.M <= 4 && !p.conv && (bits == 2 || bits == 3 || bits == 4) && p.K % 4096 == 0 &&
          p.fast_b && p.vec_a;
 }
 

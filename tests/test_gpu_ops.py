@@ -368,16 +368,20 @@ def test_linear_codebook_dtypes(gpu, xdt, odt):
 
 
 @pytest.mark.parametrize("bits", [2, 3, 4])
-@pytest.mark.parametrize("tile", ["0", "2", "6", "7", "8", "10"])
-@pytest.mark.parametrize("M,N,K,xdt", [(257, 130, 128, torch.float32), (520, 384, 192, torch.bfloat16),
-                                       (65, 256, 64, torch.float16)])
-def test_linear_codebook_large_tiles(gpu, monkeypatch, bits, tile, M, N, K, xdt):
-    """The 32x32x16 large-tile kernels (256x128 / 128x128 tiles, deep-pipeline and shared-decode
-    variants), M / N tails."""
-    monkeypatch.setenv("DIMQ_GEMM_BIG", tile)
+@pytest.mark.parametrize("M,N,K,xdt", [
+    (257, 130, 128, torch.float32),    # deep-pipeline 128x128 tile (K < 2048), fp32 staging
+    (520, 384, 192, torch.bfloat16),   # deep-pipeline 128x128 tile
+    (65, 256, 64, torch.float16),      # deep-pipeline 128x128 tile, one k stage
+    (130, 200, 2048, torch.bfloat16),  # 128x128 tile (K >= 2048)
+    (2100, 300, 192, torch.bfloat16),  # 256x256 shared-decode tile (M >= 2048, 16-bit), M / N tails
+    (2048, 256, 64, torch.float16),    # shared-decode tile, one k stage
+])
+def test_linear_codebook_large_tiles(gpu, bits, M, N, K, xdt):
+    """The 32x32x16 large-tile kernels (128x128 plain and deep-pipeline, 256x256 shared decode),
+    each reached by the shape that selects it, M / N tails."""
     ops = _ops()
     for per_channel in (True, False):
-        announce(f"linear_codebook large tile={tile} bits={bits} M={M} N={N} K={K} {xdt} pc={per_channel}")
+        announce(f"linear_codebook large bits={bits} M={M} N={N} K={K} {xdt} pc={per_channel}")
         g = _gen(bits * 7 + M + N + K)
         cb, idx, packed = _codebook_case(N, K, bits, per_channel, g)
         x = torch.randn(M, K, generator=g).to(xdt)
@@ -385,7 +389,7 @@ def test_linear_codebook_large_tiles(gpu, monkeypatch, bits, tile, M, N, K, xdt)
         y = ops.dimq_linear_codebook(x.to(gpu), packed.to(gpu), cb.to(gpu), bits, bias.to(gpu), N, K,
                                      out_dtype=torch.float32)
         ref = oracle.linear_dequant_reference(x.float(), packed, bits, cb, N, K, bias)
-        assert oracle.rel_err(y, ref) <= TOL, (bits, tile, M, N, K, per_channel, oracle.rel_err(y, ref))
+        assert oracle.rel_err(y, ref) <= TOL, (bits, M, N, K, per_channel, oracle.rel_err(y, ref))
 
 
 @pytest.mark.parametrize("bits", [2, 3, 4])
@@ -410,19 +414,32 @@ def test_linear_codebook_gemv_fast(gpu, bits, M, N, K, xdt):
 
 
 @pytest.mark.parametrize("act", [None, "gelu"])
-def test_linear_codebook_fp32_pass_same_bits(gpu, monkeypatch, act):
-    """fp32 activations on the large tiles go through one fp32 -> fp16 pass (round to nearest even, the
-    rounding the fp32 tiles apply while staging): the output must be bit-identical to the fp32 tiles'."""
-    ops = _ops()
+def test_linear_codebook_fp32_pass_same_bits(gpu, act):
+    """fp32 activations on the large tiles: the workspace entry point converts them in one fp32 -> fp16
+    pass (round to nearest even, the rounding the fp32 tiles apply while staging) and runs the fp16
+    tiles; the plain entry point stages fp32 in the tiles.  Both outputs must be the same bits."""
+    from dimq_amd import _C
     g = _gen(91)
-    cb, idx, packed = _codebook_case(384, 768, 4, True, g)
-    x = torch.randn(1576, 768, generator=g).to(gpu)
-    bias = (torch.randn(384, generator=g) * 0.1).to(gpu)
-    run = lambda: ops.dimq_linear_codebook(x, packed.to(gpu), cb.to(gpu), 4, bias, 384, 768,
-                                           out_dtype=torch.float32, activation=act)
-    y_pass = run()
-    monkeypatch.setenv("DIMQ_NO_F16_PASS", "1")
-    y_direct = run()
+    M, N, K = 1576, 384, 768
+    cb, idx, packed = _codebook_case(N, K, 4, True, g)
+    x = torch.randn(M, K, generator=g).to(gpu)
+    bias = (torch.randn(N, generator=g) * 0.1).to(gpu)
+    cbg, pg = cb.to(gpu), packed.to(gpu)
+    act_id = {None: 0, "gelu": 2}[act]
+    s = torch.cuda.current_stream().cuda_stream
+    ws_bytes = _C.lib.dimq_linear_codebook_workspace_bytes(M, K, 4, _C.F32)
+    assert ws_bytes >= M * K * 2
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=gpu)
+    y_pass = torch.empty(M, N, device=gpu)
+    y_direct = torch.empty(M, N, device=gpu)
+    rc = _C.lib.dimq_linear_codebook_ex_ws(x.data_ptr(), _C.F32, M, K, pg.data_ptr(), pg.numel(), 4, cbg.data_ptr(),
+                                           _C.F32, N, 16, bias.data_ptr(), _C.F32, N, y_pass.data_ptr(), _C.F32,
+                                           None, 0, act_id, 0, ws.data_ptr(), ws_bytes, s)
+    assert rc == 0, _C.lib.dimq_last_error()
+    rc = _C.lib.dimq_linear_codebook_ex(x.data_ptr(), _C.F32, M, K, pg.data_ptr(), pg.numel(), 4, cbg.data_ptr(),
+                                        _C.F32, N, 16, bias.data_ptr(), _C.F32, N, y_direct.data_ptr(), _C.F32,
+                                        None, 0, act_id, 0, s)
+    assert rc == 0, _C.lib.dimq_last_error()
     torch.cuda.synchronize()
     assert torch.equal(y_pass, y_direct)
 
@@ -497,18 +514,16 @@ def test_linear_codebook_fused_epilogue(gpu, case):
 
 
 @pytest.mark.parametrize("case", [
-    dict(B=2, C=64, H=20, W=18, OC=64, K=3, s=1, bits=2, prep=True, path="auto", g=1),    # resident halo
-    dict(B=2, C=128, H=12, W=12, OC=64, K=3, s=1, bits=3, prep=True, path="halo", g=1),   # decode-per-step halo
-    dict(B=2, C=256, H=9, W=9, OC=128, K=3, s=2, bits=2, prep=True, path="auto", g=1),    # implicit GEMM
-    dict(B=2, C=3, H=40, W=40, OC=64, K=7, s=2, bits=8, prep=False, path="auto", g=1),    # stem
-    dict(B=2, C=16, H=9, W=9, OC=24, K=3, s=1, bits=4, prep=False, path="auto", g=2),     # generic
+    dict(B=2, C=64, H=20, W=18, OC=64, K=3, s=1, bits=2, prep=True, g=1),    # resident halo
+    dict(B=2, C=128, H=12, W=12, OC=64, K=3, s=1, bits=3, prep=True, g=1),   # C 128 (NCHW: halo tiles)
+    dict(B=2, C=256, H=9, W=9, OC=128, K=3, s=2, bits=2, prep=True, g=1),    # implicit GEMM
+    dict(B=2, C=3, H=40, W=40, OC=64, K=7, s=2, bits=8, prep=False, g=1),    # stem
+    dict(B=2, C=16, H=9, W=9, OC=24, K=3, s=1, bits=4, prep=False, g=2),     # generic
 ])
 @pytest.mark.parametrize("layout", ["nchw", "nhwc"])
 @pytest.mark.parametrize("act", ["relu", "gelu"])
-def test_conv2d_codebook_fused_epilogue(gpu, case, layout, act, monkeypatch):
+def test_conv2d_codebook_fused_epilogue(gpu, case, layout, act):
     """y = act(conv + b + residual) on every Conv2d kernel family; the residual comes in the other memory order."""
-    if case["path"] == "halo":
-        monkeypatch.setenv("DIMQ_CONV_PATH", "halo")
     ops = _ops()
     announce(f"conv fused {case} {layout} {act}")
     g = _gen(case["C"] + case["OC"] + case["K"] + case["bits"])
@@ -691,13 +706,11 @@ def test_graph_replay_matches_eager(gpu):
     dict(B=3, C=64, H=20, W=12, OC=192, K=3, s=1, bits=4, dt=torch.float16),   # 3 channel blocks, odd bands
 ])
 @pytest.mark.parametrize("layout", ["nchw", "nhwc"])
-@pytest.mark.parametrize("path", ["auto", "halo"])
-def test_conv2d_halo_prepared_vs_oracle(gpu, case, layout, path, monkeypatch):
-    """path "halo" keeps NHWC calls of C >= 128 / 1x1 layers on the LDS-halo kernel (auto: implicit GEMM)."""
-    if path == "halo":
-        monkeypatch.setenv("DIMQ_CONV_PATH", "halo")
+def test_conv2d_halo_prepared_vs_oracle(gpu, case, layout):
+    """Prepared weights: NCHW fp32-output 3x3 C 64 stride-1 calls take the band kernel, other NCHW calls the
+    LDS-halo tiles, NHWC calls the halo tiles (C 64 stride 1) or the implicit GEMM."""
     ops = _ops()
-    announce(f"conv halo {case} {layout} {path}")
+    announce(f"conv halo {case} {layout}")
     g = _gen(case["C"] + case["OC"] * 3 + case["bits"] + case["s"])
     K = case["K"]
     pad = K // 2
@@ -719,6 +732,36 @@ def test_conv2d_halo_prepared_vs_oracle(gpu, case, layout, path, monkeypatch):
     y2 = ops.dimq_conv2d_codebook(xd, pd, cb.to(gpu), case["bits"], bias.to(gpu), shape, (case["s"],) * 2,
                                   (pad, pad), (1, 1), 1, out_dtype=torch.float32)
     assert oracle.rel_err(y, y2) <= 1e-5  # prepared (halo) and generic implicit-GEMM paths agree
+
+
+@pytest.mark.parametrize("case", [
+    dict(B=1, H=56, W=56, OC=64, bits=2, dt=torch.float16, act=None, bias=False, pc=True),   # one block per part
+    dict(B=3, H=20, W=24, OC=96, bits=3, dt=torch.bfloat16, act=None, bias=True, pc=True),   # OC tail, bf16
+    dict(B=2, H=7, W=8, OC=64, bits=4, dt=torch.float16, act="relu", bias=True, pc=False),   # partial last block
+    dict(B=40, H=56, W=56, OC=64, bits=2, dt=torch.float16, act="relu", bias=True, pc=True),  # 8 parts per image
+    dict(B=16, H=28, W=32, OC=128, bits=4, dt=torch.float16, act=None, bias=False, pc=True),  # 2 channel blocks
+])
+def test_conv2d_band_kernel(gpu, case):
+    """NCHW 3x3 stride-1 C 64 convs with fp32 NCHW output (the band kernel: runs of 32-pixel blocks per
+    work-group, two-stage halo, non-temporal stores) against the oracle, with bias / ReLU, partial blocks,
+    channel tails, 2/3/4-bit, per-layer and per-channel codebooks."""
+    ops = _ops()
+    announce(f"conv band {case}")
+    g = _gen(case["H"] * 7 + case["W"] + case["OC"] + case["bits"])
+    shape = (case["OC"], 64, 3, 3)
+    x = torch.relu(torch.randn(case["B"], 64, case["H"], case["W"], generator=g)).to(case["dt"])
+    cb, idx, packed = _codebook_case(case["OC"], 576, case["bits"], case["pc"], g)
+    bias = torch.randn(case["OC"], generator=g) * 0.1 if case["bias"] else None
+    pd = packed.to(gpu)
+    prep = ops.prepare_conv_weight(pd, case["bits"], shape)
+    y = ops.dimq_conv2d_codebook(x.to(gpu), pd, cb.to(gpu), case["bits"], None if bias is None else bias.to(gpu),
+                                 shape, (1, 1), (1, 1), (1, 1), 1, out_dtype=torch.float32, prepared_weight=prep,
+                                 activation=case["act"])
+    ref = oracle.conv2d_dequant_reference(x.float(), packed, case["bits"], cb, shape, bias, 1, 1, 1, 1)
+    if case["act"] == "relu":
+        ref = torch.relu(ref)
+    assert y.shape == ref.shape
+    assert oracle.rel_err(y, ref) <= TOL, oracle.rel_err(y, ref)
 
 
 # ---------------------------------------------------------------- implicit-GEMM conv on large tiles (C % 64 == 0)

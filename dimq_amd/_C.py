@@ -60,6 +60,8 @@ _SIGS = {
     "dimq_linear_lut_workspace_bytes": (_i64, [_i64, _i64, _int]),
     "dimq_linear_lut_ws": (_int, [_vp, _int, _i64, _vp, _i64, _vp, _int, _i64, _dbl, _i64, _vp, _int, _i64, _i64,
                                   _i64, _vp, _vp, _i64, _vp]),
+    "dimq_linear_lut_noalloc": (_int, [_vp, _int, _i64, _vp, _i64, _vp, _int, _i64, _dbl, _i64, _vp, _int, _i64,
+                                       _i64, _i64, _vp, _vp]),
     "dimq_conv2d_lut_workspace_bytes": (_i64, [_i64] * 9 + [_int]),
     "dimq_conv2d_lut_ws": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _int, _i64, _dbl, _i64, _vp,
                                   _int, _i64] + [_i64] * 11 + [_vp, _vp, _i64, _vp]),

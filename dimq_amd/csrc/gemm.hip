@@ -1,7 +1,7 @@
 // Host side of the codebook Linear: argument checks (with the reference's
 // messages where one exists, csrc/dimq_gemm_lut.cu:66-79), tile selection and
 // launch.
-#include <stdlib.h>
+#include <mutex>
 
 #include "gemm_big.h"
 #include "gemm_kernel.h"
@@ -277,11 +277,11 @@ extern "C" int dimq_linear_lut(const void* x, int x_dtype, int64_t M, const uint
 // kernels run on them with the 16-entry codebook and act_scale on the
 // accumulator, so the call takes the same fast tiles as linear_codebook.
 // Otherwise the generic A4 tiles (hi + lo fp16 codebook planes).
-extern "C" int dimq_linear_lut_ws(const void* x, int x_dtype, int64_t M, const uint8_t* packed_w,
-                                  int64_t packed_numel, const void* codebook, int cb_dtype, int64_t cb_numel,
-                                  double act_scale, int64_t act_zp, const void* bias, int bias_dtype,
-                                  int64_t bias_numel, int64_t out_features, int64_t in_features, float* y,
-                                  void* workspace, int64_t workspace_bytes, void* stream) {
+// Argument checks of linear_lut, with the messages of the reference's
+// TORCH_CHECKs (csrc/dimq_gemm_lut.cu:66-79).
+static int check_linear_lut(int x_dtype, int64_t M, int64_t packed_numel, int cb_dtype, int64_t cb_numel,
+                            double act_scale, int64_t act_zp, const void* bias, int bias_dtype, int64_t bias_numel,
+                            int64_t out_features, int64_t in_features) {
   DIMQ_CHECK(is_float_dtype(x_dtype), "linear_lut expects floating input");
   DIMQ_CHECK(is_float_dtype(cb_dtype), "codebook must be floating point");
   DIMQ_CHECK(cb_numel == 16, "codebook must have 16 entries for W4");
@@ -293,6 +293,17 @@ extern "C" int dimq_linear_lut_ws(const void* x, int x_dtype, int64_t M, const u
              "packed_weight is too small for out_features * in_features");
   if (bias) DIMQ_CHECK(bias_numel == out_features, "bias numel must equal out_features");
   DIMQ_CHECK(bias == nullptr || is_float_dtype(bias_dtype), "bias must be floating point");
+  return DIMQ_OK;
+}
+
+extern "C" int dimq_linear_lut_ws(const void* x, int x_dtype, int64_t M, const uint8_t* packed_w,
+                                  int64_t packed_numel, const void* codebook, int cb_dtype, int64_t cb_numel,
+                                  double act_scale, int64_t act_zp, const void* bias, int bias_dtype,
+                                  int64_t bias_numel, int64_t out_features, int64_t in_features, float* y,
+                                  void* workspace, int64_t workspace_bytes, void* stream) {
+  const int rc0 = check_linear_lut(x_dtype, M, packed_numel, cb_dtype, cb_numel, act_scale, act_zp, bias, bias_dtype,
+                                   bias_numel, out_features, in_features);
+  if (rc0 != DIMQ_OK) return rc0;
   DIMQ_CHECK(workspace_bytes >= 0, "workspace_bytes must be non-negative");
   if (M == 0) return DIMQ_OK;
   const int64_t need = dimq_linear_lut_workspace_bytes(M, in_features, cb_dtype);
@@ -329,4 +340,63 @@ extern "C" int dimq_linear_lut_ws(const void* x, int x_dtype, int64_t M, const u
   p.groups = 1;
   const int tile = (x_dtype != DIMQ_F64) ? gemm_fast_tile(kTile64x32, p, 4) : kTile64x32;
   return dispatch<true>(p, 4, x_dtype, tile, as_stream(stream));
+}
+
+// ---------------------------------------------------------------------------
+// dimq_linear_lut_noalloc: dimq_linear_lut_ws with the library's own scratch
+// in place of a caller workspace, for callers that cannot allocate.  The
+// scratch is one file-scope device array per GPU (a copy on every device the
+// library runs on, held until the process ends); host code reaches it only
+// through the address hipGetSymbolAddress returns for the current device.
+// Every call on a GPU shares that GPU's copy: calls that overlap on one GPU
+// (other streams, other host threads) race on it.
+
+constexpr int64_t kNoAllocScratchBytes = 16ll << 20;  // M * in_features <= 8,388,608 fp16 activations
+
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+// Device address of `scratch` on the current device, looked up once per
+// device with that device current; nullptr (and the HIP error) on failure.
+static void* scratch_address(hipError_t* err) {
+  static std::mutex mu;
+  static void* addr[64] = {};
+  int dev = 0;
+  *err = hipGetDevice(&dev);
+  if (*err != hipSuccess) return nullptr;
+  if (dev < 0 || dev >= 64) {
+    *err = hipErrorInvalidDevice;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    *err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (*err != hipSuccess) return nullptr;
+    addr[dev] = p;
+  }
+  return addr[dev];
+}
+
+extern "C" int dimq_linear_lut_noalloc(const void* x, int x_dtype, int64_t M, const uint8_t* packed_w,
+                                       int64_t packed_numel, const void* codebook, int cb_dtype, int64_t cb_numel,
+                                       double act_scale, int64_t act_zp, const void* bias, int bias_dtype,
+                                       int64_t bias_numel, int64_t out_features, int64_t in_features, float* y,
+                                       void* stream) {
+  const int rc = check_linear_lut(x_dtype, M, packed_numel, cb_dtype, cb_numel, act_scale, act_zp, bias, bias_dtype,
+                                  bias_numel, out_features, in_features);
+  if (rc != DIMQ_OK) return rc;
+  const int64_t need = dimq_linear_lut_workspace_bytes(M, in_features, cb_dtype);
+  if (need > kNoAllocScratchBytes)
+    return set_error(DIMQ_ERR_INVALID,
+                     "linear_lut_noalloc: M * in_features = %lld exceeds the scratch limit of %lld activations",
+                     (long long)(M * in_features), (long long)(kNoAllocScratchBytes / 2));
+  void* ws = nullptr;
+  if (need > 0) {
+    hipError_t err = hipSuccess;
+    ws = scratch_address(&err);
+    if (ws == nullptr)
+      return set_error(DIMQ_ERR_HIP, "linear_lut_noalloc: hipGetSymbolAddress(scratch): %s", hipGetErrorString(err));
+  }
+  return dimq_linear_lut_ws(x, x_dtype, M, packed_w, packed_numel, codebook, cb_dtype, cb_numel, act_scale, act_zp,
+                            bias, bias_dtype, bias_numel, out_features, in_features, y, ws, need, stream);
 }

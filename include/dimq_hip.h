@@ -133,6 +133,22 @@ int dimq_conv2d_lut_ws(const void* x, int x_dtype, int64_t B, int64_t C, int64_t
                        int64_t dilation_h, int64_t dilation_w, int64_t groups, float* y, void* workspace,
                        int64_t workspace_bytes, void* stream);
 
+/* No-allocation form of linear_lut.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory or pass a workspace (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, checks, messages and results as
+ * dimq_linear_lut_ws with a workspace; the fp16 activations go to a scratch
+ * array the library holds on each GPU it runs on (16 MiB per device, kept
+ * until the process ends), so M * in_features is limited to 8,388,608 with an
+ * fp16 codebook (DIMQ_ERR_INVALID beyond; other codebook dtypes use no
+ * scratch).  All calls on one GPU share that GPU's scratch: calls that
+ * overlap on one GPU (other streams or host threads) race and must be
+ * ordered by the caller. */
+int dimq_linear_lut_noalloc(const void* x, int x_dtype, int64_t M, const uint8_t* packed_w, int64_t packed_numel,
+                            const void* codebook, int cb_dtype, int64_t cb_numel, double act_scale, int64_t act_zp,
+                            const void* bias, int bias_dtype, int64_t bias_numel, int64_t out_features,
+                            int64_t in_features, float* y, void* stream);
+
 /* ---------------------------------------------------------------------------
  * 2. Generalised ops for the BASELINE configurations: b in {2,3,4,8} bits,
  *    per-layer or per-output-channel codebooks, weight-only GEMM/conv.

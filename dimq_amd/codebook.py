@@ -1,15 +1,16 @@
 """Codebook initialisation and nearest-centre assignment.
 
-* ``init_centers_1d`` restates ``quant/dimq.py:88-194`` (quantile, linspace and
-  k-means initialisers, then ``_postprocess_centers``); it is host-side data
-  preparation in torch, as in the reference.
-* ``init_centers_per_channel`` applies the same recipe to every output row at
-  once (the BASELINE configurations use per-output-channel codebooks; the
-  reference only has per-layer ones).
-* ``hard_quantize_weight`` keeps the reference signature
-  (``quant/dimq.py:197-221``) but runs the assignment on the GPU kernel
-  (``dimq_hard_quantize``); ``chunk_size`` is accepted for compatibility and
-  does not change the result.
+* ``init_centers_per_channel`` / ``init_centers_1d`` build the quantile
+  codebook of ``quant/dimq.py:88-137,175-194`` (the initialiser the BASELINE
+  configurations use): K centres at the quantiles ``linspace(0, 1, K+2)[1:-1]``
+  of a weight row, then spread so that they strictly increase and re-centred
+  on the quantiles' mean.  Both share one vectorised implementation over rows
+  (per output channel, or one row for a per-layer codebook).  The reference's
+  other initialisers (k-means, min/max linspace) belong to its QAT training
+  and are not provided.
+* ``assign_indices`` / ``hard_quantize_weight`` keep the reference semantics
+  of ``quant/dimq.py:197-221`` (argmin of the squared distance, first minimum)
+  and run on the GPU kernel (``dimq_hard_quantize``).
 """
 
 from __future__ import annotations
@@ -19,131 +20,85 @@ import torch
 from . import ops
 
 
+def _spread(centers: torch.Tensor, rows: torch.Tensor) -> torch.Tensor:
+    """Sorted, strictly increasing, re-centred codebooks of [R, K] centres for
+    their [R, n] weight rows (quant/dimq.py:175-194).
+
+    Walking up each sorted row, a centre that does not exceed its predecessor
+    is moved to predecessor + gap, gap = 1e-6 * max(span, std) of the row's
+    weights (at least 1e-12); the row is then shifted so that its mean equals
+    that of the sorted centres before the walk.  Rows whose centres are not
+    all finite restart from the linspace over mean +- 3 std of their weights.
+    """
+    K = centers.shape[1]
+    mu = rows.mean(dim=1, keepdim=True)
+    sd = rows.std(dim=1, unbiased=False, keepdim=True)
+    bad = ~torch.isfinite(centers).all(dim=1, keepdim=True)
+    if bool(bad.any()):
+        steps = torch.linspace(-3.0, 3.0, K, dtype=centers.dtype, device=centers.device)[None, :]
+        fallback = torch.where(sd > 0, mu + sd * steps, mu.expand(-1, K))
+        centers = torch.where(bad, fallback, centers)
+    base = centers.float().sort(dim=1).values
+    span = (rows.max(dim=1).values - rows.min(dim=1).values).abs()
+    gap = torch.maximum(span, sd[:, 0].abs()).clamp_min(1e-6) * 1e-6
+    walked = base.clone()
+    for i in range(1, K):
+        prev, cur = walked[:, i - 1], walked[:, i]
+        walked[:, i] = torch.where(cur <= prev, prev + gap, cur)
+    walked -= (walked.mean(dim=1) - base.mean(dim=1))[:, None]
+    return walked.sort(dim=1).values
+
+
+def _quantile_rows(rows: torch.Tensor, K: int) -> torch.Tensor:
+    """[R, K] quantile codebooks of finite [R, n] fp32 rows."""
+    if rows.shape[1] == 1:
+        centers = rows.expand(-1, K).clone()
+    else:
+        q = torch.linspace(0.0, 1.0, K + 2, dtype=rows.dtype, device=rows.device)[1:-1]
+        centers = torch.quantile(rows, q, dim=1).T.contiguous()
+    return _spread(centers, rows)
+
+
 @torch.no_grad()
-def init_centers_1d(w: torch.Tensor, K: int, method: str = "kmeans", *, kmeans_iters: int = 50,
-                    sample_size: int = 200000) -> torch.Tensor:
-    """Sorted 1-D codebook of K centres from a weight tensor (quant/dimq.py:88-130)."""
+def init_centers_1d(w: torch.Tensor, K: int, method: str = "quantile", *, sample_size: int = 200000) -> torch.Tensor:
+    """One sorted K-entry codebook for a whole weight tensor (quant/dimq.py:88-130).
+
+    Non-finite weights are left out; above ``sample_size`` weights the codebook
+    is built on ``torch.randperm(n)[:sample_size]`` of them, as the reference
+    does, so the same generator state gives the same codebook.
+    """
     if K <= 0:
         raise ValueError("K must be positive")
+    if method.lower() != "quantile":
+        raise ValueError(f"Unsupported center initialization: {method} (this backend provides 'quantile')")
     flat = w.detach().float().reshape(-1)
     if flat.numel() == 0:
         raise ValueError("Cannot initialize centers from an empty tensor")
-    finite = torch.isfinite(flat)
-    if not bool(finite.all()):
-        flat = flat[finite]
+    flat = flat[torch.isfinite(flat)]
     if flat.numel() == 0:
         raise ValueError("Cannot initialize centers because all weights are non-finite")
     if flat.numel() > sample_size:
-        perm = torch.randperm(flat.numel(), device=flat.device)[:sample_size]
-        sample = flat[perm]
-    else:
-        sample = flat
-    method = method.lower()
-    if method == "quantile":
-        centers = _quantile_centers(sample, K)
-    elif method == "linspace_std":
-        centers = _linspace_std_centers(sample, K)
-    elif method == "linspace_minmax":
-        centers = _linspace_minmax_centers(sample, K)
-    elif method == "kmeans":
-        centers = _kmeans_1d(sample, K, kmeans_iters)
-    else:
-        raise ValueError(f"Unsupported center initialization: {method}")
-    centers = _postprocess_centers(centers, sample, K)
-    return centers.to(device=w.device, dtype=w.dtype)
-
-
-def _quantile_centers(flat: torch.Tensor, K: int) -> torch.Tensor:
-    # quant/dimq.py:133-137
-    if flat.numel() == 1:
-        return flat.new_full((K,), flat.item())
-    q = torch.linspace(0.0, 1.0, K + 2, device=flat.device, dtype=flat.dtype)[1:-1]
-    return torch.quantile(flat, q)
-
-
-def _linspace_std_centers(flat: torch.Tensor, K: int) -> torch.Tensor:
-    # quant/dimq.py:140-145
-    mu = flat.mean()
-    sigma = flat.std(unbiased=False)
-    if float(sigma) <= 0.0:
-        return flat.new_full((K,), float(mu))
-    return torch.linspace(mu - 3.0 * sigma, mu + 3.0 * sigma, K, device=flat.device, dtype=flat.dtype)
-
-
-def _linspace_minmax_centers(flat: torch.Tensor, K: int) -> torch.Tensor:
-    # quant/dimq.py:148-153
-    lo = flat.min()
-    hi = flat.max()
-    if float((hi - lo).abs()) <= 0.0:
-        return flat.new_full((K,), float(lo))
-    return torch.linspace(lo, hi, K, device=flat.device, dtype=flat.dtype)
-
-
-def _kmeans_1d(flat: torch.Tensor, K: int, iters: int) -> torch.Tensor:
-    # quant/dimq.py:156-172 (Lloyd iterations from quantile seeds)
-    centers = _quantile_centers(flat, K)
-    if K == 1:
-        return centers
-    for _ in range(max(1, int(iters))):
-        assignment = ((flat[:, None] - centers[None, :]) ** 2).argmin(dim=1)
-        new_centers = centers.clone()
-        for k in range(K):
-            mask = assignment == k
-            if bool(mask.any()):
-                new_centers[k] = flat[mask].mean()
-        if torch.allclose(new_centers, centers):
-            break
-        centers = new_centers.sort().values
-    return centers
-
-
-def _postprocess_centers(centers: torch.Tensor, reference: torch.Tensor, K: int) -> torch.Tensor:
-    """quant/dimq.py:175-194: sort, enforce a strictly increasing minimum gap, re-centre."""
-    if centers.numel() != K:
-        raise ValueError(f"Expected {K} centers, got {centers.numel()}")
-    if not bool(torch.isfinite(centers).all()):
-        centers = _linspace_std_centers(reference, K)
-    centers = centers.float().sort().values
-    span = (reference.max() - reference.min()).abs()
-    sigma = reference.std(unbiased=False).abs()
-    scale = torch.maximum(span, sigma).clamp_min(1e-6)
-    min_gap = scale * 1e-6
-    fixed = centers.clone()
-    for i in range(1, K):
-        if fixed[i] <= fixed[i - 1]:
-            fixed[i] = fixed[i - 1] + min_gap
-    center_shift = fixed.mean() - centers.mean()
-    fixed = fixed - center_shift
-    return fixed.sort().values
+        flat = flat[torch.randperm(flat.numel(), device=flat.device)[:sample_size]]
+    return _quantile_rows(flat[None, :], K)[0].to(device=w.device, dtype=w.dtype)
 
 
 @torch.no_grad()
 def init_centers_per_channel(w: torch.Tensor, K: int, method: str = "quantile") -> torch.Tensor:
-    """[out_channels, K] codebook: the quantile recipe of init_centers_1d applied to every row.
+    """[out_channels, K] codebook: the quantile codebook of every output row of w.
 
-    Rows are the flattened output channels (w.reshape(out_channels, -1)); every
-    row is small enough (< 200,000 weights) that no subsampling applies.
-    """
+    Rows are ``w.reshape(out_channels, -1)``; they must be finite and are used
+    whole (a row of the BASELINE layers holds at most 4,608 weights, far below
+    the reference's 200,000-weight subsampling threshold)."""
+    if K <= 0:
+        raise ValueError("K must be positive")
+    if method.lower() != "quantile":
+        raise ValueError(f"Unsupported center initialization: {method} (this backend provides 'quantile')")
     rows = w.detach().float().reshape(w.shape[0], -1)
-    if method != "quantile":
-        return torch.stack([init_centers_1d(r, K, method) for r in rows]).to(w.dtype)
-    if rows.shape[1] == 1:
-        centers = rows.expand(-1, K).clone()
-    else:
-        q = torch.linspace(0.0, 1.0, K + 2, device=rows.device, dtype=rows.dtype)[1:-1]
-        centers = torch.quantile(rows, q, dim=1).T.contiguous()
-    # _postprocess_centers, row-wise
-    centers = centers.sort(dim=1).values
-    span = (rows.max(dim=1).values - rows.min(dim=1).values).abs()
-    sigma = rows.std(dim=1, unbiased=False).abs()
-    min_gap = (torch.maximum(span, sigma).clamp_min(1e-6) * 1e-6)
-    fixed = centers.clone()
-    for i in range(1, K):
-        bad = fixed[:, i] <= fixed[:, i - 1]
-        fixed[:, i] = torch.where(bad, fixed[:, i - 1] + min_gap, fixed[:, i])
-    shift = fixed.mean(dim=1) - centers.mean(dim=1)
-    fixed = fixed - shift[:, None]
-    return fixed.sort(dim=1).values.to(w.dtype)
+    if rows.numel() == 0:
+        raise ValueError("Cannot initialize centers from an empty tensor")
+    if not bool(torch.isfinite(rows).all()):
+        raise ValueError("per-channel codebooks need finite weights")
+    return _quantile_rows(rows, K).to(w.dtype)
 
 
 def _to_gpu(t: torch.Tensor) -> torch.Tensor:

@@ -2,9 +2,12 @@
 
 Mirrors ``dimq_backend/export.py`` (reference ``dimq_cuda_backend/dimq_backend/export.py:20-344``):
 the same public functions, argument names, errors and the ``dimq_packed_lut``
-format.  Index assignment, packing and unpacking run on the GPU kernels
-(``dimq_hard_quantize`` / ``dimq_pack_bits`` / ``dimq_unpack_bits``); CPU
-tensors are moved to the GPU and the results moved back.
+format.  Export is host-side data preparation, as in the reference: tensors on
+a GPU go through the HIP kernels (``dimq_hard_quantize`` / ``dimq_pack_bits`` /
+``dimq_unpack_bits``), CPU tensors (a compact checkpoint loaded with
+``map_location="cpu"``) through the same arithmetic in torch on the host, so
+the exporter also runs where no GPU is visible.  Both give the same bytes
+(``tests/test_export.py``).
 
 Format extension (``format_version`` 2), written only when a layer needs it:
 ``bit_w`` in {2,3,4,8}, ``codebook_granularity`` "per_layer" | "per_channel"
@@ -24,7 +27,6 @@ import torch
 import torch.nn as nn
 
 from . import ops
-from .codebook import _to_gpu
 
 QMIN_U4 = 0
 QMAX_U4 = 15
@@ -39,6 +41,19 @@ def bits_for_codebook(n_centers: int) -> int:
     raise ValueError(f"at most 256 centers are supported, got {n_centers}")
 
 
+_HOST_CHUNK = 1 << 18  # weights per host argmin pass (bounds its [chunk, K] distance matrix)
+
+
+@torch.no_grad()
+def _nearest_host(w: torch.Tensor, centers: torch.Tensor) -> torch.Tensor:
+    """uint8 argmin_c (w - c)^2 (first minimum) of fp32 weights w against one [K] codebook."""
+    flat = w.reshape(-1)
+    out = torch.empty(flat.shape, dtype=torch.uint8)
+    for s in range(0, flat.numel(), _HOST_CHUNK):
+        out[s:s + _HOST_CHUNK] = (flat[s:s + _HOST_CHUNK, None] - centers[None, :]).pow(2).argmin(dim=1)
+    return out.reshape(w.shape)
+
+
 @torch.no_grad()
 def assign_weight_indices(weight: torch.Tensor, codebook: torch.Tensor) -> torch.Tensor:
     """Nearest learned centre for every weight (export.py:24-35); per-layer codebook of <= 16 entries."""
@@ -47,8 +62,34 @@ def assign_weight_indices(weight: torch.Tensor, codebook: torch.Tensor) -> torch
         raise ValueError(f"packed u4 export supports at most 16 centers, got {centers.numel()}")
     if centers.numel() == 0:
         raise ValueError("codebook must not be empty")
-    idx, _ = ops.hard_quantize(_to_gpu(weight.detach().float()), _to_gpu(centers), False)
-    return idx.to(weight.device).reshape(weight.shape)
+    w = weight.detach().float()
+    if w.is_cuda:
+        idx, _ = ops.hard_quantize(w, centers.to(w.device), False)
+        return idx.reshape(weight.shape)
+    return _nearest_host(w, centers.cpu()).reshape(weight.shape)
+
+
+@torch.no_grad()
+def _pack_host(flat: torch.Tensor, bits: int) -> torch.Tensor:
+    """LSB-first b-bit stream of uint8 indices (index i in bits [b*i, b*i + b)), torch on the host."""
+    if bits == 8:
+        return flat.clone()
+    n = flat.numel()
+    nbytes = (n * bits + 7) // 8
+    bitv = torch.zeros(nbytes * 8, dtype=torch.uint8)
+    bitv[: n * bits] = ((flat[:, None] >> torch.arange(bits, dtype=torch.uint8)) & 1).reshape(-1)
+    place = (1 << torch.arange(8, dtype=torch.int32))[None, :]
+    return (bitv.reshape(nbytes, 8).to(torch.int32) * place).sum(dim=1).to(torch.uint8)
+
+
+@torch.no_grad()
+def _unpack_host(packed: torch.Tensor, numel: int, bits: int) -> torch.Tensor:
+    """Inverse of _pack_host."""
+    if bits == 8:
+        return packed[:numel].clone()
+    bitv = ((packed[:, None] >> torch.arange(8, dtype=torch.uint8)) & 1).reshape(-1)[: numel * bits]
+    place = (1 << torch.arange(bits, dtype=torch.int32))[None, :]
+    return (bitv.reshape(numel, bits).to(torch.int32) * place).sum(dim=1).to(torch.uint8)
 
 
 @torch.no_grad()
@@ -78,8 +119,8 @@ def pack_indices(indices: torch.Tensor, bits: int) -> torch.Tensor:
         if bits == 4:
             raise ValueError("u4 indices must be in [0, 15]")
         raise ValueError(f"{bits}-bit indices must be in [0, {(1 << bits) - 1}]")
-    packed = ops.pack_bits(_to_gpu(flat.to(torch.uint8)), bits)
-    return packed.to(indices.device)
+    flat = flat.to(torch.uint8)
+    return ops.pack_bits(flat, bits) if flat.is_cuda else _pack_host(flat, bits)
 
 
 @torch.no_grad()
@@ -94,8 +135,10 @@ def unpack_indices(packed: torch.Tensor, numel: int, bits: int, *, shape=None) -
         raise ValueError(f"packed tensor has {flat.numel()} bytes, expected at least {needed}")
     if numel == 0:
         out = flat.new_empty((0,), dtype=torch.uint8)
+    elif flat.is_cuda:
+        out = ops.unpack_bits(flat[:needed], numel, bits)
     else:
-        out = ops.unpack_bits(_to_gpu(flat[:needed]), numel, bits).to(packed.device)
+        out = _unpack_host(flat[:needed], numel, bits)
     if shape is not None:
         out = out.reshape(tuple(shape))
     return out

@@ -22,7 +22,7 @@ import torch
 import torch.nn as nn
 
 from . import ops
-from .codebook import assign_indices, init_centers_per_channel
+from .codebook import assign_indices, init_centers_1d, init_centers_per_channel
 from .export import bits_for_codebook, pack_indices
 
 
@@ -121,8 +121,7 @@ class DIMQCodebookLinear(nn.Module):
         """Quantile-initialised codebook, nearest-centre indices (GPU), packed (GPU)."""
         w = linear.weight.detach().float()
         K = 1 << int(bits)
-        centers = init_centers_per_channel(w, K) if per_channel else \
-            init_centers_per_channel(w.reshape(1, -1), K)[0]
+        centers = init_centers_per_channel(w, K) if per_channel else init_centers_1d(w, K)
         idx = assign_indices(w, centers)
         packed = pack_indices(idx, bits)
         dev = linear.weight.device
@@ -157,14 +156,20 @@ class DIMQCodebookConv2d(nn.Module):
         self._prepared_key = None
 
     def prepared_weight(self) -> torch.Tensor | None:
-        """Kernel-layout copies of packed_weight (LDS-halo and tap-major layouts), built on first use."""
+        """Kernel-layout copies of packed_weight (LDS-halo and tap-major layouts), built on first use and
+        rebuilt whenever packed_weight is replaced, moved or written in place (its version counter)."""
         if self.groups != 1:
             return None
-        key = (self.packed_weight.data_ptr(), self.packed_weight.device)
+        w = self.packed_weight
+        key = (w.data_ptr(), w.device, w._version)
         if self._prepared_key != key:
-            self._prepared = ops.prepare_conv_weight(self.packed_weight, self.bits, self.weight_shape)
+            self._prepared = ops.prepare_conv_weight(w, self.bits, self.weight_shape)
             self._prepared_key = key
         return self._prepared
+
+    def _load_from_state_dict(self, *args, **kwargs):
+        super()._load_from_state_dict(*args, **kwargs)
+        self._prepared, self._prepared_key = None, None  # the loaded weights may reuse the buffer's storage
 
     def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None,
                 activation: str | None = None) -> torch.Tensor:
@@ -184,8 +189,7 @@ class DIMQCodebookConv2d(nn.Module):
             raise ValueError("only zero padding is supported")
         w = conv.weight.detach().float()
         K = 1 << int(bits)
-        centers = init_centers_per_channel(w, K) if per_channel else \
-            init_centers_per_channel(w.reshape(1, -1), K)[0]
+        centers = init_centers_per_channel(w, K) if per_channel else init_centers_1d(w, K)
         idx = assign_indices(w, centers)
         packed = pack_indices(idx, bits)
         dev = conv.weight.device

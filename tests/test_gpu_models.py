@@ -60,3 +60,54 @@ def test_resnet18_forward_vs_dequant_reference(gpu):
     y = m(x.cuda().half().contiguous(memory_format=torch.channels_last)).float().cpu()
     ref = oracle.dequantized_model(m)(x)
     assert oracle.rel_err(y, ref) <= 3e-2
+
+
+# ---------------------------------------------------------------- BASELINE cfg4 at its real shapes
+@pytest.mark.parametrize("name,N,K,epi", [("qkv", 2304, 768, None), ("proj", 768, 768, "residual"),
+                                          ("fc1", 3072, 768, "gelu"), ("fc2", 768, 3072, "residual")])
+@pytest.mark.parametrize("out", [torch.float32, torch.bfloat16])
+@torch.no_grad()
+def test_vit_linear_shapes_full_size(gpu, name, N, K, epi, out):
+    """The four ViT-B/16 Linears at M = 64 x 197 = 12,608 tokens, bf16 activations, 4-bit per-channel
+    codebooks of N(0, 0.02) weights with the model's fused epilogue (GELU after fc1, the residual stream
+    added after proj / fc2), against dequantize-then-F.linear in fp32 on the CPU (quant/dimq_wrapper.py:237-240,
+    reference.py:91-110)."""
+    from dimq_amd import ops
+    from dimq_amd.codebook import init_centers_per_channel
+    from dimq_amd.export import pack_indices
+    announce(f"vit {name} M=12608 N={N} K={K} epi={epi} out={out}")
+    g = torch.Generator().manual_seed(N + K)
+    M = 64 * 197
+    w = torch.randn(N, K, generator=g) * 0.02
+    cb = init_centers_per_channel(w, 16)
+    idx = ((w[:, :, None] - cb[:, None, :]) ** 2).argmin(dim=2).to(torch.uint8)
+    packed = pack_indices(idx, 4)
+    bias = torch.randn(N, generator=g) * 0.02
+    x = torch.randn(M, K, generator=g).bfloat16()
+    res = (torch.randn(M, N, generator=g) * 0.5).bfloat16() if epi == "residual" else None
+    y = ops.dimq_linear_codebook(x.to(gpu), packed.to(gpu), cb.to(gpu), 4, bias.to(gpu), N, K, out_dtype=out,
+                                 residual=None if res is None else res.to(gpu),
+                                 activation="gelu" if epi == "gelu" else None)
+    ref = oracle.linear_dequant_reference(x.float(), packed, 4, cb, N, K, bias)
+    if epi == "residual":
+        ref = ref + res.float()
+    elif epi == "gelu":
+        ref = torch.nn.functional.gelu(ref)
+    tol = 2e-3 if out == torch.float32 else 8e-3  # a bf16 output alone rounds at 2^-9 relative
+    err = oracle.rel_err(y.float().cpu(), ref)
+    assert err <= tol, err
+
+
+@torch.no_grad()
+def test_vit_b16_bs64_forward_vs_dequant_reference(gpu):
+    """BASELINE cfg4 end to end: ViT-B/16, batch 64, 224x224, all 48 qkv/proj/fc1/fc2 Linears 4-bit
+    per-channel, bf16 on the GPU, against the dequantized fp32 model on the CPU."""
+    from dimq_amd.bench_models import quantize_vit, vit_b16
+    from dimq_amd.modules import DIMQCodebookLinear
+    announce("vit_b16 bs64 forward")
+    m = _cast_float_params(quantize_vit(vit_b16().to(gpu), 4, out_dtype=torch.bfloat16), torch.bfloat16).eval()
+    assert sum(isinstance(x, DIMQCodebookLinear) for x in m.modules()) == 48
+    x = torch.randn(64, 3, 224, 224, generator=torch.Generator().manual_seed(3))
+    y = m(x.to(gpu).bfloat16()).float().cpu()
+    ref = oracle.dequantized_model(m)(x)
+    assert oracle.rel_err(y, ref) <= 3e-2, oracle.rel_err(y, ref)

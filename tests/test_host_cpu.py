@@ -181,19 +181,39 @@ def test_constant_row_min_gap_behaviour():
     assert torch.equal(c1, torch.full((4,), 0.25))
 
 
-def test_per_channel_init_equals_row_wise_reference_recipe():
-    from dimq_amd.codebook import init_centers_1d, init_centers_per_channel
+def test_per_channel_init_rows():
+    from dimq_amd.codebook import init_centers_per_channel
     g = torch.Generator().manual_seed(3)
     w = torch.randn(48, 16, 3, 3, generator=g) * 0.05
-    w[5] = 0.125                                       # a constant row exercises the min-gap path
+    w[5] = 0.125                                       # a constant row: every quantile equal
+    w[9, 0, 0, 0] = float("nan")
+    with pytest.raises(ValueError, match="finite"):
+        init_centers_per_channel(w, 4)
+    w[9, 0, 0, 0] = 0.0
     pc = init_centers_per_channel(w, 4)
-    ref = torch.stack([init_centers_1d(r, 4, "quantile") for r in w.reshape(48, -1)])
-    assert torch.allclose(pc, ref, rtol=0, atol=1e-7)
+    rows = w.reshape(48, -1)
+    q = torch.quantile(rows, torch.linspace(0, 1, 6)[1:-1], dim=1).T
+    live = [r for r in range(48) if r != 5]
+    # distinct quantiles: the spread is a no-op, the codebook is torch.quantile's
+    assert torch.equal(pc[live], q[live])
+    # constant row: gap = 1e-6 * max(span, std) clamped to 1e-6 -> 1e-12, below fp32 resolution at 0.125
+    assert torch.equal(pc[5], torch.full((4,), 0.125))
 
 
-def test_kmeans_init_converges_to_cluster_means():
+def test_init_rejects_other_initialisers():
+    from dimq_amd.codebook import init_centers_1d, init_centers_per_channel
+    with pytest.raises(ValueError, match="quantile"):
+        init_centers_1d(torch.randn(10), 3, "kmeans")
+    with pytest.raises(ValueError, match="quantile"):
+        init_centers_per_channel(torch.randn(4, 10), 3, "linspace_minmax")
+
+
+def test_init_subsamples_large_tensors_with_randperm():
     from dimq_amd.codebook import init_centers_1d
-    w = torch.cat([torch.full((50,), -1.0), torch.full((50,), 0.0), torch.full((50,), 2.0)])
-    w = w + torch.linspace(-0.01, 0.01, 150)
-    c = init_centers_1d(w, 3, "kmeans")
-    assert torch.allclose(c, torch.tensor([-1.0, 0.0, 2.0]), atol=0.02)
+    g = torch.Generator().manual_seed(11)
+    w = torch.randn(250_000, generator=g)
+    torch.manual_seed(123)
+    c = init_centers_1d(w, 8, "quantile")
+    torch.manual_seed(123)
+    sample = w[torch.randperm(w.numel())[:200_000]]    # quant/dimq.py:111-113
+    assert torch.equal(c, torch.quantile(sample, torch.linspace(0, 1, 10)[1:-1]))

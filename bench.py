@@ -1,10 +1,14 @@
 """Benchmark of the DIMQ packed-index hot path on one MI355X.
 
-Default workload: BASELINE configs[1] (cfg2), the ResNet-18 layer1 3x3 conv
-with a 2-bit per-output-channel codebook: x fp16 [32,64,56,56] (ReLU of
-N(0,1)), W [64,64,3,3] Kaiming-normal, stride 1, pad 1, no bias, y fp32.
-One step = one LUT conv launch over one batch.  Other workloads:
-``--config cfg1|cfg5|codec``.
+Default run: the two halves of the BASELINE metric on one JSON line.
+* Headline (``value``): BASELINE configs[1] (cfg2), the ResNet-18 layer1 3x3
+  conv with a 2-bit per-output-channel codebook: x fp16 [32,64,56,56] (ReLU of
+  N(0,1)), W [64,64,3,3] Kaiming-normal, stride 1, pad 1, no bias, y fp32.  One
+  step = one LUT conv launch over one batch.
+* ``models.vit_b16``: BASELINE configs[3], the ViT-B/16 bs64 forward with its
+  48 Linears 4-bit, in images/s with the MFMA roofline over the forward's
+  FLOPs and the dequantized fp32 model timed on the host beside it.
+Single workloads: ``--config cfg1|cfg2|cfg5|codec|vit|resnet18|w4a4_linear|w4a4_conv``.
 
 Timing: inputs are resident in HBM before the timed region; R buffer sets
 (> 512 MB in total, so the 256 MB MALL cannot serve repeats) are rotated; the
@@ -355,7 +359,8 @@ def make_w4a4(dev, rotations, op="linear"):
 
         def cpu_step(rows):
             import oracle
-            return oracle.linear_lut(xs[0][:rows].cpu(), packed.cpu(), cb16.float(), scale, zp, b, N, K)
+            return oracle.linear_a4_dequant_reference(xs[0][:rows].cpu(), packed.cpu(), cb16.float(), scale, zp, N, K,
+                                                      b)
 
         def check():
             import oracle
@@ -380,8 +385,8 @@ def make_w4a4(dev, rotations, op="linear"):
 
         def cpu_step(batch):
             import oracle
-            return oracle.conv2d_lut(xs[0][:batch].cpu().float(), packed.cpu(), cb16.float(), scale, zp, None, shape,
-                                     1, 1, 1, 1)
+            return oracle.conv2d_a4_dequant_reference(xs[0][:batch].cpu().float(), packed.cpu(), cb16.float(), scale,
+                                                      zp, shape, None, 1, 1, 1, 1)
 
         def check():
             import oracle
@@ -398,7 +403,8 @@ def make_w4a4(dev, rotations, op="linear"):
         name=f"w4a4_{op}", workload=workload, step=step, flops=flops, alg_bytes=alg_bytes, bound="hbm",
         dtype="fp16", unit="TFLOP/s", per_step_units=flops / 1e12, cpu_step=cpu_step, cpu_full_batch=full,
         check=check, extra_config=extra, per_set_bytes=x_bytes + y_bytes,
-        cpu_cores=1, cpu_desc="C oracle of the reference LUT loop (reference.py:59-88 / 147-205), one thread",
+        cpu_desc="the reference's CPU path: u4 activations and W_hat = C[idx] dequantized, then torch CPU fp32 "
+                 "F.linear / F.conv2d (reference.py:91-144)",
     )
 
 
@@ -490,12 +496,82 @@ def time_cpu(wl, budget_s=15.0):
                        f"{wl.get('cpu_desc', 'oracle dequantize + torch CPU fp32')}; {model}")
 
 
+def run_workload(args, config, dev, steps, warmup, cpu_budget_s=15.0):
+    """Builds one workload, checks it against the oracle, times it (HIP graph replays, HIP events) and its
+    CPU baseline; returns the fields of its JSON line."""
+    make = WORKLOADS[config]
+    kw = {}
+    if config == "cfg5":
+        kw["M"] = args.m
+    if config in ("cfg1", "cfg5"):
+        kw["variant"] = args.variant
+    if config == "codec":
+        kw["direction"] = args.direction
+    if config == "cfg2":
+        kw["layout"] = args.layout
+    # rotate buffer sets totalling > 512 MB
+    if config in FIXED_ROTATIONS:
+        # end-to-end models: inputs rotate over a few sets; the packed weights are re-read every step
+        rotations = FIXED_ROTATIONS[config]
+    else:
+        probe = make(dev, 1, **kw)
+        rotations = max(2, min(64, math.ceil(512e6 / probe["per_set_bytes"]) + 1))
+        del probe
+    if args.rotations > 0:
+        rotations = args.rotations
+    torch.cuda.empty_cache()
+    wl = make(dev, rotations, **kw)
+    if "variant" in kw:
+        wl["extra_config"]["variant"] = kw["variant"]
+
+    err = None if args.no_check else wl["check"]()
+    ms, steps = time_gpu(wl, rotations, steps, warmup)
+    sec = ms / 1e3
+    value = wl["per_step_units"] / sec
+    if wl["bound"] == "hbm":
+        achieved = wl["alg_bytes"] / sec / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None}
+    else:
+        achieved = wl["flops"] / sec / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None}
+    traffic_file = ROOT / "profiles" / f"traffic_{wl['name']}.json"
+    if traffic_file.exists():
+        roof["traffic"] = json.loads(traffic_file.read_text()).get("traffic_bytes_per_launch")
+    cpu = None if args.no_cpu else time_cpu(wl, cpu_budget_s)
+    out = {
+        "metric": METRIC,
+        "metric_part": "images/s" if wl["unit"] == "images/s" else "LUT-GEMM/conv TFLOP/s + % roofline",
+        "value": round(value, 4),
+        "unit": wl["unit"],
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": wl["dtype"],
+        "data": "synthetic (seeded CPU torch.Generator, copied to HBM before timing)",
+        "config": {"workload": wl["workload"], "name": wl["name"], "rotated_buffer_sets": rotations,
+                   "algorithmic_bytes_per_step": wl["alg_bytes"], "flops_per_step": wl["flops"],
+                   "parity_max_rel_err": err, **wl["extra_config"]},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    del wl
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1600)
     ap.add_argument("--warmup", type=int, default=160)
-    ap.add_argument("--config", default="cfg2", choices=sorted(WORKLOADS))
+    ap.add_argument("--config", default=None, choices=sorted(WORKLOADS),
+                    help="one workload (default: cfg2 headline plus the ViT-B/16 bs64 forward on the same line)")
     ap.add_argument("--m", type=int, default=16, help="rows for cfg5")
     ap.add_argument("--direction", default="unpack", choices=["pack", "unpack"])
     ap.add_argument("--layout", default="nchw", choices=["nchw", "nhwc"], help="cfg2 activation layout")
@@ -514,67 +590,16 @@ def main():
         sys.exit(2)
 
     dev = torch.device("cuda:0")
-    make = WORKLOADS[args.config]
-    kw = {}
-    if args.config == "cfg5":
-        kw["M"] = args.m
-    if args.config in ("cfg1", "cfg5"):
-        kw["variant"] = args.variant
-    if args.config == "codec":
-        kw["direction"] = args.direction
-    if args.config == "cfg2":
-        kw["layout"] = args.layout
-    # rotate buffer sets totalling > 512 MB
-    if args.config in FIXED_ROTATIONS:
-        # end-to-end models: inputs rotate over a few sets; the packed weights are re-read every step
-        probe = {"per_set_bytes": 1}
-        rotations = FIXED_ROTATIONS[args.config]
+    if args.config is not None:
+        out = run_workload(args, args.config, dev, args.steps, args.warmup)
     else:
-        probe = make(dev, 1, **kw)
-        rotations = max(2, min(64, math.ceil(512e6 / probe["per_set_bytes"]) + 1))
-    if args.rotations > 0:
-        rotations = args.rotations
-    del probe
-    torch.cuda.empty_cache()
-    wl = make(dev, rotations, **kw)
-    if "variant" in kw:
-        wl["extra_config"]["variant"] = kw["variant"]
-
-    err = None if args.no_check else wl["check"]()
-    ms, steps = time_gpu(wl, rotations, args.steps, args.warmup)
-    sec = ms / 1e3
-    value = wl["per_step_units"] / sec
-    if wl["bound"] == "hbm":
-        achieved = wl["alg_bytes"] / sec / 1e9
-        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None}
-    else:
-        achieved = wl["flops"] / sec / 1e12
-        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None}
-    traffic_file = ROOT / "profiles" / f"traffic_{wl['name']}.json"
-    if traffic_file.exists():
-        roof["traffic"] = json.loads(traffic_file.read_text()).get("traffic_bytes_per_launch")
-    cpu = None if args.no_cpu else time_cpu(wl)
-    out = {
-        "metric": METRIC,
-        "value": round(value, 4),
-        "unit": wl["unit"],
-        "n_gpus": 1,
-        "steps": steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms, 6),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": wl["dtype"],
-        "data": "synthetic (seeded CPU torch.Generator, copied to HBM before timing)",
-        "config": {"workload": wl["workload"], "name": wl["name"], "rotated_buffer_sets": rotations,
-                   "algorithmic_bytes_per_step": wl["alg_bytes"], "flops_per_step": wl["flops"],
-                   "parity_max_rel_err": err, **wl["extra_config"]},
-        "roofline": roof,
-        "cpu_baseline": cpu,
-    }
+        out = run_workload(args, "cfg2", dev, args.steps, args.warmup)
+        # second half of the metric: the ViT-B/16 bs64 forward (a few graph replays of the whole forward)
+        vit = run_workload(args, "vit", dev, max(4, min(args.steps, 40)), max(1, min(args.warmup, 8)),
+                           cpu_budget_s=12.0)
+        out["models"] = {"vit_b16": {k: vit[k] for k in ("metric_part", "value", "unit", "ms_per_step", "steps",
+                                                         "dtype", "config", "roofline", "cpu_baseline")}}
+    out.pop("metric_part", None)
     print(json.dumps(out), flush=True)
 
 

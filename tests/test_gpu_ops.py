@@ -880,3 +880,20 @@ def test_max_pool2d_nhwc_vs_torch(gpu, shape, k, s, p, dt):
     torch.testing.assert_close(y.cpu().float(), ref, rtol=0, atol=0, equal_nan=True)
     with pytest.raises(RuntimeError, match="channels-last"):
         ops.max_pool2d_nhwc(x.contiguous().to(gpu), k, s, p)
+
+
+def test_benchmark_cuda_times_an_op(gpu):
+    """benchmark_cuda (dimq_backend/benchmark.py:10-26): mean milliseconds per call between two HIP events,
+    after the warm-up calls; every call runs (warmup + repeat of them)."""
+    from dimq_amd import ops
+    from dimq_amd.benchmark import benchmark_cuda
+    idx = torch.randint(0, 8, (1 << 20,), dtype=torch.uint8, device=gpu)
+    calls = []
+
+    def fn():
+        calls.append(1)
+        return ops.pack_bits(idx, 3)
+
+    ms = benchmark_cuda(fn, warmup=3, repeat=7)
+    assert len(calls) == 10
+    assert 0.0 < ms < 100.0

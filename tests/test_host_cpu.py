@@ -217,3 +217,12 @@ def test_init_subsamples_large_tensors_with_randperm():
     torch.manual_seed(123)
     sample = w[torch.randperm(w.numel())[:200_000]]    # quant/dimq.py:111-113
     assert torch.equal(c, torch.quantile(sample, torch.linspace(0, 1, 10)[1:-1]))
+
+
+def test_benchmark_cuda_needs_a_gpu():
+    """benchmark_cuda (dimq_backend/benchmark.py:10-26) times with HIP events; without a GPU it raises."""
+    from dimq_amd.benchmark import benchmark_cuda
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible (the GPU test covers the timing)")
+    with pytest.raises(RuntimeError, match="GPU"):
+        benchmark_cuda(lambda: None, warmup=1, repeat=1)

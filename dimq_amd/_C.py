@@ -79,7 +79,7 @@ _SIGS = {
                                     _i64, _i64, _vp, _int] + [_i64] * 10 + [_vp, _int, _int, _int, _vp]),
     "dimq_linear_codebook_ex": (_int, [_vp, _int, _i64, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _vp, _int,
                                        _i64, _vp, _int, _vp, _int, _int, _int, _vp]),
-    "dimq_linear_codebook_workspace_bytes": (_i64, [_i64, _i64, _int, _int]),
+    "dimq_linear_codebook_workspace_bytes": (_i64, [_i64, _i64, _i64, _int, _int]),
     "dimq_linear_codebook_ex_ws": (_int, [_vp, _int, _i64, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _vp, _int,
                                           _i64, _vp, _int, _vp, _int, _int, _int, _vp, _i64, _vp]),
     "dimq_linear_codebook_act_workspace_bytes": (_i64, [_i64, _i64]),
@@ -372,7 +372,8 @@ def linear_codebook_impl(x, packed_w, codebook, bits, bias, out_features, in_fea
         raise RuntimeError(f"residual shape {tuple(residual.shape)} must equal the output shape "
                            f"{(*x.shape[:-1], out_features)}")
     r, rp, rdt = _residual_args(None if residual is None else residual.reshape(M, out_features), y)
-    ws = _workspace(lib.dimq_linear_codebook_workspace_bytes(M, in_features, int(bits), _dtype(xc)), xc.device)
+    ws = _workspace(lib.dimq_linear_codebook_workspace_bytes(M, in_features, out_features, int(bits), _dtype(xc)),
+                    xc.device)
     with torch.cuda.device(xc.device):
         _check(lib.dimq_linear_codebook_ex_ws(_ptr(xc), _dtype(xc), M, in_features, _ptr(pw), pw.numel(), int(bits),
                                               _ptr(cb), _dtype(cb), rows, size, bp, bdt, out_features, _ptr(y),

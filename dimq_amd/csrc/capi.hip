@@ -28,4 +28,4 @@ int check_launch(const char* what) {
 
 extern "C" const char* dimq_last_error(void) { return dimq::g_last_error; }
 
-extern "C" int dimq_abi_version(void) { return 1; }
+extern "C" int dimq_abi_version(void) { return 2; }

@@ -70,6 +70,16 @@ __device__ __forceinline__ uint32_t float_to_bf16_bits(float x) {
   return u >> 16;
 }
 
+// Work-group barrier that orders LDS accesses only.  __syncthreads() is a
+// work-group release/acquire over all memory, so it also waits for every
+// global load still in flight; kernels that keep a stream of loads in flight
+// across a barrier (prefetch) use this one.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Load element i of a float tensor of runtime dtype as fp32.
 __device__ __forceinline__ float load_as_float(const void* p, int dt, int64_t i) {
   switch (dt) {
@@ -79,6 +89,37 @@ __device__ __forceinline__ float load_as_float(const void* p, int dt, int64_t i)
     case DIMQ_F64: return (float)reinterpret_cast<const double*>(p)[i];
   }
   return 0.0f;
+}
+
+// Entries [0, E) of one codebook row (size >= 1 entries) as fp32, 0 past
+// `size`.  The dtype is switched on once, and entries past `size` re-load the
+// last one and are zeroed by a select, so the E loads go out back to back with
+// no branch between them (a branch around each load makes the compiler wait
+// for every load before the next one).
+template <int E>
+__device__ __forceinline__ void load_cb_row(const void* cb, int dt, int64_t row, int size, float (&v)[E]) {
+  const int64_t base = row * size;
+  int idx[E];
+#pragma unroll
+  for (int j = 0; j < E; ++j) idx[j] = j < size ? j : size - 1;
+  if (dt == DIMQ_F32) {
+    const float* p = reinterpret_cast<const float*>(cb) + base;
+#pragma unroll
+    for (int j = 0; j < E; ++j) v[j] = p[idx[j]];
+  } else if (dt == DIMQ_F16 || dt == DIMQ_BF16) {
+    const uint16_t* p = reinterpret_cast<const uint16_t*>(cb) + base;
+    uint32_t h[E];
+#pragma unroll
+    for (int j = 0; j < E; ++j) h[j] = p[idx[j]];
+#pragma unroll
+    for (int j = 0; j < E; ++j) v[j] = dt == DIMQ_F16 ? f16_bits_to_float(h[j]) : bf16_bits_to_float(h[j]);
+  } else {
+    const double* p = reinterpret_cast<const double*>(cb) + base;
+#pragma unroll
+    for (int j = 0; j < E; ++j) v[j] = (float)p[idx[j]];
+  }
+#pragma unroll
+  for (int j = 0; j < E; ++j) v[j] = j < size ? v[j] : 0.0f;
 }
 
 __device__ __forceinline__ void store_from_float(void* p, int dt, int64_t i, float v) {

@@ -163,11 +163,7 @@ __global__ __launch_bounds__(kBandThreads, 1) void conv_band_kernel(const HaloAr
 
   // this lane's codebook row and packed weights
   float cbv[E];
-  {
-    const int64_t row = p.cb_rows == 1 ? 0 : min(ocl, p.OC - 1);
-#pragma unroll
-    for (int j = 0; j < E; ++j) cbv[j] = j < p.cb_size ? load_as_float(p.cb, p.cb_dt, row * p.cb_size + j) : 0.0f;
-  }
+  load_cb_row<E>(p.cb, p.cb_dt, p.cb_rows == 1 ? 0 : min(ocl, p.OC - 1), p.cb_size, cbv);
   uint32_t wreg[WPL];
   {
     const uint32_t* src = p.kw + ((int64_t)min(ocl, p.OC - 1) * 2 + g) * WPL;
@@ -197,7 +193,7 @@ __global__ __launch_bounds__(kBandThreads, 1) void conv_band_kernel(const HaloAr
     const int co = t & 7, side = (t >> 3) & 1, r = t >> 4;
     *reinterpret_cast<uint4*>(&halo[(r * p.IW_t + (side ? p.IW_t - 1 : 0)) * CP + 8 * co]) = make_uint4(0, 0, 0, 0);
   }
-  __syncthreads();
+  lds_barrier();  // stage B's loads stay in flight through round 0
 
   const int row_step = p.IW_t * CP;
   // nq = 1 or 2 blocks (independent accumulator chains) of this wave
@@ -249,7 +245,7 @@ __global__ __launch_bounds__(kBandThreads, 1) void conv_band_kernel(const HaloAr
     }
   }
   band_commit(p, bp.ra, tid, tB, tkb, halo);
-  __syncthreads();
+  lds_barrier();
   for (int mb = bp.blk0 + wq + kBandBlocksPerRound; mb < bp.blk1; mb += 2 * kBandBlocksPerRound) {
     const bool two = mb + kBandBlocksPerRound < bp.blk1;
     const int mbs[2] = {mb, mb + kBandBlocksPerRound};

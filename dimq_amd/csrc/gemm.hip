@@ -86,7 +86,8 @@ int gemm_dispatch(const GemmArgs& p, int bits, int xt, bool a4, int tile, hipStr
 int linear_codebook_impl(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed_w,
                          int bits, const void* codebook, int cb_dtype, int64_t cb_rows, int64_t cb_size,
                          const void* bias, int bias_dtype, int64_t N, void* y, int y_dtype, int64_t ldy,
-                         const Epi& epi, int variant, hipStream_t s, float acc_scale = 1.0f) {
+                         const Epi& epi, int variant, hipStream_t s, float acc_scale = 1.0f,
+                         void* workspace = nullptr, int64_t workspace_bytes = 0) {
   GemmArgs p{};
   p.epi = epi;
   p.acc_scale = acc_scale;
@@ -128,18 +129,18 @@ int linear_codebook_impl(const void* x, int x_dtype, int64_t M, int64_t K, int64
   // (ResNet-18 fc, M 128 x N 1000: 32 work-groups on 64-row tiles, 128 on
   // 16-row tiles; measured 28.9 -> 23.4 us per call)
   if (bits == 8 && tile == kTile64x32 && ((M + 63) / 64) * ((N + 63) / 64) < kCUs / 2) tile = kTile16x16;
-  if (tile == kTileGemv && gemv_fast_supported(p, bits)) {
-    switch (bits) {
-      case 2: return launch_gemv_fast<2>(p, x_dtype, s);
-      case 3: return launch_gemv_fast<3>(p, x_dtype, s);
-      default: return launch_gemv_fast<4>(p, x_dtype, s);
-    }
-  }
-  if (tile == kTileGemv && gemv_split_supported(p, bits)) {
-    switch (bits) {
-      case 2: return launch_gemv_split<2>(p, x_dtype, s);
-      case 3: return launch_gemv_split<3>(p, x_dtype, s);
-      default: return launch_gemv_split<4>(p, x_dtype, s);
+  if (tile == kTileGemv) {
+    const bool ws_ok = workspace != nullptr && aligned(workspace, 16);
+    GemvPlan pl;
+    bool planned = gemv_plan(p, bits, ws_ok, pl);
+    if (planned && gemv_partial_bytes(p, pl) > (ws_ok ? workspace_bytes : 0)) planned = gemv_plan(p, bits, false, pl);
+    if (planned) {
+      float* part = static_cast<float*>(workspace);
+      switch (bits) {
+        case 2: return launch_gemv_stream<2>(p, x_dtype, pl, part, s);
+        case 3: return launch_gemv_stream<3>(p, x_dtype, pl, part, s);
+        default: return launch_gemv_stream<4>(p, x_dtype, pl, part, s);
+      }
     }
   }
   return dispatch<false>(p, bits, x_dtype, tile, s);
@@ -149,6 +150,12 @@ int linear_codebook_impl(const void* x, int x_dtype, int64_t M, int64_t K, int64
 
 using namespace dimq;
 
+static int linear_codebook_checked(const void* x, int x_dtype, int64_t M, int64_t K, const uint8_t* packed_w,
+                                   int64_t packed_numel, int bits, const void* codebook, int cb_dtype, int64_t cb_rows,
+                                   int64_t cb_size, const void* bias, int bias_dtype, int64_t N, void* y, int y_dtype,
+                                   const void* residual, int residual_dtype, int activation, int variant, void* stream,
+                                   void* workspace, int64_t workspace_bytes);
+
 extern "C" int dimq_linear_codebook(const void* x, int x_dtype, int64_t M, int64_t K, const uint8_t* packed_w,
                                     int64_t packed_numel, int bits, const void* codebook, int cb_dtype,
                                     int64_t cb_rows, int64_t cb_size, const void* bias, int bias_dtype, int64_t N,
@@ -157,12 +164,25 @@ extern "C" int dimq_linear_codebook(const void* x, int x_dtype, int64_t M, int64
                                  bias, bias_dtype, N, y, y_dtype, nullptr, 0, DIMQ_ACT_NONE, variant, stream);
 }
 
-// fp32 activations on the large tiles: the tiles' fp16 form after one
-// conversion pass (the same round-to-nearest conversion the fp32 tiles apply
-// as they stage, so the results are the same bits; measured at cfg1, 1576 x
-// 768 fp32: 32.6 us for the fp32 tile against 25.2 us for the fp16 one).
-extern "C" int64_t dimq_linear_codebook_workspace_bytes(int64_t M, int64_t K, int bits, int x_dtype) {
-  if (x_dtype != DIMQ_F32 || M <= 64 || K <= 0 || K % 64 != 0 || !(bits == 2 || bits == 3 || bits == 4)) return 0;
+// Workspace of dimq_linear_codebook_ex_ws: fp32 activations on the large
+// tiles take the tiles' fp16 form after one conversion pass (the same
+// round-to-nearest conversion the fp32 tiles apply as they stage, so the
+// results are the same bits; measured at cfg1, 1576 x 768 fp32: 32.6 us for
+// the fp32 tile against 25.2 us for the fp16 one); decode shapes (M <= 16)
+// with split k ranges keep their fp32 partial sums there.
+extern "C" int64_t dimq_linear_codebook_workspace_bytes(int64_t M, int64_t K, int64_t N, int bits, int x_dtype) {
+  if (M <= 0 || K <= 0 || N <= 0 || !(bits == 2 || bits == 3 || bits == 4)) return 0;
+  if (M <= 16) {
+    GemmArgs p{};
+    p.M = M;
+    p.K = K;
+    p.N = N;
+    p.fast_b = p.vec_a = true;
+    GemvPlan pl;
+    if (!gemv_plan(p, bits, true, pl)) return 0;
+    return (gemv_partial_bytes(p, pl) + 255) / 256 * 256;
+  }
+  if (x_dtype != DIMQ_F32 || M <= 64 || K % 64 != 0) return 0;
   return (M * K * 2 + 255) / 256 * 256;
 }
 
@@ -173,7 +193,11 @@ extern "C" int dimq_linear_codebook_ex_ws(const void* x, int x_dtype, int64_t M,
                                           int activation, int variant, void* workspace, int64_t workspace_bytes,
                                           void* stream) {
   DIMQ_CHECK(workspace_bytes >= 0, "workspace_bytes must be non-negative");
-  const int64_t need = dimq_linear_codebook_workspace_bytes(M, K, bits, x_dtype);
+  if (M >= 1 && M <= 16) return linear_codebook_checked(x, x_dtype, M, K, packed_w, packed_numel, bits, codebook,
+                                                        cb_dtype, cb_rows, cb_size, bias, bias_dtype, N, y, y_dtype,
+                                                        residual, residual_dtype, activation, variant, stream,
+                                                        workspace, workspace_bytes);
+  const int64_t need = dimq_linear_codebook_workspace_bytes(M, K, N, bits, x_dtype);
   const int mode = epi_mode(Epi{residual, residual_dtype, activation, 0});
   if (workspace != nullptr && need > 0 && workspace_bytes >= need && aligned(workspace, 16) &&
       variant != DIMQ_VARIANT_SMALL_M && aligned(packed_w, 16) && aligned(x, 16) &&
@@ -238,6 +262,18 @@ extern "C" int dimq_linear_codebook_ex(const void* x, int x_dtype, int64_t M, in
                                        int64_t cb_rows, int64_t cb_size, const void* bias, int bias_dtype, int64_t N,
                                        void* y, int y_dtype, const void* residual, int residual_dtype,
                                        int activation, int variant, void* stream) {
+  return linear_codebook_checked(x, x_dtype, M, K, packed_w, packed_numel, bits, codebook, cb_dtype, cb_rows, cb_size,
+                                 bias, bias_dtype, N, y, y_dtype, residual, residual_dtype, activation, variant, stream,
+                                 nullptr, 0);
+}
+
+// Argument checks of the weight-only Linear, then the kernels; `workspace`
+// (nullable) may hold the decode GEMV's split-k partial sums.
+static int linear_codebook_checked(const void* x, int x_dtype, int64_t M, int64_t K, const uint8_t* packed_w,
+                                   int64_t packed_numel, int bits, const void* codebook, int cb_dtype, int64_t cb_rows,
+                                   int64_t cb_size, const void* bias, int bias_dtype, int64_t N, void* y, int y_dtype,
+                                   const void* residual, int residual_dtype, int activation, int variant, void* stream,
+                                   void* workspace, int64_t workspace_bytes) {
   if (!(bits == 2 || bits == 3 || bits == 4 || bits == 8))
     return set_error(DIMQ_ERR_UNSUPPORTED, "bits must be one of 2, 3, 4, 8 (got %d)", bits);
   DIMQ_CHECK(x_dtype == DIMQ_F32 || x_dtype == DIMQ_F16 || x_dtype == DIMQ_BF16,
@@ -255,7 +291,8 @@ extern "C" int dimq_linear_codebook_ex(const void* x, int x_dtype, int64_t M, in
   DIMQ_CHECK(activation >= DIMQ_ACT_NONE && activation <= DIMQ_ACT_GELU, "unknown activation %d", activation);
   const Epi epi{residual, residual_dtype, activation, residual != nullptr && aligned(residual, 16)};
   return linear_codebook_impl(x, x_dtype, M, K, K, packed_w, bits, codebook, cb_dtype, cb_rows, cb_size, bias,
-                              bias_dtype, N, y, y_dtype, N, epi, variant, as_stream(stream));
+                              bias_dtype, N, y, y_dtype, N, epi, variant, as_stream(stream), 1.0f, workspace,
+                              workspace_bytes);
 }
 
 extern "C" int64_t dimq_linear_lut_workspace_bytes(int64_t M, int64_t in_features, int cb_dtype) {

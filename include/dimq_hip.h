@@ -245,14 +245,19 @@ int dimq_linear_codebook_ex(const void* x, int x_dtype, int64_t M, int64_t K, co
 
 /* Workspace form of dimq_linear_codebook_ex (same arguments, checks and
  * results, plus a caller-owned device workspace; the library allocates
- * nothing).  With fp32 activations on the large-tile shapes (M > 64,
- * K % 64 == 0, bits 2-4) and a 16-byte aligned workspace of at least
- * dimq_linear_codebook_workspace_bytes, the activations are converted to fp16
- * once (round to nearest even, the conversion the fp32 tiles apply while
- * staging) and the fp16 tiles run: the same output bits, measured 8 % faster
- * at X fp32 [1576,768].  Otherwise it is dimq_linear_codebook_ex.  The
- * workspace is written on `stream`; calls sharing one must be ordered on it. */
-int64_t dimq_linear_codebook_workspace_bytes(int64_t M, int64_t K, int bits, int x_dtype);
+ * nothing).  With a 16-byte aligned workspace of at least
+ * dimq_linear_codebook_workspace_bytes:
+ *  - fp32 activations on the large-tile shapes (M > 64, K % 64 == 0, bits
+ *    2-4) are converted to fp16 once (round to nearest even, the conversion
+ *    the fp32 tiles apply while staging) and the fp16 tiles run: the same
+ *    output bits, measured 8 % faster at X fp32 [1576,768];
+ *  - decode shapes (4 < M <= 16, bits 2-4, N % 64 == 0, K % 1024 == 0) split
+ *    the k range over work-groups of 64 columns and keep the fp32 partial sums
+ *    there (a second, small kernel adds them), so the activations are read
+ *    by 64 columns per work-group instead of 16.
+ * Otherwise it is dimq_linear_codebook_ex.  The workspace is written on
+ * `stream`; calls sharing one must be ordered on it. */
+int64_t dimq_linear_codebook_workspace_bytes(int64_t M, int64_t K, int64_t N, int bits, int x_dtype);
 int dimq_linear_codebook_ex_ws(const void* x, int x_dtype, int64_t M, int64_t K, const uint8_t* packed_w,
                                int64_t packed_numel, int bits, const void* codebook, int cb_dtype, int64_t cb_rows,
                                int64_t cb_size, const void* bias, int bias_dtype, int64_t N, void* y, int y_dtype,

@@ -396,10 +396,13 @@ def test_linear_codebook_large_tiles(gpu, bits, M, N, K, xdt):
 @pytest.mark.parametrize("M,N,K,xdt", [(1, 300, 4096, torch.bfloat16), (4, 64, 8192, torch.float16),
                                        (3, 130, 4096, torch.float32), (16, 130, 4096, torch.bfloat16),
                                        (5, 77, 4096, torch.float16), (9, 200, 8192, torch.bfloat16),
-                                       (16, 48, 12288, torch.float32)])
+                                       (16, 48, 12288, torch.float32), (16, 256, 4096, torch.bfloat16),
+                                       (8, 128, 2048, torch.float32), (12, 64, 1024, torch.float16),
+                                       (16, 4096, 4096, torch.bfloat16)])
 def test_linear_codebook_gemv_fast(gpu, bits, M, N, K, xdt):
-    """Decode-shape GEMVs (all loads issued up front: M <= 4 one k range per lane, 4 < M <= 16 split-K
-    rounds), N tails, per-layer and per-channel codebooks."""
+    """Decode-shape GEMVs (streamed weight runs; 16-column work-groups with the k range split over waves, or
+    64-column work-groups with k split over work-groups and the partial sums added by a second kernel),
+    N tails, per-layer and per-channel codebooks, fp32 / fp16 / bf16 activations."""
     ops = _ops()
     for per_channel in (True, False):
         announce(f"linear_codebook gemv bits={bits} M={M} N={N} K={K} {xdt} pc={per_channel}")
@@ -427,7 +430,7 @@ def test_linear_codebook_fp32_pass_same_bits(gpu, act):
     cbg, pg = cb.to(gpu), packed.to(gpu)
     act_id = {None: 0, "gelu": 2}[act]
     s = torch.cuda.current_stream().cuda_stream
-    ws_bytes = _C.lib.dimq_linear_codebook_workspace_bytes(M, K, 4, _C.F32)
+    ws_bytes = _C.lib.dimq_linear_codebook_workspace_bytes(M, K, N, 4, _C.F32)
     assert ws_bytes >= M * K * 2
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=gpu)
     y_pass = torch.empty(M, N, device=gpu)

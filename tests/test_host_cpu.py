@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol(capi):
 
 def test_host_only_entry_points(capi):
     lib = capi.lib
-    assert lib.dimq_abi_version() == 1
+    assert lib.dimq_abi_version() == 2
     # LDS-halo layout words: OC * 2 lane groups * ceil(T/4) words-groups * bits, T = KH*KW*C/16,
     # followed by the tap-major layout: OC * C * KH * KW * bits / 32
     assert lib.dimq_conv2d_prepared_words(64, 64, 3, 3, 2) == 64 * 2 * 9 * 2 + 64 * 64 * 9 * 2 // 32
@@ -79,11 +79,18 @@ def test_linear_workspace_sizes_and_act_codebook_errors(capi):
     lib = capi.lib
     up = lambda b: (b + 255) // 256 * 256
     # fp32 activations on the large-tile shapes get an fp16 copy; nothing else does
-    assert lib.dimq_linear_codebook_workspace_bytes(1576, 768, 4, capi.F32) == up(1576 * 768 * 2)
-    assert lib.dimq_linear_codebook_workspace_bytes(1576, 768, 4, capi.BF16) == 0
-    assert lib.dimq_linear_codebook_workspace_bytes(64, 768, 4, capi.F32) == 0     # GEMV / small tiles
-    assert lib.dimq_linear_codebook_workspace_bytes(1576, 100, 4, capi.F32) == 0   # K % 64 != 0
-    assert lib.dimq_linear_codebook_workspace_bytes(1576, 768, 8, capi.F32) == 0   # 8-bit tiles
+    ws = lib.dimq_linear_codebook_workspace_bytes
+    assert ws(1576, 768, 3072, 4, capi.F32) == up(1576 * 768 * 2)
+    assert ws(1576, 768, 3072, 4, capi.BF16) == 0
+    assert ws(64, 768, 3072, 4, capi.F32) == 0     # small tiles
+    assert ws(1576, 100, 3072, 4, capi.F32) == 0   # K % 64 != 0
+    assert ws(1576, 768, 3072, 8, capi.F32) == 0   # 8-bit tiles
+    # decode GEMV, 4 < M <= 16: fp32 partial sums of the k splits (k ranges of 1024)
+    assert ws(16, 4096, 4096, 3, capi.BF16) == up(4 * 16 * 4096 * 4)
+    assert ws(9, 8192, 192, 2, capi.F16) == up(8 * 9 * 192 * 4)
+    assert ws(16, 4096, 4000, 3, capi.BF16) == 0   # N % 64 != 0: one k range per work-group
+    assert ws(4, 4096, 4096, 3, capi.BF16) == 0    # M <= 4: one k range per work-group
+    assert ws(16, 4096, 4096, 8, capi.BF16) == 0
     assert lib.dimq_linear_codebook_act_workspace_bytes(300, 768) == up(300 * 768 * 2)
     assert lib.dimq_linear_codebook_act_workspace_bytes(0, 768) == 0
     args = [None, capi.F32, 4, 64, None, 128, 4, None, capi.F32, 1, 16]

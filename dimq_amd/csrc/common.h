@@ -62,6 +62,53 @@ __device__ __forceinline__ uint32_t float_to_f16_bits(float x) {
   return (uint32_t)__builtin_bit_cast(uint16_t, h);
 }
 
+// Two fp32 -> one dword of fp16 (lo in bits 0-15), round to nearest even:
+// one v_cvt_pk_f16_f32.  Magnitudes >= 65520 become inf.
+__device__ __forceinline__ uint32_t f16x2_rne(float lo, float hi) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, h2));
+}
+
+// ---------------------------------------------------------------- fp16 range guard
+// The weight-only kernels round fp32 and bf16 activations to fp16 for the
+// matrix cores.  A tile's fp16 result is kept when (a) some activation of the
+// tile has magnitude >= 2^-7 (fp16 exponent field >= 8: bit 13 or 14 of a
+// half set), so fp16's subnormal step 2^-24 is at most 2^-17 of the tile's
+// largest value, and (b) every accumulator is finite (an activation beyond
+// the fp16 range rounds to inf, so its outputs come out inf or NaN).
+// Otherwise the work-group recomputes the tile in fp32 (exact_tile,
+// gemm_kernel.h).  For (a) threads OR the fp16 dwords they produce into a
+// tracker: the generic kernels over every k step, the pipelined tile kernels
+// over their first k stage only (their main loops are VALU-bound), with a
+// scan of the tile's rows when that stage shows no large value.  fp16
+// activations, and the integer codes of the W4A4 path, are exact in fp16 and
+// are not tracked.
+constexpr uint32_t kRangeBigBits = 0x60006000u;
+
+template <int XT, bool A4 = false>
+constexpr bool range_guarded() {
+  return !A4 && (XT == DIMQ_F32 || XT == DIMQ_BF16);
+}
+
+// Work-group-uniform verdict; every thread of the work-group must call it.
+__device__ __forceinline__ bool tile_needs_exact(uint32_t trk, bool finite) {
+  const int big = __syncthreads_or((trk & kRangeBigBits) != 0u);
+  const int bad = __syncthreads_or(!finite);
+  return !big || bad;
+}
+
+// trk | every dword of o (fp16 pairs).
+__device__ __forceinline__ uint32_t range_track(uint32_t trk, const uint32_t (&o)[8]) {
+  return trk | ((o[0] | o[1]) | (o[2] | o[3])) | ((o[4] | o[5]) | (o[6] | o[7]));
+}
+
+// Wave-level halves of the verdict, for kernels whose waves own disjoint
+// outputs: whether any lane of the wave saw a large activation, and whether
+// every lane's accumulators are finite (both wave-uniform).
+__device__ __forceinline__ bool wave_any(bool v) { return __ballot(v) != 0; }
+
+
 // fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
 __device__ __forceinline__ uint32_t float_to_bf16_bits(float x) {
   uint32_t u = __float_as_uint(x);
@@ -260,9 +307,12 @@ __device__ __forceinline__ float epi1_m(const Epi& e, int64_t off, float v) {
 }
 
 // u4 activation code: clamp(rint(x / s) + zp, 0, 15), IEEE divide
-// (dimq_backend/reference.py:11-21).
+// (dimq_backend/reference.py:11-21); a NaN quotient gives zp, as the
+// reference CUDA kernel's __float2int_rn (0 for NaN) plus zp does
+// (csrc/dimq_common.cuh:17-21), and +-inf clamp to 15 / 0.
 __device__ __forceinline__ int quantize_u4(float x, float s, int zp) {
-  float q = __builtin_rintf(x / s) + (float)zp;
+  const float r = __builtin_rintf(x / s);
+  float q = (r == r ? r : 0.0f) + (float)zp;
   q = q < 0.0f ? 0.0f : q;
   q = q > 15.0f ? 15.0f : q;
   return (int)q;

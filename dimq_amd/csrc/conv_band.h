@@ -89,14 +89,7 @@ __device__ __forceinline__ void band_commit(const HaloArgs& p, int r0, int t, in
   uint32_t in[8][4];
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
-    uint32_t w4[4] = {tk.v[c].x, tk.v[c].y, tk.v[c].z, tk.v[c].w};
-    if (p.x_dt != DIMQ_F16) {
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        w4[k] = to_f16_bits(w4[k] & 0xffffu, p.x_dt) | (to_f16_bits(w4[k] >> 16, p.x_dt) << 16);
-    }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) in[c][k] = w4[k];
+    in[c][0] = tk.v[c].x; in[c][1] = tk.v[c].y; in[c][2] = tk.v[c].z; in[c][3] = tk.v[c].w;
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {

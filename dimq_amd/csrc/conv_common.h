@@ -9,7 +9,7 @@ namespace dimq {
 
 struct HaloArgs {
   const void* x;
-  int x_dt, x_layout;
+  int x_layout;  // fp16 input
   int B, C, H, W, OC, OH, OW;
   int KH, KW, pad_h, pad_w;
   int TH;              // output rows per tile (band)
@@ -31,10 +31,6 @@ struct HaloArgs {
 };
 
 namespace {
-
-__device__ __forceinline__ uint32_t to_f16_bits(uint32_t raw, int dt) {
-  return dt == DIMQ_F16 ? raw : float_to_f16_bits(bf16_bits_to_float(raw));
-}
 
 // Four consecutive outputs of one lane, after the fused epilogue: one 16-byte
 // (fp32) or 8-byte (16-bit) store when `vec`, element stores otherwise.

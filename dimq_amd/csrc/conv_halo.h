@@ -73,14 +73,7 @@ __device__ __forceinline__ void stage_halo(const HaloArgs& p, int b, int ih0, ui
         uint32_t in[8][4];
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
-          uint32_t w4[4] = {v[u][c].x, v[u][c].y, v[u][c].z, v[u][c].w};
-          if (p.x_dt != DIMQ_F16) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-              w4[k] = to_f16_bits(w4[k] & 0xffffu, p.x_dt) | (to_f16_bits(w4[k] >> 16, p.x_dt) << 16);
-          }
-#pragma unroll
-          for (int k = 0; k < 4; ++k) in[c][k] = w4[k];
+          in[c][0] = v[u][c].x; in[c][1] = v[u][c].y; in[c][2] = v[u][c].z; in[c][3] = v[u][c].w;
         }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -116,8 +109,8 @@ __device__ __forceinline__ void stage_halo(const HaloArgs& p, int b, int ih0, ui
       uint32_t a = 0, bb = 0;
       if (ih >= 0 && ih < p.H && iw >= 0 && iw < p.W) {
         const int64_t off = (((int64_t)b * p.C + 2 * c2) * p.H + ih) * p.W + iw;
-        a = to_f16_bits(reinterpret_cast<const uint16_t*>(p.x)[off], p.x_dt);
-        bb = to_f16_bits(reinterpret_cast<const uint16_t*>(p.x)[off + (int64_t)p.H * p.W], p.x_dt);
+        a = reinterpret_cast<const uint16_t*>(p.x)[off];
+        bb = reinterpret_cast<const uint16_t*>(p.x)[off + (int64_t)p.H * p.W];
       }
       *reinterpret_cast<uint32_t*>(&halo[(r * p.IW_t + hc) * p.CP + 2 * c2]) = a | (bb << 16);
     }
@@ -148,15 +141,7 @@ __device__ __forceinline__ void stage_halo(const HaloArgs& p, int b, int ih0, ui
         if (t >= tasks) continue;
         const int c8 = t % (C / 8);
         const int pix = t / (C / 8);
-        uint4 o = v[u];
-        if (p.x_dt != DIMQ_F16) {
-          uint32_t w4[4] = {o.x, o.y, o.z, o.w};
-#pragma unroll
-          for (int k = 0; k < 4; ++k)
-            w4[k] = to_f16_bits(w4[k] & 0xffffu, p.x_dt) | (to_f16_bits(w4[k] >> 16, p.x_dt) << 16);
-          o = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-        }
-        *reinterpret_cast<uint4*>(&halo[pix * p.CP + 8 * c8]) = o;
+        *reinterpret_cast<uint4*>(&halo[pix * p.CP + 8 * c8]) = v[u];
       }
     }
   }

@@ -124,7 +124,7 @@ bool halo_eligible(int64_t C, int64_t KH, int64_t KW, int64_t sh, int64_t sw, in
                    int64_t groups, int64_t OH, int64_t OW, int bits, int x_dtype, int epi_mode_, int y_layout) {
   if (!halo_weight_supported(C, KH, KW, bits)) return false;
   if (!halo_mode_ok(epi_mode_, KH * KW * (C / 16) <= 36, y_layout == DIMQ_NCHW)) return false;
-  if (!(x_dtype == DIMQ_F16 || x_dtype == DIMQ_BF16)) return false;
+  if (x_dtype != DIMQ_F16) return false;  // fp16 staging (other dtypes: the guarded implicit GEMM)
   if (groups != 1 || dh != 1 || dw != 1 || sh != sw || (sh != 1 && sh != 2)) return false;
   return halo_tile_rows(C, KH, KW, sh, OH, OW) > 0;
 }
@@ -138,7 +138,7 @@ int launch_conv_halo(const void* x, int x_dtype, int x_layout, int64_t B, int64_
   p.epi = epi;
   p.acc_scale = acc_scale;
   p.x = x;
-  p.x_dt = x_dtype;
+  if (x_dtype != DIMQ_F16) return set_error(DIMQ_ERR_UNSUPPORTED, "conv halo kernel takes fp16 activations");
   p.x_layout = x_layout;
   p.B = (int)B;
   p.C = (int)C;

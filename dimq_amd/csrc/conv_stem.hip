@@ -39,7 +39,7 @@ namespace dimq {
 
 struct StemArgs {
   const void* x;
-  int x_dt, x_layout;
+  int x_layout;  // fp16 input
   int B, C, H, W, OC, OH, OW;
   int KW, pad_h, pad_w;
   int par, padc;        // pad_w & 1, pad_w + par
@@ -65,11 +65,6 @@ constexpr int kStemThreads = 256;
 constexpr int kStemOutPitch = 68;  // floats per pixel row of the epilogue tile (16-byte aligned, 4 spare)
 constexpr int kStemOutFloats = 32 * kStemOutPitch;
 
-__device__ __forceinline__ uint32_t stem_in_bits(const void* x, int dt, int64_t i) {
-  if (dt == DIMQ_F16) return reinterpret_cast<const uint16_t*>(x)[i];
-  return float_to_f16_bits(load_as_float(x, dt, i));
-}
-
 // One staged pair: input row ih, columns iw0, iw0+1 -> 8 fp16 (slot px*C+c).
 __device__ __forceinline__ uint4 stem_load_pair(const StemArgs& p, int b, int ih, int iw0) {
   uint32_t h[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
@@ -77,7 +72,7 @@ __device__ __forceinline__ uint4 stem_load_pair(const StemArgs& p, int b, int ih
     const int C = p.C;
     if (p.x_layout == DIMQ_NHWC) {
       const int64_t pix = ((int64_t)b * p.H + ih) * p.W + iw0;
-      if (p.x_dt != DIMQ_F32 && iw0 >= 0 && iw0 + 1 < p.W && ((p.W * C) & 1) == 0) {
+      if (iw0 >= 0 && iw0 + 1 < p.W && ((p.W * C) & 1) == 0) {
         // 2C halves = C dwords, 4-byte aligned (iw0 even, W*C even)
         const uint32_t* src = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(p.x) + pix * C);
         uint32_t d[4] = {0u, 0u, 0u, 0u};
@@ -93,14 +88,6 @@ __device__ __forceinline__ uint4 stem_load_pair(const StemArgs& p, int b, int ih
         } else {
           d[0] = src[0];
         }
-        if (p.x_dt == DIMQ_BF16) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const uint32_t lo = float_to_f16_bits(bf16_bits_to_float(d[q] & 0xffffu));
-            const uint32_t hi = float_to_f16_bits(bf16_bits_to_float(d[q] >> 16));
-            d[q] = lo | (hi << 16);
-          }
-        }
         return make_uint4(d[0], d[1], d[2], d[3]);
       }
 #pragma unroll
@@ -109,7 +96,7 @@ __device__ __forceinline__ uint4 stem_load_pair(const StemArgs& p, int b, int ih
         if (iw < 0 || iw >= p.W) continue;
 #pragma unroll
         for (int c = 0; c < 4; ++c)
-          if (c < C) h[px * C + c] = stem_in_bits(p.x, p.x_dt, (pix + px) * C + c);
+          if (c < C) h[px * C + c] = reinterpret_cast<const uint16_t*>(p.x)[(pix + px) * C + c];
       }
     } else {
 #pragma unroll
@@ -118,7 +105,7 @@ __device__ __forceinline__ uint4 stem_load_pair(const StemArgs& p, int b, int ih
         if (iw < 0 || iw >= p.W) continue;
 #pragma unroll
         for (int c = 0; c < 4; ++c)
-          if (c < C) h[px * C + c] = stem_in_bits(p.x, p.x_dt, (((int64_t)b * C + c) * p.H + ih) * p.W + iw);
+          if (c < C) h[px * C + c] = reinterpret_cast<const uint16_t*>(p.x)[(((int64_t)b * C + c) * p.H + ih) * p.W + iw];
       }
     }
   }
@@ -407,9 +394,10 @@ int64_t stem_rows(int64_t KH, int64_t OH, int64_t OW, int np) {
 }  // namespace
 
 bool stem_eligible(int64_t C, int64_t OC, int64_t KH, int64_t KW, int64_t sh, int64_t sw, int64_t pw,
-                   int64_t dh, int64_t dw, int64_t groups, int64_t OH, int64_t OW, int bits, int y_dtype,
-                   const void* x, const void* y, int epi_mode_) {
+                   int64_t dh, int64_t dw, int64_t groups, int64_t OH, int64_t OW, int bits, int x_dtype,
+                   int y_dtype, const void* x, const void* y, int epi_mode_) {
   if (epi_mode_ != kEpiNone && epi_mode_ != kEpiRelu) return false;  // other epilogues: generic kernel
+  if (x_dtype != DIMQ_F16) return false;  // fp16 staging (other dtypes: the guarded generic kernel)
   if (groups != 1 || C < 1 || C > 4 || OC < 1 || OC > 64 || OC % 8 != 0) return false;
   if (sh != 2 || sw != 2 || dh != 1 || dw != 1) return false;
   if (bits < 2 || bits > 8) return false;
@@ -428,7 +416,7 @@ int launch_conv_stem(const void* x, int x_dtype, int x_layout, int64_t B, int64_
   const int np = stem_np(KW, pw);
   StemArgs p{};
   p.x = x;
-  p.x_dt = x_dtype;
+  if (x_dtype != DIMQ_F16) return set_error(DIMQ_ERR_UNSUPPORTED, "conv stem kernel takes fp16 activations");
   p.x_layout = x_layout;
   p.B = (int)B; p.C = (int)C; p.H = (int)H; p.W = (int)W;
   p.OC = (int)OC; p.OH = (int)OH; p.OW = (int)OW;

@@ -164,26 +164,19 @@ extern "C" int dimq_linear_codebook(const void* x, int x_dtype, int64_t M, int64
                                  bias, bias_dtype, N, y, y_dtype, nullptr, 0, DIMQ_ACT_NONE, variant, stream);
 }
 
-// Workspace of dimq_linear_codebook_ex_ws: fp32 activations on the large
-// tiles take the tiles' fp16 form after one conversion pass (the same
-// round-to-nearest conversion the fp32 tiles apply as they stage, so the
-// results are the same bits; measured at cfg1, 1576 x 768 fp32: 32.6 us for
-// the fp32 tile against 25.2 us for the fp16 one); decode shapes (M <= 16)
-// with split k ranges keep their fp32 partial sums there.
+// Workspace of dimq_linear_codebook_ex_ws: the decode shapes (M <= 16)
+// whose k range is split over work-groups keep their fp32 partial sums there.
 extern "C" int64_t dimq_linear_codebook_workspace_bytes(int64_t M, int64_t K, int64_t N, int bits, int x_dtype) {
-  if (M <= 0 || K <= 0 || N <= 0 || !(bits == 2 || bits == 3 || bits == 4)) return 0;
-  if (M <= 16) {
-    GemmArgs p{};
-    p.M = M;
-    p.K = K;
-    p.N = N;
-    p.fast_b = p.vec_a = true;
-    GemvPlan pl;
-    if (!gemv_plan(p, bits, true, pl)) return 0;
-    return (gemv_partial_bytes(p, pl) + 255) / 256 * 256;
-  }
-  if (x_dtype != DIMQ_F32 || M <= 64 || K % 64 != 0) return 0;
-  return (M * K * 2 + 255) / 256 * 256;
+  (void)x_dtype;
+  if (M <= 0 || M > 16 || K <= 0 || N <= 0 || !(bits == 2 || bits == 3 || bits == 4)) return 0;
+  GemmArgs p{};
+  p.M = M;
+  p.K = K;
+  p.N = N;
+  p.fast_b = p.vec_a = true;
+  GemvPlan pl;
+  if (!gemv_plan(p, bits, true, pl)) return 0;
+  return (gemv_partial_bytes(p, pl) + 255) / 256 * 256;
 }
 
 extern "C" int dimq_linear_codebook_ex_ws(const void* x, int x_dtype, int64_t M, int64_t K, const uint8_t* packed_w,
@@ -193,48 +186,21 @@ extern "C" int dimq_linear_codebook_ex_ws(const void* x, int x_dtype, int64_t M,
                                           int activation, int variant, void* workspace, int64_t workspace_bytes,
                                           void* stream) {
   DIMQ_CHECK(workspace_bytes >= 0, "workspace_bytes must be non-negative");
-  if (M >= 1 && M <= 16) return linear_codebook_checked(x, x_dtype, M, K, packed_w, packed_numel, bits, codebook,
-                                                        cb_dtype, cb_rows, cb_size, bias, bias_dtype, N, y, y_dtype,
-                                                        residual, residual_dtype, activation, variant, stream,
-                                                        workspace, workspace_bytes);
-  const int64_t need = dimq_linear_codebook_workspace_bytes(M, K, N, bits, x_dtype);
-  const int mode = epi_mode(Epi{residual, residual_dtype, activation, 0});
-  if (workspace != nullptr && need > 0 && workspace_bytes >= need && aligned(workspace, 16) &&
-      variant != DIMQ_VARIANT_SMALL_M && aligned(packed_w, 16) && aligned(x, 16) &&
-      (mode == kEpiNone || mode == kEpiRelu || mode == kEpiGelu || mode == kEpiRes)) {
-    // argument checks first, as the plain entry point does them
-    DIMQ_CHECK(y_dtype == DIMQ_F32 || y_dtype == DIMQ_F16 || y_dtype == DIMQ_BF16,
-               "linear_codebook output dtype must be fp32, fp16 or bf16");
-    DIMQ_CHECK(is_float_dtype(cb_dtype), "codebook must be floating point");
-    DIMQ_CHECK(bias == nullptr || is_float_dtype(bias_dtype), "bias must be floating point");
-    DIMQ_CHECK(N > 0, "linear dimensions must be positive");
-    DIMQ_CHECK(cb_rows == 1 || cb_rows == N, "codebook must have 1 (per layer) or out_features (per channel) rows");
-    DIMQ_CHECK(cb_size >= 1 && cb_size <= (1 << bits), "codebook rows must hold between 1 and 2^bits entries");
-    DIMQ_CHECK(packed_numel >= (N * K * bits + 7) / 8, "packed_weight is too small for out_features * in_features");
-    DIMQ_CHECK(variant >= DIMQ_VARIANT_AUTO && variant <= DIMQ_VARIANT_MFMA, "unknown kernel variant %d", variant);
-    DIMQ_CHECK(residual == nullptr || is_float_dtype(residual_dtype), "residual must be floating point");
-    DIMQ_CHECK(activation >= DIMQ_ACT_NONE && activation <= DIMQ_ACT_GELU, "unknown activation %d", activation);
-    uint16_t* q = static_cast<uint16_t*>(workspace);
-    const hipStream_t st = as_stream(stream);
-    const int rc = launch_to_f16(x, x_dtype, M * K, q, st);
-    if (rc != DIMQ_OK) return rc;
-    return dimq_linear_codebook_ex(q, DIMQ_F16, M, K, packed_w, packed_numel, bits, codebook, cb_dtype, cb_rows,
-                                   cb_size, bias, bias_dtype, N, y, y_dtype, residual, residual_dtype, activation,
-                                   variant, stream);
-  }
-  return dimq_linear_codebook_ex(x, x_dtype, M, K, packed_w, packed_numel, bits, codebook, cb_dtype, cb_rows, cb_size,
+  const bool decode = M >= 1 && M <= 16;
+  return linear_codebook_checked(x, x_dtype, M, K, packed_w, packed_numel, bits, codebook, cb_dtype, cb_rows, cb_size,
                                  bias, bias_dtype, N, y, y_dtype, residual, residual_dtype, activation, variant,
-                                 stream);
+                                 stream, decode ? workspace : nullptr, decode ? workspace_bytes : 0);
 }
 
 extern "C" int64_t dimq_linear_codebook_act_workspace_bytes(int64_t M, int64_t K) {
   if (M <= 0 || K <= 0) return 0;
-  return (M * K * 2 + 255) / 256 * 256;
+  return (M * K * 4 + 255) / 256 * 256;
 }
 
-// Activations quantized to their nearest activation-codebook centre (as fp16
-// values, one element-wise pass into the workspace), then the weight-codebook
-// tiles on them: the dequantize-then-MFMA form of the weight x activation
+// Activations replaced by their nearest activation-codebook centre in x's
+// dtype (centers[idx].to(x.dtype), quant/dimq.py:217; one element-wise pass
+// into the workspace), then the weight-codebook tiles on them, under their
+// fp16 range guard: the dequantize-then-MFMA form of the weight x activation
 // codebook product.
 extern "C" int dimq_linear_codebook_act(const void* x, int x_dtype, int64_t M, int64_t K, const uint8_t* packed_w,
                                         int64_t packed_numel, int bits, const void* codebook, int cb_dtype,
@@ -250,10 +216,10 @@ extern "C" int dimq_linear_codebook_act(const void* x, int x_dtype, int64_t M, i
   const int64_t need = dimq_linear_codebook_act_workspace_bytes(M, K);
   DIMQ_CHECK(workspace != nullptr && workspace_bytes >= need && aligned(workspace, 16),
              "workspace must be 16-byte aligned and hold dimq_linear_codebook_act_workspace_bytes bytes");
-  uint16_t* q = static_cast<uint16_t*>(workspace);
-  const int rc = launch_act_codebook_f16(x, x_dtype, M * K, act_centers, static_cast<int>(n_act), q, as_stream(stream));
+  const int rc = launch_act_codebook(x, x_dtype, M * K, act_centers, static_cast<int>(n_act), workspace,
+                                     as_stream(stream));
   if (rc != DIMQ_OK) return rc;
-  return dimq_linear_codebook_ex(q, DIMQ_F16, M, K, packed_w, packed_numel, bits, codebook, cb_dtype, cb_rows, cb_size,
+  return dimq_linear_codebook_ex(workspace, x_dtype, M, K, packed_w, packed_numel, bits, codebook, cb_dtype, cb_rows, cb_size,
                                  bias, bias_dtype, N, y, y_dtype, nullptr, 0, DIMQ_ACT_NONE, variant, stream);
 }
 

@@ -12,8 +12,8 @@
 // Per 64-wide k stage:
 //   * activations: raw 16-byte global loads issued one stage ahead into
 //     registers, converted to fp16 in the k-slot order of the weight decoder
-//     (fp16: byte selects; bf16: v_cvt_pkrtz, exact for every bf16 value in
-//     the fp16 range; fp32: round to nearest) and written to a
+//     (fp16: byte selects; bf16 and fp32: round to nearest, under the
+//     range guard of common.h) and written to a
 //     double-buffered LDS tile (row pitch 72 halves: the 16-byte reads of 16
 //     consecutive rows hit distinct bank groups);
 //   * weights: each lane loads its row's 64 packed indices (8*BITS bytes,
@@ -95,7 +95,8 @@ __device__ __forceinline__ uint32_t stage_word(const uint32_t (&c)[2 * BITS], in
   }
 }
 
-// 16 raw activations -> 8 dwords of fp16 pairs in the slot order of BITS.
+// 16 raw activations -> 8 dwords of fp16 pairs in the slot order of BITS
+// (bf16: one round-to-nearest v_cvt_pk_f16_f32 per pair).
 template <int BITS, int XT>
 __device__ __forceinline__ void convert_a16_big(const RawA<XT>& r, uint32_t out[8]) {
   if constexpr (XT == DIMQ_F32) {
@@ -107,8 +108,7 @@ __device__ __forceinline__ void convert_a16_big(const RawA<XT>& r, uint32_t out[
       if constexpr (XT == DIMQ_F16) {
         w[i] = r.w[i];
       } else {
-        const auto h2 = __builtin_amdgcn_cvt_pkrtz(__uint_as_float(r.w[i] << 16), __uint_as_float(r.w[i] & 0xffff0000u));
-        w[i] = __builtin_bit_cast(uint32_t, h2);
+        w[i] = f16x2_rne(__uint_as_float(r.w[i] << 16), __uint_as_float(r.w[i] & 0xffff0000u));
       }
     }
 #pragma unroll
@@ -219,6 +219,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, big_min_waves(BITS, MBLK, NBLK, CON
   const int64_t nk = p.K / kBigKS;
   RawA<XT> ra[A_TASKS];
   uint32_t b0[NBLK][2 * BITS], b1[NBLK][2 * BITS];
+  uint32_t trk = 0;
 
   auto issue_a = [&](int64_t kt) {
     const int64_t k = (kt < nk ? kt : nk - 1) * kBigKS;
@@ -244,11 +245,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, big_min_waves(BITS, MBLK, NBLK, CON
       for (int i = 0; i < A_TASKS; ++i) issue_a16<XT>(p.x, aoff[i] + k, ra[i]);
     }
   };
-  auto commit_a = [&](int buf) {
+  auto commit_a = [&](int buf, bool track = false) {
 #pragma unroll
     for (int i = 0; i < A_TASKS; ++i) {
       uint32_t o[8];
       convert_a16_big<BITS, XT>(ra[i], o);
+      if (range_guarded<XT>() && track) trk = range_track(trk, o);
       uint4* dst = reinterpret_cast<uint4*>(&As[buf][alds[i]]);
       dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
       dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
@@ -315,7 +317,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, big_min_waves(BITS, MBLK, NBLK, CON
   // commit, which waits for them, after the MFMAs.
   issue_a(0);
   issue_b(0, b0);
-  commit_a(0);
+  commit_a(0, true);  // the range guard looks at the first k stage
   __syncthreads();
   int64_t kt = 0;
   for (; kt + 2 <= nk; kt += 2) {
@@ -335,6 +337,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, big_min_waves(BITS, MBLK, NBLK, CON
     __syncthreads();
   }
   if (kt < nk) compute(0, b0);
+
+  if constexpr (range_guarded<XT>()) {
+    if (tile_needs_exact(p, XT, m0, m0 + BM, trk, finite_acc<1>(&acc[0][0], MBLK, NBLK))) {
+      exact_tile_out(p, XT, BITS, m0, m0 + BM, n0, n0 + BN, 0, CONV);
+      return;
+    }
+  }
 
   // epilogue: acc[mb][nb][4j + i] = y[m][n], m = block row m0 + wm*MBLK*32 +
   // mb*32 + col, n = n0 + wn*NBLK*32 + nb*32 + 8j + 4g + i
@@ -459,17 +468,19 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_lds_kernel(const GemmArgs
   const int64_t nk = p.K / kBigKS;
   RawA<XT> ra0[A_TASKS], ra1[A_TASKS];
   uint32_t bq0[2 * BITS], bq1[2 * BITS];
+  uint32_t trk = 0;
   auto issue = [&](int64_t kt, RawA<XT> (&ra)[A_TASKS], uint32_t (&bq)[2 * BITS]) {
     const int64_t k = (kt < nk ? kt : nk - 1) * kBigKS;
 #pragma unroll
     for (int i = 0; i < A_TASKS; ++i) issue_a16<XT>(p.x, aoff[i] + k, ra[i]);
     issue_b_stage<BITS>(p.w, brow, p.K, k, bq);
   };
-  auto commit = [&](int buf, const RawA<XT> (&ra)[A_TASKS], const uint32_t (&bq)[2 * BITS]) {
+  auto commit = [&](int buf, const RawA<XT> (&ra)[A_TASKS], const uint32_t (&bq)[2 * BITS], bool track = false) {
 #pragma unroll
     for (int i = 0; i < A_TASKS; ++i) {
       uint32_t o[8];
       convert_a16_big<BITS, XT>(ra[i], o);
+      if (range_guarded<XT>() && track) trk = range_track(trk, o);
       uint4* dst = reinterpret_cast<uint4*>(&As[buf][alds[i]]);
       dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
       dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
@@ -528,7 +539,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_lds_kernel(const GemmArgs
       ebias[brl] = (p.bias && n0 + brl < p.N) ? load_as_float(p.bias, p.bias_dt, n0 + brl) : 0.0f;
     }
   }
-  commit(0, ra0, bq0);
+  commit(0, ra0, bq0, true);  // the range guard looks at the first k stage
   __syncthreads();
   issue(2, ra0, bq0);
   int64_t kt = 0;
@@ -541,6 +552,13 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_lds_kernel(const GemmArgs
     issue(kt + 4, ra0, bq0);
   }
   if (kt < nk) compute(0);
+
+  if constexpr (range_guarded<XT>()) {
+    if (tile_needs_exact(p, XT, m0, m0 + BM, trk, finite_acc<1>(&acc[0][0], MBLK, NBLK))) {
+      exact_tile_out(p, XT, BITS, m0, m0 + BM, n0, n0 + BN, 0);
+      return;
+    }
+  }
 
   // Epilogue through LDS, in NBLK passes: pass nb parks every wave's column
   // block nb (acc[mb][nb][4j + i] = tile row wm*MBLK*32 + mb*32 + col, column
@@ -701,17 +719,19 @@ __global__ __launch_bounds__(256) void gemm_deep_kernel(const GemmArgs p) {
 
   const int64_t nk = p.K / kBigKS;
   RawA<XT> ra0[A_TASKS], ra1[A_TASKS];
+  uint32_t trk = 0;
 
   auto issue_a = [&](int64_t kt, RawA<XT> (&dst)[A_TASKS]) {
     const int64_t k = (kt < nk ? kt : nk - 1) * kBigKS;
 #pragma unroll
     for (int i = 0; i < A_TASKS; ++i) issue_a16<XT>(p.x, aoff[i] + k, dst[i]);
   };
-  auto commit_a = [&](int buf, const RawA<XT> (&src)[A_TASKS]) {
+  auto commit_a = [&](int buf, const RawA<XT> (&src)[A_TASKS], bool track = false) {
 #pragma unroll
     for (int i = 0; i < A_TASKS; ++i) {
       uint32_t o[8];
       convert_a16_big<BITS, XT>(src[i], o);
+      if (range_guarded<XT>() && track) trk = range_track(trk, o);
       uint4* dst = reinterpret_cast<uint4*>(&As[buf][alds[i]]);
       dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
       dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
@@ -755,7 +775,7 @@ __global__ __launch_bounds__(256) void gemm_deep_kernel(const GemmArgs p) {
   dma_b(2, 2);
   issue_a(0, ra0);
   issue_a(1, ra1);
-  commit_a(0, ra0);  // waits for stage 0 (and the weight stages before it)
+  commit_a(0, ra0, true);  // waits for stage 0 (and the weight stages before it); range guard
   issue_a(2, ra0);
   __syncthreads();
   // steady state, two stages per trip (register sets alternate):
@@ -782,6 +802,13 @@ __global__ __launch_bounds__(256) void gemm_deep_kernel(const GemmArgs p) {
     slot = slot == RING - 1 ? 0 : slot + 1;
   }
   if (kt < nk) compute(0, slot);
+
+  if constexpr (range_guarded<XT>()) {
+    if (tile_needs_exact(p, XT, m0, m0 + BM, trk, finite_acc<1>(acc, MBLK, 1))) {
+      exact_tile_out(p, XT, BITS, m0, m0 + BM, n0, n0 + BN, 0);
+      return;
+    }
+  }
 
   // epilogue: acc[mb][4j + i] = y[m][n], m = m0 + mb*32 + col, n = n0 + 32*wave + 8j + 4g + i
   const bool vec = p.ldy % 4 == 0;

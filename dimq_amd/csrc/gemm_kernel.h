@@ -105,6 +105,123 @@ __device__ __forceinline__ void gather16_conv(const GemmArgs& p, int xt, int64_t
   }
 }
 
+// ---- fp32 recompute of a tile outside the fp16 range (common.h, range guard) ----
+// Index at bit position `bit` of the packed stream (fields LSB first).
+__device__ __forceinline__ uint32_t packed_index(const uint8_t* w, int64_t bit, int bits) {
+  const uint8_t* b = w + (bit >> 3);
+  const int sh = static_cast<int>(bit & 7);
+  uint32_t v = b[0] >> sh;
+  if (sh + bits > 8) v |= (uint32_t)b[1] << (8 - sh);
+  return v & ((1u << bits) - 1u);
+}
+
+// sum over k in [k0, k1) of x[m, k] * C[n][idx(n, k)] for the outputs
+// m in [m0, m1), n in [n0, n1) of group z (clipped to M and N), every
+// activation and centre read in its own dtype and accumulated in fp32 in k
+// order; store(m, n, sum) per output.  One output per thread at a time: this
+// runs only for tiles the fp16 matrix path cannot represent.
+// Convolutions read the conv_kcrs stream (k = (ci, kh, kw)), or with
+// tapmajor the NHWC implicit GEMM's re-packed stream (k = (kh, kw, c)).
+// Thread t0 of the tstride cooperating threads takes outputs t0, t0 + tstride, ...
+template <class Store>
+__device__ void exact_tile(const GemmArgs& p, int xt, int bits, int64_t m0, int64_t m1, int64_t n0, int64_t n1,
+                           int64_t k0, int64_t k1, int64_t z, bool tapmajor, int t0, int tstride, Store store) {
+  m1 = m1 < p.M ? m1 : p.M;
+  n1 = n1 < p.N ? n1 : p.N;
+  k1 = k1 < p.K ? k1 : p.K;
+  const int64_t nm = m1 - m0, nn = n1 - n0;
+  if (nm <= 0 || nn <= 0) return;
+  const int64_t cbase = z * p.cICg;
+  for (int64_t o = t0; o < nm * nn; o += tstride) {
+    const int64_t m = m0 + o / nn, n = n0 + o % nn;
+    const int64_t row = z * p.N + n;
+    const int64_t cbrow = p.cb_rows == 1 ? 0 : row;
+    float acc = 0.0f;
+    for (int64_t k = k0; k < k1; k += 16) {
+      float v[16];
+      if (p.conv && tapmajor) {
+        const int64_t hw = p.cOH * p.cOW;
+        const int64_t b = m / hw;
+        const int r = static_cast<int>(m - b * hw);
+        const int oh = r / static_cast<int>(p.cOW), ow = r - oh * static_cast<int>(p.cOW);
+        for (int j = 0; j < 16; ++j) {
+          v[j] = 0.0f;
+          if (k + j >= k1) continue;
+          const int tap = static_cast<int>((k + j) / p.cC);
+          const int64_t c = k + j - tap * p.cC;
+          const int kh = tap / p.cKW, kw = tap - kh * p.cKW;
+          const int ih = oh * p.csh - p.cph + kh * p.cdh, iw = ow * p.csw - p.cpw + kw * p.cdw;
+          if (ih >= 0 && ih < p.cH && iw >= 0 && iw < p.cW)
+            v[j] = load_as_float(p.x, xt, ((b * p.cH + ih) * p.cW + iw) * p.cC + c);
+        }
+      } else if (p.conv) {
+        gather16_conv(p, xt, m, k, cbase, v);
+      } else {
+        for (int j = 0; j < 16; ++j) v[j] = k + j < k1 ? load_as_float(p.x, xt, m * p.ldx + k + j) : 0.0f;
+      }
+      for (int j = 0; j < 16 && k + j < k1; ++j) {
+        const int i = static_cast<int>(packed_index(p.w, (row * p.K + k + j) * bits, bits));
+        const float c = i < p.cb_size ? load_as_float(p.cb, p.cb_dt, cbrow * p.cb_size + i) : 0.0f;
+        acc = fmaf(v[j], c, acc);
+      }
+    }
+    store(m, n, acc);
+  }
+}
+
+// exact_tile over the whole k range by the work-group (or, with t0 / tstride,
+// by one wave), through the kernels' epilogue.
+__device__ __forceinline__ void exact_tile_out(const GemmArgs& p, int xt, int bits, int64_t m0, int64_t m1,
+                                            int64_t n0, int64_t n1, int64_t z, bool tapmajor = false,
+                                            int t0 = -1, int tstride = 0) {
+  if (t0 < 0) {
+    t0 = threadIdx.x;
+    tstride = blockDim.x;
+  }
+  exact_tile(p, xt, bits, m0, m1, n0, n1, 0, p.K, z, tapmajor, t0, tstride, [&](int64_t m, int64_t n, float v) {
+    const float b = p.bias ? load_as_float(p.bias, p.bias_dt, z * p.N + n) : 0.0f;
+    const int64_t o = out_offset(p, m, z * p.N + n);
+    store_from_float(p.y, p.y_dt, o, epi1(p.epi, o, v * p.acc_scale + b));
+  });
+}
+
+// Every accumulator of a tile row is finite, checked on the first W entries
+// of each of the n vectors given (one per row block; their column block
+// holds every row of the lane).  One column per row is enough: a non-finite
+// activation makes every column of its row inf or NaN (the fp16 weights are
+// finite, and sums of fp16 products cannot overflow fp32).
+template <int W, class V>
+__device__ __forceinline__ bool finite_acc(const V* a, int n, int stride) {
+  bool ok = true;
+#pragma unroll
+  for (int i = 0; i < n; ++i)
+#pragma unroll
+    for (int j = 0; j < W; ++j) ok &= __builtin_isfinite(a[i * stride][j]);
+  return ok;
+}
+
+// Verdict of the range guard for kernels that track only their first k
+// stage (trk): keep the fp16 tile when every accumulator is finite and an
+// activation of magnitude >= 2^-7 was seen, in that stage or, failing that,
+// by a scan of the tile's rows (Linear; a convolution's tile goes to the fp32
+// recompute).  Work-group-uniform; every thread must call it.
+__device__ __forceinline__ bool tile_needs_exact(const GemmArgs& p, int xt, int64_t m0, int64_t m1, uint32_t trk,
+                                                 bool finite) {
+  const int bad = __syncthreads_or(!finite);
+  const int big = __syncthreads_or((trk & kRangeBigBits) != 0u);
+  if (bad) return true;
+  if (big) return false;
+  if (p.conv) return true;
+  m1 = m1 < p.M ? m1 : p.M;
+  bool seen = false;
+  const int64_t n = (m1 > m0 ? m1 - m0 : 0) * p.K;
+  for (int64_t i = threadIdx.x; i < n && !seen; i += blockDim.x) {
+    const int64_t m = m0 + i / p.K;
+    seen = fabsf(load_as_float(p.x, xt, m * p.ldx + (i - (m - m0) * p.K))) >= 0x1p-7f;
+  }
+  return !__syncthreads_or(seen);
+}
+
 // ---- activation tile loader --------------------------------------------------
 template <int XT>
 __device__ __forceinline__ void load16_as_float(const void* x, int64_t off, bool vec, int64_t kvalid, float v[16]) {
@@ -150,9 +267,10 @@ __device__ __forceinline__ void load16_as_float(const void* x, int64_t off, bool
 
 // 16 activations starting at (row gm, column k0) -> 8 dwords of fp16 pairs in
 // the slot order of BITS.
+// The fp16 dwords are ORed into trk (fp32/bf16 weight-only: range guard).
 template <int BITS, int XT, bool A4>
 __device__ __forceinline__ void load_a_group(const GemmArgs& p, int64_t gm, int64_t k0, int64_t cbase,
-                                             uint32_t out[8]) {
+                                             uint32_t out[8], uint32_t& trk) {
   float v[16];
   if (p.conv) {
     if (gm < p.M && k0 < p.K) {
@@ -181,6 +299,10 @@ __device__ __forceinline__ void load_a_group(const GemmArgs& p, int64_t gm, int6
   }
 #pragma unroll
   for (int d = 0; d < 8; ++d) out[d] = h[kperm16(BITS, 2 * d)] | (h[kperm16(BITS, 2 * d + 1)] << 16);
+  if constexpr (range_guarded<XT, A4>()) {
+#pragma unroll
+    for (int d = 0; d < 8; ++d) trk |= out[d];
+  }
 }
 
 // ---- tile scheduling -------------------------------------------------------------
@@ -327,6 +449,7 @@ __global__ __launch_bounds__(256) void gemm_cb_kernel(const GemmArgs p) {
   const int64_t nk = (p.K + kKM - 1) / kKM;
   uint32_t a_st[A_PER_T][8];
   uint32_t bc[NB][BITS], bn[NB][BITS];
+  uint32_t trk = 0;
 
   auto load_a = [&](int64_t kt) {
 #pragma unroll
@@ -334,7 +457,7 @@ __global__ __launch_bounds__(256) void gemm_cb_kernel(const GemmArgs p) {
       const int task = tid + 256 * i;
       if (A_TASKS % 256 == 0 || task < A_TASKS) {
         const int m = task >> 3, kg = task & 7;
-        load_a_group<BITS, XT, A4>(p, m0 + m, kt * kKM + 16 * kg, cbase, a_st[i]);
+        load_a_group<BITS, XT, A4>(p, m0 + m, kt * kKM + 16 * kg, cbase, a_st[i], trk);
       }
     }
   };
@@ -392,6 +515,13 @@ __global__ __launch_bounds__(256) void gemm_cb_kernel(const GemmArgs p) {
         for (int w = 0; w < BITS; ++w) bc[nb][w] = bn[nb][w];
     }
     __syncthreads();
+  }
+
+  if constexpr (range_guarded<XT, A4>()) {
+    if (tile_needs_exact(trk, finite_acc<4>(&acc[0][0], MB, NB))) {
+      exact_tile_out(p, XT, BITS, m0, m0 + BM, nt * (4 * WN), (nt + 1) * (4 * WN), blockIdx.z);
+      return;
+    }
   }
 
   // epilogue: lane holds rows 4g..4g+3 of column `col` of each 16x16 block
@@ -478,13 +608,14 @@ __global__ __launch_bounds__(256) void gemm_cb8_kernel(const GemmArgs p) {
   const int64_t nk = (p.K + kKM - 1) / kKM;
   uint32_t a_st[A_PER_T][8];
   uint32_t bc[NB][BITS], bn[NB][BITS];
+  uint32_t trk = 0;
   auto load_a = [&](int64_t kt) {
 #pragma unroll
     for (int i = 0; i < A_PER_T; ++i) {
       const int task = tid + 256 * i;
       if (A_TASKS % 256 == 0 || task < A_TASKS) {
         const int m = task >> 3, kg = task & 7;
-        load_a_group<BITS, XT, false>(p, m0 + m, kt * kKM + 16 * kg, cbase, a_st[i]);
+        load_a_group<BITS, XT, false>(p, m0 + m, kt * kKM + 16 * kg, cbase, a_st[i], trk);
       }
     }
   };
@@ -550,6 +681,13 @@ __global__ __launch_bounds__(256) void gemm_cb8_kernel(const GemmArgs p) {
     __syncthreads();
   }
 
+  if constexpr (range_guarded<XT>()) {
+    if (tile_needs_exact(trk, finite_acc<4>(&acc[0][0], MB, NB))) {
+      exact_tile_out(p, XT, BITS, m0, m0 + BM, n0, n0 + ROWS, blockIdx.z);
+      return;
+    }
+  }
+
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     const int64_t n = nw0 + nb * 16 + col;
@@ -600,13 +738,14 @@ __global__ __launch_bounds__(WPW * 64) void gemv_cb_kernel(const GemmArgs p) {
   floatx4 acc = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
   uint32_t bc[BITS];
   uint32_t av[16];  // 32 fp16 activations in slot order
+  uint32_t trk = 0;
   auto load_step = [&](int64_t kt, uint32_t (&bdst)[BITS], uint32_t (&adst)[16]) {
     load_b_chunk<BITS>(p, n, n, kt * kKM + 32 * g, bdst);
     const int64_t k0 = kt * kKM + 32 * g;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       uint32_t t[8];
-      load_a_group<BITS, XT, false>(p, arow ? (int64_t)col : p.M, k0 + 16 * h, 0, t);
+      load_a_group<BITS, XT, false>(p, arow ? (int64_t)col : p.M, k0 + 16 * h, 0, t, trk);
 #pragma unroll
       for (int d = 0; d < 8; ++d) adst[8 * h + d] = t[d];
     }
@@ -618,6 +757,12 @@ __global__ __launch_bounds__(WPW * 64) void gemv_cb_kernel(const GemmArgs p) {
       const u32x4 a4 = {av[4 * s], av[4 * s + 1], av[4 * s + 2], av[4 * s + 3]};
       const half8 bf = decode_sub<BITS>(bc, s, cb);
       acc = mfma16x16x32(__builtin_bit_cast(half8, a4), bf, acc);
+    }
+  }
+  if constexpr (range_guarded<XT>()) {
+    if (tile_needs_exact(trk, finite_acc<4>(&acc, 1, 1))) {
+      exact_tile_out(p, XT, BITS, 0, 16, static_cast<int64_t>(blockIdx.x) * 16, static_cast<int64_t>(blockIdx.x) * 16 + 16, 0);
+      return;
     }
   }
   red[wave][lane] = acc;
@@ -771,17 +916,19 @@ __global__ __launch_bounds__(256) void gemm_fast_kernel(const GemmArgs p) {
   // two raw activation register sets (even / odd steps) and two weight sets
   RawA<XT> ra0[A_PER_T], ra1[A_PER_T];
   uint32_t b0[NB][BITS], b1[NB][BITS];
+  uint32_t trk = 0;
 
   auto issue_a = [&](int64_t kt, RawA<XT> (&dst)[A_PER_T]) {
     const int64_t k = (kt < nk ? kt : nk - 1) * kKM;
 #pragma unroll
     for (int i = 0; i < A_PER_T; ++i) issue_a16<XT>(p.x, aoff[i] + k, dst[i]);
   };
-  auto commit_a = [&](int buf, const RawA<XT> (&src)[A_PER_T]) {
+  auto commit_a = [&](int buf, const RawA<XT> (&src)[A_PER_T], bool track = false) {
 #pragma unroll
     for (int i = 0; i < A_PER_T; ++i) {
       uint32_t o[8];
       convert_a16<BITS, XT, A4>(src[i], p.act_scale, p.act_zp, o);
+      if (range_guarded<XT, A4>() && track) trk = range_track(trk, o);
       uint4* dst = reinterpret_cast<uint4*>(&As[buf][alds[i]]);
       dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
       dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
@@ -819,7 +966,7 @@ __global__ __launch_bounds__(256) void gemm_fast_kernel(const GemmArgs p) {
   issue_b(0, b0);
   issue_a(1, ra1);
   issue_b(1, b1);
-  commit_a(0, ra0);
+  commit_a(0, ra0, true);  // the range guard looks at the first k step
   issue_a(2, ra0);
   __syncthreads();
   int64_t kt = 0;
@@ -838,6 +985,13 @@ __global__ __launch_bounds__(256) void gemm_fast_kernel(const GemmArgs p) {
     __syncthreads();
   }
   if (kt < nk) compute(0, b0);
+
+  if constexpr (range_guarded<XT, A4>()) {
+    if (tile_needs_exact(p, XT, m0, m0 + BM, trk, finite_acc<4>(&acc[0][0], MB, NB))) {
+      exact_tile_out(p, XT, BITS, m0, m0 + BM, n0, n0 + 4 * WN, 0);
+      return;
+    }
+  }
 
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
@@ -887,8 +1041,8 @@ int launch_prepare(const uint8_t* src, int64_t OC, int64_t C, int64_t KH, int64_
 
 // conv_stem.hip
 bool stem_eligible(int64_t C, int64_t OC, int64_t KH, int64_t KW, int64_t sh, int64_t sw, int64_t pw,
-                   int64_t dh, int64_t dw, int64_t groups, int64_t OH, int64_t OW, int bits, int y_dtype,
-                   const void* x, const void* y, int epi_mode);
+                   int64_t dh, int64_t dw, int64_t groups, int64_t OH, int64_t OW, int bits, int x_dtype,
+                   int y_dtype, const void* x, const void* y, int epi_mode);
 int launch_conv_stem(const void* x, int x_dtype, int x_layout, int64_t B, int64_t C, int64_t H, int64_t W,
                      const uint8_t* w, int64_t w_bytes, int bits, const void* cb, int cb_dtype, int64_t cb_rows,
                      int64_t cb_size, const void* bias, int bias_dtype, int64_t OC, int64_t KH, int64_t KW,
@@ -897,11 +1051,9 @@ int launch_conv_stem(const void* x, int x_dtype, int x_layout, int64_t B, int64_
 
 // quant.hip: W4A4 activations as the fp16 integers a - zp (out 16-byte aligned)
 int launch_quantize_a4_f16(const void* x, int x_dtype, int64_t n, float s, int zp, uint16_t* out, hipStream_t st);
-// quant.hip: activations -> fp16 values of their nearest activation-codebook centre
-int launch_act_codebook_f16(const void* x, int x_dtype, int64_t n, const float* centers, int K, uint16_t* out,
-                            hipStream_t st);
-// quant.hip: fp32 (fp64) activations -> fp16, round to nearest even (out 16-byte aligned)
-int launch_to_f16(const void* x, int x_dtype, int64_t n, uint16_t* out, hipStream_t st);
+// quant.hip: activations -> their nearest activation-codebook centre, in x's dtype
+int launch_act_codebook(const void* x, int x_dtype, int64_t n, const float* centers, int K, void* out,
+                        hipStream_t st);
 
 // gemm.hip
 int gemm_pick_tile(int64_t M, int64_t N, int variant);

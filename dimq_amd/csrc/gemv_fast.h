@@ -44,6 +44,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_stream_kernel(const GemmArg
   constexpr int NW = R / 32 * BITS;  // packed words of a run
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
   __shared__ floatx4 red[NCB == 1 ? 4 : 1][64];
+  __shared__ uint32_t wbig[4];  // range guard: a wave staged an activation >= 2^-7
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -60,6 +61,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_stream_kernel(const GemmArg
   constexpr int gpr = krange / 16;                   // 16-element groups per row
   const int groups = rows * gpr;
 
+  uint32_t trk = 0;  // range guard (common.h)
   // codebook row of the lane's column (issued first: its wait does not wait for the streams)
   float cbv[E];
   load_cb_row<E>(p.cb, p.cb_dt, p.cb_rows == 1 ? 0 : n, p.cb_size, cbv);
@@ -80,6 +82,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_stream_kernel(const GemmArg
       const int m = gi / gpr;
       uint32_t o[8];
       convert_a16_big<BITS, XT>(ra[u], o);
+      if constexpr (range_guarded<XT>()) trk = range_track(trk, o);
       uint4* dst = reinterpret_cast<uint4*>(xs + m * pitch + gemv_pos((gi - m * gpr) * 16));
       dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
       dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
@@ -109,6 +112,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_stream_kernel(const GemmArg
   CodebookRegs<BITS> cb;
   const int e = planes_from_lds<BITS, false>(cbv, cb, cb);
   const float colscale = ldexpf(p.acc_scale, -e);
+  constexpr bool kGuard = range_guarded<XT>();
+  if constexpr (kGuard) {
+    const bool any = wave_any((trk & kRangeBigBits) != 0u);
+    if (lane == 0) wbig[wave] = any;
+  }
   lds_barrier();  // the weight runs stay in flight
 
   // the run, 8 indices per MFMA, consumed in issue order
@@ -127,9 +135,35 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_stream_kernel(const GemmArg
     }
   }
 
+  // range guard, per wave (its outputs: NCB = 4 its 16 columns; NCB = 1 the
+  // partial sums of its k quarter): recomputed in fp32 when the work-group
+  // staged no activation >= 2^-7 or an accumulator of the wave is not finite
+  bool exact = false;
+  if constexpr (kGuard) {
+    exact = !(wbig[0] | wbig[1] | wbig[2] | wbig[3]) || wave_any(!finite_acc<4>(&acc, 1, 1));
+    if (exact && NCB == 4) {
+      const int64_t c0 = n0, c1 = n0 + 16;
+      if (KS > 1) {
+        exact_tile(p, XT, BITS, 0, 16, c0, c1, kw0, kw0 + krange, 0, false, lane, 64,
+                   [&](int64_t m, int64_t nn, float v) {
+                     partial[(static_cast<int64_t>(blockIdx.y) * p.M + m) * p.N + nn] = v * p.acc_scale;
+                   });
+      } else {
+        exact_tile_out(p, XT, BITS, 0, 16, c0, c1, 0, false, lane, 64);
+      }
+      return;
+    }
+  }
+
   // acc[i] = partial y[4g + i][n0 + col]
   if constexpr (NCB == 1) {
-    red[wave][lane] = acc;
+    if (exact) {  // this wave's k quarter in fp32, in the accumulator layout, times 2^e (colscale follows)
+      const int64_t kq = kw0 + static_cast<int64_t>(4 * wave) * R;
+      exact_tile(p, XT, BITS, 0, 16, n0, n0 + 16, kq, kq + 4 * R, 0, false, lane, 64,
+                 [&](int64_t m, int64_t nn, float v) { red[wave][(m >> 2) * 16 + (nn - n0)][m & 3] = ldexpf(v, e); });
+    } else {
+      red[wave][lane] = acc;
+    }
     __syncthreads();
     if (wave != 0) return;
     acc = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];

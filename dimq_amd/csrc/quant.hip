@@ -41,10 +41,7 @@ __global__ __launch_bounds__(kThreads) void quantize_act_kernel(const void* __re
 // over these values times s equals sum_k C[w] * (s * (a - zp)) up to fp32
 // summation order.  8 activations per thread, one 16-byte store; VEC: x is
 // 16-byte aligned (vector loads of the 8 inputs).
-// A4 = false: plain fp32/fp64 -> fp16 conversion (round to nearest even, the
-// rounding the GEMM kernels apply to fp32 activations themselves), for the
-// weight-only Linear with fp32 activations on the fp16 large tiles.
-template <int XT, bool VEC, bool A4 = true>
+template <int XT, bool VEC>
 __global__ __launch_bounds__(kThreads) void quantize_a4_f16_kernel(const void* __restrict__ x, int64_t n, float s,
                                                                    int zp, uint16_t* __restrict__ out) {
   const int64_t base = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * 8;
@@ -70,19 +67,14 @@ __global__ __launch_bounds__(kThreads) void quantize_a4_f16_kernel(const void* _
     }
     uint32_t h[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if constexpr (A4) {
-        h[j] = float_to_f16_bits((float)(quantize_u4(v[2 * j], s, zp) - zp)) |
-               (float_to_f16_bits((float)(quantize_u4(v[2 * j + 1], s, zp) - zp)) << 16);
-      } else {
-        h[j] = float_to_f16_bits(v[2 * j]) | (float_to_f16_bits(v[2 * j + 1]) << 16);
-      }
-    }
+    for (int j = 0; j < 4; ++j)
+      h[j] = float_to_f16_bits((float)(quantize_u4(v[2 * j], s, zp) - zp)) |
+             (float_to_f16_bits((float)(quantize_u4(v[2 * j + 1], s, zp) - zp)) << 16);
     *reinterpret_cast<uint4*>(out + base) = make_uint4(h[0], h[1], h[2], h[3]);
   } else {
     for (int64_t i = base; i < n; ++i) {
       const float v = load_as_float(x, XT, i);
-      out[i] = (uint16_t)float_to_f16_bits(A4 ? (float)(quantize_u4(v, s, zp) - zp) : v);
+      out[i] = (uint16_t)float_to_f16_bits((float)(quantize_u4(v, s, zp) - zp));
     }
   }
 }
@@ -146,12 +138,12 @@ __global__ __launch_bounds__(kThreads) void hard_quantize_kernel(const void* __r
 
 // Activation codebook (the QAT wrapper's activation_centers,
 // quant/dimq_wrapper.py:80-85 via hard_quantize_weight, quant/dimq.py:197-221):
-// out = fp16(C_a[argmin_c (x - C_a[c])^2]) with hard_quantize_kernel's torch
+// out = C_a[argmin_c (x - C_a[c])^2] in x's dtype, with hard_quantize_kernel's torch
 // argmin semantics (first minimum; a NaN distance wins, the first NaN kept).
 // 4 activations per thread, the K <= 256 centres in LDS.
-__global__ __launch_bounds__(kThreads) void act_codebook_f16_kernel(const void* __restrict__ x, int dt, int64_t n,
-                                                                    const float* __restrict__ centers, int K,
-                                                                    uint16_t* __restrict__ out) {
+__global__ __launch_bounds__(kThreads) void act_codebook_kernel(const void* __restrict__ x, int dt, int64_t n,
+                                                                const float* __restrict__ centers, int K,
+                                                                void* __restrict__ out) {
   __shared__ float c_s[256];
   for (int j = threadIdx.x; j < K; j += kThreads) c_s[j] = centers[j];
   __syncthreads();
@@ -179,19 +171,19 @@ __global__ __launch_bounds__(kThreads) void act_codebook_f16_kernel(const void* 
         have = true;
       }
     }
-    out[e] = (uint16_t)float_to_f16_bits(c_s[best]);
+    store_from_float(out, dt, e, c_s[best]);  // centers[idx].to(x.dtype)
   }
 }
 
 }  // namespace
 
-// Launches act_codebook_f16_kernel (K in [1, 256]).
-int launch_act_codebook_f16(const void* x, int x_dtype, int64_t n, const float* centers, int K, uint16_t* out,
-                            hipStream_t st) {
+// Launches act_codebook_kernel (K in [1, 256]); out holds n elements of x_dtype.
+int launch_act_codebook(const void* x, int x_dtype, int64_t n, const float* centers, int K, void* out,
+                        hipStream_t st) {
   if (n == 0) return DIMQ_OK;
   const int64_t blocks = (n + kThreads * 4 - 1) / (kThreads * 4);
   DIMQ_CHECK(blocks < (int64_t)1 << 31, "activations too large for one launch");
-  hipLaunchKernelGGL(act_codebook_f16_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, st, x, x_dtype,
+  hipLaunchKernelGGL(act_codebook_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, st, x, x_dtype,
                      n, centers, K, out);
   return check_launch("activation codebook");
 }
@@ -218,21 +210,6 @@ int launch_quantize_a4_f16(const void* x, int x_dtype, int64_t n, float s, int z
   return check_launch("quantize activations (W4A4 fast path)");
 }
 
-// Launches the A4 = false form: fp32 (or fp64) activations -> fp16.
-int launch_to_f16(const void* x, int x_dtype, int64_t n, uint16_t* out, hipStream_t st) {
-  if (n == 0) return DIMQ_OK;
-  const dim3 grid(static_cast<unsigned>(((n + 7) / 8 + kThreads - 1) / kThreads));
-  if (x_dtype == DIMQ_F32 && aligned(x, 16))
-    hipLaunchKernelGGL((quantize_a4_f16_kernel<DIMQ_F32, true, false>), grid, dim3(kThreads), 0, st, x, n, 1.0f, 0,
-                       out);
-  else if (x_dtype == DIMQ_F32)
-    hipLaunchKernelGGL((quantize_a4_f16_kernel<DIMQ_F32, false, false>), grid, dim3(kThreads), 0, st, x, n, 1.0f, 0,
-                       out);
-  else
-    hipLaunchKernelGGL((quantize_a4_f16_kernel<DIMQ_F64, false, false>), grid, dim3(kThreads), 0, st, x, n, 1.0f, 0,
-                       out);
-  return check_launch("activations to fp16");
-}
 }  // namespace dimq
 
 using namespace dimq;

@@ -186,9 +186,14 @@ int dimq_build_product_table_grouped(const void* codebook, int cb_dtype, int64_t
  * codebook [cb_rows, cb_size] with cb_rows in {1 (per layer), N (per output
  * channel)} and cb_size <= 2^bits; x_dtype/y_dtype in {F32, F16, BF16};
  * bias (nullable, any float dtype) [N]; fp32 accumulation.
- * Inputs are rounded to fp16 for the matrix cores (exact for fp16 and for
- * bf16 values within the fp16 range; fp32 is rounded to nearest); the
- * codebook is scaled per row by a power of two before rounding to fp16. */
+ * Activations are rounded to nearest fp16 for the matrix cores (exact for
+ * fp16, and for bf16 values within the fp16 range); the codebook is scaled
+ * per row by a power of two before rounding to fp16.  Range guard: a tile
+ * whose fp32/bf16 activations hold a value beyond the fp16 range (any
+ * accumulator inf or NaN), or none of magnitude >= 2^-7, is recomputed in
+ * fp32 from the activations and centres in their own dtypes, so results stay
+ * within fp32 rounding of the reference for every input range (such tiles
+ * run far slower than the matrix path). */
 int dimq_linear_codebook(const void* x, int x_dtype, int64_t M, int64_t K, const uint8_t* packed_w,
                          int64_t packed_numel, int bits, const void* codebook, int cb_dtype, int64_t cb_rows,
                          int64_t cb_size, const void* bias, int bias_dtype, int64_t N, void* y, int y_dtype,
@@ -246,17 +251,14 @@ int dimq_linear_codebook_ex(const void* x, int x_dtype, int64_t M, int64_t K, co
 /* Workspace form of dimq_linear_codebook_ex (same arguments, checks and
  * results, plus a caller-owned device workspace; the library allocates
  * nothing).  With a 16-byte aligned workspace of at least
- * dimq_linear_codebook_workspace_bytes:
- *  - fp32 activations on the large-tile shapes (M > 64, K % 64 == 0, bits
- *    2-4) are converted to fp16 once (round to nearest even, the conversion
- *    the fp32 tiles apply while staging) and the fp16 tiles run: the same
- *    output bits, measured 8 % faster at X fp32 [1576,768];
- *  - decode shapes (4 < M <= 16, bits 2-4, N % 64 == 0, K % 1024 == 0) split
- *    the k range over work-groups of 64 columns and keep the fp32 partial sums
- *    there (a second, small kernel adds them), so the activations are read
- *    by 64 columns per work-group instead of 16.
- * Otherwise it is dimq_linear_codebook_ex.  The workspace is written on
- * `stream`; calls sharing one must be ordered on it. */
+ * dimq_linear_codebook_workspace_bytes, decode shapes (M <= 16, bits 2-4;
+ * 4 < M with N % 64 == 0 and K % 1024 == 0, or K % 4096 == 0) split the k
+ * range over work-groups and keep the fp32 partial sums there (a second,
+ * small kernel adds them): more work-groups stream the weights, and for
+ * M > 4 the activations are read by 64 columns per work-group instead of 16.
+ * Otherwise it is dimq_linear_codebook_ex (x_dtype is not used by the query;
+ * the query returns 0 for M > 16).  The workspace is written on `stream`;
+ * calls sharing one must be ordered on it. */
 int64_t dimq_linear_codebook_workspace_bytes(int64_t M, int64_t K, int64_t N, int bits, int x_dtype);
 int dimq_linear_codebook_ex_ws(const void* x, int x_dtype, int64_t M, int64_t K, const uint8_t* packed_w,
                                int64_t packed_numel, int bits, const void* codebook, int cb_dtype, int64_t cb_rows,
@@ -270,9 +272,11 @@ int dimq_linear_codebook_ex_ws(const void* x, int x_dtype, int64_t M, int64_t K,
  * quant/dimq.py:197-221): y = Q(x) W_hat^T + b with
  * Q(x) = C_a[argmin_c (x - C_a[c])^2] (torch argmin semantics: first minimum,
  * NaN distances win).  act_centers: n_act <= 256 fp32 centres on the device.
- * The quantized activations go to the caller's workspace as fp16 (at least
+ * The quantized activations go to the caller's workspace in x's dtype, as
+ * the reference's centers[idx].to(x.dtype) (at least
  * dimq_linear_codebook_act_workspace_bytes, 16-byte aligned), then the
- * weight-codebook tiles run on them. */
+ * weight-codebook tiles run on them (fp16 matrix path with the fp32 recompute
+ * of tiles outside the fp16 range, as dimq_linear_codebook). */
 int64_t dimq_linear_codebook_act_workspace_bytes(int64_t M, int64_t K);
 int dimq_linear_codebook_act(const void* x, int x_dtype, int64_t M, int64_t K, const uint8_t* packed_w,
                              int64_t packed_numel, int bits, const void* codebook, int cb_dtype, int64_t cb_rows,

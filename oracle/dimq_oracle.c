@@ -107,15 +107,22 @@ void dimq_oracle_hard_quantize(const float* w, int64_t rows, int64_t row_len,
   }
 }
 
-/* Uniform affine u4 activation quantization: dimq_backend/reference.py:11-21,
- * q = clamp(round_half_even(x / s) + zp, 0, 15), IEEE fp32 divide. */
+/* Uniform affine u4 activation code: dimq_backend/reference.py:11-21,
+ * q = clamp(round_half_even(x / s) + zp, 0, 15), IEEE fp32 divide.  A NaN
+ * quotient gives zp: the reference CUDA kernel computes
+ * __float2int_rn(x / s) + zp (csrc/dimq_common.cuh:17-21), and the PTX
+ * conversion maps NaN to 0; +-inf and other out-of-range quotients clamp to
+ * 15 / 0 as the torch reference does. */
+static int quant_u4(float x, float s, int zp) {
+  float r = rintf(x / s);
+  float q = (r == r ? r : 0.0f) + (float)zp;
+  if (q < 0.0f) q = 0.0f;
+  if (q > 15.0f) q = 15.0f;
+  return (int)q;
+}
+
 void dimq_oracle_quantize_act_u4(const float* x, int64_t n, float s, int zp, uint8_t* out) {
-  for (int64_t i = 0; i < n; ++i) {
-    float q = rintf(x[i] / s) + (float)zp;
-    if (q < 0.0f) q = 0.0f;
-    if (q > 15.0f) q = 15.0f;
-    out[i] = (uint8_t)q;
-  }
+  for (int64_t i = 0; i < n; ++i) out[i] = (uint8_t)quant_u4(x[i], s, zp);
 }
 
 /* Product table: dimq_backend/reference.py:32-44 and
@@ -162,12 +169,10 @@ void dimq_oracle_linear_lut(const float* x, int64_t M, int64_t N, int64_t K, con
     for (int64_t n = 0; n < N; ++n) {
       float acc = 0.0f;
       for (int64_t k = 0; k < K; ++k) {
-        float q = rintf(x[m * K + k] / s) + (float)zp;
-        if (q < 0.0f) q = 0.0f;
-        if (q > 15.0f) q = 15.0f;
+        int q = quant_u4(x[m * K + k], s, zp);
         int64_t i = n * K + k;
         int w = (packed_w[i >> 1] >> ((i & 1) * 4)) & 15;
-        acc += table[w * 16 + (int)q];
+        acc += table[w * 16 + q];
       }
       if (bias) acc += bias[n];
       y[m * N + n] = acc;
@@ -200,12 +205,10 @@ void dimq_oracle_conv2d_lut(const float* x, int B, int C, int H, int W, const ui
               for (int kw = 0; kw < KW; ++kw) {
                 int iw = ow * sw + kw * dw - pw;
                 if (iw < 0 || iw >= W) continue;
-                float q = rintf(x[(((int64_t)b * C + ci) * H + ih) * W + iw] / s) + (float)zp;
-                if (q < 0.0f) q = 0.0f;
-                if (q > 15.0f) q = 15.0f;
+                int q = quant_u4(x[(((int64_t)b * C + ci) * H + ih) * W + iw], s, zp);
                 int64_t i = (((int64_t)co * ICg + cig) * KH + kh) * KW + kw;
                 int w = (packed_w[i >> 1] >> ((i & 1) * 4)) & 15;
-                acc += table[w * 16 + (int)q];
+                acc += table[w * 16 + q];
               }
             }
           }

@@ -146,6 +146,7 @@ def test_quantize_activation_golden_and_dtypes(gpu):
         q = ops.quantize_activation_u4(torch.tensor(c["x"], device=gpu), c["scale"], c["zp"])
         assert q.cpu().tolist() == c["q"], c["source"]
     x = torch.randn(3, 1001, generator=_gen(2)) * 2
+    x[0, :7] = torch.tensor([float("nan"), float("inf"), float("-inf"), 1e30, -1e30, float("nan"), 3e9])
     for dt in (torch.float32, torch.float16, torch.bfloat16, torch.float64):
         q = ops.quantize_activation_u4(x.to(dt).to(gpu), 0.2, 7)
         assert q.shape == x.shape
@@ -186,14 +187,19 @@ def test_linear_lut_vs_oracle(gpu, M, N, K, xdt):
     ops = _ops()
     announce(f"linear_lut M={M} N={N} K={K} {xdt}")
     g = _gen(M * 7 + N)
-    x = torch.randn(M, K, generator=g).to(xdt)
+    x = torch.randn(M, K, generator=g)
+    # non-finite activations: NaN codes as zp, +-inf clamp (both contribute like any code)
+    x.view(-1)[torch.randint(0, x.numel(), (3,), generator=g)] = torch.tensor([float("nan"), float("inf"),
+                                                                                 float("-inf")])
+    x = x.to(xdt)
     idx = torch.randint(0, 16, (N, K), generator=g, dtype=torch.uint8)
     cb = torch.linspace(-0.5, 0.5, 16) + 0.01 * torch.randn(16, generator=g)
     bias = torch.randn(N, generator=g)
     packed = torch.from_numpy(oracle.pack_bits(idx, 4))
     y = ops.dimq_linear_lut(x.to(gpu), packed.to(gpu), cb.to(gpu), 0.2, 7, bias.to(gpu), N, K)
     ref = oracle.linear_lut(x.float(), packed, cb, 0.2, 7, bias, N, K)
-    torch.testing.assert_close(y.cpu(), torch.from_numpy(ref), rtol=1e-5, atol=1e-5)
+    exact = _a4_levels(x, 0.2, 7) @ cb.double()[idx.long()].T + bias.double()
+    _a4_exact_check(y, ref, exact, K)
 
 
 def test_linear_lut_leading_dims_and_errors(gpu):
@@ -417,10 +423,9 @@ def test_linear_codebook_gemv_fast(gpu, bits, M, N, K, xdt):
 
 
 @pytest.mark.parametrize("act", [None, "gelu"])
-def test_linear_codebook_fp32_pass_same_bits(gpu, act):
-    """fp32 activations on the large tiles: the workspace entry point converts them in one fp32 -> fp16
-    pass (round to nearest even, the rounding the fp32 tiles apply while staging) and runs the fp16
-    tiles; the plain entry point stages fp32 in the tiles.  Both outputs must be the same bits."""
+def test_linear_codebook_ex_ws_large_m_same_bits(gpu, act):
+    """Above the decode shapes the workspace entry point needs no workspace (the query returns 0) and gives
+    the plain entry point's bits, with or without a workspace passed."""
     from dimq_amd import _C
     g = _gen(91)
     M, N, K = 1576, 384, 768
@@ -430,21 +435,20 @@ def test_linear_codebook_fp32_pass_same_bits(gpu, act):
     cbg, pg = cb.to(gpu), packed.to(gpu)
     act_id = {None: 0, "gelu": 2}[act]
     s = torch.cuda.current_stream().cuda_stream
-    ws_bytes = _C.lib.dimq_linear_codebook_workspace_bytes(M, K, N, 4, _C.F32)
-    assert ws_bytes >= M * K * 2
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=gpu)
-    y_pass = torch.empty(M, N, device=gpu)
+    assert _C.lib.dimq_linear_codebook_workspace_bytes(M, K, N, 4, _C.F32) == 0
+    ws = torch.empty(M * K * 2, dtype=torch.uint8, device=gpu)
+    y_ws = torch.empty(M, N, device=gpu)
     y_direct = torch.empty(M, N, device=gpu)
     rc = _C.lib.dimq_linear_codebook_ex_ws(x.data_ptr(), _C.F32, M, K, pg.data_ptr(), pg.numel(), 4, cbg.data_ptr(),
-                                           _C.F32, N, 16, bias.data_ptr(), _C.F32, N, y_pass.data_ptr(), _C.F32,
-                                           None, 0, act_id, 0, ws.data_ptr(), ws_bytes, s)
+                                           _C.F32, N, 16, bias.data_ptr(), _C.F32, N, y_ws.data_ptr(), _C.F32,
+                                           None, 0, act_id, 0, ws.data_ptr(), ws.numel(), s)
     assert rc == 0, _C.lib.dimq_last_error()
     rc = _C.lib.dimq_linear_codebook_ex(x.data_ptr(), _C.F32, M, K, pg.data_ptr(), pg.numel(), 4, cbg.data_ptr(),
                                         _C.F32, N, 16, bias.data_ptr(), _C.F32, N, y_direct.data_ptr(), _C.F32,
                                         None, 0, act_id, 0, s)
     assert rc == 0, _C.lib.dimq_last_error()
     torch.cuda.synchronize()
-    assert torch.equal(y_pass, y_direct)
+    assert torch.equal(y_ws, y_direct)
 
 
 def test_linear_codebook_cfg1_shape(gpu):

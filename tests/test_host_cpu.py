@@ -78,20 +78,19 @@ def test_w4a4_workspace_sizes(capi):
 def test_linear_workspace_sizes_and_act_codebook_errors(capi):
     lib = capi.lib
     up = lambda b: (b + 255) // 256 * 256
-    # fp32 activations on the large-tile shapes get an fp16 copy; nothing else does
+    # only the decode shapes (M <= 16) use a workspace; every dtype converts inside the tiles
     ws = lib.dimq_linear_codebook_workspace_bytes
-    assert ws(1576, 768, 3072, 4, capi.F32) == up(1576 * 768 * 2)
+    assert ws(1576, 768, 3072, 4, capi.F32) == 0
     assert ws(1576, 768, 3072, 4, capi.BF16) == 0
-    assert ws(64, 768, 3072, 4, capi.F32) == 0     # small tiles
-    assert ws(1576, 100, 3072, 4, capi.F32) == 0   # K % 64 != 0
-    assert ws(1576, 768, 3072, 8, capi.F32) == 0   # 8-bit tiles
+    assert ws(17, 4096, 4096, 3, capi.BF16) == 0
     # decode GEMV, 4 < M <= 16: fp32 partial sums of the k splits (k ranges of 1024)
     assert ws(16, 4096, 4096, 3, capi.BF16) == up(4 * 16 * 4096 * 4)
     assert ws(9, 8192, 192, 2, capi.F16) == up(8 * 9 * 192 * 4)
     assert ws(16, 4096, 4000, 3, capi.BF16) == 0   # N % 64 != 0: one k range per work-group
-    assert ws(4, 4096, 4096, 3, capi.BF16) == 0    # M <= 4: one k range per work-group
+    assert ws(4, 4096, 4096, 3, capi.BF16) == 0    # M <= 4, K 4096: one k range per work-group
+    assert ws(4, 8192, 4096, 3, capi.BF16) == up(2 * 4 * 4096 * 4)  # M <= 4: k ranges of 4096
     assert ws(16, 4096, 4096, 8, capi.BF16) == 0
-    assert lib.dimq_linear_codebook_act_workspace_bytes(300, 768) == up(300 * 768 * 2)
+    assert lib.dimq_linear_codebook_act_workspace_bytes(300, 768) == up(300 * 768 * 4)
     assert lib.dimq_linear_codebook_act_workspace_bytes(0, 768) == 0
     args = [None, capi.F32, 4, 64, None, 128, 4, None, capi.F32, 1, 16]
     tail = [None, capi.F32, 8, None, capi.F32, 0, None, 0, None]

@@ -119,6 +119,18 @@ def test_actquant_matches_torch_round_half_even():
         assert np.array_equal(oracle.quantize_act_u4(x, s, zp), want.numpy())
 
 
+def test_actquant_nan_inf_semantics():
+    """+-inf and out-of-range quotients clamp like the torch reference (reference.py:11-21); a NaN gives zp,
+    as the reference CUDA kernel's __float2int_rn(NaN) = 0 plus zp (csrc/dimq_common.cuh:17-21) -- torch leaves
+    NaN's uint8 cast unspecified, so the CUDA kernel is the anchor there."""
+    x = torch.tensor([float("inf"), float("-inf"), 1e30, -1e30, 3.0e9, -3.0e9])
+    for s, zp in ((0.2, 7), (2.0 ** -3, 8), (1.0, 0), (0.5, 15)):
+        want = torch.clamp(torch.round(x / float(s)) + zp, 0, 15).to(torch.uint8)
+        assert np.array_equal(oracle.quantize_act_u4(x, s, zp), want.numpy())
+        q = oracle.quantize_act_u4(np.array([float("nan"), 1.0, float("nan")], np.float32), s, zp)
+        assert q[0] == zp and q[2] == zp
+
+
 # ---------------------------------------------------------------- product table
 def test_product_table_golden():
     c = _load("product_table_vectors.json")[0]

@@ -8,7 +8,7 @@ Default run: the two halves of the BASELINE metric on one JSON line.
 * ``models.vit_b16``: BASELINE configs[3], the ViT-B/16 bs64 forward with its
   48 Linears 4-bit, in images/s with the MFMA roofline over the forward's
   FLOPs and the dequantized fp32 model timed on the host beside it.
-Single workloads: ``--config cfg1|cfg2|cfg5|codec|vit|resnet18|w4a4_linear|w4a4_conv``.
+Single workloads: ``--config cfg1|cfg2|cfg5|codec|vit|resnet18|w4a4_linear|w4a4_conv|w4a4_linear_q|w4a4_conv_q``.
 
 Timing: inputs are resident in HBM before the timed region; R buffer sets
 (> 512 MB in total, so the 256 MB MALL cannot serve repeats) are rotated; the
@@ -327,12 +327,16 @@ def make_copy(dev, rotations):
     )
 
 
-def make_w4a4(dev, rotations, op="linear"):
+def make_w4a4(dev, rotations, op="linear", chained=False):
     """The reference's own W4A4 ops (dimq::linear_lut / dimq::conv2d_lut) at the cfg1 / cfg2 shapes.
 
     One 16-entry per-layer fp16 codebook (the packed exporter's format,
     dimq_backend/export.py:167,217), u4 activations with scale/zero point;
     y fp32.  One step = one op call (activation quantization pass + GEMM/conv).
+    chained: the layer inside a chain of W4A4 layers -- its input arrives as the
+    fp16 codes a - zp from the layer before, and it writes the next layer's
+    codes (ReLU, then u4 quantization fused into its epilogue); the conv's
+    kernel-layout weight is prepared once, as a loaded layer holds it.
     """
     from dimq_amd import ops
     from dimq_amd.codebook import assign_indices
@@ -354,6 +358,14 @@ def make_w4a4(dev, rotations, op="linear"):
             return ops.dimq_linear_lut(xs[i], packed, cb_dev, scale, zp, bias, N, K)
 
         x_bytes, y_bytes = M * K * 4, M * N * 4
+        if chained:
+            xqs = [ops.quantize_activation_f16(x, scale, zp) for x in xs]
+
+            def step(i):
+                return ops.dimq_linear_lut_q(xqs[i], packed, cb_dev, scale, bias, N, K, activation="relu",
+                                             out_act=(0.125, 3))
+
+            x_bytes, y_bytes = M * K * 2, M * N * 2
         flops = 2.0 * M * N * K
         full = M
 
@@ -365,6 +377,9 @@ def make_w4a4(dev, rotations, op="linear"):
         def check():
             import oracle
             ref = oracle.linear_lut(xs[0].cpu(), packed.cpu(), cb16.float(), scale, zp, b, N, K)
+            if chained:  # the same kernels with a float output
+                return oracle.rel_err(ops.dimq_linear_lut_q(xqs[0], packed, cb_dev, scale, bias, N, K),
+                                      torch.from_numpy(ref))
             return oracle.rel_err(step(0), torch.from_numpy(ref))
 
         workload = ("reference W4A4 linear_lut at the cfg1 shape: X fp32 [1576,768], W [3072,768] 4-bit, one 16-entry "
@@ -380,6 +395,15 @@ def make_w4a4(dev, rotations, op="linear"):
             return ops.dimq_conv2d_lut(xs[i], packed, cb_dev, scale, zp, None, shape, (1, 1), (1, 1), (1, 1), 1)
 
         x_bytes, y_bytes = 32 * 64 * 56 * 56 * 2, 32 * 64 * 56 * 56 * 4
+        if chained:
+            xqs = [ops.quantize_activation_f16(x, scale, zp) for x in xs]
+            prep = ops.prepare_conv_weight(packed, 4, shape)
+
+            def step(i):
+                return ops.dimq_conv2d_lut_q(xqs[i], packed, cb_dev, scale, None, shape, 1, 1,
+                                             prepared_weight=prep, activation="relu", out_act=(0.125, 3))
+
+            y_bytes = 32 * 64 * 56 * 56 * 2
         flops = 2.0 * 32 * 56 * 56 * 64 * 64 * 9
         full = 32
 
@@ -392,15 +416,23 @@ def make_w4a4(dev, rotations, op="linear"):
             import oracle
             ref = oracle.conv2d_lut(xs[0].cpu().float(), packed.cpu(), cb16.float(), scale, zp, None, shape, 1, 1, 1,
                                     1)
+            if chained:  # the same kernels with a float output
+                return oracle.rel_err(ops.dimq_conv2d_lut_q(xqs[0], packed, cb_dev, scale, None, shape, 1, 1,
+                                                            prepared_weight=prep), torch.from_numpy(ref))
             return oracle.rel_err(step(0), torch.from_numpy(ref))
 
         workload = ("reference W4A4 conv2d_lut at the cfg2 shape: x fp16 [32,64,56,56] (ReLU N(0,1)), W [64,64,3,3] "
                     "4-bit, one 16-entry fp16 codebook, u4 activations (scale 0.25, zp 8), stride 1, pad 1, y fp32 NCHW")
         extra = {"global_batch": 32, "in_shape": [32, 64, 56, 56], "weight_shape": list(shape), "bits": 4,
                  "codebook": "per_layer_fp16", "op": "conv2d_lut"}
+    if chained:
+        workload = (workload.replace("reference W4A4 ", "chained W4A4 ") +
+                    "; input as fp16 codes a - zp from the previous layer, output the next layer's fp16 codes "
+                    "(ReLU, scale 0.125, zp 3) from the fused epilogue")
+        extra = dict(extra, op=extra["op"] + "_q", chained=True)
     alg_bytes = x_bytes + y_bytes + packed.numel() + 32
     return dict(
-        name=f"w4a4_{op}", workload=workload, step=step, flops=flops, alg_bytes=alg_bytes, bound="hbm",
+        name=f"w4a4_{op}" + ("_q" if chained else ""), workload=workload, step=step, flops=flops, alg_bytes=alg_bytes, bound="hbm",
         dtype="fp16", unit="TFLOP/s", per_step_units=flops / 1e12, cpu_step=cpu_step, cpu_full_batch=full,
         check=check, extra_config=extra, per_set_bytes=x_bytes + y_bytes,
         cpu_desc="the reference's CPU path: u4 activations and W_hat = C[idx] dequantized, then torch CPU fp32 "
@@ -412,7 +444,9 @@ FIXED_ROTATIONS = {"vit": 4, "resnet18": 4}
 WORKLOADS = {"cfg2": make_cfg2, "cfg1": make_cfg1, "cfg5": make_cfg5, "codec": make_codec, "copy": make_copy,
              "vit": make_vit, "resnet18": make_resnet18,
              "w4a4_linear": lambda dev, r: make_w4a4(dev, r, "linear"),
-             "w4a4_conv": lambda dev, r: make_w4a4(dev, r, "conv")}
+             "w4a4_conv": lambda dev, r: make_w4a4(dev, r, "conv"),
+             "w4a4_linear_q": lambda dev, r: make_w4a4(dev, r, "linear", chained=True),
+             "w4a4_conv_q": lambda dev, r: make_w4a4(dev, r, "conv", chained=True)}
 
 
 # ---------------------------------------------------------------------------

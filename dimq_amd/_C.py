@@ -65,6 +65,11 @@ _SIGS = {
     "dimq_conv2d_lut_workspace_bytes": (_i64, [_i64] * 9 + [_int]),
     "dimq_conv2d_lut_ws": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _int, _i64, _dbl, _i64, _vp,
                                   _int, _i64] + [_i64] * 11 + [_vp, _vp, _i64, _vp]),
+    "dimq_quantize_activation_f16": (_int, [_vp, _int, _i64, _dbl, _i64, _vp, _vp]),
+    "dimq_linear_lut_q": (_int, [_vp, _i64, _vp, _i64, _vp, _int, _i64, _dbl, _vp, _int, _i64, _i64, _i64, _int,
+                                 _dbl, _i64, _vp, _int, _vp]),
+    "dimq_conv2d_lut_q": (_int, [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _int, _i64, _dbl, _vp,
+                                 _int, _i64] + [_i64] * 11 + [_int, _dbl, _i64, _vp, _int, _vp]),
     "dimq_layer_norm": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp, _int, _dbl, _vp, _vp]),
     "dimq_max_pool2d_nhwc": (_int, [_vp, _int] + [_i64] * 10 + [_vp, _vp]),
     "dimq_pack_bits": (_int, [_vp, _i64, _int, _vp, _vp]),
@@ -408,6 +413,73 @@ def linear_codebook_act_impl(x, packed_w, codebook, bits, act_centers, bias, out
                                             out_features, _ptr(y), _dtype(y), int(variant), _ptr(ws),
                                             0 if ws is None else ws.numel(), _stream(xc.device)))
     return y.view(*x.shape[:-1], out_features)
+
+
+# ---------------------------------------------------------------------------
+# chained W4A4 layers: activations as the fp16 integers a - zp between layers
+def quantize_activation_f16_impl(x, act_scale, act_zp):
+    _require_cuda(x, "quantize_activation expects CUDA input")
+    xc = x.contiguous()
+    out = torch.empty(xc.shape, dtype=torch.float16, device=xc.device)
+    with torch.cuda.device(xc.device):
+        _check(lib.dimq_quantize_activation_f16(_ptr(xc), _dtype(xc), xc.numel(), float(act_scale), int(act_zp),
+                                                _ptr(out), _stream(xc.device)))
+    return out
+
+
+def _q_out(out_act, out_dtype):
+    if out_act is None:
+        return 0.0, 0, (torch.float32 if out_dtype is None else out_dtype)
+    s, zp = out_act
+    if out_dtype not in (None, torch.float16):
+        raise RuntimeError("a quantized output is written as fp16 codes")
+    return float(s), int(zp), torch.float16
+
+
+def linear_lut_q_impl(xq, packed_w, codebook, act_scale, bias, out_features, in_features, activation=0,
+                      out_act=None, out_dtype=None):
+    _require_cuda(xq, "linear_lut_q expects CUDA input")
+    if xq.dtype != torch.float16:
+        raise RuntimeError("linear_lut_q expects the fp16 activation codes a - zp")
+    if xq.dim() == 0 or xq.size(-1) != in_features:
+        raise RuntimeError("input last dimension must equal in_features")
+    xc = xq.contiguous()
+    pw = packed_w.contiguous().view(-1)
+    cb = codebook.contiguous()
+    b, bp, bdt, bn = _bias_args(bias, out_features, "out_features")
+    qs, qzp, odt = _q_out(out_act, out_dtype)
+    M = xc.numel() // in_features if in_features else 0
+    y = torch.empty((M, out_features), dtype=odt, device=xc.device)
+    with torch.cuda.device(xc.device):
+        _check(lib.dimq_linear_lut_q(_ptr(xc), M, _ptr(pw), pw.numel(), _ptr(cb), _dtype(cb), cb.numel(),
+                                     float(act_scale), bp, bdt, bn, out_features, in_features, int(activation), qs,
+                                     qzp, _ptr(y), _dtype(y), _stream(xc.device)))
+    return y.view(*xq.shape[:-1], out_features)
+
+
+def conv2d_lut_q_impl(xq, packed_w, codebook, act_scale, bias, out_channels, in_channels_per_group, kernel_h,
+                      kernel_w, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w, groups, prepared_w=None,
+                      activation=0, out_act=None, out_dtype=None):
+    _require_cuda(xq, "conv2d_lut_q expects CUDA input")
+    if xq.dtype != torch.float16 or xq.dim() != 4:
+        raise RuntimeError("conv2d_lut_q expects NCHW fp16 activation codes a - zp")
+    xc = xq.contiguous()
+    B, C, H, W = xc.shape
+    pw = packed_w.contiguous().view(-1)
+    cb = codebook.contiguous()
+    b, bp, bdt, bn = _bias_args(bias, out_channels, "out_channels")
+    qs, qzp, odt = _q_out(out_act, out_dtype)
+    OH = (H + 2 * pad_h - dilation_h * (kernel_h - 1) - 1) // stride_h + 1
+    OW = (W + 2 * pad_w - dilation_w * (kernel_w - 1) - 1) // stride_w + 1
+    y = torch.empty((B, out_channels, OH, OW), dtype=odt, device=xc.device)
+    pr = None if prepared_w is None else prepared_w.contiguous()
+    with torch.cuda.device(xc.device):
+        _check(lib.dimq_conv2d_lut_q(_ptr(xc), B, C, H, W, _ptr(pw), pw.numel(), _ptr(pr),
+                                     0 if pr is None else pr.numel(), _ptr(cb), _dtype(cb), cb.numel(),
+                                     float(act_scale), bp, bdt, bn, out_channels, in_channels_per_group, kernel_h,
+                                     kernel_w, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w, groups,
+                                     int(activation), qs, qzp, _ptr(y), _dtype(y), _stream(xc.device)))
+    return y
 
 
 def prepare_conv_weight_impl(packed_w, bits, out_channels, in_channels, kernel_h, kernel_w):

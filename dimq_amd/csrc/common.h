@@ -186,6 +186,12 @@ struct Epi {
   int res_dt;
   int act;      // enum dimq_activation
   int res_vec;  // residual 16-byte aligned: vector loads where y's stores are
+  // next layer's activation quantization (quant != 0): the value becomes the
+  // fp16 integer q - qzp, q = clamp(rint(v / qs) + qzp, 0, 15), stored into
+  // an fp16 y -- the input form of the W4A4 kernels
+  float qs = 1.0f;
+  int qzp = 0;
+  int quant = 0;
 };
 
 // GELU(v) = 0.5 v (1 + erf(v / sqrt 2)) with erf from Abramowitz & Stegun
@@ -206,9 +212,46 @@ __device__ __forceinline__ float act_apply(float v, int act) {
   return v;
 }
 
+__device__ __forceinline__ int quantize_u4(float x, float s, int zp);
+
+__device__ __forceinline__ float epi_quant(const Epi& e, float v) {
+  return (float)(quantize_u4(v, e.qs, e.qzp) - e.qzp);
+}
+
+// N values -> their codes q - zp (as quantize_u4), with one near-tie test for
+// the whole group: t = v * RN(1/s) rounded and clamped with v_med3; a lane
+// with a value within 2^-15 of a tie, a NaN / inf, or a scale whose
+// reciprocal is subnormal redoes its values with quantize_u4.
+template <int N>
+__device__ __forceinline__ void u4_codes(float (&v)[N], float s, int zp) {
+  const float rcp = 1.0f / s;
+  const float lo = (float)(-zp), hi = (float)(15 - zp);
+  bool exact = !(fabsf(rcp) >= 0x1p-126f);
+  float c[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float t = v[i] * rcp;
+    const float r = __builtin_rintf(t);
+    exact |= !(fabsf(fabsf(t - r) - 0.5f) > 0x1p-15f);  // near a tie, or NaN / inf
+    c[i] = __builtin_amdgcn_fmed3f(r, lo, hi);
+  }
+  if (__builtin_expect(exact, 0)) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) c[i] = (float)(quantize_u4(v[i], s, zp) - zp);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = c[i];
+}
+
+template <int N>
+__device__ __forceinline__ void epi_quant_n(const Epi& e, float (&v)[N]) {
+  u4_codes<N>(v, e.qs, e.qzp);
+}
+
 __device__ __forceinline__ float epi1(const Epi& e, int64_t off, float v) {
   if (e.res) v += load_as_float(e.res, e.res_dt, off);
-  return act_apply(v, e.act);
+  v = act_apply(v, e.act);
+  return e.quant ? epi_quant(e, v) : v;
 }
 
 // Residual of N (a multiple of 4) consecutive outputs.  For 16-bit residuals
@@ -271,6 +314,7 @@ __device__ __forceinline__ void epi_apply(const Epi& e, const ResPairs<N>* r, in
 #pragma unroll
     for (int i = 0; i < N; ++i) v[i] = act_apply(v[i], e.act);
   }
+  if (e.quant) epi_quant_n<N>(e, v);
 }
 
 template <int N>
@@ -282,9 +326,9 @@ __device__ __forceinline__ void epiN(const Epi& e, int64_t off, float (&v)[N], b
 // a kernel without epilogue carries none of its code): residual flag | act.
 // Combinations a kernel is not instantiated for run on the generic kernels,
 // whose epilogue is the runtime one above.
-constexpr int kEpiNone = 0, kEpiRelu = 1, kEpiGelu = 2, kEpiRes = 4, kEpiResRelu = 5;
+constexpr int kEpiNone = 0, kEpiRelu = 1, kEpiGelu = 2, kEpiRes = 4, kEpiResRelu = 5, kEpiQuant = 8;
 
-inline int epi_mode(const Epi& e) { return (e.res ? kEpiRes : 0) | e.act; }
+inline int epi_mode(const Epi& e) { return (e.res ? kEpiRes : 0) | e.act | (e.quant ? kEpiQuant : 0); }
 
 template <int MODE, int N>
 __device__ __forceinline__ void epi_m(const Epi& e, const ResPairs<N>* r, int64_t off, bool vec, float (&v)[N]) {
@@ -296,6 +340,7 @@ __device__ __forceinline__ void epi_m(const Epi& e, const ResPairs<N>* r, int64_
 #pragma unroll
     for (int i = 0; i < N; ++i) v[i] = gelu_erf(v[i]);
   }
+  if constexpr ((MODE & kEpiQuant) != 0) epi_quant_n<N>(e, v);
 }
 
 template <int MODE>
@@ -303,15 +348,45 @@ __device__ __forceinline__ float epi1_m(const Epi& e, int64_t off, float v) {
   if constexpr ((MODE & kEpiRes) != 0) v += load_as_float(e.res, e.res_dt, off);
   if constexpr ((MODE & 3) == kEpiRelu) v = v < 0.0f ? 0.0f : v;
   if constexpr ((MODE & 3) == kEpiGelu) v = gelu_erf(v);
+  if constexpr ((MODE & kEpiQuant) != 0) v = epi_quant(e, v);
   return v;
+}
+
+// Epilogue of the quantized-activation W4A4 ops: activation, then (out_act_scale
+// > 0) the next layer's activation quantization into an fp16 y.
+inline int lut_q_epilogue(int activation, double out_act_scale, int64_t out_act_zp, int y_dtype, Epi& epi) {
+  DIMQ_CHECK(activation >= DIMQ_ACT_NONE && activation <= DIMQ_ACT_GELU, "unknown activation %d", activation);
+  epi = Epi{};
+  epi.act = activation;
+  if (out_act_scale > 0.0) {
+    DIMQ_CHECK(out_act_zp >= 0 && out_act_zp <= 15, "out_act_zero_point must be in [0, 15]");
+    DIMQ_CHECK(y_dtype == DIMQ_F16, "a quantized output (out_act_scale > 0) is written as fp16 codes");
+    epi.quant = 1;
+    epi.qs = static_cast<float>(out_act_scale);
+    epi.qzp = static_cast<int>(out_act_zp);
+  } else {
+    DIMQ_CHECK(y_dtype == DIMQ_F32 || y_dtype == DIMQ_F16 || y_dtype == DIMQ_BF16,
+               "output dtype must be fp32, fp16 or bf16");
+  }
+  return DIMQ_OK;
 }
 
 // u4 activation code: clamp(rint(x / s) + zp, 0, 15), IEEE divide
 // (dimq_backend/reference.py:11-21); a NaN quotient gives zp, as the
 // reference CUDA kernel's __float2int_rn (0 for NaN) plus zp does
 // (csrc/dimq_common.cuh:17-21), and +-inf clamp to 15 / 0.
+//
+// The quotient is formed as t = x * RN(1/s): two roundings of 2^-24
+// relative put t within 2^-17.9 of RN(x / s) whenever |x / s| <= 17, so both
+// round to the same integer unless t lies within 2^-15 of a tie (then the
+// IEEE quotient is taken); beyond 17 both clamp alike.  NaN, inf and a
+// subnormal reciprocal also take the IEEE quotient.  The codes are those of
+// the plain division; the divide runs only for the rare near-tie lanes.
 __device__ __forceinline__ int quantize_u4(float x, float s, int zp) {
-  const float r = __builtin_rintf(x / s);
+  const float rcp = 1.0f / s;  // uniform over a kernel: computed once
+  const float t = x * rcp;
+  float r = __builtin_rintf(t);
+  if (!(fabsf(fabsf(t - r) - 0.5f) > 0x1p-15f) || !(fabsf(rcp) >= 0x1p-126f)) r = __builtin_rintf(x / s);
   float q = (r == r ? r : 0.0f) + (float)zp;
   q = q < 0.0f ? 0.0f : q;
   q = q > 15.0f ? 15.0f : q;

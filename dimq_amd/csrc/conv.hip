@@ -266,6 +266,53 @@ extern "C" int dimq_conv2d_lut_ws(const void* x, int x_dtype, int64_t B, int64_t
   return gemm_dispatch(p, 4, x_dtype, true, kTile64x32, st);
 }
 
+// Quantized-activation form of conv2d_lut: xq holds the input as the fp16
+// integers a - zp (NCHW), y is NCHW.  With a prepared weight (the 4-bit
+// LDS-halo layout of dimq_conv2d_prepare_weight) the halo kernels run where
+// the shape allows; otherwise the generic implicit GEMM.
+extern "C" int dimq_conv2d_lut_q(const uint16_t* xq, int64_t B, int64_t C, int64_t H, int64_t W,
+                                 const uint8_t* packed_w, int64_t packed_numel, const uint32_t* prepared_w,
+                                 int64_t prepared_words, const void* codebook, int cb_dtype, int64_t cb_numel,
+                                 double act_scale, const void* bias, int bias_dtype, int64_t bias_numel,
+                                 int64_t out_channels, int64_t in_channels_per_group, int64_t kernel_h,
+                                 int64_t kernel_w, int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                                 int64_t dilation_h, int64_t dilation_w, int64_t groups, int activation,
+                                 double out_act_scale, int64_t out_act_zp, void* y, int y_dtype, void* stream) {
+  DIMQ_CHECK(cb_dtype == DIMQ_F16, "conv2d_lut_q takes the fp16 codebook of the packed export");
+  DIMQ_CHECK(cb_numel == 16, "codebook must have 16 entries for W4");
+  DIMQ_CHECK(act_scale > 0.0, "act_scale must be positive");
+  const ConvShape s = make_shape(B, C, H, W, out_channels, in_channels_per_group, kernel_h, kernel_w, stride_h,
+                                 stride_w, pad_h, pad_w, dilation_h, dilation_w, groups);
+  int rc = check_conv(s);
+  if (rc != DIMQ_OK) return rc;
+  DIMQ_CHECK(packed_numel >= (s.OC * s.ICg * s.KH * s.KW + 1) / 2,
+             "packed_weight is too small for requested conv weight shape");
+  if (bias) DIMQ_CHECK(bias_numel == out_channels, "bias numel must equal out_channels");
+  DIMQ_CHECK(bias == nullptr || is_float_dtype(bias_dtype), "bias must be floating point");
+  Epi epi;
+  rc = lut_q_epilogue(activation, out_act_scale, out_act_zp, y_dtype, epi);
+  if (rc != DIMQ_OK) return rc;
+  if (s.B * s.OC * s.OH * s.OW == 0) return DIMQ_OK;
+  const hipStream_t st = as_stream(stream);
+  const float sc = static_cast<float>(act_scale);
+  const int64_t hw = (prepared_w && s.groups == 1) ? halo_part_words(s.OC, s.C, s.KH, s.KW, 4) : 0;
+  if (prepared_w) DIMQ_CHECK(prepared_words >= hw, "prepared weight buffer is too small");
+  if (hw > 0 && aligned(xq, 16) &&
+      halo_eligible(s.C, s.KH, s.KW, s.sh, s.sw, s.dh, s.dw, s.groups, s.OH, s.OW, 4, DIMQ_F16, epi_mode(epi),
+                    DIMQ_NCHW)) {
+    return launch_conv_halo(xq, DIMQ_F16, DIMQ_NCHW, s.B, s.C, s.H, s.W, prepared_w, 4, codebook, cb_dtype, 1, 16,
+                            bias, bias_dtype, s.OC, s.KH, s.KW, s.sh, s.ph, s.pw, s.OH, s.OW, y, y_dtype, DIMQ_NCHW,
+                            epi, st, sc);
+  }
+  GemmArgs p = conv_args(s, xq, DIMQ_NCHW, packed_w, codebook, cb_dtype, 1, 16, bias, bias_dtype, y, y_dtype,
+                         DIMQ_NCHW);
+  p.acc_scale = sc;
+  p.epi = epi;
+  int tile = gemm_pick_tile(p.M, p.N, DIMQ_VARIANT_AUTO);
+  if (tile == kTileGemv) tile = kTile16x16;  // the GEMV kernel has no im2col/group support
+  return gemm_dispatch(p, 4, DIMQ_F16, false, tile, st);
+}
+
 extern "C" int64_t dimq_conv2d_prepared_words(int64_t out_channels, int64_t in_channels, int64_t kernel_h,
                                               int64_t kernel_w, int bits) {
   if (out_channels <= 0) return 0;

@@ -1,5 +1,6 @@
-// Banded direct 3x3 convolution for NCHW activations with fp32 NCHW output
-// (the reference op's layout: BASELINE cfg2, the W4A4 conv2d_lut path).
+// Banded direct 3x3 convolution for NCHW fp16 activations with NCHW output:
+// fp32 (the reference op's layout: BASELINE cfg2, the W4A4 conv2d_lut path)
+// or fp16 (also the next layer's W4A4 codes from the quantizing epilogue).
 //
 // One 512-thread work-group (8 waves, two per SIMD) owns a contiguous run of
 // 32-pixel blocks of one image (the image's OH*OW output pixels, flattened
@@ -101,37 +102,56 @@ __device__ __forceinline__ void band_commit(const HaloArgs& p, int r0, int t, in
   }
 }
 
-// One 32-pixel x 32-channel fp32 block (lane (col, g) holds channel col's
-// pixels 8j + 4g + i) -> wave-private LDS, channel-major -> non-temporal
-// 16-byte stores of 8 whole 128-byte channel runs per instruction.
+// One 32-pixel x 32-channel block (lane (col, g) holds channel col's pixels
+// 8j + 4g + i), after the epilogue (ReLU, the next layer's activation
+// quantization), -> wave-private LDS, channel-major, then
+//   fp32 y: non-temporal 16-byte stores of 8 whole 128-byte channel runs per
+//           instruction;
+//   fp16 y: 16-byte stores of 16 channels x 64 bytes (a channel's 32 pixels)
+//           per instruction, through the L2, which joins the two 64-byte
+//           halves of a line written by neighbouring blocks.
 template <int MODE>
 __device__ __forceinline__ void band_store(const HaloArgs& p, const floatx16& acc, int b, int px1, int mb, int col,
                                            int g, int ocr, int lane, float scale, float bv, float* park) {
+  float v[16];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    float v[4];
+  for (int i = 0; i < 16; ++i) v[i] = acc[i] * scale + bv;
+  epi_m<MODE, 16>(p.epi, nullptr, 0, false, v);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[i] = acc[4 * j + i] * scale + bv;
-      if constexpr (MODE == kEpiRelu) v[i] = v[i] < 0.0f ? 0.0f : v[i];
-    }
-    *reinterpret_cast<float4*>(park + col * kParkPitch + 8 * j + 4 * g) = make_float4(v[0], v[1], v[2], v[3]);
-  }
+  for (int j = 0; j < 4; ++j)
+    *reinterpret_cast<float4*>(park + col * kParkPitch + 8 * j + 4 * g) =
+        make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   typedef float f4v __attribute__((ext_vector_type(4)));
   const int64_t ohw = (int64_t)p.OH * p.OW;
-  const int p4 = 4 * (lane & 7);
-  const int pix0 = mb * 32 + p4;
+  if (p.y_dt == DIMQ_F32) {
+    const int p4 = 4 * (lane & 7);
+    const int pix0 = mb * 32 + p4;
 #pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int c = (lane >> 3) + 8 * it;
-    const f4v v = *reinterpret_cast<const f4v*>(park + c * kParkPitch + p4);
-    const int oc = ocr + c;
-    if (oc < p.OC && pix0 < px1)  // OH*OW % 4 == 0: a 4-pixel chunk is all in or all out
-      __builtin_nontemporal_store(v, reinterpret_cast<f4v*>(reinterpret_cast<float*>(p.y) +
-                                                            ((int64_t)b * p.OC + oc) * ohw + pix0));
+    for (int it = 0; it < 4; ++it) {
+      const int c = (lane >> 3) + 8 * it;
+      const f4v v = *reinterpret_cast<const f4v*>(park + c * kParkPitch + p4);
+      const int oc = ocr + c;
+      if (oc < p.OC && pix0 < px1)  // OH*OW % 4 == 0: a 4-pixel chunk is all in or all out
+        __builtin_nontemporal_store(v, reinterpret_cast<f4v*>(reinterpret_cast<float*>(p.y) +
+                                                              ((int64_t)b * p.OC + oc) * ohw + pix0));
+    }
+  } else {
+    const int p8 = 8 * (lane & 3);
+    const int pix0 = mb * 32 + p8;
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int c = (lane >> 2) + 16 * it;
+      const f4v a = *reinterpret_cast<const f4v*>(park + c * kParkPitch + p8);
+      const f4v d = *reinterpret_cast<const f4v*>(park + c * kParkPitch + p8 + 4);
+      const uint4 h = make_uint4(f16x2_rne(a[0], a[1]), f16x2_rne(a[2], a[3]), f16x2_rne(d[0], d[1]),
+                                 f16x2_rne(d[2], d[3]));
+      const int oc = ocr + c;
+      uint16_t* dst = reinterpret_cast<uint16_t*>(p.y) + ((int64_t)b * p.OC + oc) * ohw + pix0;
+      if (oc < p.OC && pix0 < px1) *reinterpret_cast<uint4*>(dst) = h;  // OH*OW % 8 == 0 (setup)
+    }
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -252,7 +272,13 @@ __global__ __launch_bounds__(kBandThreads, 1) void conv_band_kernel(const HaloAr
 
 template <int BITS>
 int launch_band_bits(const HaloArgs& p, int mode, hipStream_t s) {
-  auto k = mode == kEpiRelu ? conv_band_kernel<BITS, kEpiRelu> : conv_band_kernel<BITS, kEpiNone>;
+  auto k = conv_band_kernel<BITS, kEpiNone>;
+  switch (mode) {
+    case kEpiRelu: k = conv_band_kernel<BITS, kEpiRelu>; break;
+    case kEpiQuant: k = conv_band_kernel<BITS, kEpiQuant>; break;
+    case kEpiRelu | kEpiQuant: k = conv_band_kernel<BITS, kEpiRelu | kEpiQuant>; break;
+    default: break;
+  }
   const size_t lds = (size_t)p.IH_t * p.IW_t * 72 * sizeof(uint16_t) + (size_t)8 * kParkFloats * sizeof(float);
   const hipError_t e =
       hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);

@@ -475,10 +475,11 @@ __global__ __launch_bounds__(256, 2) void conv_resident_kernel(const HaloArgs p)
 
 // Epilogue modes each kernel is instantiated for (others: generic kernels).
 // Resident kernel, NHWC output: none / relu / residual / residual + relu (the
-// ResNet blocks); NCHW output: none / relu; decode-per-step kernel: none.
+// ResNet blocks); NCHW output: none / relu, each also with the next layer's
+// activation quantization (chained W4A4 layers); decode-per-step kernel: none.
 inline bool halo_mode_ok(int mode, bool resident, bool nchw) {
   if (!resident) return mode == kEpiNone;
-  if (nchw) return mode == kEpiNone || mode == kEpiRelu;
+  if (nchw) return mode == kEpiNone || mode == kEpiRelu || mode == kEpiQuant || mode == (kEpiRelu | kEpiQuant);
   return mode == kEpiNone || mode == kEpiRelu || mode == kEpiRes || mode == kEpiResRelu;
 }
 
@@ -504,8 +505,13 @@ template <int BITS, int CC, int STRIDE, int KHW>
 int launch_halo_k(const HaloArgs& p, int mode, dim3 grid, size_t lds, hipStream_t s) {
   if constexpr (KHW * CC <= 36) {
     if (p.y_layout == DIMQ_NCHW) {
-      return mode == kEpiRelu ? launch_resident<BITS, CC, STRIDE, KHW, true, kEpiRelu>(p, grid, lds, s)
-                              : launch_resident<BITS, CC, STRIDE, KHW, true, kEpiNone>(p, grid, lds, s);
+      switch (mode) {
+        case kEpiRelu: return launch_resident<BITS, CC, STRIDE, KHW, true, kEpiRelu>(p, grid, lds, s);
+        case kEpiQuant: return launch_resident<BITS, CC, STRIDE, KHW, true, kEpiQuant>(p, grid, lds, s);
+        case kEpiRelu | kEpiQuant:
+          return launch_resident<BITS, CC, STRIDE, KHW, true, kEpiRelu | kEpiQuant>(p, grid, lds, s);
+        default: return launch_resident<BITS, CC, STRIDE, KHW, true, kEpiNone>(p, grid, lds, s);
+      }
     }
     switch (mode) {
       case kEpiRelu: return launch_resident<BITS, CC, STRIDE, KHW, false, kEpiRelu>(p, grid, lds, s);

@@ -29,7 +29,9 @@ int gemm_fast_tile(int tile, const GemmArgs& p, int bits) {
 int gemm_big_tile(const GemmArgs& p, int bits, int x_dtype, int variant) {
   if (variant == DIMQ_VARIANT_SMALL_M || p.conv || !(bits == 2 || bits == 3 || bits == 4)) return -1;
   const int mode = epi_mode(p.epi);  // epilogues the large tiles are instantiated for
-  if (!(mode == kEpiNone || mode == kEpiRelu || mode == kEpiGelu || mode == kEpiRes)) return -1;
+  const bool qmode = x_dtype == DIMQ_F16 && (mode == kEpiQuant || mode == (kEpiRelu | kEpiQuant) ||
+                                             mode == (kEpiGelu | kEpiQuant));
+  if (!(mode == kEpiNone || mode == kEpiRelu || mode == kEpiGelu || mode == kEpiRes || qmode)) return -1;
   if (p.M <= 64 || p.K % 64 != 0 || !p.fast_b || !p.vec_a) return -1;
   // 256x256 shared-decode tiles for large M (measured on the ViT-B/16 shapes at
   // M 12,608, bf16: qkv 84 vs 104 us, proj 40 vs 50, fc1 114 vs 134, fc2 104 vs
@@ -343,6 +345,24 @@ extern "C" int dimq_linear_lut_ws(const void* x, int x_dtype, int64_t M, const u
   p.groups = 1;
   const int tile = (x_dtype != DIMQ_F64) ? gemm_fast_tile(kTile64x32, p, 4) : kTile64x32;
   return dispatch<true>(p, 4, x_dtype, tile, as_stream(stream));
+}
+
+extern "C" int dimq_linear_lut_q(const uint16_t* xq, int64_t M, const uint8_t* packed_w, int64_t packed_numel,
+                                 const void* codebook, int cb_dtype, int64_t cb_numel, double act_scale,
+                                 const void* bias, int bias_dtype, int64_t bias_numel, int64_t out_features,
+                                 int64_t in_features, int activation, double out_act_scale, int64_t out_act_zp,
+                                 void* y, int y_dtype, void* stream) {
+  int rc = check_linear_lut(DIMQ_F16, M, packed_numel, cb_dtype, cb_numel, act_scale, 0, bias, bias_dtype, bias_numel,
+                            out_features, in_features);
+  if (rc != DIMQ_OK) return rc;
+  DIMQ_CHECK(cb_dtype == DIMQ_F16, "linear_lut_q takes the fp16 codebook of the packed export");
+  Epi epi;
+  rc = lut_q_epilogue(activation, out_act_scale, out_act_zp, y_dtype, epi);
+  if (rc != DIMQ_OK) return rc;
+  if (M == 0) return DIMQ_OK;
+  return linear_codebook_impl(xq, DIMQ_F16, M, in_features, in_features, packed_w, 4, codebook, cb_dtype, 1, 16, bias,
+                              bias_dtype, out_features, y, y_dtype, out_features, epi, DIMQ_VARIANT_AUTO,
+                              as_stream(stream), static_cast<float>(act_scale));
 }
 
 // ---------------------------------------------------------------------------

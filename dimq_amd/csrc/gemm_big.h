@@ -928,9 +928,26 @@ int launch_big_conv_bits(const GemmArgs& p, int xt, int tile, hipStream_t s) {
 // Linear tile ids (WGM x WGN waves of (MBLK*32) x (NBLK*32)):
 //   2: 128x128 (2x2, 64x64)   7: 128x128 deep pipeline
 //  10: 256x256 shared decode (4x2, 64x128), next stage's decode woven between the MFMAs
-// Epilogue modes: none / relu / gelu / residual on each.
+// Epilogue modes: none / relu / gelu / residual on each; for fp16 inputs (the
+// W4A4 activation codes) also none / relu / gelu with the next layer's
+// activation quantization.
 template <int BITS, int XT>
 int launch_big_linear_modes(const GemmArgs& p, int tile, int mode, hipStream_t s) {
+  if constexpr (XT == DIMQ_F16) {
+    if ((mode & kEpiQuant) != 0) {
+      switch (mode) {
+#define DIMQ_QMODE(M)                                                                \
+  case M:                                                                            \
+    if (tile == 10) return launch_lds<BITS, XT, 4, 2, 2, 4, M, 8>(p, s);             \
+    if (tile == 7) return launch_deep<BITS, XT, 4, M>(p, s);                         \
+    return launch_big<BITS, XT, 2, 2, 2, 2, false, M>(p, s);
+        DIMQ_QMODE(kEpiQuant)
+        DIMQ_QMODE(kEpiRelu | kEpiQuant)
+        DIMQ_QMODE(kEpiGelu | kEpiQuant)
+#undef DIMQ_QMODE
+      }
+    }
+  }
   if (tile == 10) {
     switch (mode) {
       case kEpiRelu: return launch_lds<BITS, XT, 4, 2, 2, 4, kEpiRelu, 8>(p, s);

@@ -65,11 +65,10 @@ __global__ __launch_bounds__(kThreads) void quantize_a4_f16_kernel(const void* _
 #pragma unroll
       for (int j = 0; j < 8; ++j) v[j] = load_as_float(x, XT, base + j);
     }
+    u4_codes<8>(v, s, zp);
     uint32_t h[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      h[j] = float_to_f16_bits((float)(quantize_u4(v[2 * j], s, zp) - zp)) |
-             (float_to_f16_bits((float)(quantize_u4(v[2 * j + 1], s, zp) - zp)) << 16);
+    for (int j = 0; j < 4; ++j) h[j] = f16x2_rne(v[2 * j], v[2 * j + 1]);
     *reinterpret_cast<uint4*>(out + base) = make_uint4(h[0], h[1], h[2], h[3]);
   } else {
     for (int64_t i = base; i < n; ++i) {
@@ -213,6 +212,20 @@ int launch_quantize_a4_f16(const void* x, int x_dtype, int64_t n, float s, int z
 }  // namespace dimq
 
 using namespace dimq;
+
+// The W4A4 input form of a tensor: out = fp16(q - zp), q the reference's u4
+// code (reference.py:11-21).  Entry point of a chain of W4A4 layers whose
+// later inputs come from the quantizing epilogue of the layer before.
+extern "C" int dimq_quantize_activation_f16(const void* x, int x_dtype, int64_t numel, double act_scale,
+                                            int64_t act_zp, uint16_t* out, void* stream) {
+  DIMQ_CHECK(is_float_dtype(x_dtype), "quantize_activation expects floating input");
+  DIMQ_CHECK(act_scale > 0.0, "act_scale must be positive");
+  DIMQ_CHECK(act_zp >= 0 && act_zp <= 15, "act_zero_point must be in [0, 15]");
+  DIMQ_CHECK(numel >= 0, "numel must be non-negative");
+  DIMQ_CHECK(aligned(out, 16), "out must be 16-byte aligned");
+  return launch_quantize_a4_f16(x, x_dtype, numel, static_cast<float>(act_scale), static_cast<int>(act_zp), out,
+                                as_stream(stream));
+}
 
 extern "C" int dimq_quantize_activation_u4(const void* x, int x_dtype, int64_t numel, double act_scale,
                                            int64_t act_zp, uint8_t* out, void* stream) {

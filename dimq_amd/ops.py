@@ -211,6 +211,51 @@ def dimq_linear_codebook_act(x: torch.Tensor, packed_weight: torch.Tensor, codeb
                                               int(out_features), int(in_features), out_dtype, VARIANTS[variant])
 
 
+# ---------------------------------------------------------------------------
+# Chained W4A4 layers.  Between layers the activations travel as the fp16
+# integers a - zp (a = clamp(rint(x / s) + zp, 0, 15), the reference's u4 code,
+# dimq_backend/reference.py:11-21), so a layer's epilogue can quantize its
+# output for the next layer instead of the next layer re-reading a float tensor.
+def quantize_activation_f16(x: torch.Tensor, act_scale: float, act_zp: int) -> torch.Tensor:
+    """fp16 tensor of x's shape holding a - zp: the input form of linear_lut_q / conv2d_lut_q."""
+    require_extension()
+    from . import _C
+
+    return _C.quantize_activation_f16_impl(x, act_scale, act_zp)
+
+
+def dimq_linear_lut_q(xq: torch.Tensor, packed_weight: torch.Tensor, codebook: torch.Tensor, act_scale: float,
+                      bias: torch.Tensor | None, out_features: int, in_features: int, *,
+                      activation: str | None = None, out_act: tuple[float, int] | None = None,
+                      out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """linear_lut on pre-quantized activations: y = act(s * sum_k C[w] (a - zp) + bias), xq = a - zp (fp16),
+    s = act_scale.  With out_act = (s', zp') the result is returned as the next layer's codes (fp16 q' - zp');
+    otherwise as out_dtype (default fp32).  codebook: the 16-entry fp16 codebook of the packed export."""
+    require_extension()
+    from . import _C
+
+    return _C.linear_lut_q_impl(xq, packed_weight, codebook, act_scale, bias, int(out_features), int(in_features),
+                                ACTIVATIONS[activation], out_act, out_dtype)
+
+
+def dimq_conv2d_lut_q(xq: torch.Tensor, packed_weight: torch.Tensor, codebook: torch.Tensor, act_scale: float,
+                      bias: torch.Tensor | None, weight_shape: Sequence[int], stride=1, padding=0, dilation=1,
+                      groups: int = 1, *, prepared_weight: torch.Tensor | None = None,
+                      activation: str | None = None, out_act: tuple[float, int] | None = None,
+                      out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """conv2d_lut on pre-quantized NCHW activations (xq = a - zp, fp16); output NCHW.  prepared_weight: the 4-bit
+    kernel layout of prepare_conv_weight (optional).  activation / out_act / out_dtype as dimq_linear_lut_q."""
+    require_extension()
+    from . import _C
+
+    oc, cin_g, kh, kw = [int(v) for v in weight_shape]
+    sh, sw = _pair(stride)
+    ph, pw = _pair(padding)
+    dh, dw = _pair(dilation)
+    return _C.conv2d_lut_q_impl(xq, packed_weight, codebook, act_scale, bias, oc, cin_g, kh, kw, sh, sw, ph, pw, dh,
+                                dw, int(groups), prepared_weight, ACTIVATIONS[activation], out_act, out_dtype)
+
+
 def layer_norm(x: torch.Tensor, weight: torch.Tensor | None, bias: torch.Tensor | None,
                eps: float = 1e-5) -> torch.Tensor:
     """LayerNorm over the last dimension on the HIP kernel (fp16/bf16 x; the ViT workload's LayerNorms)."""

@@ -149,6 +149,39 @@ int dimq_linear_lut_noalloc(const void* x, int x_dtype, int64_t M, const uint8_t
                             const void* bias, int bias_dtype, int64_t bias_numel, int64_t out_features,
                             int64_t in_features, float* y, void* stream);
 
+/* Chained W4A4 layers with the next layer's activation quantization fused
+ * into the producing layer's epilogue (no kernel counterpart in the
+ * reference, whose linear_lut / conv2d_lut each quantize
+ * their float input themselves, csrc/dimq_gemm_lut.cu:45-49,
+ * csrc/dimq_conv2d_lut.cu:62-81).  The activations travel between layers as
+ * the fp16 integers a - zp (a = clamp(rint(x / s) + zp, 0, 15), the
+ * reference's u4 code; exact in fp16):
+ *  - dimq_quantize_activation_f16 writes that form of a float tensor (the
+ *    chain's first input; out 16-byte aligned);
+ *  - dimq_linear_lut_q / dimq_conv2d_lut_q take it (xq [M, in_features] /
+ *    NCHW, with its act_scale s) and compute
+ *      y = act(s * sum_k C[w] (a - zp) + bias),
+ *    the reference's linear_lut / conv2d_lut on the dequantized codes,
+ *    activation in {none, relu, gelu}; with out_act_scale > 0, y (fp16) is
+ *    the next layer's codes q' - zp' of that result (same rounding as
+ *    dimq_quantize_activation_f16), else y holds it in y_dtype.
+ * The codebook is the 16-entry fp16 codebook of the packed export.  For the
+ * conv, prepared_w (nullable) is dimq_conv2d_prepare_weight's layout at 4
+ * bits, prepared once per layer; the output layout is NCHW. */
+int dimq_quantize_activation_f16(const void* x, int x_dtype, int64_t numel, double act_scale, int64_t act_zp,
+                                 uint16_t* out, void* stream);
+int dimq_linear_lut_q(const uint16_t* xq, int64_t M, const uint8_t* packed_w, int64_t packed_numel,
+                      const void* codebook, int cb_dtype, int64_t cb_numel, double act_scale, const void* bias,
+                      int bias_dtype, int64_t bias_numel, int64_t out_features, int64_t in_features, int activation,
+                      double out_act_scale, int64_t out_act_zp, void* y, int y_dtype, void* stream);
+int dimq_conv2d_lut_q(const uint16_t* xq, int64_t B, int64_t C, int64_t H, int64_t W, const uint8_t* packed_w,
+                      int64_t packed_numel, const uint32_t* prepared_w, int64_t prepared_words,
+                      const void* codebook, int cb_dtype, int64_t cb_numel, double act_scale, const void* bias,
+                      int bias_dtype, int64_t bias_numel, int64_t out_channels, int64_t in_channels_per_group,
+                      int64_t kernel_h, int64_t kernel_w, int64_t stride_h, int64_t stride_w, int64_t pad_h,
+                      int64_t pad_w, int64_t dilation_h, int64_t dilation_w, int64_t groups, int activation,
+                      double out_act_scale, int64_t out_act_zp, void* y, int y_dtype, void* stream);
+
 /* ---------------------------------------------------------------------------
  * 2. Generalised ops for the BASELINE configurations: b in {2,3,4,8} bits,
  *    per-layer or per-output-channel codebooks, weight-only GEMM/conv.

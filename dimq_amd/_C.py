@@ -90,6 +90,13 @@ _SIGS = {
     "dimq_linear_codebook_act_workspace_bytes": (_i64, [_i64, _i64]),
     "dimq_linear_codebook_act": (_int, [_vp, _int, _i64, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _vp, _i64, _vp,
                                         _int, _i64, _vp, _int, _int, _vp, _i64, _vp]),
+    "dimq_build_codebook_product_table": (_int, [_vp, _int, _i64, _i64, _vp, _i64, _vp, _vp]),
+    "dimq_linear_lut_act": (_int, [_vp, _i64, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _vp, _i64, _int, _vp,
+                                   _int, _i64, _vp, _int, _vp]),
+    "dimq_conv2d_codebook_act_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
+    "dimq_conv2d_codebook_act": (_int, [_vp, _int, _int, _i64, _i64, _i64, _i64, _vp, _i64, _int, _vp, _i64, _vp,
+                                        _int, _i64, _i64, _vp, _i64, _vp, _int] + [_i64] * 10 +
+                                 [_vp, _int, _int, _int, _vp, _i64, _vp]),
     "dimq_conv2d_codebook_ex": (_int, [_vp, _int, _int, _i64, _i64, _i64, _i64, _vp, _i64, _int, _vp, _i64, _vp,
                                        _int, _i64, _i64, _vp, _int] + [_i64] * 10 +
                                 [_vp, _int, _int, _vp, _int, _int, _int, _vp]),
@@ -479,6 +486,73 @@ def conv2d_lut_q_impl(xq, packed_w, codebook, act_scale, bias, out_channels, in_
                                      float(act_scale), bp, bdt, bn, out_channels, in_channels_per_group, kernel_h,
                                      kernel_w, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w, groups,
                                      int(activation), qs, qzp, _ptr(y), _dtype(y), _stream(xc.device)))
+    return y
+
+
+def build_codebook_product_table_impl(codebook, act_values):
+    _require_cuda(codebook, "build_codebook_product_table expects CUDA codebook")
+    cb = codebook.contiguous()
+    ca = act_values.detach().reshape(-1).float().contiguous().to(cb.device)
+    rows = cb.shape[0] if cb.dim() == 2 else 1
+    kw = cb.shape[-1]
+    table = torch.empty((rows, kw, ca.numel()), dtype=torch.float32, device=cb.device)
+    with torch.cuda.device(cb.device):
+        _check(lib.dimq_build_codebook_product_table(_ptr(cb), _dtype(cb), rows, kw, _ptr(ca), ca.numel(),
+                                                     _ptr(table), _stream(cb.device)))
+    return table
+
+
+def linear_lut_act_impl(act_idx, packed_w, codebook, bits, act_centers, x_dtype, bias, out_features, in_features,
+                        out_dtype=torch.float32):
+    _require_cuda(act_idx, "linear_lut_act expects CUDA activation indices")
+    if act_idx.dtype != torch.uint8 or act_idx.size(-1) != in_features:
+        raise RuntimeError("activation indices must be uint8 [..., in_features]")
+    ai = act_idx.contiguous()
+    if ai.data_ptr() % 16:
+        ai = ai.clone()  # 16-byte index loads
+    pw = packed_w.contiguous().view(-1)
+    cb = codebook.contiguous()
+    ac = act_centers.detach().reshape(-1).float().contiguous()
+    rows, size = _cb_shape(cb, out_features)
+    b, bp, bdt, _ = _bias_args(bias, out_features, "out_features")
+    M = ai.numel() // in_features
+    y = torch.empty((M, out_features), dtype=out_dtype, device=ai.device)
+    with torch.cuda.device(ai.device):
+        _check(lib.dimq_linear_lut_act(_ptr(ai), M, in_features, _ptr(pw), pw.numel(), int(bits), _ptr(cb), _dtype(cb),
+                                       rows, size, _ptr(ac), ac.numel(), _DT[x_dtype], bp, bdt, out_features, _ptr(y),
+                                       _dtype(y), _stream(ai.device)))
+    return y.view(*act_idx.shape[:-1], out_features)
+
+
+def conv2d_codebook_act_impl(x, packed_w, codebook, bits, act_centers, bias, out_channels, in_channels_per_group,
+                             kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w, groups,
+                             out_dtype=None, prepared_w=None, variant=0):
+    _require_cuda(x, "conv2d_codebook_act expects CUDA input")
+    if x.dim() != 4:
+        raise RuntimeError("conv2d_codebook_act expects NCHW-shaped input")
+    nhwc = x.is_contiguous(memory_format=torch.channels_last) and not x.is_contiguous()
+    mf = torch.channels_last if nhwc else torch.contiguous_format
+    xc = x.contiguous(memory_format=mf)
+    B, C, H, W = xc.shape
+    pw = packed_w.contiguous().view(-1)
+    cb = codebook.contiguous()
+    ac = act_centers.detach().reshape(-1).float().contiguous()
+    rows, size = _cb_shape(cb, out_channels)
+    b, bp, bdt, _ = _bias_args(bias, out_channels, "out_channels")
+    OH = (H + 2 * pad_h - dilation_h * (kernel_h - 1) - 1) // stride_h + 1
+    OW = (W + 2 * pad_w - dilation_w * (kernel_w - 1) - 1) // stride_w + 1
+    odt = x.dtype if out_dtype is None else out_dtype
+    y = torch.empty((B, out_channels, OH, OW), dtype=odt, device=xc.device, memory_format=mf)
+    ws = _workspace(lib.dimq_conv2d_codebook_act_workspace_bytes(B, C, H, W), xc.device)
+    pr = None if prepared_w is None else prepared_w.contiguous()
+    lay = NHWC if nhwc else NCHW
+    with torch.cuda.device(xc.device):
+        _check(lib.dimq_conv2d_codebook_act(_ptr(xc), _dtype(xc), lay, B, C, H, W, _ptr(pw), pw.numel(), int(bits),
+                                            _ptr(pr), 0 if pr is None else pr.numel(), _ptr(cb), _dtype(cb), rows,
+                                            size, _ptr(ac), ac.numel(), bp, bdt, out_channels, kernel_h, kernel_w,
+                                            stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w, groups,
+                                            _ptr(y), _dtype(y), lay, int(variant), _ptr(ws),
+                                            0 if ws is None else ws.numel(), _stream(xc.device)))
     return y
 
 

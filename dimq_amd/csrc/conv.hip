@@ -313,6 +313,43 @@ extern "C" int dimq_conv2d_lut_q(const uint16_t* xq, int64_t B, int64_t C, int64
   return gemm_dispatch(p, 4, DIMQ_F16, false, tile, st);
 }
 
+// Weight x activation codebook Conv2d: x replaced by its nearest activation
+// centre in x's dtype (the QAT wrapper's fake_quant_activation before
+// F.conv2d, quant/dimq_wrapper.py:80-85,189-197), then the weight-codebook
+// conv on it (dequantize-then-MFMA).  Workspace: B*C*H*W elements of x's
+// dtype, fp32 at most.
+extern "C" int64_t dimq_conv2d_codebook_act_workspace_bytes(int64_t B, int64_t C, int64_t H, int64_t W) {
+  if (B <= 0 || C <= 0 || H <= 0 || W <= 0) return 0;
+  return (B * C * H * W * 4 + 255) / 256 * 256;
+}
+
+extern "C" int dimq_conv2d_codebook_act(const void* x, int x_dtype, int x_layout, int64_t B, int64_t C, int64_t H,
+                                        int64_t W, const uint8_t* packed_w, int64_t packed_numel, int bits,
+                                        const uint32_t* prepared_w, int64_t prepared_words, const void* codebook,
+                                        int cb_dtype, int64_t cb_rows, int64_t cb_size, const float* act_centers,
+                                        int64_t n_act, const void* bias, int bias_dtype, int64_t out_channels,
+                                        int64_t kernel_h, int64_t kernel_w, int64_t stride_h, int64_t stride_w,
+                                        int64_t pad_h, int64_t pad_w, int64_t dilation_h, int64_t dilation_w,
+                                        int64_t groups, void* y, int y_dtype, int y_layout, int variant,
+                                        void* workspace, int64_t workspace_bytes, void* stream) {
+  DIMQ_CHECK(x_dtype == DIMQ_F32 || x_dtype == DIMQ_F16 || x_dtype == DIMQ_BF16,
+             "conv2d_codebook_act expects fp32, fp16 or bf16 input");
+  DIMQ_CHECK(n_act >= 1 && n_act <= 256, "activation codebook must hold between 1 and 256 centres");
+  DIMQ_CHECK(act_centers != nullptr, "activation codebook is required");
+  DIMQ_CHECK(B >= 0 && C > 0 && H >= 0 && W >= 0, "input sizes must be non-negative");
+  const int64_t need = dimq_conv2d_codebook_act_workspace_bytes(B, C, H, W);
+  if (need == 0) return DIMQ_OK;
+  DIMQ_CHECK(workspace != nullptr && workspace_bytes >= need && aligned(workspace, 16),
+             "workspace must be 16-byte aligned and hold dimq_conv2d_codebook_act_workspace_bytes bytes");
+  const int rc = launch_act_codebook(x, x_dtype, B * C * H * W, act_centers, static_cast<int>(n_act), workspace,
+                                     as_stream(stream));
+  if (rc != DIMQ_OK) return rc;
+  return dimq_conv2d_codebook_ex(workspace, x_dtype, x_layout, B, C, H, W, packed_w, packed_numel, bits, prepared_w,
+                                 prepared_words, codebook, cb_dtype, cb_rows, cb_size, bias, bias_dtype, out_channels,
+                                 kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w, groups,
+                                 y, y_dtype, y_layout, nullptr, 0, DIMQ_ACT_NONE, variant, stream);
+}
+
 extern "C" int64_t dimq_conv2d_prepared_words(int64_t out_channels, int64_t in_channels, int64_t kernel_h,
                                               int64_t kernel_w, int bits) {
   if (out_channels <= 0) return 0;

@@ -218,6 +218,23 @@ extern "C" int dimq_linear_codebook_act(const void* x, int x_dtype, int64_t M, i
   const int64_t need = dimq_linear_codebook_act_workspace_bytes(M, K);
   DIMQ_CHECK(workspace != nullptr && workspace_bytes >= need && aligned(workspace, 16),
              "workspace must be 16-byte aligned and hold dimq_linear_codebook_act_workspace_bytes bytes");
+  // DIMQ_VARIANT_SMALL_M: activation indices into the workspace, then the
+  // index x index LUT gather (the weight and activation codebooks' product
+  // table formed per work-group); otherwise the dequantize-then-GEMM form,
+  // the faster one on MI355X at every M
+  const bool gather = variant == DIMQ_VARIANT_SMALL_M && lut_act_supported(M, K, bits, cb_rows, n_act) &&
+                      aligned(packed_w, 4) && is_float_dtype(cb_dtype) && (cb_rows == 1 || cb_rows == N) &&
+                      cb_size >= 1 && cb_size <= (1 << bits) && packed_numel >= (N * K * bits + 7) / 8;
+  if (gather) {
+    uint8_t* idx = static_cast<uint8_t*>(workspace);
+    int r = dimq_hard_quantize(x, x_dtype, 1, M * K, act_centers, n_act, 0, idx, nullptr, stream);
+    if (r != DIMQ_OK) return r;
+    DIMQ_CHECK(bias == nullptr || is_float_dtype(bias_dtype), "bias must be floating point");
+    DIMQ_CHECK(y_dtype == DIMQ_F32 || y_dtype == DIMQ_F16 || y_dtype == DIMQ_BF16,
+               "linear_codebook output dtype must be fp32, fp16 or bf16");
+    return launch_lut_act(idx, M, K, packed_w, bits, codebook, cb_dtype, cb_rows, cb_size, act_centers, n_act, x_dtype,
+                          bias, bias_dtype, N, y, y_dtype, /*clamp=*/false, as_stream(stream));
+  }
   const int rc = launch_act_codebook(x, x_dtype, M * K, act_centers, static_cast<int>(n_act), workspace,
                                      as_stream(stream));
   if (rc != DIMQ_OK) return rc;

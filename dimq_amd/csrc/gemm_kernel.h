@@ -1051,6 +1051,11 @@ int launch_conv_stem(const void* x, int x_dtype, int x_layout, int64_t B, int64_
 
 // quant.hip: W4A4 activations as the fp16 integers a - zp (out 16-byte aligned)
 int launch_quantize_a4_f16(const void* x, int x_dtype, int64_t n, float s, int zp, uint16_t* out, hipStream_t st);
+// lut_act.hip: index x index LUT gather of the weight x activation codebook Linear
+bool lut_act_supported(int64_t M, int64_t K, int bits, int64_t cb_rows, int64_t Ka);
+int launch_lut_act(const uint8_t* aidx, int64_t M, int64_t K, const uint8_t* w, int bits, const void* cw, int cw_dt,
+                   int64_t cb_rows, int64_t cb_size, const float* ca, int64_t Ka, int x_dtype, const void* bias,
+                   int bias_dt, int64_t N, void* y, int y_dt, bool clamp, hipStream_t s);
 // quant.hip: activations -> their nearest activation-codebook centre, in x's dtype
 int launch_act_codebook(const void* x, int x_dtype, int64_t n, const float* centers, int K, void* out,
                         hipStream_t st);

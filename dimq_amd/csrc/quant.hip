@@ -90,101 +90,137 @@ __global__ __launch_bounds__(kThreads) void product_table_kernel(const void* __r
   table[i] = w * ahat;
 }
 
-// Nearest centre, exact argmin semantics of torch on fp32 distances:
-// d = (w - c)^2 with one rounding per operation; strict '<' keeps the first
-// minimum; a NaN distance wins and the first NaN is kept.
-// Block = one row segment of 256*4 weights; the row's centres sit in LDS and
-// are read as broadcasts.
-__global__ __launch_bounds__(kThreads) void hard_quantize_kernel(const void* __restrict__ w, int dt, int64_t rows,
-                                                                 int64_t row_len, const float* __restrict__ centers,
-                                                                 int K, int per_channel, uint8_t* __restrict__ idx,
-                                                                 void* __restrict__ values, int64_t seg_per_row) {
-  __shared__ float c_s[256];
+// Nearest centre with torch's argmin semantics on fp32 distances
+// d(c) = RN(RN(x - c)^2) (quant/dimq.py:213-214): the first minimum wins, a
+// NaN distance beats every number and the first NaN is kept.
+//
+// RN is monotone, so for a finite x, d(c) does not increase as c rises
+// towards x and does not decrease as c rises beyond it: over the centres in
+// ascending order the minimum sits at one of x's two neighbours, and the
+// centres with that distance form one run around them.  The work-group sorts
+// its row's centres in LDS once (rank sort on (value, index)), and each
+// element costs a binary search, two distances and a scan of the tied run
+// (usually one step), whatever the number of centres.  NaN distances come
+// only from NaN centres, a NaN x, or an infinite x meeting the same
+// infinity; those cases are answered from the first-index flags below.
+struct CentreRow {
+  float sv[256];  // centres in ascending order (ties by index)
+  int si[256];    // their indices
+  float raw[256];
+  int first_nan, first_pinf, first_ninf;  // first NaN / +inf / -inf centre, K if none
+};
+
+__device__ __forceinline__ float centre_dist(float x, float c) {
+  const float diff = x - c;
+  return __fmul_rn(diff, diff);
+}
+
+// Whole work-group: the row's K (1..256) centres into `r`.
+__device__ void centre_row_setup(const float* __restrict__ c, int K, CentreRow& r) {
+  if (threadIdx.x == 0) {
+    r.first_nan = K;
+    r.first_pinf = K;
+    r.first_ninf = K;
+  }
+  for (int j = threadIdx.x; j < K; j += blockDim.x) r.raw[j] = c[j];
+  __syncthreads();
+  for (int j = threadIdx.x; j < K; j += blockDim.x) {
+    const float v = r.raw[j];
+    if (v != v) atomicMin(&r.first_nan, j);
+    if (v == __builtin_inff()) atomicMin(&r.first_pinf, j);
+    if (v == -__builtin_inff()) atomicMin(&r.first_ninf, j);
+    int rank = 0;
+#pragma unroll 8
+    for (int i = 0; i < K; ++i) {
+      const float u = r.raw[i];
+      rank += (u < v) || (u == v && i < j);
+    }
+    // with a NaN centre ranks can collide; the sorted view is then unused
+    r.sv[rank] = v;
+    r.si[rank] = j;
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ int nearest_centre(float x, const CentreRow& r, int K) {
+  if (x != x) return 0;  // every distance NaN
+  if (x == __builtin_inff() || x == -__builtin_inff()) {
+    // NaN distances: the NaN centres and the centres equal to x; else all inf
+    const int f = min(r.first_nan, x > 0.0f ? r.first_pinf : r.first_ninf);
+    return f < K ? f : 0;
+  }
+  if (r.first_nan < K) return r.first_nan;
+  int pos = 0;  // number of centres <= x
+#pragma unroll
+  for (int step = 256; step > 0; step >>= 1)
+    if (pos + step <= K && r.sv[pos + step - 1] <= x) pos += step;
+  const int L = pos - 1, R = pos;
+  const float dl = L >= 0 ? centre_dist(x, r.sv[L]) : 0.0f;
+  const float dr = R < K ? centre_dist(x, r.sv[R]) : 0.0f;
+  const float ds = L < 0 ? dr : (R >= K ? dl : fminf(dl, dr));
+  int best = K;
+  if (L >= 0 && dl == ds)
+    for (int i = L; i >= 0 && centre_dist(x, r.sv[i]) == ds; --i) best = min(best, r.si[i]);
+  if (R < K && dr == ds)
+    for (int i = R; i < K && centre_dist(x, r.sv[i]) == ds; ++i) best = min(best, r.si[i]);
+  return best;
+}
+
+// Nearest-centre assignment of a [rows, row_len] tensor (per_channel: row r
+// uses centres[r * K ..]; else one set for all).  One work-group per segment
+// of seg_len = 256 * ept elements of a row; writes the index (idx, nullable)
+// and / or centres[idx].to(dtype) (values, nullable).  hard_quantize_weight,
+// quant/dimq.py:197-221.
+__global__ __launch_bounds__(kThreads) void nearest_centre_kernel(const void* __restrict__ w, int dt, int64_t row_len,
+                                                                  const float* __restrict__ centers, int K,
+                                                                  int per_channel, uint8_t* __restrict__ idx,
+                                                                  void* __restrict__ values, int64_t seg_per_row,
+                                                                  int ept) {
+  __shared__ CentreRow r;
   const int64_t row = static_cast<int64_t>(blockIdx.x) / seg_per_row;
   const int64_t seg = static_cast<int64_t>(blockIdx.x) % seg_per_row;
-  const float* c = centers + (per_channel ? row * K : 0);
-  for (int j = threadIdx.x; j < K; j += kThreads) c_s[j] = c[j];
-  __syncthreads();
-  const int64_t start = seg * (kThreads * 4);
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int64_t k = start + r * kThreads + threadIdx.x;
+  const int64_t start = seg * (static_cast<int64_t>(kThreads) * ept);
+  // the first element is requested before the centres are sorted
+  const float x0 = start + threadIdx.x < row_len ? load_as_float(w, dt, row * row_len + start + threadIdx.x) : 0.0f;
+  centre_row_setup(centers + (per_channel ? row * K : 0), K, r);
+  for (int q = 0; q < ept; ++q) {
+    const int64_t k = start + q * kThreads + threadIdx.x;
     if (k >= row_len) break;
     const int64_t e = row * row_len + k;
-    const float x = load_as_float(w, dt, e);
-    int best = 0;
-    float best_d = __builtin_inff();
-    bool have = false;
-    bool have_nan = false;
-    for (int j = 0; j < K; ++j) {
-      const float diff = x - c_s[j];
-      const float d = __fmul_rn(diff, diff);
-      if (d != d) {
-        if (!have_nan) {
-          best = j;
-          have_nan = true;
-        }
-      } else if (!have_nan && (!have || d < best_d)) {
-        best = j;
-        best_d = d;
-        have = true;
-      }
-    }
-    idx[e] = (uint8_t)best;
-    if (values) store_from_float(values, dt, e, c_s[best]);
+    const int best = nearest_centre(q == 0 ? x0 : load_as_float(w, dt, e), r, K);
+    if (idx) idx[e] = static_cast<uint8_t>(best);
+    if (values) store_from_float(values, dt, e, r.raw[best]);  // centers[idx].to(dtype)
   }
 }
 
-// Activation codebook (the QAT wrapper's activation_centers,
-// quant/dimq_wrapper.py:80-85 via hard_quantize_weight, quant/dimq.py:197-221):
-// out = C_a[argmin_c (x - C_a[c])^2] in x's dtype, with hard_quantize_kernel's torch
-// argmin semantics (first minimum; a NaN distance wins, the first NaN kept).
-// 4 activations per thread, the K <= 256 centres in LDS.
-__global__ __launch_bounds__(kThreads) void act_codebook_kernel(const void* __restrict__ x, int dt, int64_t n,
-                                                                const float* __restrict__ centers, int K,
-                                                                void* __restrict__ out) {
-  __shared__ float c_s[256];
-  for (int j = threadIdx.x; j < K; j += kThreads) c_s[j] = centers[j];
-  __syncthreads();
-  const int64_t start = static_cast<int64_t>(blockIdx.x) * (kThreads * 4);
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int64_t e = start + r * kThreads + threadIdx.x;
-    if (e >= n) break;
-    const float v = load_as_float(x, dt, e);
-    int best = 0;
-    float best_d = __builtin_inff();
-    bool have = false;
-    bool have_nan = false;
-    for (int j = 0; j < K; ++j) {
-      const float diff = v - c_s[j];
-      const float d = __fmul_rn(diff, diff);
-      if (d != d) {
-        if (!have_nan) {
-          best = j;
-          have_nan = true;
-        }
-      } else if (!have_nan && (!have || d < best_d)) {
-        best = j;
-        best_d = d;
-        have = true;
-      }
-    }
-    store_from_float(out, dt, e, c_s[best]);  // centers[idx].to(x.dtype)
-  }
+// Elements per thread: 1 while that leaves fewer than 2048 work-groups, up to
+// 16 for large tensors (the centre sort is paid once per work-group).
+inline int nearest_ept(int64_t rows, int64_t row_len) {
+  int ept = 1;
+  while (ept < 16 && rows * ((row_len + kThreads * ept - 1) / (kThreads * ept)) >= 4096) ept *= 2;
+  return ept;
+}
+
+int launch_nearest_centre(const void* w, int dt, int64_t rows, int64_t row_len, const float* centers, int K,
+                          int per_channel, uint8_t* idx, void* values, hipStream_t st) {
+  if (rows == 0 || row_len == 0) return DIMQ_OK;
+  const int ept = nearest_ept(rows, row_len);
+  const int64_t seg = (row_len + kThreads * ept - 1) / (kThreads * ept);
+  const int64_t blocks = rows * seg;
+  DIMQ_CHECK(blocks < (int64_t)1 << 31, "tensor too large for one launch");
+  hipLaunchKernelGGL(nearest_centre_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, st, w, dt,
+                     row_len, centers, K, per_channel ? 1 : 0, idx, values, seg, ept);
+  return check_launch("nearest centre");
 }
 
 }  // namespace
 
-// Launches act_codebook_kernel (K in [1, 256]); out holds n elements of x_dtype.
+// Activation codebook (the QAT wrapper's activation_centers,
+// quant/dimq_wrapper.py:80-85 via hard_quantize_weight, quant/dimq.py:197-221):
+// out = C_a[argmin_c (x - C_a[c])^2] in x's dtype (K in [1, 256]).
 int launch_act_codebook(const void* x, int x_dtype, int64_t n, const float* centers, int K, void* out,
                         hipStream_t st) {
-  if (n == 0) return DIMQ_OK;
-  const int64_t blocks = (n + kThreads * 4 - 1) / (kThreads * 4);
-  DIMQ_CHECK(blocks < (int64_t)1 << 31, "activations too large for one launch");
-  hipLaunchKernelGGL(act_codebook_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, st, x, x_dtype,
-                     n, centers, K, out);
-  return check_launch("activation codebook");
+  return launch_nearest_centre(x, x_dtype, 1, n, centers, K, 0, nullptr, out, st);
 }
 
 // Launches quantize_a4_f16_kernel; out must be 16-byte aligned.
@@ -270,11 +306,6 @@ extern "C" int dimq_hard_quantize(const void* w, int w_dtype, int64_t rows, int6
   DIMQ_CHECK(n_centers <= 256, "at most 256 centers are supported (uint8 indices), got %lld",
              (long long)n_centers);
   DIMQ_CHECK(rows >= 0 && row_len >= 0, "weight shape must be non-negative");
-  if (rows == 0 || row_len == 0) return DIMQ_OK;
-  const int64_t seg = (row_len + kThreads * 4 - 1) / (kThreads * 4);
-  const int64_t blocks = rows * seg;
-  DIMQ_CHECK(blocks < (int64_t)1 << 31, "weight too large for one launch");
-  hipLaunchKernelGGL(hard_quantize_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, as_stream(stream), w, w_dtype,
-                     rows, row_len, centers, static_cast<int>(n_centers), per_channel ? 1 : 0, indices, values, seg);
-  return check_launch("hard_quantize");
+  return launch_nearest_centre(w, w_dtype, rows, row_len, centers, static_cast<int>(n_centers), per_channel,
+                               indices, values, as_stream(stream));
 }

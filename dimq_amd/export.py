@@ -12,9 +12,12 @@ the exporter also runs where no GPU is visible.  Both give the same bytes
 Format extension (``format_version`` 2), written only when a layer needs it:
 ``bit_w`` in {2,3,4,8}, ``codebook_granularity`` "per_layer" | "per_channel"
 (``codebook`` [K] or [out_channels, K]), ``activation_quantization`` "none"
-for weight-only layers, ``weight_encoding`` "packed_lsb_first_indices".  A
-compact checkpoint whose layers all hold 16 per-layer centres exports to the
-reference's version-1 layout unchanged.
+for weight-only layers, or "codebook" with the layer's ``activation_centers``
+(fp32 [Ka]) and ``bit_a`` when the compact layer carries the QAT wrapper's
+activation codebook (``quant/export_dimq.py:81-86``), ``weight_encoding``
+"packed_lsb_first_indices".  A compact checkpoint whose layers all hold 16
+per-layer centres exports to the reference's version-1 layout unchanged (its
+uniform u4 activations; ``weight_only=True`` keeps activation codebooks).
 """
 
 from __future__ import annotations
@@ -268,7 +271,13 @@ def export_packed_dimq_checkpoint(
             "codebook_granularity": "per_channel" if per_channel else "per_layer",
             "bias": bias.detach().cpu().to(dtype=codebook_dtype) if bias is not None else None,
         }
-        if weight_only:
+        if weight_only and layer.get("activation_centers") is not None:
+            # the QAT wrapper's activation codebook (quant/export_dimq.py:81-86): kept as is, applied at run time
+            ac = torch.as_tensor(layer["activation_centers"]).detach().float().reshape(-1).cpu()
+            entry["bit_a"] = int(layer.get("activation_bits", bits_for_codebook(ac.numel())))
+            entry["activation_quantization"] = "codebook"
+            entry["activation_centers"] = ac
+        elif weight_only:
             entry["bit_a"] = None
             entry["activation_quantization"] = "none"
         else:
@@ -307,7 +316,8 @@ def export_packed_dimq_checkpoint(
         "model_meta": compact.get("model_meta", {}),
         "quant_cfg": compact.get("quant_cfg", {}),
         "weight_encoding": "packed_lsb_first_indices" if weight_only else "packed_u4_indices",
-        "activation_quantization": "none" if weight_only else "uniform_affine_u4",
+        "activation_quantization": ("uniform_affine_u4" if not weight_only else
+                                    "codebook" if any("activation_centers" in l for l in layers.values()) else "none"),
         "layers": layers,
         "non_quantized_state_dict": non_quantized,
     }

@@ -95,11 +95,16 @@ class DIMQCodebookLinear(nn.Module):
     """Weight-only Linear: y = x @ W_hat^T + b, W_hat[n, k] = codebook[n or 0, idx[n, k]] (b-bit idx)."""
 
     def __init__(self, packed_weight, codebook, bits, out_features, in_features, bias=None, *,
-                 out_dtype: torch.dtype | None = None, variant: str = "auto") -> None:
+                 out_dtype: torch.dtype | None = None, variant: str = "auto",
+                 activation_centers: torch.Tensor | None = None) -> None:
         super().__init__()
         self.register_buffer("packed_weight", packed_weight.contiguous().to(torch.uint8))
         self.register_buffer("codebook", codebook.contiguous())
         self.register_buffer("bias", None if bias is None else bias.contiguous())
+        # the QAT wrapper's activation codebook (quant/dimq_wrapper.py:80-85): when set, activations are
+        # quantized to their nearest centre before the weight-codebook product
+        self.register_buffer("activation_centers",
+                             None if activation_centers is None else activation_centers.detach().float().reshape(-1))
         self.bits = int(bits)
         self.out_features = int(out_features)
         self.in_features = int(in_features)
@@ -110,6 +115,12 @@ class DIMQCodebookLinear(nn.Module):
                 activation: str | None = None) -> torch.Tensor:
         """act(linear(x) + residual); residual and activation ("relu", "gelu") are fused into the kernel."""
         _require_gpu(x, self.packed_weight, True, "DIMQCodebookLinear")
+        if self.activation_centers is not None:
+            if residual is not None or activation is not None:
+                raise RuntimeError("activation-codebook layers take no fused residual / activation")
+            return ops.dimq_linear_codebook_act(x, self.packed_weight, self.codebook, self.bits,
+                                                self.activation_centers, self.bias, self.out_features,
+                                                self.in_features, out_dtype=self.out_dtype, variant=self.variant)
         return ops.dimq_linear_codebook(x, self.packed_weight, self.codebook, self.bits, self.bias,
                                         self.out_features, self.in_features, out_dtype=self.out_dtype,
                                         variant=self.variant, residual=residual, activation=activation)
@@ -132,18 +143,21 @@ class DIMQCodebookLinear(nn.Module):
     @classmethod
     def from_export_layer(cls, layer: Mapping[str, Any]) -> "DIMQCodebookLinear":
         return cls(layer["packed_weight"], layer["codebook"], layer["bit_w"], layer["out_features"],
-                   layer["in_features"], layer.get("bias"))
+                   layer["in_features"], layer.get("bias"), activation_centers=layer.get("activation_centers"))
 
 
 class DIMQCodebookConv2d(nn.Module):
     """Weight-only Conv2d with b-bit codebook indices (conv_kcrs layout)."""
 
     def __init__(self, packed_weight, codebook, bits, weight_shape, bias=None, *, stride=1, padding=0, dilation=1,
-                 groups=1, out_dtype: torch.dtype | None = None, variant: str = "auto") -> None:
+                 groups=1, out_dtype: torch.dtype | None = None, variant: str = "auto",
+                 activation_centers: torch.Tensor | None = None) -> None:
         super().__init__()
         self.register_buffer("packed_weight", packed_weight.contiguous().to(torch.uint8))
         self.register_buffer("codebook", codebook.contiguous())
         self.register_buffer("bias", None if bias is None else bias.contiguous())
+        self.register_buffer("activation_centers",
+                             None if activation_centers is None else activation_centers.detach().float().reshape(-1))
         self.bits = int(bits)
         self.weight_shape = tuple(int(v) for v in weight_shape)
         self.stride = _pair(stride)
@@ -175,6 +189,13 @@ class DIMQCodebookConv2d(nn.Module):
                 activation: str | None = None) -> torch.Tensor:
         """act(conv(x) + residual); residual and activation ("relu", "gelu") are fused into the kernel."""
         _require_gpu(x, self.packed_weight, True, "DIMQCodebookConv2d")
+        if self.activation_centers is not None:
+            if residual is not None or activation is not None:
+                raise RuntimeError("activation-codebook layers take no fused residual / activation")
+            return ops.dimq_conv2d_codebook_act(x, self.packed_weight, self.codebook, self.bits,
+                                                self.activation_centers, self.bias, self.weight_shape, self.stride,
+                                                self.padding, self.dilation, self.groups, out_dtype=self.out_dtype,
+                                                prepared_weight=self.prepared_weight(), variant=self.variant)
         return ops.dimq_conv2d_codebook(x, self.packed_weight, self.codebook, self.bits, self.bias,
                                         self.weight_shape, self.stride, self.padding, self.dilation, self.groups,
                                         out_dtype=self.out_dtype, variant=self.variant,
@@ -202,7 +223,8 @@ class DIMQCodebookConv2d(nn.Module):
     def from_export_layer(cls, layer: Mapping[str, Any]) -> "DIMQCodebookConv2d":
         return cls(layer["packed_weight"], layer["codebook"], layer["bit_w"], layer["weight_shape"], layer.get("bias"),
                    stride=layer.get("stride", (1, 1)), padding=layer.get("padding", (0, 0)),
-                   dilation=layer.get("dilation", (1, 1)), groups=layer.get("groups", 1))
+                   dilation=layer.get("dilation", (1, 1)), groups=layer.get("groups", 1),
+                   activation_centers=layer.get("activation_centers"))
 
 
 class DIMQLayerNorm(nn.LayerNorm):
@@ -249,7 +271,8 @@ class DIMQMaxPool2d(nn.MaxPool2d):
 
 def make_packed_layer(layer: Mapping[str, Any], *, use_cuda_kernel: bool = True) -> nn.Module:
     """modules.py:153-158, extended with weight-only (format v2) layers."""
-    weight_only = layer.get("activation_quantization") == "none" or layer.get("bit_a", 4) is None
+    weight_only = (layer.get("activation_quantization") in ("none", "codebook") or layer.get("bit_a", 4) is None
+                   or "activation_centers" in layer)
     if layer["type"] == "linear":
         if weight_only:
             return DIMQCodebookLinear.from_export_layer(layer)

@@ -211,6 +211,47 @@ def dimq_linear_codebook_act(x: torch.Tensor, packed_weight: torch.Tensor, codeb
                                               int(out_features), int(in_features), out_dtype, VARIANTS[variant])
 
 
+def build_codebook_product_table(codebook: torch.Tensor, act_values: torch.Tensor) -> torch.Tensor:
+    """[rows, Kw, Ka] fp32 table codebook[g][w] * act_values[a] (one rounding): the weight x activation codebook
+    products a LUT GEMM gathers from.  act_values: the activation centres as the activations take them (in the
+    activations' dtype)."""
+    require_extension()
+    from . import _C
+
+    return _C.build_codebook_product_table_impl(codebook, act_values)
+
+
+def dimq_linear_lut_act(act_idx: torch.Tensor, packed_weight: torch.Tensor, codebook: torch.Tensor, bits: int,
+                        act_centers: torch.Tensor, x_dtype: torch.dtype, bias: torch.Tensor | None, out_features: int,
+                        in_features: int, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """Index x index LUT GEMM (M <= 16): y[m, n] = sum_k (C_w[n][w[n, k]] * C_a[a[m, k]]) + bias[n], act_idx the
+    uint8 activation-centre indices, C_a rounded to x_dtype (the reference's centers[idx].to(x.dtype))."""
+    require_extension()
+    from . import _C
+
+    return _C.linear_lut_act_impl(act_idx, packed_weight, codebook, int(bits), act_centers, x_dtype, bias,
+                                  int(out_features), int(in_features), out_dtype)
+
+
+def dimq_conv2d_codebook_act(x: torch.Tensor, packed_weight: torch.Tensor, codebook: torch.Tensor, bits: int,
+                             act_centers: torch.Tensor, bias: torch.Tensor | None, weight_shape: Sequence[int],
+                             stride=1, padding=0, dilation=1, groups: int = 1, *,
+                             out_dtype: torch.dtype | None = None, prepared_weight: torch.Tensor | None = None,
+                             variant: str = "auto") -> torch.Tensor:
+    """Weight x activation codebook Conv2d: x quantized to its nearest activation centre (the QAT wrapper's
+    activation_centers, quant/dimq_wrapper.py:80-85), then the weight-codebook conv."""
+    require_extension()
+    from . import _C
+
+    oc, cin_g, kh, kw = [int(v) for v in weight_shape]
+    sh, sw = _pair(stride)
+    ph, pw = _pair(padding)
+    dh, dw = _pair(dilation)
+    return _C.conv2d_codebook_act_impl(x, packed_weight, codebook, int(bits), act_centers, bias, oc, cin_g, kh, kw,
+                                       sh, sw, ph, pw, dh, dw, int(groups), out_dtype, prepared_weight,
+                                       VARIANTS[variant])
+
+
 # ---------------------------------------------------------------------------
 # Chained W4A4 layers.  Between layers the activations travel as the fp16
 # integers a - zp (a = clamp(rint(x / s) + zp, 0, 15), the reference's u4 code,

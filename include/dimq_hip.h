@@ -309,13 +309,52 @@ int dimq_linear_codebook_ex_ws(const void* x, int x_dtype, int64_t M, int64_t K,
  * the reference's centers[idx].to(x.dtype) (at least
  * dimq_linear_codebook_act_workspace_bytes, 16-byte aligned), then the
  * weight-codebook tiles run on them (fp16 matrix path with the fp32 recompute
- * of tiles outside the fp16 range, as dimq_linear_codebook). */
+ * of tiles outside the fp16 range, as dimq_linear_codebook).  With
+ * DIMQ_VARIANT_SMALL_M and a shape dimq_linear_lut_act runs, the workspace
+ * takes the activation indices instead and the index x index LUT gather
+ * computes y. */
 int64_t dimq_linear_codebook_act_workspace_bytes(int64_t M, int64_t K);
 int dimq_linear_codebook_act(const void* x, int x_dtype, int64_t M, int64_t K, const uint8_t* packed_w,
                              int64_t packed_numel, int bits, const void* codebook, int cb_dtype, int64_t cb_rows,
                              int64_t cb_size, const float* act_centers, int64_t n_act, const void* bias, int bias_dtype,
                              int64_t N, void* y, int y_dtype, int variant, void* workspace, int64_t workspace_bytes,
                              void* stream);
+
+/* Weight x activation codebook product table (no kernel counterpart in the
+ * reference; the LUT GEMM of its activation codebooks, quant/dimq_wrapper.py
+ * :80-85 with quant/dimq.py:197-221): table[g][w][a] = w_codebook[g][w] *
+ * act_centers[a] in fp32 (one rounding), g < rows, w < Kw, a < Ka <= 256.
+ * act_centers are the values the activations take (the centres in the
+ * activations' dtype, widened to fp32). */
+int dimq_build_codebook_product_table(const void* w_codebook, int cw_dtype, int64_t rows, int64_t Kw,
+                                      const float* act_centers, int64_t Ka, float* table, void* stream);
+
+/* Index x index LUT GEMM of the weight x activation codebook Linear (decode
+ * shapes; dimq_linear_codebook_act uses it with DIMQ_VARIANT_SMALL_M for
+ * M <= 16, its default being the faster dequantize-then-GEMM form): y[m, n] = sum_k T[n or 0][w[n,k]][a[m,k]]
+ * + bias[n] with T = codebook x act_centers rounded to x_dtype, formed per
+ * work-group in LDS.  act_idx [M, K] uint8 activation-centre indices
+ * (entries >= n_act read centre n_act - 1); M <= 16, K % 32 == 0, bits 1-4,
+ * n_act <= 256; act_idx 16-byte and packed_w 4-byte aligned. */
+int dimq_linear_lut_act(const uint8_t* act_idx, int64_t M, int64_t K, const uint8_t* packed_w, int64_t packed_numel,
+                        int bits, const void* codebook, int cb_dtype, int64_t cb_rows, int64_t cb_size,
+                        const float* act_centers, int64_t n_act, int x_dtype, const void* bias, int bias_dtype,
+                        int64_t N, void* y, int y_dtype, void* stream);
+
+/* Weight x activation codebook Conv2d (the Conv2d form of
+ * dimq_linear_codebook_act): x replaced by its nearest activation centre in
+ * x's dtype, written to the caller's workspace (at least
+ * dimq_conv2d_codebook_act_workspace_bytes, 16-byte aligned, x's layout),
+ * then dimq_conv2d_codebook_ex on it (no residual / activation). */
+int64_t dimq_conv2d_codebook_act_workspace_bytes(int64_t B, int64_t C, int64_t H, int64_t W);
+int dimq_conv2d_codebook_act(const void* x, int x_dtype, int x_layout, int64_t B, int64_t C, int64_t H, int64_t W,
+                             const uint8_t* packed_w, int64_t packed_numel, int bits, const uint32_t* prepared_w,
+                             int64_t prepared_words, const void* codebook, int cb_dtype, int64_t cb_rows,
+                             int64_t cb_size, const float* act_centers, int64_t n_act, const void* bias,
+                             int bias_dtype, int64_t out_channels, int64_t kernel_h, int64_t kernel_w,
+                             int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w, int64_t dilation_h,
+                             int64_t dilation_w, int64_t groups, void* y, int y_dtype, int y_layout, int variant,
+                             void* workspace, int64_t workspace_bytes, void* stream);
 
 int dimq_conv2d_codebook_ex(const void* x, int x_dtype, int x_layout, int64_t B, int64_t C, int64_t H, int64_t W,
                             const uint8_t* packed_w, int64_t packed_numel, int bits, const uint32_t* prepared_w,

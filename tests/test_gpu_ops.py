@@ -139,6 +139,47 @@ def test_hard_quantize_half_inputs(gpu):
         assert torch.equal(val.cpu(), torch.from_numpy(wv).to(dt))
 
 
+def _argmin_ref(w, c):
+    """The reference's assignment, (w - c)^2 in fp32 then argmin (quant/dimq.py:213-215), on the CPU."""
+    return ((w.float().reshape(-1)[:, None] - c.float()[None, :]) ** 2).argmin(1)
+
+
+@pytest.mark.parametrize("K", [1, 2, 3, 16, 255, 256])
+def test_hard_quantize_ties_and_specials(gpu, K):
+    """The sorted-search assignment against the full argmin: unsorted and duplicated centres, values exactly
+    between two centres (equal distances: the first index wins), +-0, infinite centres and inputs, distances that
+    overflow to inf, NaN centres, inputs beyond every centre, and a tensor large enough for several elements per
+    thread."""
+    ops = _ops()
+    announce(f"hard_quantize ties/specials K={K}")
+    g = _gen(K)
+    grid = torch.randint(-12, 13, (K,), generator=g).float() * 0.25  # duplicates for K > 25
+    c = grid[torch.randperm(K, generator=g)]
+    mids = torch.arange(-60, 61).float() * 0.125                    # every midpoint of the 0.25 grid
+    specials = torch.tensor([0.0, -0.0, 1e30, -1e30, 3.4e38, -3.4e38, 1e-40, float("inf"), float("-inf"),
+                             float("nan"), 100.0, -100.0])
+    w = torch.cat([mids, specials, torch.randn(2000, generator=g) * 2])
+    cases = [c, torch.where(torch.arange(K) % 5 == 1, -c, c)]
+    if K >= 3:
+        cz = c.clone(); cz[0], cz[1] = 0.0, -0.0
+        ci = c.clone(); ci[K // 2] = float("inf"); ci[K - 1] = float("-inf")
+        cd = c.clone(); cd[K - 1] = 2e30; cd[0] = -2e30
+        cn = c.clone(); cn[K // 2] = float("nan")
+        cases += [cz, ci, cd, cn]
+    for cc in cases:
+        idx, val = ops.hard_quantize(w.to(gpu), cc.to(gpu), False)
+        want = _argmin_ref(w, cc)
+        bad = (idx.cpu().long() != want).nonzero().flatten()
+        assert bad.numel() == 0, [(float(w[i]), int(idx[i]), int(want[i])) for i in bad[:5]]
+        assert np.array_equal(idx.cpu().numpy(), oracle.hard_quantize(w, cc)[0])
+    big = torch.randn(3, 1 << 20, generator=g)   # 4096+ segments: 16 elements per thread
+    cb = torch.randn(3, K, generator=g)
+    idx, val = ops.hard_quantize(big.to(gpu), cb.to(gpu), True)
+    for r in range(3):
+        assert torch.equal(idx[r].cpu().long(), _argmin_ref(big[r], cb[r]))
+        assert torch.equal(val[r].cpu(), cb[r][idx[r].cpu().long()])
+
+
 # ---------------------------------------------------------------- activation quantization / product table
 def test_quantize_activation_golden_and_dtypes(gpu):
     ops = _ops()
@@ -484,7 +525,8 @@ def test_linear_codebook_act_vs_reference(gpu, M, N, K, bits, xdt, n_act):
     y = ops.dimq_linear_codebook_act(x.to(gpu), packed.to(gpu), cb.to(gpu), bits, ca.to(gpu), bias.to(gpu), N, K,
                                      out_dtype=torch.float32)
     xf = x.float()
-    q = ca[((xf.reshape(-1)[:, None] - ca[None, :]) ** 2).argmin(1)].reshape(M, K)
+    # centers[idx].to(x.dtype), as the reference's hard_quantize_weight returns them
+    q = ca[((xf.reshape(-1)[:, None] - ca[None, :]) ** 2).argmin(1)].reshape(M, K).to(xdt).float()
     ref = oracle.linear_dequant_reference(q, packed, bits, cb, N, K, bias)
     assert oracle.rel_err(y, ref) <= TOL, oracle.rel_err(y, ref)
 

@@ -71,6 +71,7 @@ _SIGS = {
     "dimq_conv2d_lut_q": (_int, [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _int, _i64, _dbl, _vp,
                                  _int, _i64] + [_i64] * 11 + [_int, _dbl, _i64, _vp, _int, _vp]),
     "dimq_layer_norm": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp, _int, _dbl, _vp, _vp]),
+    "dimq_layer_norm_ex": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp, _int, _dbl, _vp, _int, _vp]),
     "dimq_max_pool2d_nhwc": (_int, [_vp, _int] + [_i64] * 10 + [_vp, _vp]),
     "dimq_pack_bits": (_int, [_vp, _i64, _int, _vp, _vp]),
     "dimq_unpack_bits": (_int, [_vp, _i64, _i64, _int, _vp, _vp]),
@@ -618,8 +619,9 @@ def conv2d_codebook_impl(x, packed_w, codebook, bits, bias, out_channels, in_cha
     return y
 
 
-def layer_norm_impl(x, normalized_size, weight, bias, eps):
-    """LayerNorm over the last dimension (support op of the ViT workload)."""
+def layer_norm_impl(x, normalized_size, weight, bias, eps, out_dtype=None):
+    """LayerNorm over the last dimension (support op of the ViT workload); output in out_dtype (fp16 / bf16,
+    default x's dtype)."""
     _require_cuda(x, "layer_norm expects CUDA input")
     if x.dtype not in (torch.float16, torch.bfloat16):
         raise RuntimeError("layer_norm expects fp16 or bf16 input")
@@ -641,10 +643,13 @@ def layer_norm_impl(x, normalized_size, weight, bias, eps):
     b = bias.contiguous() if bias is not None else None
     if w is not None or b is not None:
         wdt = _dtype(w if w is not None else b)
-    y = torch.empty(xv.shape, dtype=x.dtype, device=x.device)
+    odt = x.dtype if out_dtype is None else out_dtype
+    if odt not in (torch.float16, torch.bfloat16):
+        raise RuntimeError("layer_norm writes fp16 or bf16 output")
+    y = torch.empty(xv.shape, dtype=odt, device=x.device)
     with torch.cuda.device(x.device):
-        _check(lib.dimq_layer_norm(_ptr(xv), _dtype(xv), xv.shape[0], D, xv.stride(0), _ptr(w), _ptr(b), wdt,
-                                   float(eps), _ptr(y), _stream(x.device)))
+        _check(lib.dimq_layer_norm_ex(_ptr(xv), _dtype(xv), xv.shape[0], D, xv.stride(0), _ptr(w), _ptr(b), wdt,
+                                      float(eps), _ptr(y), _dtype(y), _stream(x.device)))
     return y.view(x.shape)
 
 
@@ -707,7 +712,8 @@ _SCHEMAS = {
                             "Tensor act_centers, Tensor? bias, int out_features, int in_features, "
                             "ScalarType? out_dtype=None, int variant=0) -> Tensor", linear_codebook_act_impl),
     # support op of the end-to-end ViT workload
-    "layer_norm": ("layer_norm(Tensor x, int normalized_size, Tensor? weight, Tensor? bias, float eps) -> Tensor",
+    "layer_norm": ("layer_norm(Tensor x, int normalized_size, Tensor? weight, Tensor? bias, float eps, "
+                   "ScalarType? out_dtype=None) -> Tensor",
                    layer_norm_impl),
     "max_pool2d_nhwc": ("max_pool2d_nhwc(Tensor x, int kernel_h, int kernel_w, int stride_h, int stride_w, int pad_h, "
                         "int pad_w) -> Tensor", max_pool2d_impl),

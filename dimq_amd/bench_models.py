@@ -127,9 +127,14 @@ def vit_b16(seed: int = 3) -> ViT:
     return m
 
 
-def quantize_vit(model: ViT, bits: int = 4, out_dtype: torch.dtype = torch.bfloat16) -> ViT:
+def quantize_vit(model: ViT, bits: int = 4, out_dtype: torch.dtype = torch.bfloat16, fp16_links: bool = True) -> ViT:
     """cfg4: qkv / proj / fc1 / fc2 -> weight-only codebook layers (per-output-channel codebooks);
-    the LayerNorms -> DIMQLayerNorm (the HIP LayerNorm kernel, same parameters)."""
+    the LayerNorms -> DIMQLayerNorm (the HIP LayerNorm kernel, same parameters).
+
+    fp16_links: the tensors that only feed a codebook GEMM -- ln_1 -> qkv, ln_2 -> fc1 and fc1 (GELU) -> fc2 --
+    are written in fp16 instead of bf16 (one rounding of the same fp32 result, with three more mantissa bits), so
+    those GEMMs stage their activations without a bf16 -> fp16 conversion; the residual stream, attention and the
+    head stay bf16."""
     def pick(name, module):
         leaf = name.rsplit(".", 1)[-1]
         return bits if leaf in ("qkv", "proj", "fc1", "fc2") else None
@@ -140,7 +145,11 @@ def quantize_vit(model: ViT, bits: int = 4, out_dtype: torch.dtype = torch.bfloa
             parts = name.split(".")
             for part in parts[:-1]:
                 parent = parent._modules[part]
-            parent._modules[parts[-1]] = DIMQLayerNorm.from_layer_norm(mod)
+            link = fp16_links and parts[-1] in ("ln_1", "ln_2")
+            parent._modules[parts[-1]] = DIMQLayerNorm.from_layer_norm(mod, torch.float16 if link else None)
+    if fp16_links:
+        for blk in model.blocks:
+            blk.fc1.out_dtype = torch.float16
     return model
 
 

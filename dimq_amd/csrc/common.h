@@ -169,6 +169,52 @@ __device__ __forceinline__ void load_cb_row(const void* cb, int dt, int64_t row,
   for (int j = 0; j < E; ++j) v[j] = j < size ? v[j] : 0.0f;
 }
 
+// load_cb_row in two halves for kernels that issue their other loads behind
+// it: cb_row_issue only issues the row's raw loads (no conversion, so no wait
+// on them), cb_row_finish converts later, once the loads issued after it are
+// in flight too.
+template <int E>
+struct CbRaw {
+  uint32_t w[2 * E];  // entry j: w[j] (32- and 16-bit dtypes), w[2j], w[2j+1] (fp64)
+};
+
+template <int E>
+__device__ __forceinline__ void cb_row_issue(const void* cb, int dt, int64_t row, int size, CbRaw<E>& r) {
+  const int64_t base = row * size;
+#pragma unroll
+  for (int j = 0; j < 2 * E; ++j) r.w[j] = 0;
+  if (dt == DIMQ_F32) {
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(cb) + base;
+#pragma unroll
+    for (int j = 0; j < E; ++j) r.w[j] = p[j < size ? j : size - 1];
+  } else if (dt == DIMQ_F16 || dt == DIMQ_BF16) {
+    const uint16_t* p = reinterpret_cast<const uint16_t*>(cb) + base;
+#pragma unroll
+    for (int j = 0; j < E; ++j) r.w[j] = p[j < size ? j : size - 1];
+  } else {
+    const uint2* p = reinterpret_cast<const uint2*>(cb) + base;
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      const uint2 d = p[j < size ? j : size - 1];
+      r.w[2 * j] = d.x;
+      r.w[2 * j + 1] = d.y;
+    }
+  }
+}
+
+template <int E>
+__device__ __forceinline__ void cb_row_finish(const CbRaw<E>& r, int dt, int size, float (&v)[E]) {
+#pragma unroll
+  for (int j = 0; j < E; ++j) {
+    float f;
+    if (dt == DIMQ_F32) f = __uint_as_float(r.w[j]);
+    else if (dt == DIMQ_F16) f = f16_bits_to_float(r.w[j]);
+    else if (dt == DIMQ_BF16) f = bf16_bits_to_float(r.w[j]);
+    else f = static_cast<float>(__hiloint2double(static_cast<int>(r.w[2 * j + 1]), static_cast<int>(r.w[2 * j])));
+    v[j] = j < size ? f : 0.0f;
+  }
+}
+
 __device__ __forceinline__ void store_from_float(void* p, int dt, int64_t i, float v) {
   switch (dt) {
     case DIMQ_F32: reinterpret_cast<float*>(p)[i] = v; break;

@@ -9,16 +9,16 @@
 // write the same cache line.
 //
 // Schedule of a work-group:
-//   1. each lane loads its output channel's packed weights and codebook row,
-//      and every thread issues the loads of its share of the input rows: stage
-//      A = the halo rows of the first round of blocks, stage B = the rest;
-//   2. while those loads are in flight, each lane decodes its 36 weight
-//      fragments into VGPRs (resident for the whole work-group);
-//   3. stage A is transposed NCHW -> [row][col][channel] fp16 into LDS
-//      (8x8 transposes in registers), barrier, round 0 runs (one block-half
-//      per wave) while the other waves commit stage B, barrier, the remaining
-//      blocks run two accumulator chains per wave;
-//   4. each finished 32x32 block goes through a wave-private LDS area and
+//   1. each lane loads its output channel's packed weights and codebook row
+//      and decodes its 36 weight fragments into VGPRs (resident for the
+//      whole work-group), then every thread requests its share of stage A
+//      (the halo rows of the first round of blocks);
+//   2. stage A is transposed NCHW -> [row][col][channel] fp16 into LDS
+//      (8x8 transposes in registers), barrier, the loads of stage B (the
+//      remaining rows) go out, round 0 runs (one block-half per wave), stage B
+//      is committed, barrier, the remaining blocks run two accumulator chains
+//      per wave;
+//   3. each finished 32x32 block goes through a wave-private LDS area and
 //      leaves as non-temporal 16-byte stores, 8 channels x 128 bytes per
 //      instruction: the output is written once and never re-read here, and
 //      streaming it past the L2 keeps the 25 MB fp32 output of a cfg2 call
@@ -58,9 +58,12 @@ __host__ __device__ inline BandPart band_part(int nblk, int parts, int part, int
 }
 
 // Staging task: (channel octet co, input row r of the stage, 8 columns q):
-// eight 16-byte loads, one per channel of the octet.
+// eight 16-byte loads, one per channel of the octet.  A row outside the image
+// loads row 0 and is written as zeros at commit (zeroing the registers here
+// would make every stage wait for its loads before the next is issued).
 struct BandTask {
   uint4 v[8];
+  bool live;
 };
 
 __device__ __forceinline__ void band_issue(const HaloArgs& p, int b, int ih_first, int t, int tasks, BandTask& tk) {
@@ -68,15 +71,12 @@ __device__ __forceinline__ void band_issue(const HaloArgs& p, int b, int ih_firs
   const int tt = t < tasks ? t : 0;
   const int co = tt & 7, rest = tt >> 3, q = rest % qn, r = rest / qn;
   const int ih = ih_first + r;
-  const bool live = t < tasks && ih >= 0 && ih < p.H;
-  const int ihc = live ? ih : 0;
+  tk.live = t < tasks && ih >= 0 && ih < p.H;
+  const int ihc = tk.live ? ih : 0;
   const uint16_t* src =
       reinterpret_cast<const uint16_t*>(p.x) + (((int64_t)b * p.C + 8 * co) * p.H + ihc) * p.W + 8 * q;
 #pragma unroll
   for (int c = 0; c < 8; ++c) tk.v[c] = *reinterpret_cast<const uint4*>(src + (int64_t)c * p.H * p.W);
-#pragma unroll
-  for (int c = 0; c < 8; ++c)
-    if (!live) tk.v[c] = make_uint4(0, 0, 0, 0);
 }
 
 // Halo row r0 + r of task t: pixels 8q .. 8q + 7 (halo columns + 1 for the
@@ -96,8 +96,9 @@ __device__ __forceinline__ void band_commit(const HaloArgs& p, int r0, int t, in
   for (int j = 0; j < 8; ++j) {
     // pixel j: channels 2w, 2w+1 from half (j & 1) of word j / 2 of rows 2w, 2w+1
     const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-    const uint4 o = make_uint4(perm(in[1][j >> 1], in[0][j >> 1], sel), perm(in[3][j >> 1], in[2][j >> 1], sel),
-                               perm(in[5][j >> 1], in[4][j >> 1], sel), perm(in[7][j >> 1], in[6][j >> 1], sel));
+    const uint4 o = tk.live ? make_uint4(perm(in[1][j >> 1], in[0][j >> 1], sel), perm(in[3][j >> 1], in[2][j >> 1], sel),
+                                         perm(in[5][j >> 1], in[4][j >> 1], sel), perm(in[7][j >> 1], in[6][j >> 1], sel))
+                            : make_uint4(0, 0, 0, 0);
     *reinterpret_cast<uint4*>(&halo[(r * p.IW_t + 8 * q + j + 1) * CP + 8 * co]) = o;
   }
 }
@@ -174,22 +175,25 @@ __global__ __launch_bounds__(kBandThreads, 1) void conv_band_kernel(const HaloAr
   const int ocl = oc0 + 32 * wn + col;
   float* park = reinterpret_cast<float*>(halo + (size_t)p.IH_t * p.IW_t * CP) + wave * kParkFloats;
 
-  // this lane's codebook row and packed weights
-  float cbv[E];
-  load_cb_row<E>(p.cb, p.cb_dt, p.cb_rows == 1 ? 0 : min(ocl, p.OC - 1), p.cb_size, cbv);
+  // this lane's codebook row, bias and packed weights first, decoded before
+  // any input row is requested: with every load in flight at once the weights
+  // come back no sooner than the rows (measured: the first MFMA ~1 us later)
+  CbRaw<E> cbraw;
+  cb_row_issue<E>(p.cb, p.cb_dt, p.cb_rows == 1 ? 0 : min(ocl, p.OC - 1), p.cb_size, cbraw);
+  const bool has_bias = p.bias && ocl < p.OC;
+  CbRaw<1> braw{};
+  if (has_bias) cb_row_issue<1>(p.bias, p.bias_dt, ocl, 1, braw);
   uint32_t wreg[WPL];
   {
     const uint32_t* src = p.kw + ((int64_t)min(ocl, p.OC - 1) * 2 + g) * WPL;
 #pragma unroll
     for (int w = 0; w < WPL; ++w) wreg[w] = src[w];
   }
-  const float bv = (p.bias && ocl < p.OC) ? load_as_float(p.bias, p.bias_dt, ocl) : 0.0f;
-
-  const int tA = bp.ra * p.W, tB = (bp.IH - bp.ra) * p.W;  // 8 * rows * W / 8
-  BandTask tka, tkb;
-  band_issue(p, b, ih_first, tid, tA, tka);
-  band_issue(p, b, ih_first + bp.ra, tid, tB, tkb);
-
+  float cbv[E];
+  cb_row_finish<E>(cbraw, p.cb_dt, p.cb_size, cbv);
+  float bvv[1];
+  cb_row_finish<1>(braw, p.bias_dt, 1, bvv);
+  const float bv = has_bias ? bvv[0] : 0.0f;
   CodebookRegs<BITS> cbr;
   const int e = planes_from_lds<BITS, false>(cbv, cbr, cbr);
   const float scale = ldexpf(p.acc_scale, -e);
@@ -201,12 +205,19 @@ __global__ __launch_bounds__(kBandThreads, 1) void conv_band_kernel(const HaloAr
     for (int w = 0; w < BITS; ++w) chunk[w] = wreg[(t >> 2) * BITS + w];
     wf[t] = decode_sub<BITS>(chunk, t & 3, cbr);
   }
+  // then stage A alone (stage B is requested once A is in LDS, and lands
+  // while round 0 runs)
+  __builtin_amdgcn_sched_barrier(0);
+  const int tA = bp.ra * p.W, tB = (bp.IH - bp.ra) * p.W;  // 8 * rows * W / 8
+  BandTask tka, tkb;
+  band_issue(p, b, ih_first, tid, tA, tka);
   band_commit(p, 0, tid, tA, tka, halo);
   for (int t = tid; t < bp.IH * 16; t += kBandThreads) {  // left and right padding columns
     const int co = t & 7, side = (t >> 3) & 1, r = t >> 4;
     *reinterpret_cast<uint4*>(&halo[(r * p.IW_t + (side ? p.IW_t - 1 : 0)) * CP + 8 * co]) = make_uint4(0, 0, 0, 0);
   }
-  lds_barrier();  // stage B's loads stay in flight through round 0
+  lds_barrier();
+  band_issue(p, b, ih_first + bp.ra, tid, tB, tkb);  // in flight through round 0
 
   const int row_step = p.IW_t * CP;
   // nq = 1 or 2 blocks (independent accumulator chains) of this wave
@@ -226,7 +237,10 @@ __global__ __launch_bounds__(kBandThreads, 1) void conv_band_kernel(const HaloAr
     };
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[0][i] = acc[1][i] = 0.0f;
-    constexpr int DEPTH = 4;
+    // fragment reads issued DEPTH MFMAs ahead, the order pinned: left to the
+    // scheduler, the reads trail the MFMAs by one or two and every MFMA waits
+    // for the LDS
+    constexpr int DEPTH = 6;
     half8 xr[DEPTH];
     if (nq == 2) {
       constexpr int U = 2 * T;
@@ -235,7 +249,9 @@ __global__ __launch_bounds__(kBandThreads, 1) void conv_band_kernel(const HaloAr
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         acc[u & 1] = mfma32x32x16(xr[u % DEPTH], wf[u >> 1], acc[u & 1]);
+        __builtin_amdgcn_sched_barrier(0);
         if (u + DEPTH < U) xr[u % DEPTH] = frag((u + DEPTH) >> 1, (u + DEPTH) & 1);
+        __builtin_amdgcn_sched_barrier(0);
       }
     } else {
 #pragma unroll
@@ -243,7 +259,9 @@ __global__ __launch_bounds__(kBandThreads, 1) void conv_band_kernel(const HaloAr
 #pragma unroll
       for (int u = 0; u < T; ++u) {
         acc[0] = mfma32x32x16(xr[u % DEPTH], wf[u], acc[0]);
+        __builtin_amdgcn_sched_barrier(0);
         if (u + DEPTH < T) xr[u % DEPTH] = frag(u + DEPTH, 0);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   };

@@ -1,7 +1,9 @@
 // LayerNorm over the last dimension for the ViT-B/16 workload (its 25
 // LayerNorms, eps 1e-6, bf16 activations): y = (x - mean) * rstd * w + b with
 // mean and variance in fp32 over each row (biased variance, as
-// torch.nn.functional.layer_norm), one rounding to the activation dtype.
+// torch.nn.functional.layer_norm), one rounding to the output dtype (the
+// input's, or fp16 / bf16 for a consumer that wants the other format: the
+// ViT workload's LayerNorms feed fp16 to the codebook GEMMs).
 //
 // One wave per row at a time: lane l holds 16-byte chunks l, l + 64, ... of
 // the row in registers, so the row is read from HBM once; the mean and then
@@ -52,7 +54,7 @@ __device__ __forceinline__ void load8_param(const void* p, int k0, float out[8])
 // keeps its lanes' weight and bias chunks in registers and walks rows
 // row0, row0 + stride, ...; the next row's loads are issued before the
 // current row's reductions.
-template <int XT, int WT, int NCH>
+template <int XT, int WT, int YT, int NCH>
 __global__ __launch_bounds__(256) void layer_norm_kernel(const void* __restrict__ x, int64_t ldx, int64_t rows, int D,
                                                          const void* __restrict__ w, const void* __restrict__ b,
                                                          float eps, void* __restrict__ y) {
@@ -120,8 +122,8 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const void* __restrict_
       uint32_t o[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        o[j] = to_bits16((f[c][2 * j] - mean) * rstd * wv[c][2 * j] + bv[c][2 * j], XT) |
-               (to_bits16((f[c][2 * j + 1] - mean) * rstd * wv[c][2 * j + 1] + bv[c][2 * j + 1], XT) << 16);
+        o[j] = to_bits16((f[c][2 * j] - mean) * rstd * wv[c][2 * j] + bv[c][2 * j], YT) |
+               (to_bits16((f[c][2 * j + 1] - mean) * rstd * wv[c][2 * j + 1] + bv[c][2 * j + 1], YT) << 16);
       }
       *reinterpret_cast<uint4*>(yr + 8 * q) = make_uint4(o[0], o[1], o[2], o[3]);
     }
@@ -130,27 +132,27 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const void* __restrict_
   }
 }
 
-template <int XT, int WT>
+template <int XT, int WT, int YT>
 void launch_ln(const void* x, int64_t ldx, int64_t rows, int D, const void* w, const void* b, float eps, void* y,
                hipStream_t s) {
   // about 3 rows per wave at the ViT shape (12,608 rows): 1024 work-groups of 4 waves
   const int64_t want = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
   const dim3 grid(static_cast<unsigned>(want < 1024 ? want : 1024));
   if (D <= 512)
-    hipLaunchKernelGGL((layer_norm_kernel<XT, WT, 1>), grid, dim3(256), 0, s, x, ldx, rows, D, w, b, eps, y);
+    hipLaunchKernelGGL((layer_norm_kernel<XT, WT, YT, 1>), grid, dim3(256), 0, s, x, ldx, rows, D, w, b, eps, y);
   else if (D <= 1024)
-    hipLaunchKernelGGL((layer_norm_kernel<XT, WT, 2>), grid, dim3(256), 0, s, x, ldx, rows, D, w, b, eps, y);
+    hipLaunchKernelGGL((layer_norm_kernel<XT, WT, YT, 2>), grid, dim3(256), 0, s, x, ldx, rows, D, w, b, eps, y);
   else
-    hipLaunchKernelGGL((layer_norm_kernel<XT, WT, 4>), grid, dim3(256), 0, s, x, ldx, rows, D, w, b, eps, y);
+    hipLaunchKernelGGL((layer_norm_kernel<XT, WT, YT, 4>), grid, dim3(256), 0, s, x, ldx, rows, D, w, b, eps, y);
 }
 
-template <int XT>
+template <int XT, int YT>
 void launch_ln_w(const void* x, int64_t ldx, int64_t rows, int D, const void* w, const void* b, int wdt, float eps,
                  void* y, hipStream_t s) {
   switch (wdt) {
-    case DIMQ_F32: launch_ln<XT, DIMQ_F32>(x, ldx, rows, D, w, b, eps, y, s); break;
-    case DIMQ_F16: launch_ln<XT, DIMQ_F16>(x, ldx, rows, D, w, b, eps, y, s); break;
-    default: launch_ln<XT, DIMQ_BF16>(x, ldx, rows, D, w, b, eps, y, s); break;
+    case DIMQ_F32: launch_ln<XT, DIMQ_F32, YT>(x, ldx, rows, D, w, b, eps, y, s); break;
+    case DIMQ_F16: launch_ln<XT, DIMQ_F16, YT>(x, ldx, rows, D, w, b, eps, y, s); break;
+    default: launch_ln<XT, DIMQ_BF16, YT>(x, ldx, rows, D, w, b, eps, y, s); break;
   }
 }
 
@@ -159,10 +161,11 @@ void launch_ln_w(const void* x, int64_t ldx, int64_t rows, int D, const void* w,
 
 using namespace dimq;
 
-extern "C" int dimq_layer_norm(const void* x, int x_dtype, int64_t rows, int64_t dim, int64_t ldx,
-                               const void* weight, const void* bias, int wb_dtype, double eps, void* y,
-                               void* stream) {
+extern "C" int dimq_layer_norm_ex(const void* x, int x_dtype, int64_t rows, int64_t dim, int64_t ldx,
+                                  const void* weight, const void* bias, int wb_dtype, double eps, void* y, int y_dtype,
+                                  void* stream) {
   DIMQ_CHECK(x_dtype == DIMQ_F16 || x_dtype == DIMQ_BF16, "layer_norm expects fp16 or bf16 input");
+  DIMQ_CHECK(y_dtype == DIMQ_F16 || y_dtype == DIMQ_BF16, "layer_norm writes fp16 or bf16 output");
   DIMQ_CHECK(rows >= 0 && dim > 0, "layer_norm dimensions must be positive");
   DIMQ_CHECK(dim % 8 == 0 && dim <= 2048, "layer_norm supports a normalized size that is a multiple of 8, at most 2048");
   DIMQ_CHECK(ldx >= dim && ldx % 8 == 0, "layer_norm row stride must be a multiple of 8 and at least dim");
@@ -175,9 +178,21 @@ extern "C" int dimq_layer_norm(const void* x, int x_dtype, int64_t rows, int64_t
   DIMQ_CHECK(rows / kRowsPerBlock < (int64_t)1 << 31, "layer_norm: too many rows for one launch");
   if (rows == 0) return DIMQ_OK;
   const hipStream_t s = as_stream(stream);
-  if (x_dtype == DIMQ_F16)
-    launch_ln_w<DIMQ_F16>(x, ldx, rows, (int)dim, weight, bias, wb_dtype, (float)eps, y, s);
+  const float e = static_cast<float>(eps);
+  const int D = static_cast<int>(dim);
+  if (x_dtype == DIMQ_F16 && y_dtype == DIMQ_F16)
+    launch_ln_w<DIMQ_F16, DIMQ_F16>(x, ldx, rows, D, weight, bias, wb_dtype, e, y, s);
+  else if (x_dtype == DIMQ_F16)
+    launch_ln_w<DIMQ_F16, DIMQ_BF16>(x, ldx, rows, D, weight, bias, wb_dtype, e, y, s);
+  else if (y_dtype == DIMQ_F16)
+    launch_ln_w<DIMQ_BF16, DIMQ_F16>(x, ldx, rows, D, weight, bias, wb_dtype, e, y, s);
   else
-    launch_ln_w<DIMQ_BF16>(x, ldx, rows, (int)dim, weight, bias, wb_dtype, (float)eps, y, s);
+    launch_ln_w<DIMQ_BF16, DIMQ_BF16>(x, ldx, rows, D, weight, bias, wb_dtype, e, y, s);
   return check_launch("layer_norm");
+}
+
+extern "C" int dimq_layer_norm(const void* x, int x_dtype, int64_t rows, int64_t dim, int64_t ldx,
+                               const void* weight, const void* bias, int wb_dtype, double eps, void* y,
+                               void* stream) {
+  return dimq_layer_norm_ex(x, x_dtype, rows, dim, ldx, weight, bias, wb_dtype, eps, y, x_dtype, stream);
 }

@@ -233,13 +233,16 @@ class DIMQLayerNorm(nn.LayerNorm):
     dict as nn.LayerNorm; other inputs raise: the CPU reference model converts
     it back to nn.LayerNorm (torch's own op)."""
 
+    out_dtype: torch.dtype | None = None  # the output's dtype (fp16 / bf16); None: the input's
+
     @classmethod
-    def from_layer_norm(cls, ln: nn.LayerNorm) -> "DIMQLayerNorm":
+    def from_layer_norm(cls, ln: nn.LayerNorm, out_dtype: torch.dtype | None = None) -> "DIMQLayerNorm":
         if len(ln.normalized_shape) != 1:
             raise ValueError("DIMQLayerNorm normalizes over the last dimension only")
         new = cls(ln.normalized_shape[0], eps=ln.eps, elementwise_affine=ln.elementwise_affine,
                   bias=ln.bias is not None, device=ln.weight.device if ln.weight is not None else None,
                   dtype=ln.weight.dtype if ln.weight is not None else None)
+        new.out_dtype = out_dtype
         if ln.weight is not None:
             new.weight.data.copy_(ln.weight.data)
         if ln.bias is not None:
@@ -249,7 +252,7 @@ class DIMQLayerNorm(nn.LayerNorm):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if not x.is_cuda:
             raise RuntimeError("DIMQLayerNorm runs on CUDA (HIP) tensors only")
-        return ops.layer_norm(x, self.weight, self.bias, self.eps)
+        return ops.layer_norm(x, self.weight, self.bias, self.eps, self.out_dtype)
 
 
 class DIMQMaxPool2d(nn.MaxPool2d):

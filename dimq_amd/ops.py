@@ -298,10 +298,11 @@ def dimq_conv2d_lut_q(xq: torch.Tensor, packed_weight: torch.Tensor, codebook: t
 
 
 def layer_norm(x: torch.Tensor, weight: torch.Tensor | None, bias: torch.Tensor | None,
-               eps: float = 1e-5) -> torch.Tensor:
-    """LayerNorm over the last dimension on the HIP kernel (fp16/bf16 x; the ViT workload's LayerNorms)."""
+               eps: float = 1e-5, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """LayerNorm over the last dimension on the HIP kernel (fp16/bf16 x; the ViT workload's LayerNorms); the
+    output in out_dtype (fp16 / bf16, default x's dtype)."""
     require_extension()
-    return torch.ops.dimq.layer_norm(x, int(x.shape[-1]), weight, bias, float(eps))
+    return torch.ops.dimq.layer_norm(x, int(x.shape[-1]), weight, bias, float(eps), out_dtype)
 
 
 def max_pool2d_nhwc(x: torch.Tensor, kernel_size, stride=None, padding=0) -> torch.Tensor:

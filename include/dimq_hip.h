@@ -378,6 +378,11 @@ int dimq_conv2d_codebook_ex(const void* x, int x_dtype, int x_layout, int64_t B,
  * dim % 8 == 0, dim <= 2048, 16-byte aligned x and y. */
 int dimq_layer_norm(const void* x, int x_dtype, int64_t rows, int64_t dim, int64_t ldx, const void* weight,
                     const void* bias, int wb_dtype, double eps, void* y, void* stream);
+/* dimq_layer_norm with the output in y_dtype (fp16 or bf16) instead of x's
+ * dtype: one rounding of the fp32 result to y_dtype (the ViT workload feeds
+ * fp16 to its codebook GEMMs). */
+int dimq_layer_norm_ex(const void* x, int x_dtype, int64_t rows, int64_t dim, int64_t ldx, const void* weight,
+                       const void* bias, int wb_dtype, double eps, void* y, int y_dtype, void* stream);
 
 /* 2-D max pooling over channels-last activations (the ResNet-18 workload's
  * stem pool; the reference's ResNet runs torch's max_pool2d, torchvision

@@ -65,17 +65,19 @@ def test_resnet18_forward_vs_dequant_reference(gpu):
 # ---------------------------------------------------------------- BASELINE cfg4 at its real shapes
 @pytest.mark.parametrize("name,N,K,epi", [("qkv", 2304, 768, None), ("proj", 768, 768, "residual"),
                                           ("fc1", 3072, 768, "gelu"), ("fc2", 768, 3072, "residual")])
-@pytest.mark.parametrize("out", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("out,xdt", [(torch.float32, torch.bfloat16), (torch.bfloat16, torch.bfloat16),
+                                     (torch.bfloat16, torch.float16), (torch.float16, torch.float16)])
 @torch.no_grad()
-def test_vit_linear_shapes_full_size(gpu, name, N, K, epi, out):
-    """The four ViT-B/16 Linears at M = 64 x 197 = 12,608 tokens, bf16 activations, 4-bit per-channel
+def test_vit_linear_shapes_full_size(gpu, name, N, K, epi, out, xdt):
+    """The four ViT-B/16 Linears at M = 64 x 197 = 12,608 tokens, bf16 or fp16 activations (the model's fp16
+    links: LayerNorm -> qkv / fc1, fc1 -> fc2), 4-bit per-channel
     codebooks of N(0, 0.02) weights with the model's fused epilogue (GELU after fc1, the residual stream
     added after proj / fc2), against dequantize-then-F.linear in fp32 on the CPU (quant/dimq_wrapper.py:237-240,
     reference.py:91-110)."""
     from dimq_amd import ops
     from dimq_amd.codebook import init_centers_per_channel
     from dimq_amd.export import pack_indices
-    announce(f"vit {name} M=12608 N={N} K={K} epi={epi} out={out}")
+    announce(f"vit {name} M=12608 N={N} K={K} epi={epi} out={out} x={xdt}")
     g = torch.Generator().manual_seed(N + K)
     M = 64 * 197
     w = torch.randn(N, K, generator=g) * 0.02
@@ -83,7 +85,7 @@ def test_vit_linear_shapes_full_size(gpu, name, N, K, epi, out):
     idx = ((w[:, :, None] - cb[:, None, :]) ** 2).argmin(dim=2).to(torch.uint8)
     packed = pack_indices(idx, 4)
     bias = torch.randn(N, generator=g) * 0.02
-    x = torch.randn(M, K, generator=g).bfloat16()
+    x = torch.randn(M, K, generator=g).to(xdt)
     res = (torch.randn(M, N, generator=g) * 0.5).bfloat16() if epi == "residual" else None
     y = ops.dimq_linear_codebook(x.to(gpu), packed.to(gpu), cb.to(gpu), 4, bias.to(gpu), N, K, out_dtype=out,
                                  residual=None if res is None else res.to(gpu),
@@ -93,7 +95,7 @@ def test_vit_linear_shapes_full_size(gpu, name, N, K, epi, out):
         ref = ref + res.float()
     elif epi == "gelu":
         ref = torch.nn.functional.gelu(ref)
-    tol = 2e-3 if out == torch.float32 else 8e-3  # a bf16 output alone rounds at 2^-9 relative
+    tol = {torch.float32: 2e-3, torch.float16: 2e-3}.get(out, 8e-3)  # a bf16 output alone rounds at 2^-9 relative
     err = oracle.rel_err(y.float().cpu(), ref)
     assert err <= tol, err
 

@@ -892,6 +892,12 @@ def test_layer_norm_vs_torch_fp32(gpu, rows, D, dt):
     ulp = 2.0 ** -8 if dt == torch.bfloat16 else 2.0 ** -11  # half an output ulp is the rounding bound
     assert y.dtype == dt and y.shape == x.shape
     assert ((y.float() - ref).abs() <= ulp * ref.abs() + 1e-4).all()
+    # the other 16-bit output format: the same fp32 result, rounded once to it
+    odt = torch.float16 if dt == torch.bfloat16 else torch.bfloat16
+    y2 = ops.layer_norm(x.to(gpu), w.to(gpu), b.to(gpu), 1e-6, out_dtype=odt).cpu()
+    ulp2 = 2.0 ** -8 if odt == torch.bfloat16 else 2.0 ** -11
+    assert y2.dtype == odt and y2.shape == x.shape
+    assert ((y2.float() - ref).abs() <= ulp2 * ref.abs() + 1e-4).all()
 
 
 def test_layer_norm_strided_rows_and_module(gpu):

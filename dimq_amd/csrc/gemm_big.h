@@ -679,17 +679,9 @@ __global__ __launch_bounds__(256) void gemm_deep_kernel(const GemmArgs p) {
   const int64_t m0 = mt * BM;
   const int64_t n0 = nt * BN;
 
-  stage_codebook<E>(p.cb, p.cb_dt, p.cb_rows, p.cb_size, n0, BN, p.N, cbs, tid, 256);
-  if (tid < BN) ebias[tid] = (p.bias && n0 + tid < p.N) ? load_as_float(p.bias, p.bias_dt, n0 + tid) : 0.0f;
-  __syncthreads();
-  CodebookRegs<BITS> cb;
-  float rscale;
   const int nl = wave * 32 + col;  // this lane's weight row within the tile
-  {
-    const int rl = (p.cb_rows == 1) ? 0 : nl;
-    const int e = planes_from_lds<BITS, false>(cbs + rl * E, cb, cb);
-    rscale = ldexpf(p.acc_scale, -e);
-  }
+  CodebookRegs<BITS> cb;           // set in the prologue, once the first stages' loads are out
+  float rscale = 1.0f;
 
   int64_t aoff[A_TASKS];
   int alds[A_TASKS];
@@ -769,12 +761,21 @@ __global__ __launch_bounds__(256) void gemm_deep_kernel(const GemmArgs p) {
     }
   };
 
-  // prologue: weight stages 0..2 and activation stages 0, 1 in flight
+  // prologue: weight stages 0..2 and activation stages 0, 1 in flight, then
+  // the codebook rows and bias (their latency overlaps the stages')
   dma_b(0, 0);
   dma_b(1, 1);
   dma_b(2, 2);
   issue_a(0, ra0);
   issue_a(1, ra1);
+  stage_codebook<E>(p.cb, p.cb_dt, p.cb_rows, p.cb_size, n0, BN, p.N, cbs, tid, 256);
+  if (tid < BN) ebias[tid] = (p.bias && n0 + tid < p.N) ? load_as_float(p.bias, p.bias_dt, n0 + tid) : 0.0f;
+  __syncthreads();
+  {
+    const int rl = (p.cb_rows == 1) ? 0 : nl;
+    const int e = planes_from_lds<BITS, false>(cbs + rl * E, cb, cb);
+    rscale = ldexpf(p.acc_scale, -e);
+  }
   commit_a(0, ra0, true);  // waits for stage 0 (and the weight stages before it); range guard
   issue_a(2, ra0);
   __syncthreads();

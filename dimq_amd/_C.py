@@ -101,6 +101,14 @@ _SIGS = {
     "dimq_conv2d_codebook_ex": (_int, [_vp, _int, _int, _i64, _i64, _i64, _i64, _vp, _i64, _int, _vp, _i64, _vp,
                                        _int, _i64, _i64, _vp, _int] + [_i64] * 10 +
                                 [_vp, _int, _int, _vp, _int, _int, _int, _vp]),
+    "dimq_qat_workspace_bytes": (_i64, [_i64, _i64]),
+    "dimq_softmin_loss_forward": (_int, [_vp, _int, _i64, _vp, _i64, _dbl, _int, _vp, _vp, _vp, _i64, _vp]),
+    "dimq_softmin_loss_backward": (_int, [_vp, _int, _i64, _vp, _i64, _dbl, _int, _vp, _vp, _vp, _int, _vp, _vp, _i64,
+                                          _vp]),
+    "dimq_soft_dequantize_forward": (_int, [_vp, _int, _i64, _vp, _i64, _dbl, _vp, _vp, _vp]),
+    "dimq_soft_dequantize_backward": (_int, [_vp, _int, _i64, _vp, _i64, _dbl, _vp, _vp, _int, _vp, _int, _vp, _vp,
+                                             _i64, _vp]),
+    "dimq_separation_loss": (_int, [_vp, _int, _i64, _vp, _i64, _dbl, _dbl, _vp, _vp, _vp, _i64, _vp]),
 }
 
 for _name, (_res, _args) in _SIGS.items():
@@ -729,3 +737,89 @@ def _register() -> torch.library.Library:
 
 
 _LIBRARY = _register()
+
+
+# ---------------------------------------------------------------------------
+# QAT kernels (quant/dimq.py:197-296): host wrappers used by dimq_amd.qat
+def _qat_inputs(w, centers):
+    _require_cuda(w, "QAT kernels expect CUDA weights")
+    _require_cuda(centers, "QAT kernels expect CUDA centers")
+    if w.dtype not in (torch.float32, torch.float16, torch.bfloat16, torch.float64):
+        raise RuntimeError("weights must be fp32, fp16, bf16 or fp64")
+    wc = w.detach().contiguous()
+    c = centers.detach().reshape(-1).float().contiguous()
+    if c.numel() == 0:
+        raise ValueError("centers must be non-empty")
+    if c.numel() > 256:
+        raise RuntimeError("at most 256 centers are supported")
+    return wc, c
+
+
+def _qat_ws(n, K, device):
+    return torch.empty(int(lib.dimq_qat_workspace_bytes(n, K)), dtype=torch.uint8, device=device)
+
+
+def softmin_loss_forward_impl(w, centers, tau, mean):
+    """(loss fp32 scalar, aux [n, 2] fp32: (dmin_i, log s_i) for the backward)."""
+    wc, c = _qat_inputs(w, centers)
+    n = wc.numel()
+    aux = torch.empty((n, 2), dtype=torch.float32, device=wc.device)
+    loss = torch.empty((), dtype=torch.float32, device=wc.device)
+    ws = _qat_ws(n, c.numel(), wc.device)
+    with torch.cuda.device(wc.device):
+        _check(lib.dimq_softmin_loss_forward(_ptr(wc), _dtype(wc), n, _ptr(c), c.numel(), float(tau), int(bool(mean)),
+                                             _ptr(aux), _ptr(loss), _ptr(ws), ws.numel(), _stream(wc.device)))
+    return loss, aux
+
+
+def softmin_loss_backward_impl(w, centers, tau, aux, grad_loss):
+    """(grad_w in w's dtype, grad_centers fp32) of the sum reduction for the upstream scalar grad_loss."""
+    wc, c = _qat_inputs(w, centers)
+    n = wc.numel()
+    g = grad_loss.detach().reshape(()).float().contiguous()
+    gw = torch.empty_like(wc)
+    gc = torch.empty(c.numel(), dtype=torch.float32, device=wc.device)
+    ws = _qat_ws(n, c.numel(), wc.device)
+    with torch.cuda.device(wc.device):
+        _check(lib.dimq_softmin_loss_backward(_ptr(wc), _dtype(wc), n, _ptr(c), c.numel(), float(tau), 0, _ptr(aux),
+                                              _ptr(g), _ptr(gw), _dtype(gw), _ptr(gc), _ptr(ws), ws.numel(),
+                                              _stream(wc.device)))
+    return gw, gc
+
+
+def soft_dequantize_forward_impl(w, centers, tau):
+    wc, c = _qat_inputs(w, centers)
+    n = wc.numel()
+    out = torch.empty_like(wc)
+    aux = torch.empty((n, 2), dtype=torch.float32, device=wc.device)
+    with torch.cuda.device(wc.device):
+        _check(lib.dimq_soft_dequantize_forward(_ptr(wc), _dtype(wc), n, _ptr(c), c.numel(), float(tau), _ptr(out),
+                                                _ptr(aux), _stream(wc.device)))
+    return out, aux
+
+
+def soft_dequantize_backward_impl(w, centers, tau, aux, grad_out):
+    wc, c = _qat_inputs(w, centers)
+    n = wc.numel()
+    go = grad_out.detach().contiguous()
+    gw = torch.empty_like(wc)
+    gc = torch.empty(c.numel(), dtype=torch.float32, device=wc.device)
+    ws = _qat_ws(n, c.numel(), wc.device)
+    with torch.cuda.device(wc.device):
+        _check(lib.dimq_soft_dequantize_backward(_ptr(wc), _dtype(wc), n, _ptr(c), c.numel(), float(tau), _ptr(aux),
+                                                 _ptr(go), _dtype(go), _ptr(gw), _dtype(gw), _ptr(gc), _ptr(ws),
+                                                 ws.numel(), _stream(wc.device)))
+    return gw, gc
+
+
+def separation_loss_impl(w, centers, eta, eps):
+    """(loss fp32 scalar, d loss / d centers fp32) -- the margin uses std(w), no gradient to w."""
+    wc, c = _qat_inputs(w, centers)
+    n = wc.numel()
+    loss = torch.empty((), dtype=torch.float32, device=wc.device)
+    gc = torch.empty(c.numel(), dtype=torch.float32, device=wc.device)
+    ws = _qat_ws(n, c.numel(), wc.device)
+    with torch.cuda.device(wc.device):
+        _check(lib.dimq_separation_loss(_ptr(wc), _dtype(wc), n, _ptr(c), c.numel(), float(eta), float(eps),
+                                        _ptr(loss), _ptr(gc), _ptr(ws), ws.numel(), _stream(wc.device)))
+    return loss, gc

@@ -111,8 +111,9 @@ struct CentreRow {
 };
 
 __device__ __forceinline__ float centre_dist(float x, float c) {
+#pragma clang fp contract(off)  // one rounding of the square, never fused into a later add
   const float diff = x - c;
-  return __fmul_rn(diff, diff);
+  return diff * diff;
 }
 
 // Whole work-group: the row's K (1..256) centres into `r`.

@@ -384,6 +384,51 @@ int dimq_layer_norm(const void* x, int x_dtype, int64_t rows, int64_t dim, int64
 int dimq_layer_norm_ex(const void* x, int x_dtype, int64_t rows, int64_t dim, int64_t ldx, const void* weight,
                        const void* bias, int wb_dtype, double eps, void* y, int y_dtype, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * QAT kernels (the training step before the packed path; quant/dimq.py).
+ * fp32 arithmetic on w.float() and centers (K <= 256 fp32 values on the
+ * device), as the reference; d_ij = (w_i - c_j)^2, p_ij = softmax_j(-d_ij/tau).
+ * Sums over elements go through per-work-group partials in the caller's
+ * workspace (dimq_qat_workspace_bytes) and a fixed-order final pass.
+ * aux: 2 floats per element, (min_j d_ij, log sum_j exp(-(d_ij - min d)/tau)),
+ * written by a forward and read by its backward.
+ * ------------------------------------------------------------------------- */
+int64_t dimq_qat_workspace_bytes(int64_t n, int64_t n_centers);
+
+/* dimq_softmin_loss (quant/dimq.py:244-273): loss = sum_i -tau (logsumexp_j(
+ * -d_ij/tau) - log K), divided by n when mean_reduction ("mean_per_layer");
+ * fp32 scalar into *loss (device). */
+int dimq_softmin_loss_forward(const void* w, int w_dtype, int64_t n, const float* centers, int64_t n_centers,
+                              double tau, int mean_reduction, float* aux, float* loss, void* workspace,
+                              int64_t workspace_bytes, void* stream);
+/* Gradients of the sum reduction for the upstream scalar *grad_loss (device):
+ * grad_w = g sum_j p_ij 2 (w_i - c_j) (nullable, grad_w_dtype),
+ * grad_centers = -2 g sum_i p_ij (w_i - c_j) (fp32).  mean_reduction must be 0:
+ * the mean's gradient is the sum's with g / n. */
+int dimq_softmin_loss_backward(const void* w, int w_dtype, int64_t n, const float* centers, int64_t n_centers,
+                               double tau, int mean_reduction, const float* aux, const float* grad_loss, void* grad_w,
+                               int grad_w_dtype, float* grad_centers, void* workspace, int64_t workspace_bytes,
+                               void* stream);
+
+/* soft_dequantize_weight (quant/dimq.py:224-241): out_i = sum_j p_ij c_j in
+ * w's dtype; and its backward for the upstream grad_out:
+ * grad_w_i = g_i sum_j p_ij (c_j - out_i)(-2 (w_i - c_j)/tau),
+ * grad_c_j = sum_i g_i p_ij (1 + (c_j - out_i) 2 (w_i - c_j)/tau). */
+int dimq_soft_dequantize_forward(const void* w, int w_dtype, int64_t n, const float* centers, int64_t n_centers,
+                                 double tau, void* out, float* aux, void* stream);
+int dimq_soft_dequantize_backward(const void* w, int w_dtype, int64_t n, const float* centers, int64_t n_centers,
+                                  double tau, const float* aux, const void* grad_out, int grad_out_dtype, void* grad_w,
+                                  int grad_w_dtype, float* grad_centers, void* workspace, int64_t workspace_bytes,
+                                  void* stream);
+
+/* separation_loss (quant/dimq.py:276-296): delta = eta * 6 * max(std(w), 1e-12)
+ * / K (population std of w, n >= 1), loss = sum_{a<b} relu(delta -
+ * sqrt((c_a - c_b)^2 + eps))^2 into *loss, and d loss / d centers (nullable;
+ * the margin carries no gradient to w, as the reference's w.detach()). */
+int dimq_separation_loss(const void* w, int w_dtype, int64_t n, const float* centers, int64_t n_centers, double eta,
+                         double eps, float* loss, float* grad_centers, void* workspace, int64_t workspace_bytes,
+                         void* stream);
+
 /* 2-D max pooling over channels-last activations (the ResNet-18 workload's
  * stem pool; the reference's ResNet runs torch's max_pool2d, torchvision
  * resnet18): y[b,oh,ow,c] = max over the window's in-image taps, NaN

@@ -250,3 +250,59 @@ def test_a4_exact_bar_accepts_summation_order_and_rejects_planted_zero_point():
     planted = torch.from_numpy(oracle.linear_lut(x, packed, cb.float(), 0.2, 6, bias, N, K))
     with pytest.raises(AssertionError):
         a4_exact_check(planted, ref, exact, K)
+
+
+# ---------------------------------------------------------------- QAT oracle (oracle/qat.py)
+def test_qat_oracle_closed_forms():
+    """The float64 restatements of quant/dimq.py:224-296 against closed forms that do not retype them."""
+    import math
+    import torch
+    from oracle import qat
+
+    g = torch.Generator().manual_seed(4)
+    w = torch.randn(500, generator=g, dtype=torch.float64) * 0.1
+    # one centre: the softmin term is the plain squared distance, for any tau
+    c1 = torch.tensor([0.03], dtype=torch.float64)
+    for tau in (1e-6, 0.01, 10.0):
+        assert torch.allclose(qat.softmin_loss(w, c1, tau), ((w - 0.03) ** 2).sum(), rtol=1e-12, atol=1e-15)
+    # two centres: min(d) - tau (log1p(exp(-|d1 - d2| / tau)) - log 2) per element
+    c2 = torch.tensor([-0.05, 0.07], dtype=torch.float64)
+    d1, d2 = (w + 0.05) ** 2, (w - 0.07) ** 2
+    for tau in (1e-4, 0.003, 0.5):
+        want = (torch.minimum(d1, d2) - tau * (torch.log1p(torch.exp(-(d1 - d2).abs() / tau)) - math.log(2))).sum()
+        assert torch.allclose(qat.softmin_loss(w, c2, tau), want, rtol=1e-10)
+        assert torch.allclose(qat.softmin_loss(w, c2, tau, "mean_per_layer"), want / w.numel(), rtol=1e-10)
+        # soft dequantization with two centres: a logistic blend
+        p1 = 1.0 / (1.0 + torch.exp(-(d2 - d1) / tau))
+        assert torch.allclose(qat.soft_dequantize(w, c2, tau), p1 * -0.05 + (1 - p1) * 0.07, rtol=1e-10, atol=1e-15)
+    # tau -> 0: the hard nearest-centre distortion; tau -> inf: the mean over the centres
+    c = torch.randn(8, generator=g, dtype=torch.float64) * 0.1
+    d = (w[:, None] - c[None, :]) ** 2
+    assert torch.allclose(qat.softmin_loss(w, c, 1e-12), d.min(dim=1).values.sum(), rtol=1e-9)
+    assert torch.allclose(qat.softmin_loss(w, c, 1e6), d.mean(dim=1).sum(), rtol=1e-6)
+    assert torch.allclose(qat.soft_dequantize(w, c, 1e9), torch.full_like(w, float(c.mean())), rtol=1e-6)
+    nearest = c[d.argmin(dim=1)]
+    assert torch.allclose(qat.soft_dequantize(w, c, 1e-12), nearest)
+    # separation: two centres closer than the margin, and far apart
+    sigma = float(w.std(unbiased=False))
+    for gap in (0.1 * sigma, 10 * sigma):
+        cc = torch.tensor([0.0, gap], dtype=torch.float64)
+        want = max(0.0, 1.5 * 6 * sigma / 2 - math.sqrt(gap * gap + 1e-12)) ** 2
+        assert math.isclose(float(qat.separation_loss(w, cc, 1.5)), want, rel_tol=1e-12, abs_tol=1e-18)
+    assert float(qat.separation_loss(w, c1)) == 0.0
+
+
+def test_qat_oracle_finite_differences():
+    """Autograd of the restatements against finite differences (float64): the gradients the reference gets
+    from torch's autograd."""
+    import torch
+    from oracle import qat
+
+    g = torch.Generator().manual_seed(5)
+    w = (torch.randn(40, generator=g, dtype=torch.float64) * 0.1).requires_grad_()
+    c = (torch.randn(6, generator=g, dtype=torch.float64) * 0.1).requires_grad_()
+    for tau in (1e-3, 0.05):
+        assert torch.autograd.gradcheck(lambda a, b: qat.softmin_loss(a, b, tau), (w, c))
+        assert torch.autograd.gradcheck(lambda a, b: qat.soft_dequantize(a, b, tau), (w, c))
+    cs = torch.tensor([0.0, 0.01, 0.015, 0.3], dtype=torch.float64, requires_grad=True)
+    assert torch.autograd.gradcheck(lambda b: qat.separation_loss(w.detach(), b, 2.0), (cs,))

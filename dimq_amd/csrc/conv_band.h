@@ -9,10 +9,10 @@
 // write the same cache line.
 //
 // Schedule of a work-group:
-//   1. each lane loads its output channel's packed weights and codebook row
-//      and decodes its 36 weight fragments into VGPRs (resident for the
-//      whole work-group), then every thread requests its share of stage A
-//      (the halo rows of the first round of blocks);
+//   1. every thread requests its share of stage A (the halo rows of the
+//      first round of blocks), then each lane loads its output channel's
+//      packed weights and codebook row and decodes its 36 weight fragments
+//      into VGPRs (resident for the whole work-group) while the rows land;
 //   2. stage A is transposed NCHW -> [row][col][channel] fp16 into LDS
 //      (8x8 transposes in registers), barrier, the loads of stage B (the
 //      remaining rows) go out, round 0 runs (one block-half per wave), stage B
@@ -175,9 +175,14 @@ __global__ __launch_bounds__(kBandThreads, 1) void conv_band_kernel(const HaloAr
   const int ocl = oc0 + 32 * wn + col;
   float* park = reinterpret_cast<float*>(halo + (size_t)p.IH_t * p.IW_t * CP) + wave * kParkFloats;
 
-  // this lane's codebook row, bias and packed weights first, decoded before
-  // any input row is requested: with every load in flight at once the weights
-  // come back no sooner than the rows (measured: the first MFMA ~1 us later)
+  // stage A's input rows are requested first, then this lane's codebook row,
+  // bias and packed weights, decoded while the rows land; stage B is requested
+  // only once A is in LDS and lands while round 0 runs.  Measured: with stage B
+  // in flight beside A, or the rows requested after the decode, the first MFMA
+  // starts 1.5-2 us later.
+  const int tA = bp.ra * p.W, tB = (bp.IH - bp.ra) * p.W;  // 8 * rows * W / 8
+  BandTask tka, tkb;
+  band_issue(p, b, ih_first, tid, tA, tka);
   CbRaw<E> cbraw;
   cb_row_issue<E>(p.cb, p.cb_dt, p.cb_rows == 1 ? 0 : min(ocl, p.OC - 1), p.cb_size, cbraw);
   const bool has_bias = p.bias && ocl < p.OC;
@@ -205,12 +210,6 @@ __global__ __launch_bounds__(kBandThreads, 1) void conv_band_kernel(const HaloAr
     for (int w = 0; w < BITS; ++w) chunk[w] = wreg[(t >> 2) * BITS + w];
     wf[t] = decode_sub<BITS>(chunk, t & 3, cbr);
   }
-  // then stage A alone (stage B is requested once A is in LDS, and lands
-  // while round 0 runs)
-  __builtin_amdgcn_sched_barrier(0);
-  const int tA = bp.ra * p.W, tB = (bp.IH - bp.ra) * p.W;  // 8 * rows * W / 8
-  BandTask tka, tkb;
-  band_issue(p, b, ih_first, tid, tA, tka);
   band_commit(p, 0, tid, tA, tka, halo);
   for (int t = tid; t < bp.IH * 16; t += kBandThreads) {  // left and right padding columns
     const int co = t & 7, side = (t >> 3) & 1, r = t >> 4;

@@ -14,6 +14,11 @@ constexpr int64_t kCUs = 256;
 
 }  // namespace
 
+// gemm_pd.hip: the pre-decoded-weight path for large M (weights decoded once
+// per call into the workspace, then an fp16 GEMM fed by global_load_lds).
+int64_t predecoded_ws_bytes(int64_t M, int64_t K, int64_t N, int bits, int x_dtype);
+int launch_predecoded(const GemmArgs& p, int bits, int x_dtype, void* ws, int64_t ws_bytes, hipStream_t s);
+
 // Fast-path tiles need K % 128 == 0, aligned rows/streams and a Linear layout.
 int gemm_fast_tile(int tile, const GemmArgs& p, int bits) {
   if (bits == 8 || p.conv || !p.fast_b || !p.vec_a || p.K % kKM != 0) return tile;
@@ -115,6 +120,10 @@ int linear_codebook_impl(const void* x, int x_dtype, int64_t M, int64_t K, int64
   p.vec_a = aligned(x, 16) && ((ldx * xs) % 16 == 0);
   p.groups = 1;
   if (M == 0 || N == 0) return DIMQ_OK;
+  if (workspace != nullptr && variant != DIMQ_VARIANT_SMALL_M) {
+    const int rc = launch_predecoded(p, bits, x_dtype, workspace, workspace_bytes, s);
+    if (rc >= 0) return rc;
+  }
   const int big = gemm_big_tile(p, bits, x_dtype, variant);
   if (big >= 0) {
     switch (bits) {
@@ -167,9 +176,11 @@ extern "C" int dimq_linear_codebook(const void* x, int x_dtype, int64_t M, int64
 }
 
 // Workspace of dimq_linear_codebook_ex_ws: the decode shapes (M <= 16)
-// whose k range is split over work-groups keep their fp32 partial sums there.
+// whose k range is split over work-groups keep their fp32 partial sums there;
+// large-M shapes with fp16 activations keep the weights decoded to fp16.
 extern "C" int64_t dimq_linear_codebook_workspace_bytes(int64_t M, int64_t K, int64_t N, int bits, int x_dtype) {
-  (void)x_dtype;
+  const int64_t pd = predecoded_ws_bytes(M, K, N, bits, x_dtype);
+  if (pd > 0) return pd;
   if (M <= 0 || M > 16 || K <= 0 || N <= 0 || !(bits == 2 || bits == 3 || bits == 4)) return 0;
   GemmArgs p{};
   p.M = M;
@@ -188,7 +199,7 @@ extern "C" int dimq_linear_codebook_ex_ws(const void* x, int x_dtype, int64_t M,
                                           int activation, int variant, void* workspace, int64_t workspace_bytes,
                                           void* stream) {
   DIMQ_CHECK(workspace_bytes >= 0, "workspace_bytes must be non-negative");
-  const bool decode = M >= 1 && M <= 16;
+  const bool decode = (M >= 1 && M <= 16) || predecoded_ws_bytes(M, K, N, bits, x_dtype) > 0;
   return linear_codebook_checked(x, x_dtype, M, K, packed_w, packed_numel, bits, codebook, cb_dtype, cb_rows, cb_size,
                                  bias, bias_dtype, N, y, y_dtype, residual, residual_dtype, activation, variant,
                                  stream, decode ? workspace : nullptr, decode ? workspace_bytes : 0);

@@ -1,0 +1,423 @@
+// Pre-decoded-weight GEMM for the large-M Linear shapes (ViT-B/16 at
+// M = 12,608): y[M,N] = epilogue(x[M,K] W_hat^T), in two launches.
+//
+//   1. predecode_kernel: the packed b-bit indices (dimq_packed_lut layout,
+//      LSB-first, row-major [N, K]) and the codebook rows -> W_hat as fp16
+//      [N, K] in natural k order, each row scaled by the power of two 2^e of
+//      the register-codebook kernels (max|c| 2^e in [2^14, 2^15), decode.h),
+//      plus the per-row factor acc_scale 2^-e, in the caller's workspace.
+//      Every weight is decoded once per call.  The fused kernels decode it
+//      once per 256-row activation tile (50 times at M 12,608), which rocprof
+//      counters put at about two thirds of their VALU instructions, the VALU
+//      being busy as long as the matrix cores.
+//   2. gemm_pd_kernel: an fp16 x fp16 GEMM whose operands reach LDS through
+//      global_load_lds (16 bytes per lane, no registers held, no VALU in the
+//      main loop), in a ring of S stages of 32 k.  LDS rows are 64 bytes with
+//      their four 16-byte chunks XOR-swizzled by (row >> 2) & 3, so the
+//      16-byte fragment reads of sixteen consecutive rows cover all 64 banks.
+//      Work-group = 8 waves (4 along m x 2 along n) on a 256 x 256 tile, wave
+//      tile 64 x 128, v_mfma_f32_32x32x16_f16 with the weights as the A
+//      operand (rows = output columns n) and the activations as the B operand,
+//      so a lane's accumulator holds 4 consecutive n of one m.  The epilogue
+//      parks each column pass in LDS and stores 8-column runs of rows.
+//
+// fp16 activations only (the model's LayerNorm and fc1 outputs): their values
+// are exact in the fp16 operand, so no range guard is needed.
+#include "gemm_big.h"
+
+namespace dimq {
+namespace {
+
+constexpr int kPdK = 32;  // k (halves) per pipeline stage: 64 bytes of a row
+
+// Below this many activation rows the fused kernels' per-tile decode costs
+// less than the extra launch and the fp16 weight copy.
+constexpr int64_t kPredecodeMinM = 2048;
+
+// The 16-byte chunk c of stage row r lives at r * 64 + ((c ^ pd_swz(r)) << 4):
+// sixteen consecutive rows (the lanes one 16-byte LDS read serves per clock,
+// 256 bytes over gfx950's 64 banks) then hit sixteen distinct 16-byte slots.
+__device__ __forceinline__ int pd_swz(int r) { return (r >> 2) & 3; }
+
+// s_waitcnt vmcnt(n), leaving the other counters alone (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// One global_load_lds of 16 bytes per lane into LDS at byte address lds + 16 * lane.
+// Issued as inline assembly so that the compiler's wait insertion, which
+// would otherwise make every later LDS read wait for all such loads still in
+// flight (it cannot tell the ring's slots apart), leaves the waits to the
+// kernel: wait_vmcnt before the barrier that publishes a stage.
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gptr), "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
+
+constexpr int kPdRows = 2;     // weight rows per predecode work-group
+constexpr int kPdGroups = 16;  // 8-index groups per thread held in registers (K <= 4096 in one pass)
+
+template <int BITS>
+__global__ __launch_bounds__(256) void predecode_kernel(const uint8_t* __restrict__ w, const void* cb, int cb_dt,
+                                                        int64_t cb_rows, int cb_size, int64_t N, int64_t K,
+                                                        float acc_scale, uint16_t* __restrict__ wd,
+                                                        float* __restrict__ rs) {
+  constexpr int E = 1 << BITS;
+  __shared__ float cbs[kPdRows * E];
+  __shared__ uint32_t tab[kPdRows * E];  // fp16 bits of the scaled entries
+  const int tid = threadIdx.x;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kPdRows;
+  const int gpr = static_cast<int>(K >> 3);  // 8-index groups per row (K % 32 == 0)
+  const int nr = N - r0 < kPdRows ? static_cast<int>(N - r0) : kPdRows;
+  const int total = nr * gpr;
+  // group gi = tid + 256 u: row gi / gpr, indices 8 (gi % gpr) .. + 7 = BITS whole bytes
+  auto load_group = [&](int gi) -> uint32_t {
+    const int r = gi / gpr;
+    const uint8_t* src = w + ((((r0 + r) * K) + 8 * (gi - r * gpr)) * BITS >> 3);
+    if constexpr (BITS == 2) return *reinterpret_cast<const uint16_t*>(src);
+    if constexpr (BITS == 4) return *reinterpret_cast<const uint32_t*>(src);
+    return static_cast<uint32_t>(src[0]) | (static_cast<uint32_t>(src[1]) << 8) | (static_cast<uint32_t>(src[2]) << 16);
+  };
+  // the packed words first: their latency overlaps the codebook loads
+  uint32_t v[kPdGroups];
+#pragma unroll
+  for (int u = 0; u < kPdGroups; ++u) {
+    const int gi = tid + 256 * u;
+    v[u] = gi < total ? load_group(gi) : 0u;
+  }
+  if (tid < kPdRows * E) {
+    const int r = tid / E, j = tid - r * E;
+    const int64_t row = cb_rows == 1 ? 0 : (r0 + r < N ? r0 + r : N - 1);
+    cbs[tid] = j < cb_size ? load_as_float(cb, cb_dt, row * cb_size + j) : 0.0f;
+  }
+  __syncthreads();
+  // the scaled fp16 entries (one thread per entry, the row's exponent from the staged row)
+  if (tid < kPdRows * E) {
+    const int r = tid / E;
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < E; ++j) mx = fmaxf(mx, fabsf(cbs[r * E + j]));
+    const int e = cb_exponent(mx);
+    tab[tid] = float_to_f16_bits(ldexpf(cbs[tid], e));
+    if (tid - r * E == 0 && r < nr) rs[r0 + r] = ldexpf(acc_scale, -e);
+  }
+  __syncthreads();
+  auto store_group = [&](int gi, uint32_t x) {
+    const int r = gi / gpr;
+    const uint32_t* t = tab + r * E;
+    uint32_t h[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      h[i] = t[(x >> (2 * i * BITS)) & (E - 1)] | (t[(x >> ((2 * i + 1) * BITS)) & (E - 1)] << 16);
+    *reinterpret_cast<uint4*>(wd + (r0 + r) * K + 8 * (gi - r * gpr)) = make_uint4(h[0], h[1], h[2], h[3]);
+  };
+#pragma unroll
+  for (int u = 0; u < kPdGroups; ++u) {
+    const int gi = tid + 256 * u;
+    if (gi < total) store_group(gi, v[u]);
+  }
+  for (int gi = tid + 256 * kPdGroups; gi < total; gi += 256) store_group(gi, load_group(gi));
+}
+
+template <int WGM, int WGN, int MBLK, int NBLK, int MODE, int S>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs p, const uint16_t* __restrict__ wd,
+                                                                 const float* __restrict__ rs) {
+  constexpr int NT = 64 * WGM * WGN;
+  constexpr int BM = WGM * MBLK * 32;
+  constexpr int BN = WGN * NBLK * 32;
+  constexpr int RSTAGE = (BN + BM) * 64;    // bytes of one stage: weight rows, then activation rows
+  constexpr int LPT = (BN + BM) * 4 / NT;   // 16-byte loads per thread and stage
+  static_assert(LPT * NT == (BN + BM) * 4, "a stage splits evenly over the threads");
+  static_assert(BN % 16 == 0 && BM % 16 == 0, "a wave's load covers 16 rows of one operand");
+  static_assert((S - 1) * LPT < 64, "outstanding loads fit the vmcnt counter");
+  __shared__ __attribute__((aligned(16))) uint8_t sm[S * RSTAGE];
+  // after the main loop: the tile's column factors at the end of the ring
+  float* escale = reinterpret_cast<float*>(sm + S * RSTAGE) - 2 * BN;
+  float* ebias = escale + BN;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 31;
+  const int g = lane >> 5;
+  const int wm = wave / WGN;
+  const int wn = wave - wm * WGN;
+  int64_t mt, nt;
+  tile_coords((p.N + BN - 1) / BN, mt, nt);
+  const int64_t m0 = mt * BM;
+  const int64_t n0 = nt * BN;
+
+  // the tile's column factors first: their loads are then older than every
+  // stage load, so the stage waits below cover them
+  float my_scale = 0.0f, my_bias = 0.0f;
+  if (tid < BN) {
+    const int64_t n = n0 + tid < p.N ? n0 + tid : p.N - 1;
+    my_scale = rs[n];
+    if (p.bias) my_bias = load_as_float(p.bias, p.bias_dt, n);
+  }
+
+  // load j of this thread: the wave's block b = j * (NT / 64) + wave holds
+  // stage rows 16 b .. 16 b + 15 (weight rows first, then activation rows);
+  // lane l fills LDS chunk l & 3 of row 16 b + (l >> 2), i.e. global chunk
+  // (l & 3) ^ swizzle.  Rows past N or M repeat the last row (not stored).
+  const uint16_t* xh = reinterpret_cast<const uint16_t*>(p.x);
+  const uint16_t* src[LPT];
+#pragma unroll
+  for (int j = 0; j < LPT; ++j) {
+    const int row = 16 * (j * (NT / 64) + wave) + (lane >> 2);
+    const int c = (lane & 3) ^ pd_swz(row);
+    if (row < BN) {
+      const int64_t n = n0 + row < p.N ? n0 + row : p.N - 1;
+      src[j] = wd + n * p.K + 8 * c;
+    } else {
+      const int64_t m = m0 + (row - BN) < p.M ? m0 + (row - BN) : p.M - 1;
+      src[j] = xh + m * p.ldx + 8 * c;
+    }
+  }
+  const int64_t nk = p.K / kPdK;
+  const uint32_t smb = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_g*)sm));  // LDS address of the ring
+  auto issue = [&](int64_t kt, int slot) {
+    const int64_t k = (kt < nk ? kt : nk - 1) * kPdK;  // past the end: a repeat, never read
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+      dma16(src[j] + k, smb + slot * RSTAGE + (j * (NT / 64) + wave) * 1024);
+    }
+  };
+
+  floatx16g acc[MBLK][NBLK];
+#pragma unroll
+  for (int mb = 0; mb < MBLK; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NBLK; ++nb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[mb][nb][i] = 0.0f;
+
+  // fragment offsets: rows rbase + col (rbase % 16 == 0) share the swizzle of col
+  const int sw = pd_swz(col);
+  const int fo[2] = {col * 64 + ((g ^ sw) << 4), col * 64 + (((2 + g) ^ sw) << 4)};
+  // fragments of k16 step s (0, 1) of the stage in ring slot `slot`
+  auto load = [&](int slot, int s, half8 (&wf)[NBLK], half8 (&xf)[MBLK]) {
+    const uint8_t* base = sm + slot * RSTAGE;
+#pragma unroll
+    for (int nb = 0; nb < NBLK; ++nb)
+      wf[nb] = *reinterpret_cast<const half8*>(base + (wn * NBLK + nb) * 2048 + fo[s]);
+#pragma unroll
+    for (int mb = 0; mb < MBLK; ++mb)
+      xf[mb] = *reinterpret_cast<const half8*>(base + BN * 64 + (wm * MBLK + mb) * 2048 + fo[s]);
+  };
+  auto mma = [&](const half8 (&wf)[NBLK], const half8 (&xf)[MBLK]) {
+#pragma unroll
+    for (int nb = 0; nb < NBLK; ++nb)
+#pragma unroll
+      for (int mb = 0; mb < MBLK; ++mb) acc[mb][nb] = mfma32(wf[nb], xf[mb], acc[mb][nb]);
+  };
+
+  // Ring of S slots, stage kt in slot kt % S.  Each step's fragment reads are
+  // issued before the previous step's MFMAs, so LDS latency hides behind the
+  // matrix cores; the barrier that publishes stage kt + 1 sits between the
+  // two steps of stage kt, after which slot kt % S (read completely: the
+  // barrier's fence waits for this wave's LDS reads) takes stage kt + S.
+#pragma unroll
+  for (int s = 0; s < S; ++s) issue(s, s);
+  wait_vmcnt<(S - 1) * LPT>();
+  lds_barrier();
+  half8 wa[NBLK], xa[MBLK], wb[NBLK], xb[MBLK];
+  load(0, 0, wa, xa);
+  int slot = 0;
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    load(slot, 1, wb, xb);
+    mma(wa, xa);
+    const int next = slot == S - 1 ? 0 : slot + 1;
+    wait_vmcnt<(S - 2) * LPT>();  // this thread's loads of stage kt + 1 have landed
+    lds_barrier();
+    issue(kt + S, slot);
+    if (kt + 1 < nk) load(next, 0, wa, xa);
+    mma(wb, xb);
+    slot = next;
+  }
+  wait_vmcnt<0>();  // the repeat loads past the end still write the ring:
+  __syncthreads();  // every wave's have landed before the ring is reused
+  if (tid < BN) {
+    escale[tid] = my_scale;
+    ebias[tid] = my_bias;
+  }
+  __syncthreads();
+
+  // Epilogue in NBLK passes: pass nb parks every wave's column block nb
+  // (acc[mb][nb][4j + i] = tile row wm*MBLK*32 + mb*32 + col, pass column
+  // wn*32 + 8j + 4g + i) as fp32 in the ring, then the work-group stores it
+  // as 8-column runs of rows.
+  constexpr int PW = WGN * 32;
+  constexpr int OTP = PW + 4;
+  static_assert(BM * OTP * 4 + 2 * BN * 4 <= S * RSTAGE, "a parked pass and the column factors fit in the ring");
+  constexpr int CH = BM * PW / 8;
+  constexpr int CPT = (CH + NT - 1) / NT;
+  float* ot = reinterpret_cast<float*>(sm);
+  const bool vec8 = p.ldy % 8 == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0 && p.y_dt != DIMQ_F64;
+  for (int nb = 0; nb < NBLK; ++nb) {
+    static_for<NBLK>([&](auto nbc) {
+      constexpr int NB = decltype(nbc)::value;
+      if (NB != nb) return;
+#pragma unroll
+      for (int mb = 0; mb < MBLK; ++mb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          *reinterpret_cast<float4*>(ot + (wm * MBLK * 32 + mb * 32 + col) * OTP + wn * 32 + 8 * j + 4 * g) =
+              make_float4(acc[mb][NB][4 * j], acc[mb][NB][4 * j + 1], acc[mb][NB][4 * j + 2], acc[mb][NB][4 * j + 3]);
+    });
+    __syncthreads();
+    ResPairs<8> rr[CPT];
+    if ((MODE & kEpiRes) && res_pairs(p.epi, vec8)) {
+#pragma unroll
+      for (int u = 0; u < CPT; ++u) {
+        const int c = tid + u * NT;
+        const int r = c / (PW / 8), q = c - r * (PW / 8);
+        const int64_t m = m0 + r;
+        const int64_t n = n0 + (q >> 2) * NBLK * 32 + nb * 32 + 8 * (q & 3);
+        if (c < CH && m < p.M && n + 8 <= p.N) res_issue<8>(p.epi, m * p.ldy + n, rr[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+      const int c = tid + u * NT;
+      if (c >= CH) break;
+      const int r = c / (PW / 8), q = c - r * (PW / 8);
+      const int64_t m = m0 + r;
+      const int nl = (q >> 2) * NBLK * 32 + nb * 32 + 8 * (q & 3);  // column within the tile
+      const int64_t n = n0 + nl;
+      if (m >= p.M) continue;
+      const float4 a0 = *reinterpret_cast<const float4*>(ot + r * OTP + 8 * q);
+      const float4 a1 = *reinterpret_cast<const float4*>(ot + r * OTP + 8 * q + 4);
+      float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int ni = nl + i < BN ? nl + i : BN - 1;
+        v[i] = v[i] * escale[ni] + ebias[ni];
+      }
+      const int64_t off = m * p.ldy + n;
+      if (vec8 && n + 8 <= p.N) {
+        epi_m<MODE, 8>(p.epi, &rr[u], off, true, v);
+        if (p.y_dt == DIMQ_F32) {
+          float* yp = reinterpret_cast<float*>(p.y) + off;
+          *reinterpret_cast<float4*>(yp) = make_float4(v[0], v[1], v[2], v[3]);
+          *reinterpret_cast<float4*>(yp + 4) = make_float4(v[4], v[5], v[6], v[7]);
+        } else {
+          uint32_t h[8];
+          if (p.y_dt == DIMQ_F16) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) h[i] = float_to_f16_bits(v[i]);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) h[i] = float_to_bf16_bits(v[i]);
+          }
+          *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p.y) + off) =
+              make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+        }
+      } else {
+        for (int i = 0; i < 8; ++i)
+          if (n + i < p.N) store_from_float(p.y, p.y_dt, off + i, epi1_m<MODE>(p.epi, off + i, v[i]));
+      }
+    }
+    __syncthreads();  // the next pass overwrites the parked values
+  }
+}
+
+// Tile shapes (WGM x WGN waves of (MBLK*32) x (NBLK*32), ring of 3 stages),
+// measured on the ViT-B/16 shapes at M 12,608 (kernel time, fp16 x, bf16 y):
+//   0: 256 x 256, 8 waves of 64 x 128, one work-group per CU: qkv (N 2304)
+//      70.3 us against 78.9 for tile 1;
+//   1: 128 (m) x 256 (n), 4 waves of 64 x 128, 72 KB of LDS so two
+//      work-groups share a CU and one's epilogue overlaps the other's main
+//      loop: fc1 (N 3072) 93.6 us (98.7 with the fused GELU) against 100.3
+//      (110.7) for tile 0, whose 600 tiles leave a third round a third full;
+//   2: 128 (m) x 384 (n), 8 waves of 64 x 96: N 768 (proj, fc2) as 198 tiles
+//      instead of 150 on 256 CUs, fc2 73.7 us against 79.3.
+template <int TILE>
+struct PdTile;
+template <>
+struct PdTile<0> {
+  static constexpr int WGM = 4, WGN = 2, MBLK = 2, NBLK = 4;
+};
+template <>
+struct PdTile<1> {
+  static constexpr int WGM = 2, WGN = 2, MBLK = 2, NBLK = 4;
+};
+template <>
+struct PdTile<2> {
+  static constexpr int WGM = 2, WGN = 4, MBLK = 2, NBLK = 3;
+};
+constexpr int kPdStages = 3;
+
+int pd_pick_tile(int64_t M, int64_t N) {
+  if (N % 384 == 0 && N <= 1536) return 2;
+  const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
+  const int64_t rem = tiles % 256;  // work-groups of the last round of tile 0
+  return (rem != 0 && rem * 2 < 256) ? 1 : 0;
+}
+
+template <int TILE, int MODE>
+int launch_pd_gemm(const GemmArgs& p, const uint16_t* wd, const float* rs, hipStream_t s) {
+  using T = PdTile<TILE>;
+  constexpr int BM = T::WGM * T::MBLK * 32, BN = T::WGN * T::NBLK * 32;
+  const int64_t tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+  hipLaunchKernelGGL((gemm_pd_kernel<T::WGM, T::WGN, T::MBLK, T::NBLK, MODE, kPdStages>),
+                     dim3(static_cast<unsigned>(tiles)), dim3(64 * T::WGM * T::WGN), 0, s, p, wd, rs);
+  return check_launch("linear_codebook (pre-decoded weights)");
+}
+
+template <int TILE>
+int launch_pd_modes(const GemmArgs& p, int mode, const uint16_t* wd, const float* rs, hipStream_t s) {
+  switch (mode) {
+    case kEpiRelu: return launch_pd_gemm<TILE, kEpiRelu>(p, wd, rs, s);
+    case kEpiGelu: return launch_pd_gemm<TILE, kEpiGelu>(p, wd, rs, s);
+    case kEpiRes: return launch_pd_gemm<TILE, kEpiRes>(p, wd, rs, s);
+    default: return launch_pd_gemm<TILE, kEpiNone>(p, wd, rs, s);
+  }
+}
+
+}  // namespace
+
+// Workspace of the pre-decoded path: W_hat fp16 [N, K], then N fp32 factors.
+int64_t predecoded_ws_bytes(int64_t M, int64_t K, int64_t N, int bits, int x_dtype) {
+  if (M < kPredecodeMinM || K <= 0 || N <= 0 || K % kPdK != 0 || !(bits >= 2 && bits <= 4) || x_dtype != DIMQ_F16)
+    return 0;
+  return (N * K * 2 + 255) / 256 * 256 + (N * 4 + 255) / 256 * 256;
+}
+
+// Runs the two launches; -1 when the call does not take this path (shape,
+// dtype, epilogue, alignment or too small a workspace).
+int launch_predecoded(const GemmArgs& p, int bits, int x_dtype, void* ws, int64_t ws_bytes, hipStream_t s) {
+  const int64_t need = predecoded_ws_bytes(p.M, p.K, p.N, bits, x_dtype);
+  if (need == 0 || ws == nullptr || ws_bytes < need || (reinterpret_cast<uintptr_t>(ws) & 255) != 0) return -1;
+  if (p.conv || !p.fast_b || !p.vec_a || p.ldx % 8 != 0) return -1;
+  const int mode = epi_mode(p.epi);
+  if (!(mode == kEpiNone || mode == kEpiRelu || mode == kEpiGelu || mode == kEpiRes)) return -1;
+  uint16_t* wd = static_cast<uint16_t*>(ws);
+  float* rs = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + (p.N * p.K * 2 + 255) / 256 * 256);
+  const unsigned blocks = static_cast<unsigned>((p.N + kPdRows - 1) / kPdRows);
+  switch (bits) {
+    case 2:
+      hipLaunchKernelGGL(predecode_kernel<2>, dim3(blocks), dim3(256), 0, s, p.w, p.cb, p.cb_dt, p.cb_rows, p.cb_size,
+                         p.N, p.K, p.acc_scale, wd, rs);
+      break;
+    case 3:
+      hipLaunchKernelGGL(predecode_kernel<3>, dim3(blocks), dim3(256), 0, s, p.w, p.cb, p.cb_dt, p.cb_rows, p.cb_size,
+                         p.N, p.K, p.acc_scale, wd, rs);
+      break;
+    default:
+      hipLaunchKernelGGL(predecode_kernel<4>, dim3(blocks), dim3(256), 0, s, p.w, p.cb, p.cb_dt, p.cb_rows, p.cb_size,
+                         p.N, p.K, p.acc_scale, wd, rs);
+      break;
+  }
+  const int rc = check_launch("linear_codebook (weight pre-decode)");
+  if (rc != DIMQ_OK) return rc;
+  switch (pd_pick_tile(p.M, p.N)) {
+    case 1: return launch_pd_modes<1>(p, mode, wd, rs, s);
+    case 2: return launch_pd_modes<2>(p, mode, wd, rs, s);
+    default: return launch_pd_modes<0>(p, mode, wd, rs, s);
+  }
+}
+
+}  // namespace dimq

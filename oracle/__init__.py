@@ -158,7 +158,9 @@ def dequantize(packed, bits: int, codebook, N: int, K: int) -> np.ndarray:
     """dimq_backend/reference.py:47-56: W_hat[n,k] = C[idx] (C[n, idx] per channel)."""
     pk, pp = _u8(_np(packed).reshape(-1))
     cb = _np(codebook).astype(np.float32)
-    per_channel = cb.ndim == 2
+    if cb.ndim == 2 and cb.shape[0] not in (1, int(N)):
+        raise ValueError(f"codebook rows {cb.shape[0]} must be 1 or {int(N)}")
+    per_channel = cb.ndim == 2 and cb.shape[0] != 1  # a [1, E] codebook is the per-layer one
     Kc = cb.shape[-1]
     ca, cp = _f32(cb.reshape(-1))
     out = np.zeros(max(int(N) * int(K), 1), dtype=np.float32)

@@ -1,0 +1,115 @@
+"""The pre-decoded-weight Linear path (large M, fp16 activations): the weights
+decoded once per call into the workspace as fp16, then an fp16 GEMM fed by
+global_load_lds.  Checked against dequantize-then-F.linear in fp32 on the CPU
+(reference.py:91-110, oracle.linear_dequant_reference) at the weight-only bar
+2e-3 (bf16 outputs 8e-3), over bit widths, per-layer and per-output-channel
+codebooks, ragged M / N tails, K not a multiple of 64, and every fused
+epilogue the path instantiates."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle
+from tests.conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(M, N, K, bits, per_channel, seed):
+    g = torch.Generator().manual_seed(seed)
+    E = 1 << bits
+    rows = N if per_channel else 1
+    cb = (torch.randn(rows, E, generator=g) * 0.05).sort(dim=1).values
+    idx = torch.randint(0, E, (N, K), generator=g, dtype=torch.uint8)
+    packed = torch.from_numpy(oracle.pack_bits(idx, bits))
+    x = torch.randn(M, K, generator=g).half()
+    bias = torch.randn(N, generator=g) * 0.05
+    return cb, packed, x, bias
+
+
+def test_workspace_query_selects_the_path():
+    from dimq_amd import _C
+    lib = _C.lib
+    F16, BF16 = 1, 2  # DIMQ_F16, DIMQ_BF16
+    assert lib.dimq_linear_codebook_workspace_bytes(12608, 768, 3072, 4, F16) >= 3072 * 768 * 2 + 3072 * 4
+    assert lib.dimq_linear_codebook_workspace_bytes(2048, 96, 352, 3, F16) >= 352 * 96 * 2 + 352 * 4
+    assert lib.dimq_linear_codebook_workspace_bytes(2047, 768, 3072, 4, F16) == 0  # below the M threshold
+    assert lib.dimq_linear_codebook_workspace_bytes(12608, 768, 3072, 4, BF16) == 0
+    assert lib.dimq_linear_codebook_workspace_bytes(12608, 80, 3072, 4, F16) == 0  # K % 32 != 0
+    assert lib.dimq_linear_codebook_workspace_bytes(12608, 768, 3072, 8, F16) == 0
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("per_channel", [True, False])
+@torch.no_grad()
+def test_predecoded_linear_vs_dequant_reference(gpu, bits, per_channel):
+    from dimq_amd import ops
+    M, N, K = 2085, 352, 96  # tails: M % 256 = 37, N % 256 = 96, K % 64 = 32
+    announce(f"predecode bits={bits} per_channel={per_channel} M={M} N={N} K={K}")
+    cb, packed, x, bias = _case(M, N, K, bits, per_channel, 10 * bits + per_channel)
+    y = ops.dimq_linear_codebook(x.to(gpu), packed.to(gpu), cb.to(gpu), bits, bias.to(gpu), N, K,
+                                 out_dtype=torch.float32)
+    ref = oracle.linear_dequant_reference(x.float(), packed, bits, cb, N, K, bias)
+    assert oracle.rel_err(y.cpu(), ref) <= 2e-3
+
+
+@pytest.mark.parametrize("epi,out", [("relu", torch.float32), ("gelu", torch.float16), ("residual", torch.bfloat16),
+                                     (None, torch.bfloat16)])
+@torch.no_grad()
+def test_predecoded_linear_epilogues(gpu, epi, out):
+    from dimq_amd import ops
+    M, N, K = 2304, 512, 256
+    announce(f"predecode epilogue={epi} out={out}")
+    cb, packed, x, bias = _case(M, N, K, 4, True, 7)
+    res = (torch.randn(M, N, generator=torch.Generator().manual_seed(8)) * 0.5).bfloat16() \
+        if epi == "residual" else None
+    y = ops.dimq_linear_codebook(x.to(gpu), packed.to(gpu), cb.to(gpu), 4, bias.to(gpu), N, K, out_dtype=out,
+                                 residual=None if res is None else res.to(gpu),
+                                 activation=epi if epi in ("relu", "gelu") else None)
+    ref = oracle.linear_dequant_reference(x.float(), packed, 4, cb, N, K, bias)
+    if epi == "residual":
+        ref = ref + res.float()
+    elif epi == "gelu":
+        ref = torch.nn.functional.gelu(ref)
+    elif epi == "relu":
+        ref = torch.relu(ref)
+    tol = 8e-3 if out == torch.bfloat16 else 2e-3
+    assert oracle.rel_err(y.float().cpu(), ref) <= tol
+
+
+@torch.no_grad()
+def test_predecoded_small_centres_keep_precision(gpu):
+    """Per-channel centres around 1e-6 (fp16 subnormals unscaled): the per-row power-of-two scaling of the
+    decoded rows keeps 11 significant bits."""
+    from dimq_amd import ops
+    M, N, K = 2048, 256, 128
+    announce("predecode tiny centres")
+    cb, packed, x, bias = _case(M, N, K, 4, True, 11)
+    cb = cb * 2e-5
+    y = ops.dimq_linear_codebook(x.to(gpu), packed.to(gpu), cb.to(gpu), 4, None, N, K, out_dtype=torch.float32)
+    ref = oracle.linear_dequant_reference(x.float(), packed, 4, cb, N, K, None)
+    assert oracle.rel_err(y.cpu(), ref) <= 2e-3
+
+
+@torch.no_grad()
+def test_predecoded_matches_fused_path(gpu):
+    """The same call with and without a workspace (the fused shared-decode tile): both within the bar of the
+    oracle and of each other."""
+    from dimq_amd import _C, ops
+    M, N, K = 4096, 768, 768
+    announce("predecode vs fused")
+    cb, packed, x, bias = _case(M, N, K, 4, True, 12)
+    xg, pg, cg, bg = x.to(gpu), packed.to(gpu), cb.to(gpu), bias.to(gpu)
+    y_pd = ops.dimq_linear_codebook(xg, pg, cg, 4, bg, N, K, out_dtype=torch.float32)
+    y_fu = torch.empty_like(y_pd)
+    with torch.cuda.device(gpu):
+        rc = _C.lib.dimq_linear_codebook(xg.data_ptr(), 1, M, K, pg.data_ptr(), pg.numel(), 4, cg.data_ptr(), 0, N,
+                                         16, bg.data_ptr(), 0, N, y_fu.data_ptr(), 0, 0,
+                                         torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    ref = oracle.linear_dequant_reference(x.float(), packed, 4, cb, N, K, bias)
+    assert oracle.rel_err(y_pd.cpu(), ref) <= 2e-3
+    assert oracle.rel_err(y_fu.cpu(), ref) <= 2e-3
+    assert oracle.rel_err(y_pd.cpu(), y_fu.cpu()) <= 2e-3

@@ -1,7 +1,7 @@
 // Pre-decoded-weight GEMM for the large-M Linear shapes (ViT-B/16 at
 // M = 12,608): y[M,N] = epilogue(x[M,K] W_hat^T), in two launches.
 //
-//   1. predecode_kernel: the packed b-bit indices (dimq_packed_lut layout,
+//   1. prep_kernel: the packed b-bit indices (dimq_packed_lut layout,
 //      LSB-first, row-major [N, K]) and the codebook rows -> W_hat as fp16
 //      [N, K] in natural k order, each row scaled by the power of two 2^e of
 //      the register-codebook kernels (max|c| 2^e in [2^14, 2^15), decode.h),
@@ -21,8 +21,9 @@
 //      so a lane's accumulator holds 4 consecutive n of one m.  The epilogue
 //      parks each column pass in LDS and stores 8-column runs of rows.
 //
-// fp16 activations only (the model's LayerNorm and fc1 outputs): their values
-// are exact in the fp16 operand, so no range guard is needed.
+// fp16 activations (the model's LayerNorm and fc1 outputs) are read as they
+// are; bf16 and fp32 activations are converted to fp16 in the first launch,
+// with the range guard of common.h applied per tile from per-row flags.
 #include "gemm_big.h"
 
 namespace dimq {
@@ -31,7 +32,8 @@ namespace {
 constexpr int kPdK = 32;  // k (halves) per pipeline stage: 64 bytes of a row
 
 // Below this many activation rows the fused kernels' per-tile decode costs
-// less than the extra launch and the fp16 weight copy.
+// no more than the extra launch and the fp16 copies (cfg1, M 1576 fp32: 29.5
+// us either way, same box).
 constexpr int64_t kPredecodeMinM = 2048;
 
 // The 16-byte chunk c of stage row r lives at r * 64 + ((c ^ pd_swz(r)) << 4):
@@ -59,16 +61,16 @@ __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds) {
 constexpr int kPdRows = 2;     // weight rows per predecode work-group
 constexpr int kPdGroups = 16;  // 8-index groups per thread held in registers (K <= 4096 in one pass)
 
+// Weight rows 2 b, 2 b + 1 -> fp16 in wd, their factors acc_scale 2^-e in rs.
 template <int BITS>
-__global__ __launch_bounds__(256) void predecode_kernel(const uint8_t* __restrict__ w, const void* cb, int cb_dt,
-                                                        int64_t cb_rows, int cb_size, int64_t N, int64_t K,
-                                                        float acc_scale, uint16_t* __restrict__ wd,
-                                                        float* __restrict__ rs) {
+__device__ __forceinline__ void predecode_rows(const uint8_t* __restrict__ w, const void* cb, int cb_dt,
+                                               int64_t cb_rows, int cb_size, int64_t N, int64_t K, float acc_scale,
+                                               uint16_t* __restrict__ wd, float* __restrict__ rs, int64_t b) {
   constexpr int E = 1 << BITS;
   __shared__ float cbs[kPdRows * E];
   __shared__ uint32_t tab[kPdRows * E];  // fp16 bits of the scaled entries
   const int tid = threadIdx.x;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kPdRows;
+  const int64_t r0 = b * kPdRows;
   const int gpr = static_cast<int>(K >> 3);  // 8-index groups per row (K % 32 == 0)
   const int nr = N - r0 < kPdRows ? static_cast<int>(N - r0) : kPdRows;
   const int total = nr * gpr;
@@ -121,9 +123,74 @@ __global__ __launch_bounds__(256) void predecode_kernel(const uint8_t* __restric
   for (int gi = tid + 256 * kPdGroups; gi < total; gi += 256) store_group(gi, load_group(gi));
 }
 
-template <int WGM, int WGN, int MBLK, int NBLK, int MODE, int S>
+constexpr int kPxRows = 8;  // activation rows per conversion work-group
+
+// Activation rows 8 b .. 8 b + 7 (bf16 or fp32) -> fp16 in xh (row pitch K),
+// rounded to nearest; flags[m] != 0 when row m holds a value of magnitude
+// >= 2^-7 after the rounding (the range guard's test, common.h).
+template <int XT>
+__device__ __forceinline__ void convert_rows(const void* __restrict__ x, int64_t M, int64_t K, int64_t ldx,
+                                             uint16_t* __restrict__ xh, uint32_t* __restrict__ flags, int64_t b) {
+  __shared__ uint32_t fl[kPxRows];
+  const int tid = threadIdx.x;
+  const int64_t r0 = b * kPxRows;
+  const int gpr = static_cast<int>(K >> 3);
+  const int nr = M - r0 < kPxRows ? static_cast<int>(M - r0) : kPxRows;
+  if (tid < kPxRows) fl[tid] = 0u;
+  __syncthreads();
+  for (int gi = tid; gi < nr * gpr; gi += 256) {
+    const int r = gi / gpr;
+    const int64_t m = r0 + r, k = 8 * static_cast<int64_t>(gi - r * gpr);
+    float v[8];
+    if constexpr (XT == DIMQ_F32) {
+      const float4* s4 = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(x) + m * ldx + k);
+      const float4 a = s4[0], c = s4[1];
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = c.x; v[5] = c.y; v[6] = c.z; v[7] = c.w;
+    } else {
+      const uint4 t = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(x) + m * ldx + k);
+      const uint32_t u[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = __uint_as_float(u[i] << 16);
+        v[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+      }
+    }
+    uint32_t h[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) h[i] = f16x2_rne(v[2 * i], v[2 * i + 1]);
+    *reinterpret_cast<uint4*>(xh + m * K + k) = make_uint4(h[0], h[1], h[2], h[3]);
+    const uint32_t big = ((h[0] | h[1]) | (h[2] | h[3])) & kRangeBigBits;
+    if (big) atomicOr(&fl[r], 1u);
+  }
+  __syncthreads();
+  if (tid < nr) flags[r0 + tid] = fl[tid];
+}
+
+// One launch: work-groups [0, nbw) decode weight row pairs, the rest (when
+// XT is not fp16) convert activation rows.
+template <int BITS, int XT>
+__global__ __launch_bounds__(256) void prep_kernel(const uint8_t* __restrict__ w, const void* cb, int cb_dt,
+                                                   int64_t cb_rows, int cb_size, int64_t N, int64_t K,
+                                                   float acc_scale, uint16_t* __restrict__ wd, float* __restrict__ rs,
+                                                   int64_t nbw, const void* __restrict__ x, int64_t M, int64_t ldx,
+                                                   uint16_t* __restrict__ xh, uint32_t* __restrict__ flags) {
+  const int64_t b = blockIdx.x;
+  if (b < nbw) {
+    predecode_rows<BITS>(w, cb, cb_dt, cb_rows, cb_size, N, K, acc_scale, wd, rs, b);
+  } else if constexpr (XT != DIMQ_F16) {
+    convert_rows<XT>(x, M, K, ldx, xh, flags, b - nbw);
+  }
+}
+
+// xop / lda: the fp16 activations the matrix cores read (x itself, or its
+// converted copy); with GUARD the copy's per-row flags decide, with the
+// accumulators' finiteness, whether the tile is recomputed in fp32 from p.x
+// (of dtype xt) and the packed weights.
+template <int WGM, int WGN, int MBLK, int NBLK, int MODE, int S, bool GUARD>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs p, const uint16_t* __restrict__ wd,
-                                                                 const float* __restrict__ rs) {
+                                                                 const float* __restrict__ rs,
+                                                                 const uint16_t* __restrict__ xop, int64_t lda,
+                                                                 const uint32_t* __restrict__ flags, int xt, int bits) {
   constexpr int NT = 64 * WGM * WGN;
   constexpr int BM = WGM * MBLK * 32;
   constexpr int BN = WGN * NBLK * 32;
@@ -131,7 +198,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs 
   constexpr int LPT = (BN + BM) * 4 / NT;   // 16-byte loads per thread and stage
   static_assert(LPT * NT == (BN + BM) * 4, "a stage splits evenly over the threads");
   static_assert(BN % 16 == 0 && BM % 16 == 0, "a wave's load covers 16 rows of one operand");
-  static_assert((S - 1) * LPT < 64, "outstanding loads fit the vmcnt counter");
+  static_assert(S * LPT < 64, "outstanding loads fit the vmcnt counter");
   __shared__ __attribute__((aligned(16))) uint8_t sm[S * RSTAGE];
   // after the main loop: the tile's column factors at the end of the ring
   float* escale = reinterpret_cast<float*>(sm + S * RSTAGE) - 2 * BN;
@@ -162,7 +229,6 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs 
   // stage rows 16 b .. 16 b + 15 (weight rows first, then activation rows);
   // lane l fills LDS chunk l & 3 of row 16 b + (l >> 2), i.e. global chunk
   // (l & 3) ^ swizzle.  Rows past N or M repeat the last row (not stored).
-  const uint16_t* xh = reinterpret_cast<const uint16_t*>(p.x);
   const uint16_t* src[LPT];
 #pragma unroll
   for (int j = 0; j < LPT; ++j) {
@@ -173,17 +239,26 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs 
       src[j] = wd + n * p.K + 8 * c;
     } else {
       const int64_t m = m0 + (row - BN) < p.M ? m0 + (row - BN) : p.M - 1;
-      src[j] = xh + m * p.ldx + 8 * c;
+      src[j] = xop + m * lda + 8 * c;
     }
   }
   const int64_t nk = p.K / kPdK;
   const uint32_t smb = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_g*)sm));  // LDS address of the ring
   auto issue = [&](int64_t kt, int slot) {
-    const int64_t k = (kt < nk ? kt : nk - 1) * kPdK;  // past the end: a repeat, never read
+    if (kt >= nk) return;
+    const int64_t k = kt * kPdK;
 #pragma unroll
     for (int j = 0; j < LPT; ++j) {
       dma16(src[j] + k, smb + slot * RSTAGE + (j * (NT / 64) + wave) * 1024);
     }
+  };
+  // s_waitcnt leaving this thread's loads of the n youngest issued stages in
+  // flight (0 <= n < S)
+  auto wait_stages = [&](int64_t n) {
+    static_for<S>([&](auto ic) {
+      constexpr int I = decltype(ic)::value;
+      if (I == n) wait_vmcnt<I * LPT>();
+    });
   };
 
   floatx16g acc[MBLK][NBLK];
@@ -221,7 +296,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs 
   // barrier's fence waits for this wave's LDS reads) takes stage kt + S.
 #pragma unroll
   for (int s = 0; s < S; ++s) issue(s, s);
-  wait_vmcnt<(S - 1) * LPT>();
+  wait_stages(nk - 1 < S - 1 ? nk - 1 : S - 1);  // stage 0 landed; stages 1 .. S - 1 may be in flight
   lds_barrier();
   half8 wa[NBLK], xa[MBLK], wb[NBLK], xb[MBLK];
   load(0, 0, wa, xa);
@@ -230,15 +305,24 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs 
     load(slot, 1, wb, xb);
     mma(wa, xa);
     const int next = slot == S - 1 ? 0 : slot + 1;
-    wait_vmcnt<(S - 2) * LPT>();  // this thread's loads of stage kt + 1 have landed
+    // stage kt + 1 landed; stages kt + 2 .. min(kt + S - 1, nk - 1) may be in flight
+    if (kt + 1 < nk) wait_stages(nk - 2 - kt < S - 2 ? nk - 2 - kt : S - 2);
     lds_barrier();
     issue(kt + S, slot);
     if (kt + 1 < nk) load(next, 0, wa, xa);
     mma(wb, xb);
     slot = next;
   }
-  wait_vmcnt<0>();  // the repeat loads past the end still write the ring:
-  __syncthreads();  // every wave's have landed before the ring is reused
+  __syncthreads();  // every wave is done with the ring before it is reused
+  if constexpr (GUARD) {
+    bool big = false;
+    for (int r = tid; r < BM; r += NT) big |= m0 + r < p.M && flags[m0 + r] != 0u;
+    const int bad = __syncthreads_or(!finite_acc<1>(&acc[0][0], MBLK, NBLK));
+    if (!__syncthreads_or(big) || bad) {
+      exact_tile_out(p, xt, bits, m0, m0 + BM, n0, n0 + BN, 0);
+      return;
+    }
+  }
   if (tid < BN) {
     escale[tid] = my_scale;
     ebias[tid] = my_bias;
@@ -256,6 +340,22 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs 
   constexpr int CPT = (CH + NT - 1) / NT;
   float* ot = reinterpret_cast<float*>(sm);
   const bool vec8 = p.ldy % 8 == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0 && p.y_dt != DIMQ_F64;
+  // 16-bit residuals of pass nb + 1 are requested before pass nb's stores
+  const bool rpair = (MODE & kEpiRes) && res_pairs(p.epi, vec8);
+  auto res_load = [&](int nb, ResPairs<8> (&rr)[CPT]) {
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+      const int c = tid + u * NT;
+      const int r = c / (PW / 8), q = c - r * (PW / 8);
+      const int64_t m = m0 + r;
+      const int64_t n = n0 + (q >> 2) * NBLK * 32 + nb * 32 + 8 * (q & 3);
+      if (c < CH && m < p.M && n + 8 <= p.N) res_issue<8>(p.epi, m * p.ldy + n, rr[u]);
+    }
+  };
+  ResPairs<8> rr[CPT], rn[CPT];
+  if constexpr ((MODE & kEpiRes) != 0) {
+    if (rpair) res_load(0, rr);
+  }
   for (int nb = 0; nb < NBLK; ++nb) {
     static_for<NBLK>([&](auto nbc) {
       constexpr int NB = decltype(nbc)::value;
@@ -268,16 +368,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs 
               make_float4(acc[mb][NB][4 * j], acc[mb][NB][4 * j + 1], acc[mb][NB][4 * j + 2], acc[mb][NB][4 * j + 3]);
     });
     __syncthreads();
-    ResPairs<8> rr[CPT];
-    if ((MODE & kEpiRes) && res_pairs(p.epi, vec8)) {
-#pragma unroll
-      for (int u = 0; u < CPT; ++u) {
-        const int c = tid + u * NT;
-        const int r = c / (PW / 8), q = c - r * (PW / 8);
-        const int64_t m = m0 + r;
-        const int64_t n = n0 + (q >> 2) * NBLK * 32 + nb * 32 + 8 * (q & 3);
-        if (c < CH && m < p.M && n + 8 <= p.N) res_issue<8>(p.epi, m * p.ldy + n, rr[u]);
-      }
+    if constexpr ((MODE & kEpiRes) != 0) {
+      if (rpair && nb + 1 < NBLK) res_load(nb + 1, rn);
     }
 #pragma unroll
     for (int u = 0; u < CPT; ++u) {
@@ -321,6 +413,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs 
       }
     }
     __syncthreads();  // the next pass overwrites the parked values
+    if constexpr ((MODE & kEpiRes) != 0) {
+#pragma unroll
+      for (int u = 0; u < CPT; ++u) rr[u] = rn[u];
+    }
   }
 }
 
@@ -348,42 +444,87 @@ template <>
 struct PdTile<2> {
   static constexpr int WGM = 2, WGN = 4, MBLK = 2, NBLK = 3;
 };
+//   3: 128 x 128, 4 waves of 64 x 64, 48 KB of LDS: shapes whose tile-1 grid
+//      would leave CUs idle (small N).
+template <>
+struct PdTile<3> {
+  static constexpr int WGM = 2, WGN = 2, MBLK = 2, NBLK = 2;
+};
 constexpr int kPdStages = 3;
 
 int pd_pick_tile(int64_t M, int64_t N) {
   if (N % 384 == 0 && N <= 1536) return 2;
+  if (((M + 127) / 128) * ((N + 255) / 256) < 256) return 3;
   const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
   const int64_t rem = tiles % 256;  // work-groups of the last round of tile 0
   return (rem != 0 && rem * 2 < 256) ? 1 : 0;
 }
 
+struct PdOperands {
+  const uint16_t* wd;
+  const float* rs;
+  const uint16_t* xa;
+  int64_t lda;
+  const uint32_t* flags;  // null: fp16 activations, no guard
+  int xt, bits;
+};
+
 template <int TILE, int MODE>
-int launch_pd_gemm(const GemmArgs& p, const uint16_t* wd, const float* rs, hipStream_t s) {
+int launch_pd_gemm(const GemmArgs& p, const PdOperands& o, hipStream_t s) {
   using T = PdTile<TILE>;
   constexpr int BM = T::WGM * T::MBLK * 32, BN = T::WGN * T::NBLK * 32;
   const int64_t tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-  hipLaunchKernelGGL((gemm_pd_kernel<T::WGM, T::WGN, T::MBLK, T::NBLK, MODE, kPdStages>),
-                     dim3(static_cast<unsigned>(tiles)), dim3(64 * T::WGM * T::WGN), 0, s, p, wd, rs);
+  if (o.flags) {
+    hipLaunchKernelGGL((gemm_pd_kernel<T::WGM, T::WGN, T::MBLK, T::NBLK, MODE, kPdStages, true>),
+                       dim3(static_cast<unsigned>(tiles)), dim3(64 * T::WGM * T::WGN), 0, s, p, o.wd, o.rs, o.xa,
+                       o.lda, o.flags, o.xt, o.bits);
+  } else {
+    hipLaunchKernelGGL((gemm_pd_kernel<T::WGM, T::WGN, T::MBLK, T::NBLK, MODE, kPdStages, false>),
+                       dim3(static_cast<unsigned>(tiles)), dim3(64 * T::WGM * T::WGN), 0, s, p, o.wd, o.rs, o.xa,
+                       o.lda, o.flags, o.xt, o.bits);
+  }
   return check_launch("linear_codebook (pre-decoded weights)");
 }
 
 template <int TILE>
-int launch_pd_modes(const GemmArgs& p, int mode, const uint16_t* wd, const float* rs, hipStream_t s) {
+int launch_pd_modes(const GemmArgs& p, int mode, const PdOperands& o, hipStream_t s) {
   switch (mode) {
-    case kEpiRelu: return launch_pd_gemm<TILE, kEpiRelu>(p, wd, rs, s);
-    case kEpiGelu: return launch_pd_gemm<TILE, kEpiGelu>(p, wd, rs, s);
-    case kEpiRes: return launch_pd_gemm<TILE, kEpiRes>(p, wd, rs, s);
-    default: return launch_pd_gemm<TILE, kEpiNone>(p, wd, rs, s);
+    case kEpiRelu: return launch_pd_gemm<TILE, kEpiRelu>(p, o, s);
+    case kEpiGelu: return launch_pd_gemm<TILE, kEpiGelu>(p, o, s);
+    case kEpiRes: return launch_pd_gemm<TILE, kEpiRes>(p, o, s);
+    default: return launch_pd_gemm<TILE, kEpiNone>(p, o, s);
+  }
+}
+
+template <int BITS, int XT>
+void launch_prep(const GemmArgs& p, uint16_t* wd, float* rs, uint16_t* xh, uint32_t* flags, hipStream_t s) {
+  const int64_t nbw = (p.N + kPdRows - 1) / kPdRows;
+  const int64_t nbx = XT == DIMQ_F16 ? 0 : (p.M + kPxRows - 1) / kPxRows;
+  hipLaunchKernelGGL((prep_kernel<BITS, XT>), dim3(static_cast<unsigned>(nbw + nbx)), dim3(256), 0, s, p.w, p.cb,
+                     p.cb_dt, p.cb_rows, p.cb_size, p.N, p.K, p.acc_scale, wd, rs, nbw, p.x, p.M, p.ldx, xh, flags);
+}
+
+template <int BITS>
+void launch_prep_bits(const GemmArgs& p, int xt, uint16_t* wd, float* rs, uint16_t* xh, uint32_t* flags,
+                      hipStream_t s) {
+  switch (xt) {
+    case DIMQ_F16: launch_prep<BITS, DIMQ_F16>(p, wd, rs, xh, flags, s); break;
+    case DIMQ_BF16: launch_prep<BITS, DIMQ_BF16>(p, wd, rs, xh, flags, s); break;
+    default: launch_prep<BITS, DIMQ_F32>(p, wd, rs, xh, flags, s); break;
   }
 }
 
 }  // namespace
 
-// Workspace of the pre-decoded path: W_hat fp16 [N, K], then N fp32 factors.
+constexpr int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
+
+// Workspace of the pre-decoded path: W_hat fp16 [N, K], N fp32 factors and,
+// for bf16 / fp32 activations, their fp16 copy [M, K] and M row flags.
 int64_t predecoded_ws_bytes(int64_t M, int64_t K, int64_t N, int bits, int x_dtype) {
-  if (M < kPredecodeMinM || K <= 0 || N <= 0 || K % kPdK != 0 || !(bits >= 2 && bits <= 4) || x_dtype != DIMQ_F16)
-    return 0;
-  return (N * K * 2 + 255) / 256 * 256 + (N * 4 + 255) / 256 * 256;
+  if (M < kPredecodeMinM || K <= 0 || N <= 0 || K % kPdK != 0 || !(bits >= 2 && bits <= 4)) return 0;
+  if (!(x_dtype == DIMQ_F16 || x_dtype == DIMQ_BF16 || x_dtype == DIMQ_F32)) return 0;
+  const int64_t w = align256(N * K * 2) + align256(N * 4);
+  return x_dtype == DIMQ_F16 ? w : w + align256(M * K * 2) + align256(M * 4);
 }
 
 // Runs the two launches; -1 when the call does not take this path (shape,
@@ -391,32 +532,32 @@ int64_t predecoded_ws_bytes(int64_t M, int64_t K, int64_t N, int bits, int x_dty
 int launch_predecoded(const GemmArgs& p, int bits, int x_dtype, void* ws, int64_t ws_bytes, hipStream_t s) {
   const int64_t need = predecoded_ws_bytes(p.M, p.K, p.N, bits, x_dtype);
   if (need == 0 || ws == nullptr || ws_bytes < need || (reinterpret_cast<uintptr_t>(ws) & 255) != 0) return -1;
-  if (p.conv || !p.fast_b || !p.vec_a || p.ldx % 8 != 0) return -1;
+  const int xs = x_dtype == DIMQ_F32 ? 4 : 2;
+  if (p.conv || !p.fast_b || !p.vec_a || (p.ldx * xs) % 16 != 0) return -1;
   const int mode = epi_mode(p.epi);
   if (!(mode == kEpiNone || mode == kEpiRelu || mode == kEpiGelu || mode == kEpiRes)) return -1;
-  uint16_t* wd = static_cast<uint16_t*>(ws);
-  float* rs = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + (p.N * p.K * 2 + 255) / 256 * 256);
-  const unsigned blocks = static_cast<unsigned>((p.N + kPdRows - 1) / kPdRows);
+  uint8_t* base = static_cast<uint8_t*>(ws);
+  uint16_t* wd = reinterpret_cast<uint16_t*>(base);
+  float* rs = reinterpret_cast<float*>(base + align256(p.N * p.K * 2));
+  uint16_t* xh = nullptr;
+  uint32_t* flags = nullptr;
+  if (x_dtype != DIMQ_F16) {
+    xh = reinterpret_cast<uint16_t*>(base + align256(p.N * p.K * 2) + align256(p.N * 4));
+    flags = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(xh) + align256(p.M * p.K * 2));
+  }
   switch (bits) {
-    case 2:
-      hipLaunchKernelGGL(predecode_kernel<2>, dim3(blocks), dim3(256), 0, s, p.w, p.cb, p.cb_dt, p.cb_rows, p.cb_size,
-                         p.N, p.K, p.acc_scale, wd, rs);
-      break;
-    case 3:
-      hipLaunchKernelGGL(predecode_kernel<3>, dim3(blocks), dim3(256), 0, s, p.w, p.cb, p.cb_dt, p.cb_rows, p.cb_size,
-                         p.N, p.K, p.acc_scale, wd, rs);
-      break;
-    default:
-      hipLaunchKernelGGL(predecode_kernel<4>, dim3(blocks), dim3(256), 0, s, p.w, p.cb, p.cb_dt, p.cb_rows, p.cb_size,
-                         p.N, p.K, p.acc_scale, wd, rs);
-      break;
+    case 2: launch_prep_bits<2>(p, x_dtype, wd, rs, xh, flags, s); break;
+    case 3: launch_prep_bits<3>(p, x_dtype, wd, rs, xh, flags, s); break;
+    default: launch_prep_bits<4>(p, x_dtype, wd, rs, xh, flags, s); break;
   }
   const int rc = check_launch("linear_codebook (weight pre-decode)");
   if (rc != DIMQ_OK) return rc;
+  const PdOperands o{wd, rs, xh ? xh : static_cast<const uint16_t*>(p.x), xh ? p.K : p.ldx, flags, x_dtype, bits};
   switch (pd_pick_tile(p.M, p.N)) {
-    case 1: return launch_pd_modes<1>(p, mode, wd, rs, s);
-    case 2: return launch_pd_modes<2>(p, mode, wd, rs, s);
-    default: return launch_pd_modes<0>(p, mode, wd, rs, s);
+    case 1: return launch_pd_modes<1>(p, mode, o, s);
+    case 2: return launch_pd_modes<2>(p, mode, o, s);
+    case 3: return launch_pd_modes<3>(p, mode, o, s);
+    default: return launch_pd_modes<0>(p, mode, o, s);
   }
 }
 

@@ -1,10 +1,11 @@
-"""The pre-decoded-weight Linear path (large M, fp16 activations): the weights
-decoded once per call into the workspace as fp16, then an fp16 GEMM fed by
+"""The pre-decoded-weight Linear path (M >= 2048): the weights decoded once per
+call into the workspace as fp16 (bf16 / fp32 activations converted to fp16
+there too, with per-row range flags), then an fp16 GEMM fed by
 global_load_lds.  Checked against dequantize-then-F.linear in fp32 on the CPU
 (reference.py:91-110, oracle.linear_dequant_reference) at the weight-only bar
 2e-3 (bf16 outputs 8e-3), over bit widths, per-layer and per-output-channel
-codebooks, ragged M / N tails, K not a multiple of 64, and every fused
-epilogue the path instantiates."""
+codebooks, activation dtypes, ragged M / N tails, K not a multiple of 64,
+each tile shape and every fused epilogue the path instantiates."""
 
 from __future__ import annotations
 
@@ -17,14 +18,14 @@ from tests.conftest import announce
 pytestmark = pytest.mark.gpu
 
 
-def _case(M, N, K, bits, per_channel, seed):
+def _case(M, N, K, bits, per_channel, seed, xdt=torch.float16):
     g = torch.Generator().manual_seed(seed)
     E = 1 << bits
     rows = N if per_channel else 1
     cb = (torch.randn(rows, E, generator=g) * 0.05).sort(dim=1).values
     idx = torch.randint(0, E, (N, K), generator=g, dtype=torch.uint8)
     packed = torch.from_numpy(oracle.pack_bits(idx, bits))
-    x = torch.randn(M, K, generator=g).half()
+    x = torch.randn(M, K, generator=g).to(xdt)
     bias = torch.randn(N, generator=g) * 0.05
     return cb, packed, x, bias
 
@@ -32,37 +33,45 @@ def _case(M, N, K, bits, per_channel, seed):
 def test_workspace_query_selects_the_path():
     from dimq_amd import _C
     lib = _C.lib
-    F16, BF16 = 1, 2  # DIMQ_F16, DIMQ_BF16
+    F32, F16, BF16, F64 = 0, 1, 2, 3
     assert lib.dimq_linear_codebook_workspace_bytes(12608, 768, 3072, 4, F16) >= 3072 * 768 * 2 + 3072 * 4
     assert lib.dimq_linear_codebook_workspace_bytes(2048, 96, 352, 3, F16) >= 352 * 96 * 2 + 352 * 4
+    # bf16 / fp32 activations also keep their fp16 copy and one flag per row
+    assert lib.dimq_linear_codebook_workspace_bytes(2048, 768, 3072, 4, F32) >= \
+        3072 * 768 * 2 + 3072 * 4 + 2048 * 768 * 2 + 2048 * 4
+    assert lib.dimq_linear_codebook_workspace_bytes(12608, 768, 768, 4, BF16) >= \
+        768 * 768 * 2 + 768 * 4 + 12608 * 768 * 2 + 12608 * 4
     assert lib.dimq_linear_codebook_workspace_bytes(2047, 768, 3072, 4, F16) == 0  # below the M threshold
-    assert lib.dimq_linear_codebook_workspace_bytes(12608, 768, 3072, 4, BF16) == 0
+    assert lib.dimq_linear_codebook_workspace_bytes(1576, 768, 3072, 4, F32) == 0  # cfg1: the fused deep tile
+    assert lib.dimq_linear_codebook_workspace_bytes(12608, 768, 3072, 4, F64) == 0
     assert lib.dimq_linear_codebook_workspace_bytes(12608, 80, 3072, 4, F16) == 0  # K % 32 != 0
     assert lib.dimq_linear_codebook_workspace_bytes(12608, 768, 3072, 8, F16) == 0
 
 
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("bits", [2, 3, 4])
 @pytest.mark.parametrize("per_channel", [True, False])
 @torch.no_grad()
-def test_predecoded_linear_vs_dequant_reference(gpu, bits, per_channel):
+def test_predecoded_linear_vs_dequant_reference(gpu, bits, per_channel, xdt):
     from dimq_amd import ops
     M, N, K = 2085, 352, 96  # tails: M % 256 = 37, N % 256 = 96, K % 64 = 32
-    announce(f"predecode bits={bits} per_channel={per_channel} M={M} N={N} K={K}")
-    cb, packed, x, bias = _case(M, N, K, bits, per_channel, 10 * bits + per_channel)
+    announce(f"predecode bits={bits} per_channel={per_channel} x={xdt} M={M} N={N} K={K}")
+    cb, packed, x, bias = _case(M, N, K, bits, per_channel, 10 * bits + per_channel, xdt)
     y = ops.dimq_linear_codebook(x.to(gpu), packed.to(gpu), cb.to(gpu), bits, bias.to(gpu), N, K,
                                  out_dtype=torch.float32)
     ref = oracle.linear_dequant_reference(x.float(), packed, bits, cb, N, K, bias)
     assert oracle.rel_err(y.cpu(), ref) <= 2e-3
 
 
-@pytest.mark.parametrize("epi,out", [("relu", torch.float32), ("gelu", torch.float16), ("residual", torch.bfloat16),
-                                     (None, torch.bfloat16)])
+@pytest.mark.parametrize("M,N,K", [(2304, 512, 256), (2200, 768, 64), (8704, 2048, 32)])  # tiles 3, 2, 1
+@pytest.mark.parametrize("epi,out,xdt", [("relu", torch.float32, torch.float16), ("gelu", torch.float16, torch.float16),
+                                         ("residual", torch.bfloat16, torch.float16), (None, torch.bfloat16, torch.float16),
+                                         ("residual", torch.bfloat16, torch.bfloat16), (None, torch.float32, torch.float32)])
 @torch.no_grad()
-def test_predecoded_linear_epilogues(gpu, epi, out):
+def test_predecoded_linear_epilogues(gpu, M, N, K, epi, out, xdt):
     from dimq_amd import ops
-    M, N, K = 2304, 512, 256
-    announce(f"predecode epilogue={epi} out={out}")
-    cb, packed, x, bias = _case(M, N, K, 4, True, 7)
+    announce(f"predecode epilogue={epi} out={out} x={xdt} M={M} N={N} K={K}")
+    cb, packed, x, bias = _case(M, N, K, 4, True, 7, xdt)
     res = (torch.randn(M, N, generator=torch.Generator().manual_seed(8)) * 0.5).bfloat16() \
         if epi == "residual" else None
     y = ops.dimq_linear_codebook(x.to(gpu), packed.to(gpu), cb.to(gpu), 4, bias.to(gpu), N, K, out_dtype=out,

@@ -54,7 +54,7 @@ def _scaled(x, mode, g):
 
 
 LINEAR_CASES = [
-    # id, M, N, K, bits
+    # id, M, N, K, bits; the ops entry allocates the workspace its query asks for
     ("gemv_stream", 1, 256, 4096, 3),
     ("gemv_stream_splitk_4col", 8, 128, 2048, 4),
     ("gemv_cb", 5, 77, 1000, 3),
@@ -63,8 +63,28 @@ LINEAR_CASES = [
     ("gemm_cb8", 40, 64, 256, 8),
     ("deep_128x128", 200, 256, 768, 4),
     ("big_128x128", 130, 200, 2048, 3),
-    ("lds_256x256", 2100, 300, 192, 4),
+    # M >= 2048: activations converted to fp16 in the pre-decode launch, per-row flags, one tile shape each
+    ("predecoded_128x128", 2100, 300, 192, 4),
+    ("predecoded_128x384", 2200, 768, 64, 3),
+    ("predecoded_256x256", 8192, 1024, 32, 2),
+    ("predecoded_128x256", 8704, 2048, 32, 4),
+    # the same shape through the plain C entry (no workspace): the shared-decode 256x256 tile, 16-bit only
+    ("lds_256x256_no_workspace", 2100, 300, 192, 4),
 ]
+
+
+def _linear_no_workspace(gpu, x, packed, cb, bits, bias, N, K):
+    from dimq_amd import _C
+    y = torch.empty(x.shape[0], N, dtype=torch.float32, device=gpu)
+    xg, pg, cg, bg = x.to(gpu), packed.to(gpu), cb.to(gpu), bias.to(gpu)
+    dt = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+    with torch.cuda.device(gpu):
+        rc = _C.lib.dimq_linear_codebook(xg.data_ptr(), dt[x.dtype], x.shape[0], K, pg.data_ptr(), pg.numel(), bits,
+                                         cg.data_ptr(), 0, cg.shape[0] if cg.dim() == 2 else 1, cg.shape[-1],
+                                         bg.data_ptr(), 0, N, y.data_ptr(), 0, 0,
+                                         torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, _C.lib.dimq_last_error()
+    return y
 
 
 @pytest.mark.parametrize("mode", ["huge", "tiny", "mixed", "one"])
@@ -72,7 +92,7 @@ LINEAR_CASES = [
 @pytest.mark.parametrize("case", LINEAR_CASES, ids=[c[0] for c in LINEAR_CASES])
 def test_linear_codebook_activation_range(gpu, case, xdt, mode):
     name, M, N, K, bits = case
-    if name == "lds_256x256" and xdt == torch.float32:
+    if name == "lds_256x256_no_workspace" and xdt == torch.float32:
         pytest.skip("fp32 activations do not take the 256x256 tile")
     ops = _ops()
     announce(f"range linear {name} {xdt} {mode}")
@@ -81,8 +101,11 @@ def test_linear_codebook_activation_range(gpu, case, xdt, mode):
     x, s = _scaled(torch.randn(M, K, generator=g), mode, g)
     x = x.to(xdt)
     bias = torch.randn(N, generator=g) * 0.1 * float(s.min())
-    y = ops.dimq_linear_codebook(x.to(gpu), packed.to(gpu), cb.to(gpu), bits, bias.to(gpu), N, K,
-                                 out_dtype=torch.float32)
+    if name.endswith("no_workspace"):
+        y = _linear_no_workspace(gpu, x, packed, cb, bits, bias, N, K)
+    else:
+        y = ops.dimq_linear_codebook(x.to(gpu), packed.to(gpu), cb.to(gpu), bits, bias.to(gpu), N, K,
+                                     out_dtype=torch.float32)
     ref = oracle.linear_dequant_reference(x.float(), packed, bits, cb, N, K, bias)
     assert bool(torch.isfinite(y).all())
     assert oracle.rel_err(y, ref) <= TOL, (name, mode, oracle.rel_err(y, ref))
@@ -91,16 +114,18 @@ def test_linear_codebook_activation_range(gpu, case, xdt, mode):
             assert oracle.rel_err(y.cpu()[sel], ref[sel]) <= TOL, (name, mode, oracle.rel_err(y.cpu()[sel], ref[sel]))
 
 
-def test_linear_codebook_range_inf_nan_inputs(gpu):
+@pytest.mark.parametrize("M", [300, 2200])  # 2200: the pre-decoded path's guard
+def test_linear_codebook_range_inf_nan_inputs(gpu, M):
     """Genuine inf / NaN activations give the reference's inf / NaN pattern (the tiles holding them are
     recomputed in fp32), and the other rows stay exact to tolerance."""
     ops = _ops()
     g = _gen(5)
-    M, N, K = 300, 256, 768
+    N, K = 256, 768
     cb, packed = _codebook_case(N, K, 4, True, g)
     x = torch.randn(M, K, generator=g)
     x[3, 10] = float("inf")
     x[150, 0] = float("nan")
+    x[M - 2, 5] = float("-inf")
     for xdt in (torch.bfloat16, torch.float32):
         announce(f"range linear inf/nan {xdt}")
         xd = x.to(xdt)

@@ -440,13 +440,82 @@ def make_w4a4(dev, rotations, op="linear", chained=False):
     )
 
 
+VIT_LINEARS = {  # name: N, K, activation dtype, epilogue, output dtype (as in the bs64 forward)
+    "qkv": (2304, 768, torch.float16, None, torch.bfloat16),
+    "proj": (768, 768, torch.bfloat16, "residual", torch.bfloat16),
+    "fc1": (3072, 768, torch.float16, "gelu", torch.float16),
+    "fc2": (768, 3072, torch.float16, "residual", torch.bfloat16),
+}
+
+
+def make_vit_linear(dev, rotations, shape="qkv", path="auto"):
+    """One Linear of the ViT-B/16 bs64 forward at M = 64 x 197 tokens, 4-bit per-channel codebook of N(0, 0.02)
+    weights, with its fused epilogue; path "fused" calls the C entry without a workspace (the shared-decode
+    tile) instead of the pre-decoded path the ops take."""
+    from dimq_amd import _C, ops
+    from dimq_amd.codebook import assign_indices, init_centers_per_channel
+    from dimq_amd.export import pack_indices
+
+    N, K, xdt, epi, odt = VIT_LINEARS[shape]
+    M = 64 * 197
+    g = torch.Generator().manual_seed(N + K)
+    w = torch.randn(N, K, generator=g) * 0.02
+    b = torch.randn(N, generator=g) * 0.02
+    centers = init_centers_per_channel(w, 16)
+    packed = pack_indices(assign_indices(w, centers), 4).to(dev)
+    cb, bias = centers.to(dev), b.to(dev)
+    xs = [torch.randn(M, K, generator=g).to(xdt).to(dev) for _ in range(rotations)]
+    res = (torch.randn(M, N, generator=g) * 0.5).bfloat16().to(dev) if epi == "residual" else None
+    ys = [torch.empty(M, N, dtype=odt, device=dev) for _ in range(rotations)]
+    dt = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+    def step(i):
+        if path == "auto":
+            return ops.dimq_linear_codebook(xs[i], packed, cb, 4, bias, N, K, out_dtype=odt, residual=res,
+                                            activation="gelu" if epi == "gelu" else None)
+        rc = _C.lib.dimq_linear_codebook_ex(xs[i].data_ptr(), dt[xdt], M, K, packed.data_ptr(), packed.numel(), 4,
+                                            cb.data_ptr(), 0, N, 16, bias.data_ptr(), 0, N, ys[i].data_ptr(), dt[odt],
+                                            0 if res is None else res.data_ptr(), 2, 2 if epi == "gelu" else 0, 0,
+                                            torch.cuda.current_stream().cuda_stream)
+        if rc != 0:
+            raise RuntimeError(_C.lib.dimq_last_error())
+        return ys[i]
+
+    flops = 2.0 * M * N * K
+
+    def ref(rows):
+        import oracle
+        r = oracle.linear_dequant_reference(xs[0][:rows].float().cpu(), packed.cpu(), 4, centers, N, K, b)
+        if epi == "residual":
+            r = r + res[:rows].float().cpu()
+        elif epi == "gelu":
+            r = torch.nn.functional.gelu(r)
+        return r
+
+    def check():
+        import oracle
+        return oracle.rel_err(step(0).float().cpu()[:2048], ref(2048))
+
+    return dict(
+        name=f"vit_{shape}",
+        workload=f"ViT-B/16 bs64 {shape} Linear: X {str(xdt)[6:]} [{M},{K}], W [{N},{K}] N(0,0.02) 4-bit per-channel "
+                 f"codebook, bias{', ' + epi if epi else ''}, Y {str(odt)[6:]} ({path} path)",
+        step=step, flops=flops, alg_bytes=M * K * xdt.itemsize + packed.numel() + M * N * odt.itemsize,
+        bound="mfma", dtype="fp16", unit="TFLOP/s", per_step_units=flops / 1e12,
+        cpu_step=lambda rows: ref(rows), cpu_full_batch=M, check=check,
+        extra_config={"M": M, "N": N, "K": K, "bits": 4, "codebook": "per_channel", "path": path},
+        per_set_bytes=M * K * xdt.itemsize + M * N * odt.itemsize,
+    )
+
+
 FIXED_ROTATIONS = {"vit": 4, "resnet18": 4}
 WORKLOADS = {"cfg2": make_cfg2, "cfg1": make_cfg1, "cfg5": make_cfg5, "codec": make_codec, "copy": make_copy,
              "vit": make_vit, "resnet18": make_resnet18,
              "w4a4_linear": lambda dev, r: make_w4a4(dev, r, "linear"),
              "w4a4_conv": lambda dev, r: make_w4a4(dev, r, "conv"),
              "w4a4_linear_q": lambda dev, r: make_w4a4(dev, r, "linear", chained=True),
-             "w4a4_conv_q": lambda dev, r: make_w4a4(dev, r, "conv", chained=True)}
+             "w4a4_conv_q": lambda dev, r: make_w4a4(dev, r, "conv", chained=True),
+             "vit_linear": make_vit_linear}
 
 
 # ---------------------------------------------------------------------------
@@ -543,6 +612,9 @@ def run_workload(args, config, dev, steps, warmup, cpu_budget_s=15.0):
         kw["direction"] = args.direction
     if config == "cfg2":
         kw["layout"] = args.layout
+    if config == "vit_linear":
+        kw["shape"] = args.shape
+        kw["path"] = args.path
     # rotate buffer sets totalling > 512 MB
     if config in FIXED_ROTATIONS:
         # end-to-end models: inputs rotate over a few sets; the packed weights are re-read every step
@@ -611,6 +683,9 @@ def main():
     ap.add_argument("--layout", default="nchw", choices=["nchw", "nhwc"], help="cfg2 activation layout")
     ap.add_argument("--variant", default="auto", choices=["auto", "small_m", "mfma"],
                     help="cfg1/cfg5: force the LUT-gather (small_m) or dequant+MFMA kernel family")
+    ap.add_argument("--shape", default="qkv", choices=sorted(VIT_LINEARS), help="vit_linear: which Linear")
+    ap.add_argument("--path", default="auto", choices=["auto", "fused"],
+                    help="vit_linear: the ops' path (pre-decoded weights) or the no-workspace shared-decode tile")
     ap.add_argument("--rotations", type=int, default=0,
                     help="buffer sets to rotate (0 = enough for > 512 MB; smaller values let the MALL serve repeats)")
     ap.add_argument("--no-cpu", action="store_true")

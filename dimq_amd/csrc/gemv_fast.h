@@ -65,13 +65,15 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_stream_kernel(const GemmArg
   // codebook row of the lane's column (issued first: its wait does not wait for the streams)
   float cbv[E];
   load_cb_row<E>(p.cb, p.cb_dt, p.cb_rows == 1 ? 0 : n, p.cb_size, cbv);
+  // groups past the staged rows issue no load (at M = 1 seven of the eight
+  // would re-read group 0 and hold up the address path ahead of the weights)
   auto issue_x = [&](int base, RawA<XT> (&ra)[8]) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int gi = base + u * kGemvThreads + tid;
-      const int gg = gi < groups ? gi : 0;
-      const int m = gg / gpr;
-      issue_a16<XT>(p.x, (int64_t)m * p.ldx + kw0 + (int64_t)(gg - m * gpr) * 16, ra[u]);
+      if (gi >= groups) break;
+      const int m = gi / gpr;
+      issue_a16<XT>(p.x, (int64_t)m * p.ldx + kw0 + (int64_t)(gi - m * gpr) * 16, ra[u]);
     }
   };
   auto commit_x = [&](int base, const RawA<XT> (&ra)[8]) {

@@ -29,17 +29,22 @@
 namespace dimq {
 namespace {
 
-constexpr int kPdK = 32;  // k (halves) per pipeline stage: 64 bytes of a row
+constexpr int kPdK = 32;  // k granularity of the path (halves): the shorter stage
 
 // Below this many activation rows the fused kernels' per-tile decode costs
 // no more than the extra launch and the fp16 copies (cfg1, M 1576 fp32: 29.5
 // us either way, same box).
 constexpr int64_t kPredecodeMinM = 2048;
 
-// The 16-byte chunk c of stage row r lives at r * 64 + ((c ^ pd_swz(r)) << 4):
-// sixteen consecutive rows (the lanes one 16-byte LDS read serves per clock,
-// 256 bytes over gfx950's 64 banks) then hit sixteen distinct 16-byte slots.
-__device__ __forceinline__ int pd_swz(int r) { return (r >> 2) & 3; }
+// A stage row holds CH 16-byte chunks (CH 4: 32 k, CH 8: 64 k); chunk c of
+// row r lives at r * 16 CH + ((c ^ pd_swz<CH>(r)) << 4).  A 16-byte LDS read
+// serves 16 lanes (256 bytes, gfx950's 64 banks) per clock, i.e. 256 / (16 CH)
+// rows per bank window; the swizzle gives the 16 rows of one read 16
+// distinct 16-byte slots.
+template <int CH>
+__device__ __forceinline__ int pd_swz(int r) {
+  return (r / (16 / CH)) & (CH - 1);
+}
 
 // s_waitcnt vmcnt(n), leaving the other counters alone (gfx9 encoding:
 // vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
@@ -186,7 +191,7 @@ __global__ __launch_bounds__(256) void prep_kernel(const uint8_t* __restrict__ w
 // converted copy); with GUARD the copy's per-row flags decide, with the
 // accumulators' finiteness, whether the tile is recomputed in fp32 from p.x
 // (of dtype xt) and the packed weights.
-template <int WGM, int WGN, int MBLK, int NBLK, int MODE, int S, bool GUARD>
+template <int WGM, int WGN, int MBLK, int NBLK, int MODE, int S, bool GUARD, int CH>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs p, const uint16_t* __restrict__ wd,
                                                                  const float* __restrict__ rs,
                                                                  const uint16_t* __restrict__ xop, int64_t lda,
@@ -194,10 +199,15 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs 
   constexpr int NT = 64 * WGM * WGN;
   constexpr int BM = WGM * MBLK * 32;
   constexpr int BN = WGN * NBLK * 32;
-  constexpr int RSTAGE = (BN + BM) * 64;    // bytes of one stage: weight rows, then activation rows
-  constexpr int LPT = (BN + BM) * 4 / NT;   // 16-byte loads per thread and stage
-  static_assert(LPT * NT == (BN + BM) * 4, "a stage splits evenly over the threads");
-  static_assert(BN % 16 == 0 && BM % 16 == 0, "a wave's load covers 16 rows of one operand");
+  constexpr int KS = 8 * CH;                // k per stage
+  constexpr int RB = 16 * CH;               // bytes of a stage row
+  constexpr int RPB = 64 / CH;              // rows one wave-wide 16-byte load fills
+  constexpr int NSTEP = CH / 2;             // k16 steps per stage
+  constexpr int RSTAGE = (BN + BM) * RB;    // bytes of one stage: weight rows, then activation rows
+  constexpr int LPT = (BN + BM) * CH / NT;  // 16-byte loads per thread and stage
+  static_assert(CH == 4 || CH == 8, "32 or 64 k per stage");
+  static_assert(LPT * NT == (BN + BM) * CH, "a stage splits evenly over the threads");
+  static_assert(BN % RPB == 0 && BM % RPB == 0, "a wave's load covers rows of one operand");
   static_assert(S * LPT < 64, "outstanding loads fit the vmcnt counter");
   __shared__ __attribute__((aligned(16))) uint8_t sm[S * RSTAGE];
   // after the main loop: the tile's column factors at the end of the ring
@@ -226,14 +236,14 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs 
   }
 
   // load j of this thread: the wave's block b = j * (NT / 64) + wave holds
-  // stage rows 16 b .. 16 b + 15 (weight rows first, then activation rows);
-  // lane l fills LDS chunk l & 3 of row 16 b + (l >> 2), i.e. global chunk
-  // (l & 3) ^ swizzle.  Rows past N or M repeat the last row (not stored).
+  // stage rows RPB b .. RPB b + RPB - 1 (weight rows first, then activation
+  // rows); lane l fills LDS chunk l % CH of row RPB b + l / CH, i.e. global
+  // chunk (l % CH) ^ swizzle.  Rows past N or M repeat the last row (not stored).
   const uint16_t* src[LPT];
 #pragma unroll
   for (int j = 0; j < LPT; ++j) {
-    const int row = 16 * (j * (NT / 64) + wave) + (lane >> 2);
-    const int c = (lane & 3) ^ pd_swz(row);
+    const int row = RPB * (j * (NT / 64) + wave) + lane / CH;
+    const int c = (lane % CH) ^ pd_swz<CH>(row);
     if (row < BN) {
       const int64_t n = n0 + row < p.N ? n0 + row : p.N - 1;
       src[j] = wd + n * p.K + 8 * c;
@@ -242,11 +252,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs 
       src[j] = xop + m * lda + 8 * c;
     }
   }
-  const int64_t nk = p.K / kPdK;
+  const int64_t nk = p.K / KS;
   const uint32_t smb = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_g*)sm));  // LDS address of the ring
   auto issue = [&](int64_t kt, int slot) {
     if (kt >= nk) return;
-    const int64_t k = kt * kPdK;
+    const int64_t k = kt * KS;
 #pragma unroll
     for (int j = 0; j < LPT; ++j) {
       dma16(src[j] + k, smb + slot * RSTAGE + (j * (NT / 64) + wave) * 1024);
@@ -269,18 +279,17 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs 
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[mb][nb][i] = 0.0f;
 
-  // fragment offsets: rows rbase + col (rbase % 16 == 0) share the swizzle of col
-  const int sw = pd_swz(col);
-  const int fo[2] = {col * 64 + ((g ^ sw) << 4), col * 64 + (((2 + g) ^ sw) << 4)};
-  // fragments of k16 step s (0, 1) of the stage in ring slot `slot`
+  // fragment offsets: rows rbase + col (rbase % 32 == 0) share the swizzle of col
+  const int sw = pd_swz<CH>(col);
+  // fragments of k16 step s of the stage in ring slot `slot`: chunk 2 s + g
   auto load = [&](int slot, int s, half8 (&wf)[NBLK], half8 (&xf)[MBLK]) {
-    const uint8_t* base = sm + slot * RSTAGE;
+    const uint8_t* base = sm + slot * RSTAGE + col * RB + (((2 * s + g) ^ sw) << 4);
 #pragma unroll
     for (int nb = 0; nb < NBLK; ++nb)
-      wf[nb] = *reinterpret_cast<const half8*>(base + (wn * NBLK + nb) * 2048 + fo[s]);
+      wf[nb] = *reinterpret_cast<const half8*>(base + (wn * NBLK + nb) * 32 * RB);
 #pragma unroll
     for (int mb = 0; mb < MBLK; ++mb)
-      xf[mb] = *reinterpret_cast<const half8*>(base + BN * 64 + (wm * MBLK + mb) * 2048 + fo[s]);
+      xf[mb] = *reinterpret_cast<const half8*>(base + BN * RB + (wm * MBLK + mb) * 32 * RB);
   };
   auto mma = [&](const half8 (&wf)[NBLK], const half8 (&xf)[MBLK]) {
 #pragma unroll
@@ -291,26 +300,31 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs 
 
   // Ring of S slots, stage kt in slot kt % S.  Each step's fragment reads are
   // issued before the previous step's MFMAs, so LDS latency hides behind the
-  // matrix cores; the barrier that publishes stage kt + 1 sits between the
-  // two steps of stage kt, after which slot kt % S (read completely: the
+  // matrix cores; the barrier that publishes stage kt + 1 sits before the
+  // last step of stage kt, after which slot kt % S (read completely: the
   // barrier's fence waits for this wave's LDS reads) takes stage kt + S.
 #pragma unroll
   for (int s = 0; s < S; ++s) issue(s, s);
   wait_stages(nk - 1 < S - 1 ? nk - 1 : S - 1);  // stage 0 landed; stages 1 .. S - 1 may be in flight
   lds_barrier();
-  half8 wa[NBLK], xa[MBLK], wb[NBLK], xb[MBLK];
-  load(0, 0, wa, xa);
+  half8 wfr[2][NBLK], xfr[2][MBLK];  // fragments of two consecutive k16 steps (NSTEP is even)
+  load(0, 0, wfr[0], xfr[0]);
   int slot = 0;
   for (int64_t kt = 0; kt < nk; ++kt) {
-    load(slot, 1, wb, xb);
-    mma(wa, xa);
     const int next = slot == S - 1 ? 0 : slot + 1;
-    // stage kt + 1 landed; stages kt + 2 .. min(kt + S - 1, nk - 1) may be in flight
-    if (kt + 1 < nk) wait_stages(nk - 2 - kt < S - 2 ? nk - 2 - kt : S - 2);
-    lds_barrier();
-    issue(kt + S, slot);
-    if (kt + 1 < nk) load(next, 0, wa, xa);
-    mma(wb, xb);
+#pragma unroll
+    for (int st = 0; st < NSTEP; ++st) {
+      if (st + 1 < NSTEP) {
+        load(slot, st + 1, wfr[(st + 1) & 1], xfr[(st + 1) & 1]);
+      } else {
+        // stage kt + 1 landed; stages kt + 2 .. min(kt + S - 1, nk - 1) may be in flight
+        if (kt + 1 < nk) wait_stages(nk - 2 - kt < S - 2 ? nk - 2 - kt : S - 2);
+        lds_barrier();
+        issue(kt + S, slot);
+        if (kt + 1 < nk) load(next, 0, wfr[0], xfr[0]);
+      }
+      mma(wfr[st & 1], xfr[st & 1]);
+    }
     slot = next;
   }
   __syncthreads();  // every wave is done with the ring before it is reused
@@ -336,8 +350,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs 
   constexpr int PW = WGN * 32;
   constexpr int OTP = PW + 4;
   static_assert(BM * OTP * 4 + 2 * BN * 4 <= S * RSTAGE, "a parked pass and the column factors fit in the ring");
-  constexpr int CH = BM * PW / 8;
-  constexpr int CPT = (CH + NT - 1) / NT;
+  constexpr int NCHUNK = BM * PW / 8;
+  constexpr int CPT = (NCHUNK + NT - 1) / NT;
   float* ot = reinterpret_cast<float*>(sm);
   const bool vec8 = p.ldy % 8 == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0 && p.y_dt != DIMQ_F64;
   // 16-bit residuals of pass nb + 1 are requested before pass nb's stores
@@ -349,7 +363,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs 
       const int r = c / (PW / 8), q = c - r * (PW / 8);
       const int64_t m = m0 + r;
       const int64_t n = n0 + (q >> 2) * NBLK * 32 + nb * 32 + 8 * (q & 3);
-      if (c < CH && m < p.M && n + 8 <= p.N) res_issue<8>(p.epi, m * p.ldy + n, rr[u]);
+      if (c < NCHUNK && m < p.M && n + 8 <= p.N) res_issue<8>(p.epi, m * p.ldy + n, rr[u]);
     }
   };
   ResPairs<8> rr[CPT], rn[CPT];
@@ -374,7 +388,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs 
 #pragma unroll
     for (int u = 0; u < CPT; ++u) {
       const int c = tid + u * NT;
-      if (c >= CH) break;
+      if (c >= NCHUNK) break;
       const int r = c / (PW / 8), q = c - r * (PW / 8);
       const int64_t m = m0 + r;
       const int nl = (q >> 2) * NBLK * 32 + nb * 32 + 8 * (q & 3);  // column within the tile
@@ -420,8 +434,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs 
   }
 }
 
-// Tile shapes (WGM x WGN waves of (MBLK*32) x (NBLK*32), ring of 3 stages),
-// measured on the ViT-B/16 shapes at M 12,608 (kernel time, fp16 x, bf16 y):
+// Tile shapes (WGM x WGN waves of (MBLK*32) x (NBLK*32), a ring of S stages
+// of 8 CH k), measured on the ViT-B/16 shapes at M 12,608 (kernel time, fp16
+// x, bf16 y; 64-k stages in two slots measured 3-8 % faster than 32-k stages
+// in three for tiles 0 and 2, the same box, pre-decode launch included):
 //   0: 256 x 256, 8 waves of 64 x 128, one work-group per CU: qkv (N 2304)
 //      70.3 us against 78.9 for tile 1;
 //   1: 128 (m) x 256 (n), 4 waves of 64 x 128, 72 KB of LDS so two
@@ -434,30 +450,31 @@ template <int TILE>
 struct PdTile;
 template <>
 struct PdTile<0> {
-  static constexpr int WGM = 4, WGN = 2, MBLK = 2, NBLK = 4;
+  static constexpr int WGM = 4, WGN = 2, MBLK = 2, NBLK = 4, S = 2, CH = 8;
 };
 template <>
 struct PdTile<1> {
-  static constexpr int WGM = 2, WGN = 2, MBLK = 2, NBLK = 4;
+  static constexpr int WGM = 2, WGN = 2, MBLK = 2, NBLK = 4, S = 3, CH = 4;
 };
 template <>
 struct PdTile<2> {
-  static constexpr int WGM = 2, WGN = 4, MBLK = 2, NBLK = 3;
+  static constexpr int WGM = 2, WGN = 4, MBLK = 2, NBLK = 3, S = 2, CH = 8;
 };
 //   3: 128 x 128, 4 waves of 64 x 64, 48 KB of LDS: shapes whose tile-1 grid
 //      would leave CUs idle (small N).
 template <>
 struct PdTile<3> {
-  static constexpr int WGM = 2, WGN = 2, MBLK = 2, NBLK = 2;
+  static constexpr int WGM = 2, WGN = 2, MBLK = 2, NBLK = 2, S = 3, CH = 4;
 };
-constexpr int kPdStages = 3;
 
-int pd_pick_tile(int64_t M, int64_t N) {
-  if (N % 384 == 0 && N <= 1536) return 2;
+// Tiles 0 and 2 stage 64 k at a time (two slots of 64 KB) and need K % 64 == 0.
+int pd_pick_tile(int64_t M, int64_t N, int64_t K) {
+  const bool k64 = K % 64 == 0;
+  if (k64 && N % 384 == 0 && N <= 1536) return 2;
   if (((M + 127) / 128) * ((N + 255) / 256) < 256) return 3;
   const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
   const int64_t rem = tiles % 256;  // work-groups of the last round of tile 0
-  return (rem != 0 && rem * 2 < 256) ? 1 : 0;
+  return (!k64 || (rem != 0 && rem * 2 < 256)) ? 1 : 0;
 }
 
 struct PdOperands {
@@ -475,11 +492,11 @@ int launch_pd_gemm(const GemmArgs& p, const PdOperands& o, hipStream_t s) {
   constexpr int BM = T::WGM * T::MBLK * 32, BN = T::WGN * T::NBLK * 32;
   const int64_t tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
   if (o.flags) {
-    hipLaunchKernelGGL((gemm_pd_kernel<T::WGM, T::WGN, T::MBLK, T::NBLK, MODE, kPdStages, true>),
+    hipLaunchKernelGGL((gemm_pd_kernel<T::WGM, T::WGN, T::MBLK, T::NBLK, MODE, T::S, true, T::CH>),
                        dim3(static_cast<unsigned>(tiles)), dim3(64 * T::WGM * T::WGN), 0, s, p, o.wd, o.rs, o.xa,
                        o.lda, o.flags, o.xt, o.bits);
   } else {
-    hipLaunchKernelGGL((gemm_pd_kernel<T::WGM, T::WGN, T::MBLK, T::NBLK, MODE, kPdStages, false>),
+    hipLaunchKernelGGL((gemm_pd_kernel<T::WGM, T::WGN, T::MBLK, T::NBLK, MODE, T::S, false, T::CH>),
                        dim3(static_cast<unsigned>(tiles)), dim3(64 * T::WGM * T::WGN), 0, s, p, o.wd, o.rs, o.xa,
                        o.lda, o.flags, o.xt, o.bits);
   }
@@ -553,7 +570,7 @@ int launch_predecoded(const GemmArgs& p, int bits, int x_dtype, void* ws, int64_
   const int rc = check_launch("linear_codebook (weight pre-decode)");
   if (rc != DIMQ_OK) return rc;
   const PdOperands o{wd, rs, xh ? xh : static_cast<const uint16_t*>(p.x), xh ? p.K : p.ldx, flags, x_dtype, bits};
-  switch (pd_pick_tile(p.M, p.N)) {
+  switch (pd_pick_tile(p.M, p.N, p.K)) {
     case 1: return launch_pd_modes<1>(p, mode, o, s);
     case 2: return launch_pd_modes<2>(p, mode, o, s);
     case 3: return launch_pd_modes<3>(p, mode, o, s);

@@ -46,7 +46,7 @@ def _conv_weight_cfg2(g):
     return w
 
 
-def make_cfg2(dev, rotations, layout="nchw"):
+def make_cfg2(dev, rotations, layout="nchw", variant="auto"):
     from dimq_amd import ops
     from dimq_amd.codebook import assign_indices, init_centers_per_channel
     from dimq_amd.export import pack_indices
@@ -64,7 +64,7 @@ def make_cfg2(dev, rotations, layout="nchw"):
 
     def step(i):
         return ops.dimq_conv2d_codebook(xs[i], packed, cb, 2, None, (64, 64, 3, 3), (1, 1), (1, 1), (1, 1), 1,
-                                        out_dtype=torch.float32, prepared_weight=prepared)
+                                        out_dtype=torch.float32, prepared_weight=prepared, variant=variant)
 
     x_bytes = 32 * 64 * 56 * 56 * 2
     y_bytes = 32 * 64 * 56 * 56 * 4
@@ -606,7 +606,7 @@ def run_workload(args, config, dev, steps, warmup, cpu_budget_s=15.0):
     kw = {}
     if config == "cfg5":
         kw["M"] = args.m
-    if config in ("cfg1", "cfg5"):
+    if config in ("cfg1", "cfg5", "cfg2"):
         kw["variant"] = args.variant
     if config == "codec":
         kw["direction"] = args.direction
@@ -682,7 +682,8 @@ def main():
     ap.add_argument("--direction", default="unpack", choices=["pack", "unpack"])
     ap.add_argument("--layout", default="nchw", choices=["nchw", "nhwc"], help="cfg2 activation layout")
     ap.add_argument("--variant", default="auto", choices=["auto", "small_m", "mfma"],
-                    help="cfg1/cfg5: force the LUT-gather (small_m) or dequant+MFMA kernel family")
+                    help="cfg1/cfg5: force the LUT-gather (small_m) or dequant+MFMA kernel family; cfg2 (nhwc): "
+                         "mfma forces the implicit-GEMM tiles over the LDS-halo kernel")
     ap.add_argument("--shape", default="qkv", choices=sorted(VIT_LINEARS), help="vit_linear: which Linear")
     ap.add_argument("--path", default="auto", choices=["auto", "fused"],
                     help="vit_linear: the ops' path (pre-decoded weights) or the no-workspace shared-decode tile")

@@ -441,7 +441,9 @@ extern "C" int dimq_conv2d_codebook_ex(const void* x, int x_dtype, int x_layout,
   const bool halo_ok = hw > 0 && variant != DIMQ_VARIANT_SMALL_M && aligned(x, 16) &&
                        halo_eligible(s.C, s.KH, s.KW, s.sh, s.sw, s.dh, s.dw, s.groups, s.OH, s.OW, bits, x_dtype,
                                      epi_mode(epi), y_layout);
-  if (gemm_ok && (!halo_ok || prefer_gemm_conv(s.C, s.KH, s.KW, s.sh))) {
+  // DIMQ_VARIANT_MFMA forces the implicit-GEMM tiles over the LDS-halo kernel
+  // (A/B runs of the choice prefer_gemm_conv makes)
+  if (gemm_ok && (!halo_ok || variant == DIMQ_VARIANT_MFMA || prefer_gemm_conv(s.C, s.KH, s.KW, s.sh))) {
     GemmArgs p = conv_args(s, x, x_layout, reinterpret_cast<const uint8_t*>(prepared_w + hw), codebook, cb_dtype,
                            cb_rows, cb_size, bias, bias_dtype, y, y_dtype, y_layout);
     p.ldy = s.OC;

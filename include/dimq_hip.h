@@ -54,7 +54,9 @@ enum dimq_activation {
 enum dimq_variant {
   DIMQ_VARIANT_AUTO = 0,
   DIMQ_VARIANT_SMALL_M = 1, /* register-codebook gather, 16-row tiles (decode / GEMV) */
-  DIMQ_VARIANT_MFMA = 2     /* dequant-to-fp16 + MFMA, 64/128-row tiles */
+  DIMQ_VARIANT_MFMA = 2     /* dequant-to-fp16 + MFMA, 64/128-row tiles; for a conv with a prepared weight
+                               and NHWC 16-bit input, the implicit-GEMM tiles even where the LDS-halo
+                               kernel is the default */
 };
 
 /* Thread-local message of the last failing call on this thread. */

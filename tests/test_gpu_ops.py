@@ -668,6 +668,26 @@ def test_conv2d_codebook_vs_oracle(gpu, case, layout):
     assert oracle.rel_err(y.float(), ref) <= TOL, oracle.rel_err(y.float(), ref)
 
 
+@pytest.mark.parametrize("variant", ["auto", "mfma"])
+def test_conv2d_prepared_variants_agree(gpu, variant):
+    """ResNet layer1 form (C 64, 3x3/1, NHWC fp16, prepared weight): the default LDS-halo kernel and, with
+    variant "mfma", the implicit-GEMM tiles both meet the bar against the CPU reference."""
+    ops = _ops()
+    announce(f"conv prepared variant {variant}")
+    g = _gen(1234)
+    shape = (64, 64, 3, 3)
+    x = torch.relu(torch.randn(2, 64, 20, 18, generator=g)).half()
+    cb, idx, packed = _codebook_case(64, 576, 2, True, g)
+    bias = torch.randn(64, generator=g) * 0.1
+    pdv = packed.to(gpu)
+    prep = ops.prepare_conv_weight(pdv, 2, shape)
+    y = ops.dimq_conv2d_codebook(x.to(gpu).to(memory_format=torch.channels_last), pdv, cb.to(gpu), 2, bias.to(gpu),
+                                 shape, (1, 1), (1, 1), (1, 1), 1, out_dtype=torch.float32, prepared_weight=prep,
+                                 variant=variant)
+    ref = oracle.conv2d_dequant_reference(x.float(), packed, 2, cb, shape, bias, 1, 1, 1, 1)
+    assert oracle.rel_err(y.float(), ref) <= TOL
+
+
 # ---------------------------------------------------------------- small-channel stride-2 stem conv
 @pytest.mark.parametrize("case", [
     dict(B=2, C=3, H=224, W=224, OC=64, K=7, p=3, bits=8, dt=torch.float16, out=torch.float16, pc=True),  # ResNet stem

@@ -64,7 +64,8 @@ def test_predecoded_linear_vs_dequant_reference(gpu, bits, per_channel, xdt):
 
 
 @pytest.mark.parametrize("M,N,K", [(2304, 512, 256), (2200, 768, 64), (8704, 2048, 32), (8192, 1024, 64),
-                                   (8192, 1024, 96)])  # tiles 3, 2, 1, 0; K % 64 = 32 moves tile 0's shape to 1
+                                   (8192, 1024, 96), (8192, 128, 64)])
+# tiles 3, 2, 1, 0; K % 64 = 32 moves tile 0's shape to 1; N <= 128 takes tile 3
 @pytest.mark.parametrize("epi,out,xdt", [("relu", torch.float32, torch.float16), ("gelu", torch.float16, torch.float16),
                                          ("residual", torch.bfloat16, torch.float16), (None, torch.bfloat16, torch.float16),
                                          ("residual", torch.bfloat16, torch.bfloat16), (None, torch.float32, torch.float32)])

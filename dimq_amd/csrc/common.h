@@ -70,6 +70,15 @@ __device__ __forceinline__ uint32_t f16x2_rne(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, h2));
 }
 
+// Two fp32 -> one dword of bf16 (lo in bits 0-15), round to nearest even:
+// one v_cvt_pk_bf16_f32, the same bits as float_to_bf16_bits for every
+// non-NaN input (fp32 denormals kept); a NaN stays a NaN.
+__device__ __forceinline__ uint32_t bf16x2_rne(float lo, float hi) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, b2));
+}
+
 // ---------------------------------------------------------------- fp16 range guard
 // The weight-only kernels round fp32 and bf16 activations to fp16 for the
 // matrix cores.  A tile's fp16 result is kept when (a) some activation of the

@@ -422,7 +422,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_lds_kernel(const GemmArgs
   constexpr int TPR = 8 / B_TASKS;  // threads per weight row
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kBigLDA];
   __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * kBigLDA];
-  __shared__ float escale[BN], ebias[BN];  // per tile column: 2^-e and the bias
+  __shared__ __attribute__((aligned(16))) float escale[BN];  // per tile column: 2^-e
+  __shared__ __attribute__((aligned(16))) float ebias[BN];   // and the bias
   // the codebook rows are staged in the second weight buffer, which is first
   // written after the barrier that follows the codebook planes' setup
   static_assert(BN * E * 4 <= BN * kBigLDA * 2, "codebook staging fits in one weight stage buffer");
@@ -600,45 +601,57 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_lds_kernel(const GemmArgs
         if (c < CH && m < p.M && n + 8 <= p.N) res_issue<8>(p.epi, m * p.ldy + n, rr[u]);
       }
     }
+    // A thread's chunks share column group q = tid % (PW / 8) (NT is a
+    // multiple of PW / 8): its 8 column factors are read once per pass as
+    // aligned 16-byte loads, and every chunk's parked values before any is
+    // used, so the LDS latencies overlap; per-chunk branches only guard stores.
+    static_assert(NT % (PW / 8) == 0, "a thread's chunks share one column group");
+    const int qg = tid % (PW / 8);
+    const int nlg = (qg >> 2) * NBLK * 32 + nb * 32 + 8 * (qg & 3);  // a multiple of 8, nlg + 7 < BN
+    const float4 s0 = reinterpret_cast<const float4*>(escale)[nlg / 4];
+    const float4 s1 = reinterpret_cast<const float4*>(escale)[nlg / 4 + 1];
+    const float4 b0 = reinterpret_cast<const float4*>(ebias)[nlg / 4];
+    const float4 b1 = reinterpret_cast<const float4*>(ebias)[nlg / 4 + 1];
+    float v[CPT][8];
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+      const int r = (tid + u * NT < CH ? tid + u * NT : CH - 1) / (PW / 8);
+      const float4* a4 = reinterpret_cast<const float4*>(ot + r * OTP) + 2 * qg;
+      const float4 a0 = a4[0], a1 = a4[1];
+      v[u][0] = a0.x * s0.x + b0.x; v[u][1] = a0.y * s0.y + b0.y;
+      v[u][2] = a0.z * s0.z + b0.z; v[u][3] = a0.w * s0.w + b0.w;
+      v[u][4] = a1.x * s1.x + b1.x; v[u][5] = a1.y * s1.y + b1.y;
+      v[u][6] = a1.z * s1.z + b1.z; v[u][7] = a1.w * s1.w + b1.w;
+    }
 #pragma unroll
     for (int u = 0; u < CPT; ++u) {
       const int c = tid + u * NT;
-      if (c >= CH) break;
-      const int r = c / (PW / 8), q = c - r * (PW / 8);
+      if (CH % NT != 0 && c >= CH) break;
+      const int r = c / (PW / 8);
       const int64_t m = m0 + r;
-      const int nl = (q >> 2) * NBLK * 32 + nb * 32 + 8 * (q & 3);  // column within the tile
-      const int64_t n = n0 + nl;
+      const int64_t n = n0 + (qg >> 2) * NBLK * 32 + nb * 32 + 8 * (qg & 3);
       if (m >= p.M) continue;
-      const float4 a0 = *reinterpret_cast<const float4*>(ot + r * OTP + 8 * q);
-      const float4 a1 = *reinterpret_cast<const float4*>(ot + r * OTP + 8 * q + 4);
-      float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int ni = nl + i < BN ? nl + i : BN - 1;
-        v[i] = v[i] * escale[ni] + ebias[ni];
-      }
       const int64_t off = m * p.ldy + n;
       if (vec8 && n + 8 <= p.N) {
-        epi_m<MODE, 8>(p.epi, &rr[u], off, true, v);
+        epi_m<MODE, 8>(p.epi, &rr[u], off, true, v[u]);
         if (p.y_dt == DIMQ_F32) {
           float* yp = reinterpret_cast<float*>(p.y) + off;
-          *reinterpret_cast<float4*>(yp) = make_float4(v[0], v[1], v[2], v[3]);
-          *reinterpret_cast<float4*>(yp + 4) = make_float4(v[4], v[5], v[6], v[7]);
+          *reinterpret_cast<float4*>(yp) = make_float4(v[u][0], v[u][1], v[u][2], v[u][3]);
+          *reinterpret_cast<float4*>(yp + 4) = make_float4(v[u][4], v[u][5], v[u][6], v[u][7]);
         } else {
-          uint32_t h[8];
+          uint32_t h[4];
           if (p.y_dt == DIMQ_F16) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) h[i] = float_to_f16_bits(v[i]);
+            for (int i = 0; i < 4; ++i) h[i] = f16x2_rne(v[u][2 * i], v[u][2 * i + 1]);
           } else {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) h[i] = float_to_bf16_bits(v[i]);
+            for (int i = 0; i < 4; ++i) h[i] = bf16x2_rne(v[u][2 * i], v[u][2 * i + 1]);
           }
-          *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p.y) + off) =
-              make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+          *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p.y) + off) = make_uint4(h[0], h[1], h[2], h[3]);
         }
       } else {
         for (int i = 0; i < 8; ++i)
-          if (n + i < p.N) store_from_float(p.y, p.y_dt, off + i, epi1_m<MODE>(p.epi, off + i, v[i]));
+          if (n + i < p.N) store_from_float(p.y, p.y_dt, off + i, epi1_m<MODE>(p.epi, off + i, v[u][i]));
       }
     }
     __syncthreads();  // the next pass overwrites the parked values

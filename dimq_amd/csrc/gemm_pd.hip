@@ -12,11 +12,11 @@
 //      being busy as long as the matrix cores.
 //   2. gemm_pd_kernel: an fp16 x fp16 GEMM whose operands reach LDS through
 //      global_load_lds (16 bytes per lane, no registers held, no VALU in the
-//      main loop), in a ring of S stages of 32 k.  LDS rows are 64 bytes with
-//      their four 16-byte chunks XOR-swizzled by (row >> 2) & 3, so the
-//      16-byte fragment reads of sixteen consecutive rows cover all 64 banks.
-//      Work-group = 8 waves (4 along m x 2 along n) on a 256 x 256 tile, wave
-//      tile 64 x 128, v_mfma_f32_32x32x16_f16 with the weights as the A
+//      main loop), in a ring of S stages of 32 or 64 k.  A stage row's 16-byte
+//      chunks are XOR-swizzled (pd_swz) so the 16-byte fragment reads of
+//      sixteen consecutive rows cover all 64 banks.  Tile shapes are listed
+//      at PdTile; e.g. 8 waves (4 along m x 2 along n) on a 256 x 256 tile,
+//      wave tile 64 x 128, v_mfma_f32_32x32x16_f16 with the weights as the A
 //      operand (rows = output columns n) and the activations as the B operand,
 //      so a lane's accumulator holds 4 consecutive n of one m.  The epilogue
 //      parks each column pass in LDS and stores 8-column runs of rows.
@@ -254,14 +254,25 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs 
   }
   const int64_t nk = p.K / KS;
   const uint32_t smb = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_g*)sm));  // LDS address of the ring
-  auto issue = [&](int64_t kt, int slot) {
+  // loads J0 .. J1 - 1 of stage kt into ring slot `slot`
+  auto issue_part = [&](int64_t kt, int slot, auto j0c, auto j1c) {
     if (kt >= nk) return;
     const int64_t k = kt * KS;
+    constexpr int J0 = decltype(j0c)::value, J1 = decltype(j1c)::value;
 #pragma unroll
-    for (int j = 0; j < LPT; ++j) {
+    for (int j = J0; j < J1; ++j) {
       dma16(src[j] + k, smb + slot * RSTAGE + (j * (NT / 64) + wave) * 1024);
     }
   };
+  using J0c = std::integral_constant<int, 0>;
+  using JHc = std::integral_constant<int, LPT / 2>;
+  using JLc = std::integral_constant<int, LPT>;
+  auto issue = [&](int64_t kt, int slot) { issue_part(kt, slot, J0c{}, JLc{}); };
+  // With two slots the stage that refills the slot freed by a barrier is
+  // requested in two halves, after the barrier and after the next k16 step's
+  // MFMAs: eight 16-byte loads per lane at once held the waves at the
+  // vector-memory issue (qkv 70.8 -> 65.8 us, fc2 -3 %, same box).
+  constexpr bool SPLIT = S == 2 && NSTEP >= 2;
   // s_waitcnt leaving this thread's loads of the n youngest issued stages in
   // flight (0 <= n < S)
   auto wait_stages = [&](int64_t n) {
@@ -320,10 +331,16 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs 
         // stage kt + 1 landed; stages kt + 2 .. min(kt + S - 1, nk - 1) may be in flight
         if (kt + 1 < nk) wait_stages(nk - 2 - kt < S - 2 ? nk - 2 - kt : S - 2);
         lds_barrier();
-        issue(kt + S, slot);
+        if constexpr (SPLIT) issue_part(kt + S, slot, J0c{}, JHc{});
+        else issue(kt + S, slot);
         if (kt + 1 < nk) load(next, 0, wfr[0], xfr[0]);
       }
       mma(wfr[st & 1], xfr[st & 1]);
+      // the second half of stage kt + 1 (slot `next`), whose first half the
+      // previous barrier requested; the prologue requested stage 1 whole
+      if constexpr (SPLIT) {
+        if (st == 0 && kt > 0) issue_part(kt + 1, next, JHc{}, JLc{});
+      }
     }
     slot = next;
   }
@@ -385,45 +402,59 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs 
     if constexpr ((MODE & kEpiRes) != 0) {
       if (rpair && nb + 1 < NBLK) res_load(nb + 1, rn);
     }
+    // Chunk c = tid + u NT covers row c / (PW / 8) and the 8 columns nl ..
+    // nl + 7 of column group q = c % (PW / 8), the same for all of this
+    // thread's chunks (NT is a multiple of PW / 8): its column factors are
+    // read once per pass as four aligned 16-byte loads.  Every chunk's parked
+    // values are read before any is used, so the LDS latencies overlap;
+    // per-chunk control flow only guards the stores.
+    static_assert(NT % (PW / 8) == 0, "a thread's chunks share one column group");
+    const int qg = tid % (PW / 8);
+    const int nlg = (qg >> 2) * NBLK * 32 + nb * 32 + 8 * (qg & 3);  // a multiple of 8, nlg + 7 < BN
+    const float4* es4 = reinterpret_cast<const float4*>(escale) + nlg / 4;
+    const float4* eb4 = reinterpret_cast<const float4*>(ebias) + nlg / 4;
+    const float4 s0 = es4[0], s1 = es4[1], b0 = eb4[0], b1 = eb4[1];
+    float v[CPT][8];
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+      const int c = tid + u * NT < NCHUNK ? tid + u * NT : NCHUNK - 1;
+      const int r = c / (PW / 8);
+      const float4* a4 = reinterpret_cast<const float4*>(ot + r * OTP) + 2 * qg;
+      const float4 a0 = a4[0], a1 = a4[1];
+      v[u][0] = a0.x * s0.x + b0.x; v[u][1] = a0.y * s0.y + b0.y;
+      v[u][2] = a0.z * s0.z + b0.z; v[u][3] = a0.w * s0.w + b0.w;
+      v[u][4] = a1.x * s1.x + b1.x; v[u][5] = a1.y * s1.y + b1.y;
+      v[u][6] = a1.z * s1.z + b1.z; v[u][7] = a1.w * s1.w + b1.w;
+    }
 #pragma unroll
     for (int u = 0; u < CPT; ++u) {
       const int c = tid + u * NT;
-      if (c >= NCHUNK) break;
+      if (NCHUNK % NT != 0 && c >= NCHUNK) break;
       const int r = c / (PW / 8), q = c - r * (PW / 8);
       const int64_t m = m0 + r;
-      const int nl = (q >> 2) * NBLK * 32 + nb * 32 + 8 * (q & 3);  // column within the tile
-      const int64_t n = n0 + nl;
+      const int64_t n = n0 + (q >> 2) * NBLK * 32 + nb * 32 + 8 * (q & 3);
       if (m >= p.M) continue;
-      const float4 a0 = *reinterpret_cast<const float4*>(ot + r * OTP + 8 * q);
-      const float4 a1 = *reinterpret_cast<const float4*>(ot + r * OTP + 8 * q + 4);
-      float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int ni = nl + i < BN ? nl + i : BN - 1;
-        v[i] = v[i] * escale[ni] + ebias[ni];
-      }
       const int64_t off = m * p.ldy + n;
       if (vec8 && n + 8 <= p.N) {
-        epi_m<MODE, 8>(p.epi, &rr[u], off, true, v);
+        epi_m<MODE, 8>(p.epi, &rr[u], off, true, v[u]);
         if (p.y_dt == DIMQ_F32) {
           float* yp = reinterpret_cast<float*>(p.y) + off;
-          *reinterpret_cast<float4*>(yp) = make_float4(v[0], v[1], v[2], v[3]);
-          *reinterpret_cast<float4*>(yp + 4) = make_float4(v[4], v[5], v[6], v[7]);
+          *reinterpret_cast<float4*>(yp) = make_float4(v[u][0], v[u][1], v[u][2], v[u][3]);
+          *reinterpret_cast<float4*>(yp + 4) = make_float4(v[u][4], v[u][5], v[u][6], v[u][7]);
         } else {
-          uint32_t h[8];
+          uint32_t h[4];
           if (p.y_dt == DIMQ_F16) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) h[i] = float_to_f16_bits(v[i]);
+            for (int i = 0; i < 4; ++i) h[i] = f16x2_rne(v[u][2 * i], v[u][2 * i + 1]);
           } else {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) h[i] = float_to_bf16_bits(v[i]);
+            for (int i = 0; i < 4; ++i) h[i] = bf16x2_rne(v[u][2 * i], v[u][2 * i + 1]);
           }
-          *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p.y) + off) =
-              make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+          *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p.y) + off) = make_uint4(h[0], h[1], h[2], h[3]);
         }
       } else {
         for (int i = 0; i < 8; ++i)
-          if (n + i < p.N) store_from_float(p.y, p.y_dt, off + i, epi1_m<MODE>(p.epi, off + i, v[i]));
+          if (n + i < p.N) store_from_float(p.y, p.y_dt, off + i, epi1_m<MODE>(p.epi, off + i, v[u][i]));
       }
     }
     __syncthreads();  // the next pass overwrites the parked values

@@ -84,7 +84,8 @@ def test_codec_errors(gpu):
 
 
 def test_codec_stress_2p27_3bit_round_trip(gpu):
-    """cfg5: 2^27 random 3-bit indices, bit-exact pack/unpack round trip; packed bytes checked on a slice."""
+    """cfg5: 2^27 random 3-bit indices, bit-exact pack/unpack round trip; the whole packed stream equals the
+    oracle's (C packer, a few seconds on the host), and the oracle's stream unpacks to the indices."""
     ops = _ops()
     announce("codec stress 2^27 3-bit")
     n = 1 << 27
@@ -94,10 +95,9 @@ def test_codec_stress_2p27_3bit_round_trip(gpu):
     assert packed.numel() == n * 3 // 8
     back = ops.unpack_bits(packed, n, 3)
     assert torch.equal(back, d)
-    sl = slice(1 << 20, (1 << 20) + 4096)  # a 4096-index window on a 3-byte boundary
-    ref = oracle.pack_bits(idx[sl], 3)
-    byte0 = (1 << 20) * 3 // 8
-    assert np.array_equal(packed[byte0:byte0 + ref.size].cpu().numpy(), ref)
+    ref = oracle.pack_bits(idx, 3)
+    assert np.array_equal(packed.cpu().numpy(), ref)
+    assert torch.equal(ops.unpack_bits(torch.from_numpy(ref).to(gpu), n, 3), d)
 
 
 # ---------------------------------------------------------------- hard quantization

@@ -204,11 +204,14 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs 
   constexpr int RPB = 64 / CH;              // rows one wave-wide 16-byte load fills
   constexpr int NSTEP = CH / 2;             // k16 steps per stage
   constexpr int RSTAGE = (BN + BM) * RB;    // bytes of one stage: weight rows, then activation rows
-  constexpr int LPT = (BN + BM) * CH / NT;  // 16-byte loads per thread and stage
+  constexpr int NW = NT / 64;
+  constexpr int NLB = (BN + BM) / RPB;       // wave-wide 16-byte loads per stage
+  constexpr int LPT = (NLB + NW - 1) / NW;   // loads per thread and stage; the last may cover only some waves
+  constexpr int LPT_MIN = NLB / NW;          // loads every wave issues per stage
   static_assert(CH == 4 || CH == 8, "32 or 64 k per stage");
-  static_assert(LPT * NT == (BN + BM) * CH, "a stage splits evenly over the threads");
   static_assert(BN % RPB == 0 && BM % RPB == 0, "a wave's load covers rows of one operand");
-  static_assert(S * LPT < 64, "outstanding loads fit the vmcnt counter");
+  static_assert(LPT_MIN >= 1 && S * LPT < 64, "outstanding loads fit the vmcnt counter");
+  static_assert(BN <= NT, "one thread per tile column stages the column factors");
   __shared__ __attribute__((aligned(16))) uint8_t sm[S * RSTAGE];
   // after the main loop: the tile's column factors at the end of the ring
   float* escale = reinterpret_cast<float*>(sm + S * RSTAGE) - 2 * BN;
@@ -242,7 +245,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs 
   const uint16_t* src[LPT];
 #pragma unroll
   for (int j = 0; j < LPT; ++j) {
-    const int row = RPB * (j * (NT / 64) + wave) + lane / CH;
+    const int lb = j * NW + wave < NLB ? j * NW + wave : NLB - 1;  // past NLB: not issued
+    const int row = RPB * lb + lane / CH;
     const int c = (lane % CH) ^ pd_swz<CH>(row);
     if (row < BN) {
       const int64_t n = n0 + row < p.N ? n0 + row : p.N - 1;
@@ -261,7 +265,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs 
     constexpr int J0 = decltype(j0c)::value, J1 = decltype(j1c)::value;
 #pragma unroll
     for (int j = J0; j < J1; ++j) {
-      dma16(src[j] + k, smb + slot * RSTAGE + (j * (NT / 64) + wave) * 1024);
+      if (LPT != LPT_MIN && j == LPT - 1 && j * NW + wave >= NLB) break;  // wave-uniform
+      dma16(src[j] + k, smb + slot * RSTAGE + (j * NW + wave) * 1024);
     }
   };
   using J0c = std::integral_constant<int, 0>;
@@ -273,12 +278,14 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pd_kernel(const GemmArgs 
   // MFMAs: eight 16-byte loads per lane at once held the waves at the
   // vector-memory issue (qkv 70.8 -> 65.8 us, fc2 -3 %, same box).
   constexpr bool SPLIT = S == 2 && NSTEP >= 2;
-  // s_waitcnt leaving this thread's loads of the n youngest issued stages in
-  // flight (0 <= n < S)
+  // s_waitcnt leaving at most n stages' worth of this thread's youngest loads
+  // in flight (0 <= n < S): n LPT_MIN, which a wave that issues LPT loads per
+  // stage satisfies only once some of the youngest stage's loads have landed
+  // too (a conservative wait, never a short one)
   auto wait_stages = [&](int64_t n) {
     static_for<S>([&](auto ic) {
       constexpr int I = decltype(ic)::value;
-      if (I == n) wait_vmcnt<I * LPT>();
+      if (I == n) wait_vmcnt<I * LPT_MIN>();
     });
   };
 
@@ -498,10 +505,20 @@ template <>
 struct PdTile<3> {
   static constexpr int WGM = 2, WGN = 2, MBLK = 2, NBLK = 2, S = 3, CH = 4;
 };
+//   4: 160 x 256, 10 waves of 32 x 128 (the last of a stage's six 16-byte
+//      loads per lane covers two waves): N 768 as 237 tiles instead of 198
+//      on 256 CUs; proj (K 768) 40.3-41.5 -> 37.9-38.1 us, both launches,
+//      same box; fc2 (K 3072) no faster, its main loop dominating (wave tiles
+//      of 32 x 128 read 1.25 fragments per MFMA against 0.83).
+template <>
+struct PdTile<4> {
+  static constexpr int WGM = 5, WGN = 2, MBLK = 1, NBLK = 4, S = 2, CH = 8;
+};
 
-// Tiles 0 and 2 stage 64 k at a time (two slots of 64 KB) and need K % 64 == 0.
+// Tiles 0, 2 and 4 stage 64 k at a time (two slots) and need K % 64 == 0.
 int pd_pick_tile(int64_t M, int64_t N, int64_t K) {
   const bool k64 = K % 64 == 0;
+  if (k64 && N % 256 == 0 && N <= 768 && K <= 1024 && M >= 4096) return 4;
   if (k64 && N % 384 == 0 && N <= 1536) return 2;
   if (N <= 128 || ((M + 127) / 128) * ((N + 255) / 256) < 256) return 3;
   const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
@@ -606,6 +623,7 @@ int launch_predecoded(const GemmArgs& p, int bits, int x_dtype, void* ws, int64_
     case 1: return launch_pd_modes<1>(p, mode, o, s);
     case 2: return launch_pd_modes<2>(p, mode, o, s);
     case 3: return launch_pd_modes<3>(p, mode, o, s);
+    case 4: return launch_pd_modes<4>(p, mode, o, s);
     default: return launch_pd_modes<0>(p, mode, o, s);
   }
 }

@@ -64,8 +64,9 @@ def test_predecoded_linear_vs_dequant_reference(gpu, bits, per_channel, xdt):
 
 
 @pytest.mark.parametrize("M,N,K", [(2304, 512, 256), (2200, 768, 64), (8704, 2048, 32), (8192, 1024, 64),
-                                   (8192, 1024, 96), (8192, 128, 64)])
-# tiles 3, 2, 1, 0; K % 64 = 32 moves tile 0's shape to 1; N <= 128 takes tile 3
+                                   (8192, 1024, 96), (8192, 128, 64), (4200, 768, 192), (4100, 512, 1024)])
+# tiles 3, 2, 1, 0; K % 64 = 32 moves tile 0's shape to 1; N <= 128 takes tile 3; the last two take tile 4
+# (160 x 256, ragged M: 4200 % 160 = 40, 4100 % 160 = 100)
 @pytest.mark.parametrize("epi,out,xdt", [("relu", torch.float32, torch.float16), ("gelu", torch.float16, torch.float16),
                                          ("residual", torch.bfloat16, torch.float16), (None, torch.bfloat16, torch.float16),
                                          ("residual", torch.bfloat16, torch.bfloat16), (None, torch.float32, torch.float32)])

@@ -66,6 +66,7 @@ LINEAR_CASES = [
     # M >= 2048: activations converted to fp16 in the pre-decode launch, per-row flags, one tile shape each
     ("predecoded_128x128", 2100, 300, 192, 4),
     ("predecoded_128x384", 2200, 768, 64, 3),
+    ("predecoded_160x256", 4200, 768, 192, 2),
     ("predecoded_256x256", 8192, 1024, 64, 2),
     ("predecoded_128x256", 8704, 2048, 32, 4),
     # the same shape through the plain C entry (no workspace): the shared-decode 256x256 tile, 16-bit only

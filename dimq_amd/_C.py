@@ -88,6 +88,10 @@ _SIGS = {
     "dimq_linear_codebook_workspace_bytes": (_i64, [_i64, _i64, _i64, _int, _int]),
     "dimq_linear_codebook_ex_ws": (_int, [_vp, _int, _i64, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _vp, _int,
                                           _i64, _vp, _int, _vp, _int, _int, _int, _vp, _i64, _vp]),
+    "dimq_codebook_predecode_bytes": (_i64, [_i64, _i64, _int]),
+    "dimq_codebook_predecode_batch": (_int, [_vp, _int, _vp]),
+    "dimq_linear_codebook_predecoded": (_int, [_vp, _int, _i64, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _vp,
+                                               _int, _i64, _vp, _int, _vp, _int, _int, _int, _vp, _vp, _i64, _vp]),
     "dimq_linear_codebook_act_workspace_bytes": (_i64, [_i64, _i64]),
     "dimq_linear_codebook_act": (_int, [_vp, _int, _i64, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _vp, _i64, _vp,
                                         _int, _i64, _vp, _int, _int, _vp, _i64, _vp]),
@@ -373,7 +377,7 @@ def _residual_args(residual: torch.Tensor | None, y: torch.Tensor, mf=torch.cont
 
 
 def linear_codebook_impl(x, packed_w, codebook, bits, bias, out_features, in_features, out_dtype=None, variant=0,
-                         residual=None, activation=0):
+                         residual=None, activation=0, decoded=None):
     _require_cuda(x, "linear_codebook expects CUDA input")
     _require_cuda(packed_w, "linear_codebook expects CUDA packed_weight")
     _require_cuda(codebook, "linear_codebook expects CUDA codebook")
@@ -396,11 +400,66 @@ def linear_codebook_impl(x, packed_w, codebook, bits, bias, out_features, in_fea
     ws = _workspace(lib.dimq_linear_codebook_workspace_bytes(M, in_features, out_features, int(bits), _dtype(xc)),
                     xc.device)
     with torch.cuda.device(xc.device):
-        _check(lib.dimq_linear_codebook_ex_ws(_ptr(xc), _dtype(xc), M, in_features, _ptr(pw), pw.numel(), int(bits),
-                                              _ptr(cb), _dtype(cb), rows, size, bp, bdt, out_features, _ptr(y),
-                                              _dtype(y), rp, rdt, int(activation), int(variant), _ptr(ws),
-                                              0 if ws is None else ws.numel(), _stream(xc.device)))
+        if decoded is None:
+            _check(lib.dimq_linear_codebook_ex_ws(_ptr(xc), _dtype(xc), M, in_features, _ptr(pw), pw.numel(),
+                                                  int(bits), _ptr(cb), _dtype(cb), rows, size, bp, bdt, out_features,
+                                                  _ptr(y), _dtype(y), rp, rdt, int(activation), int(variant),
+                                                  _ptr(ws), 0 if ws is None else ws.numel(), _stream(xc.device)))
+        else:
+            _require_cuda(decoded, "decoded weights must be CUDA")
+            if decoded.dtype != torch.uint8 or decoded.numel() < lib.dimq_codebook_predecode_bytes(
+                    out_features, in_features, int(bits)):
+                raise RuntimeError("decoded must be the uint8 buffer predecode_codebook_weights made for this layer")
+            _check(lib.dimq_linear_codebook_predecoded(_ptr(xc), _dtype(xc), M, in_features, _ptr(pw), pw.numel(),
+                                                       int(bits), _ptr(cb), _dtype(cb), rows, size, bp, bdt,
+                                                       out_features, _ptr(y), _dtype(y), rp, rdt, int(activation),
+                                                       int(variant), _ptr(decoded), _ptr(ws),
+                                                       0 if ws is None else ws.numel(), _stream(xc.device)))
     return y.view(*x.shape[:-1], out_features)
+
+
+class PredecodeJob(ctypes.Structure):
+    """DimqPredecodeJob of include/dimq_hip.h."""
+    _fields_ = [("packed_w", _vp), ("packed_numel", _i64), ("bits", _int), ("codebook", _vp), ("cb_dtype", _int),
+                ("cb_rows", _i64), ("cb_size", _i64), ("out_features", _i64), ("in_features", _i64),
+                ("decoded", _vp)]
+
+
+def predecode_codebook_weights_impl(layers):
+    """Decodes every (packed_w, codebook, bits, out_features, in_features) of ``layers`` with one
+    dimq_codebook_predecode_batch call: one uint8 device buffer, and per layer a 256-byte aligned view of
+    dimq_codebook_predecode_bytes(...) bytes (None for a layer the batch cannot decode: bits 8, in_features
+    not a multiple of 32)."""
+    if not layers:
+        return None, []
+    dev = layers[0][0].device
+    sizes = [int(lib.dimq_codebook_predecode_bytes(int(n), int(k), int(b))) for (_, _, b, n, k) in layers]
+    total = sum(sizes)
+    if total == 0:
+        return None, [None] * len(layers)
+    buf = torch.empty(total + 256, dtype=torch.uint8, device=dev)
+    off = (-buf.data_ptr()) % 256
+    views, jobs, keep = [], [], []
+    for (pw, cb, b, n, k), nbytes in zip(layers, sizes):
+        if nbytes == 0:
+            views.append(None)
+            continue
+        _require_cuda(pw, "predecode expects CUDA packed weights")
+        _require_cuda(cb, "predecode expects CUDA codebooks")
+        if pw.device != dev or cb.device != dev:
+            raise RuntimeError("predecode: all layers must be on one device")
+        pwc, cbc = pw.contiguous().view(-1), cb.contiguous()
+        rows, size = _cb_shape(cbc, int(n))
+        keep += [pwc, cbc]
+        v = buf[off:off + nbytes]
+        views.append(v)
+        jobs.append(PredecodeJob(_ptr(pwc), pwc.numel(), int(b), _ptr(cbc), _dtype(cbc), rows, size, int(n), int(k),
+                                 _ptr(v)))
+        off += nbytes
+    arr = (PredecodeJob * len(jobs))(*jobs)
+    with torch.cuda.device(dev):
+        _check(lib.dimq_codebook_predecode_batch(ctypes.cast(arr, _vp), len(jobs), _stream(dev)))
+    return buf, views
 
 
 def linear_codebook_act_impl(x, packed_w, codebook, bits, act_centers, bias, out_features, in_features,
@@ -706,7 +765,7 @@ _SCHEMAS = {
                                     "-> Tensor", build_product_table_grouped_impl),
     "linear_codebook": ("linear_codebook(Tensor x, Tensor packed_w, Tensor codebook, int bits, Tensor? bias, "
                         "int out_features, int in_features, ScalarType? out_dtype=None, int variant=0, "
-                        "Tensor? residual=None, int activation=0) -> Tensor",
+                        "Tensor? residual=None, int activation=0, Tensor? decoded=None) -> Tensor",
                         linear_codebook_impl),
     "conv2d_codebook": ("conv2d_codebook(Tensor x, Tensor packed_w, Tensor codebook, int bits, Tensor? bias, "
                         "int out_channels, int in_channels_per_group, int kernel_h, int kernel_w, int stride_h, "

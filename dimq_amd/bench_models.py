@@ -25,7 +25,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .modules import DIMQCodebookConv2d, DIMQCodebookLinear, DIMQLayerNorm, DIMQMaxPool2d, quantize_model_weight_only
+from .modules import (DIMQCodebookConv2d, DIMQCodebookLinear, DIMQLayerNorm, DIMQMaxPool2d, decoded_weights,
+                      quantize_model_weight_only)
 
 
 def _fused(mod: nn.Module, x: torch.Tensor, residual: torch.Tensor | None = None,
@@ -105,8 +106,11 @@ class ViT(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         x = self.embed(x)
         x = torch.cat([self.class_token.expand(x.shape[0], -1, -1), x], dim=1) + self.pos_embedding
+        # each block's codebook Linears decode their weights in one launch at the block's start (one
+        # batch for the whole forward left the decoded weights cold by the time the later blocks read them)
         for blk in self.blocks:
-            x = blk(x)
+            with decoded_weights(blk, x.shape[0] * x.shape[1]):
+                x = blk(x)
         return self.head(self.ln(x[:, 0]))
 
 

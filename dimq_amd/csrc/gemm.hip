@@ -17,7 +17,10 @@ constexpr int64_t kCUs = 256;
 // gemm_pd.hip: the pre-decoded-weight path for large M (weights decoded once
 // per call into the workspace, then an fp16 GEMM fed by global_load_lds).
 int64_t predecoded_ws_bytes(int64_t M, int64_t K, int64_t N, int bits, int x_dtype);
-int launch_predecoded(const GemmArgs& p, int bits, int x_dtype, void* ws, int64_t ws_bytes, hipStream_t s);
+int launch_predecoded(const GemmArgs& p, int bits, int x_dtype, void* ws, int64_t ws_bytes, hipStream_t s,
+                      const void* decoded = nullptr);
+int64_t predecoded_w_bytes(int64_t N, int64_t K, int bits);
+int launch_predecode_jobs(const DimqPredecodeJob* jobs, int count, hipStream_t s);
 
 // Fast-path tiles need K % 128 == 0, aligned rows/streams and a Linear layout.
 int gemm_fast_tile(int tile, const GemmArgs& p, int bits) {
@@ -94,7 +97,7 @@ int linear_codebook_impl(const void* x, int x_dtype, int64_t M, int64_t K, int64
                          int bits, const void* codebook, int cb_dtype, int64_t cb_rows, int64_t cb_size,
                          const void* bias, int bias_dtype, int64_t N, void* y, int y_dtype, int64_t ldy,
                          const Epi& epi, int variant, hipStream_t s, float acc_scale = 1.0f,
-                         void* workspace = nullptr, int64_t workspace_bytes = 0) {
+                         void* workspace = nullptr, int64_t workspace_bytes = 0, const void* decoded = nullptr) {
   GemmArgs p{};
   p.epi = epi;
   p.acc_scale = acc_scale;
@@ -120,8 +123,8 @@ int linear_codebook_impl(const void* x, int x_dtype, int64_t M, int64_t K, int64
   p.vec_a = aligned(x, 16) && ((ldx * xs) % 16 == 0);
   p.groups = 1;
   if (M == 0 || N == 0) return DIMQ_OK;
-  if (workspace != nullptr && variant != DIMQ_VARIANT_SMALL_M) {
-    const int rc = launch_predecoded(p, bits, x_dtype, workspace, workspace_bytes, s);
+  if ((workspace != nullptr || decoded != nullptr) && variant != DIMQ_VARIANT_SMALL_M) {
+    const int rc = launch_predecoded(p, bits, x_dtype, workspace, workspace_bytes, s, decoded);
     if (rc >= 0) return rc;
   }
   const int big = gemm_big_tile(p, bits, x_dtype, variant);
@@ -165,7 +168,7 @@ static int linear_codebook_checked(const void* x, int x_dtype, int64_t M, int64_
                                    int64_t packed_numel, int bits, const void* codebook, int cb_dtype, int64_t cb_rows,
                                    int64_t cb_size, const void* bias, int bias_dtype, int64_t N, void* y, int y_dtype,
                                    const void* residual, int residual_dtype, int activation, int variant, void* stream,
-                                   void* workspace, int64_t workspace_bytes);
+                                   void* workspace, int64_t workspace_bytes, const void* decoded = nullptr);
 
 extern "C" int dimq_linear_codebook(const void* x, int x_dtype, int64_t M, int64_t K, const uint8_t* packed_w,
                                     int64_t packed_numel, int bits, const void* codebook, int cb_dtype,
@@ -203,6 +206,44 @@ extern "C" int dimq_linear_codebook_ex_ws(const void* x, int x_dtype, int64_t M,
   return linear_codebook_checked(x, x_dtype, M, K, packed_w, packed_numel, bits, codebook, cb_dtype, cb_rows, cb_size,
                                  bias, bias_dtype, N, y, y_dtype, residual, residual_dtype, activation, variant,
                                  stream, decode ? workspace : nullptr, decode ? workspace_bytes : 0);
+}
+
+extern "C" int64_t dimq_codebook_predecode_bytes(int64_t out_features, int64_t in_features, int bits) {
+  return predecoded_w_bytes(out_features, in_features, bits);
+}
+
+extern "C" int dimq_codebook_predecode_batch(const DimqPredecodeJob* jobs, int count, void* stream) {
+  DIMQ_CHECK(count >= 0 && (count == 0 || jobs != nullptr), "jobs must hold count entries");
+  for (int j = 0; j < count; ++j) {
+    const DimqPredecodeJob& J = jobs[j];
+    if (predecoded_w_bytes(J.out_features, J.in_features, J.bits) == 0)
+      return set_error(DIMQ_ERR_UNSUPPORTED, "job %d: pre-decode needs bits 2-4 and in_features %% 32 == 0", j);
+    DIMQ_CHECK(J.packed_w != nullptr && J.codebook != nullptr && J.decoded != nullptr, "job %d: null pointer", j);
+    DIMQ_CHECK(aligned(J.packed_w, 16), "job %d: packed_w must be 16-byte aligned", j);
+    DIMQ_CHECK(aligned(J.decoded, 256), "job %d: decoded must be 256-byte aligned", j);
+    DIMQ_CHECK(is_float_dtype(J.cb_dtype), "job %d: codebook must be floating point", j);
+    DIMQ_CHECK(J.cb_rows == 1 || J.cb_rows == J.out_features,
+               "job %d: codebook must have 1 (per layer) or out_features (per channel) rows", j);
+    DIMQ_CHECK(J.cb_size >= 1 && J.cb_size <= (1 << J.bits), "job %d: codebook rows must hold 1 to 2^bits entries", j);
+    DIMQ_CHECK(J.packed_numel >= (J.out_features * J.in_features * J.bits + 7) / 8,
+               "job %d: packed_weight is too small for out_features * in_features", j);
+  }
+  return launch_predecode_jobs(jobs, count, as_stream(stream));
+}
+
+extern "C" int dimq_linear_codebook_predecoded(const void* x, int x_dtype, int64_t M, int64_t K,
+                                               const uint8_t* packed_w, int64_t packed_numel, int bits,
+                                               const void* codebook, int cb_dtype, int64_t cb_rows, int64_t cb_size,
+                                               const void* bias, int bias_dtype, int64_t N, void* y, int y_dtype,
+                                               const void* residual, int residual_dtype, int activation, int variant,
+                                               const void* decoded, void* workspace, int64_t workspace_bytes,
+                                               void* stream) {
+  DIMQ_CHECK(workspace_bytes >= 0, "workspace_bytes must be non-negative");
+  DIMQ_CHECK(decoded == nullptr || aligned(decoded, 256), "decoded must be 256-byte aligned");
+  const bool decode = (M >= 1 && M <= 16) || predecoded_ws_bytes(M, K, N, bits, x_dtype) > 0;
+  return linear_codebook_checked(x, x_dtype, M, K, packed_w, packed_numel, bits, codebook, cb_dtype, cb_rows, cb_size,
+                                 bias, bias_dtype, N, y, y_dtype, residual, residual_dtype, activation, variant,
+                                 stream, decode ? workspace : nullptr, decode ? workspace_bytes : 0, decoded);
 }
 
 extern "C" int64_t dimq_linear_codebook_act_workspace_bytes(int64_t M, int64_t K) {
@@ -269,7 +310,7 @@ static int linear_codebook_checked(const void* x, int x_dtype, int64_t M, int64_
                                    int64_t packed_numel, int bits, const void* codebook, int cb_dtype, int64_t cb_rows,
                                    int64_t cb_size, const void* bias, int bias_dtype, int64_t N, void* y, int y_dtype,
                                    const void* residual, int residual_dtype, int activation, int variant, void* stream,
-                                   void* workspace, int64_t workspace_bytes) {
+                                   void* workspace, int64_t workspace_bytes, const void* decoded) {
   if (!(bits == 2 || bits == 3 || bits == 4 || bits == 8))
     return set_error(DIMQ_ERR_UNSUPPORTED, "bits must be one of 2, 3, 4, 8 (got %d)", bits);
   DIMQ_CHECK(x_dtype == DIMQ_F32 || x_dtype == DIMQ_F16 || x_dtype == DIMQ_BF16,
@@ -288,7 +329,7 @@ static int linear_codebook_checked(const void* x, int x_dtype, int64_t M, int64_
   const Epi epi{residual, residual_dtype, activation, residual != nullptr && aligned(residual, 16)};
   return linear_codebook_impl(x, x_dtype, M, K, K, packed_w, bits, codebook, cb_dtype, cb_rows, cb_size, bias,
                               bias_dtype, N, y, y_dtype, N, epi, variant, as_stream(stream), 1.0f, workspace,
-                              workspace_bytes);
+                              workspace_bytes, decoded);
 }
 
 extern "C" int64_t dimq_linear_lut_workspace_bytes(int64_t M, int64_t in_features, int cb_dtype) {

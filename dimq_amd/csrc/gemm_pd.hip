@@ -562,22 +562,51 @@ int launch_pd_modes(const GemmArgs& p, int mode, const PdOperands& o, hipStream_
   }
 }
 
+// with_w false: the weights are decoded already, only the activations are
+// converted (nothing to launch for fp16 activations)
 template <int BITS, int XT>
-void launch_prep(const GemmArgs& p, uint16_t* wd, float* rs, uint16_t* xh, uint32_t* flags, hipStream_t s) {
-  const int64_t nbw = (p.N + kPdRows - 1) / kPdRows;
+void launch_prep(const GemmArgs& p, bool with_w, uint16_t* wd, float* rs, uint16_t* xh, uint32_t* flags,
+                 hipStream_t s) {
+  const int64_t nbw = with_w ? (p.N + kPdRows - 1) / kPdRows : 0;
   const int64_t nbx = XT == DIMQ_F16 ? 0 : (p.M + kPxRows - 1) / kPxRows;
+  if (nbw + nbx == 0) return;
   hipLaunchKernelGGL((prep_kernel<BITS, XT>), dim3(static_cast<unsigned>(nbw + nbx)), dim3(256), 0, s, p.w, p.cb,
                      p.cb_dt, p.cb_rows, p.cb_size, p.N, p.K, p.acc_scale, wd, rs, nbw, p.x, p.M, p.ldx, xh, flags);
 }
 
 template <int BITS>
-void launch_prep_bits(const GemmArgs& p, int xt, uint16_t* wd, float* rs, uint16_t* xh, uint32_t* flags,
-                      hipStream_t s) {
+void launch_prep_bits(const GemmArgs& p, int xt, bool with_w, uint16_t* wd, float* rs, uint16_t* xh,
+                      uint32_t* flags, hipStream_t s) {
   switch (xt) {
-    case DIMQ_F16: launch_prep<BITS, DIMQ_F16>(p, wd, rs, xh, flags, s); break;
-    case DIMQ_BF16: launch_prep<BITS, DIMQ_BF16>(p, wd, rs, xh, flags, s); break;
-    default: launch_prep<BITS, DIMQ_F32>(p, wd, rs, xh, flags, s); break;
+    case DIMQ_F16: launch_prep<BITS, DIMQ_F16>(p, with_w, wd, rs, xh, flags, s); break;
+    case DIMQ_BF16: launch_prep<BITS, DIMQ_BF16>(p, with_w, wd, rs, xh, flags, s); break;
+    default: launch_prep<BITS, DIMQ_F32>(p, with_w, wd, rs, xh, flags, s); break;
   }
+}
+
+// Several layers' weights decoded in one launch (the per-call decode of the
+// first launch above, batched): job j's work-groups start at b0.
+constexpr int kPdBatchMax = 32;
+struct PdJob {
+  const uint8_t* w;
+  const void* cb;
+  uint16_t* wd;
+  float* rs;
+  int64_t cb_rows, N, K, b0;
+  int cb_dt, cb_size;
+};
+struct PdBatch {
+  PdJob job[kPdBatchMax];
+  int count;
+};
+
+template <int BITS>
+__global__ __launch_bounds__(256) void predecode_batch_kernel(const PdBatch bt) {
+  const int64_t b = blockIdx.x;
+  int j = 0;
+  for (int i = 1; i < bt.count; ++i) j = b >= bt.job[i].b0 ? i : j;
+  const PdJob& J = bt.job[j];
+  predecode_rows<BITS>(J.w, J.cb, J.cb_dt, J.cb_rows, J.cb_size, J.N, J.K, 1.0f, J.wd, J.rs, b - J.b0);
 }
 
 }  // namespace
@@ -593,28 +622,92 @@ int64_t predecoded_ws_bytes(int64_t M, int64_t K, int64_t N, int bits, int x_dty
   return x_dtype == DIMQ_F16 ? w : w + align256(M * K * 2) + align256(M * 4);
 }
 
+// Bytes of one layer's decoded weights: W_hat fp16 [N, K], then N fp32 row
+// factors (0: the layer cannot take the pre-decoded path).
+int64_t predecoded_w_bytes(int64_t N, int64_t K, int bits) {
+  if (K <= 0 || N <= 0 || K % kPdK != 0 || !(bits >= 2 && bits <= 4)) return 0;
+  return align256(N * K * 2) + align256(N * 4);
+}
+
+// Decodes jobs [0, count) (all of `bits`) into their wd / rs, kPdBatchMax per launch.
+int launch_predecode_batch(const PdJob* jobs, int count, int bits, hipStream_t s) {
+  for (int j0 = 0; j0 < count; j0 += kPdBatchMax) {
+    PdBatch bt{};
+    int64_t nb = 0;
+    bt.count = count - j0 < kPdBatchMax ? count - j0 : kPdBatchMax;
+    for (int i = 0; i < bt.count; ++i) {
+      bt.job[i] = jobs[j0 + i];
+      bt.job[i].b0 = nb;
+      nb += (bt.job[i].N + kPdRows - 1) / kPdRows;
+    }
+    if (nb == 0) continue;
+    switch (bits) {
+      case 2: hipLaunchKernelGGL(predecode_batch_kernel<2>, dim3(static_cast<unsigned>(nb)), dim3(256), 0, s, bt); break;
+      case 3: hipLaunchKernelGGL(predecode_batch_kernel<3>, dim3(static_cast<unsigned>(nb)), dim3(256), 0, s, bt); break;
+      default: hipLaunchKernelGGL(predecode_batch_kernel<4>, dim3(static_cast<unsigned>(nb)), dim3(256), 0, s, bt); break;
+    }
+    const int rc = check_launch("codebook weight pre-decode (batch)");
+    if (rc != DIMQ_OK) return rc;
+  }
+  return DIMQ_OK;
+}
+
+// Jobs of any bit width: one batch of launches per width present.
+int launch_predecode_jobs(const DimqPredecodeJob* jobs, int count, hipStream_t s) {
+  for (int bits = 2; bits <= 4; ++bits) {
+    PdJob pj[kPdBatchMax];
+    int n = 0;
+    for (int j = 0; j < count; ++j) {
+      const DimqPredecodeJob& J = jobs[j];
+      if (J.bits != bits) continue;
+      uint8_t* d = static_cast<uint8_t*>(J.decoded);
+      pj[n++] = PdJob{J.packed_w, J.codebook, reinterpret_cast<uint16_t*>(d),
+                      reinterpret_cast<float*>(d + align256(J.out_features * J.in_features * 2)), J.cb_rows,
+                      J.out_features, J.in_features, 0, J.cb_dtype, static_cast<int>(J.cb_size)};
+      if (n == kPdBatchMax) {
+        const int rc = launch_predecode_batch(pj, n, bits, s);
+        if (rc != DIMQ_OK) return rc;
+        n = 0;
+      }
+    }
+    if (n > 0) {
+      const int rc = launch_predecode_batch(pj, n, bits, s);
+      if (rc != DIMQ_OK) return rc;
+    }
+  }
+  return DIMQ_OK;
+}
+
 // Runs the two launches; -1 when the call does not take this path (shape,
-// dtype, epilogue, alignment or too small a workspace).
-int launch_predecoded(const GemmArgs& p, int bits, int x_dtype, void* ws, int64_t ws_bytes, hipStream_t s) {
-  const int64_t need = predecoded_ws_bytes(p.M, p.K, p.N, bits, x_dtype);
-  if (need == 0 || ws == nullptr || ws_bytes < need || (reinterpret_cast<uintptr_t>(ws) & 255) != 0) return -1;
+// dtype, epilogue, alignment or too small a workspace).  With `decoded`
+// (predecoded_w_bytes of this layer, 256-byte aligned, filled by
+// launch_predecode_batch) the first launch only converts bf16 / fp32
+// activations, into a workspace of the activation part's size.
+int launch_predecoded(const GemmArgs& p, int bits, int x_dtype, void* ws, int64_t ws_bytes, hipStream_t s,
+                      const void* decoded) {
+  const int64_t need_all = predecoded_ws_bytes(p.M, p.K, p.N, bits, x_dtype);
+  if (need_all == 0) return -1;
+  const int64_t wbytes = predecoded_w_bytes(p.N, p.K, bits);
+  const int64_t need = decoded ? need_all - wbytes : need_all;
+  if (decoded && (reinterpret_cast<uintptr_t>(decoded) & 255) != 0) return -1;
+  if (need > 0 && (ws == nullptr || ws_bytes < need || (reinterpret_cast<uintptr_t>(ws) & 255) != 0)) return -1;
   const int xs = x_dtype == DIMQ_F32 ? 4 : 2;
   if (p.conv || !p.fast_b || !p.vec_a || (p.ldx * xs) % 16 != 0) return -1;
   const int mode = epi_mode(p.epi);
   if (!(mode == kEpiNone || mode == kEpiRelu || mode == kEpiGelu || mode == kEpiRes)) return -1;
-  uint8_t* base = static_cast<uint8_t*>(ws);
-  uint16_t* wd = reinterpret_cast<uint16_t*>(base);
-  float* rs = reinterpret_cast<float*>(base + align256(p.N * p.K * 2));
+  uint8_t* wbase = decoded ? static_cast<uint8_t*>(const_cast<void*>(decoded)) : static_cast<uint8_t*>(ws);
+  uint16_t* wd = reinterpret_cast<uint16_t*>(wbase);
+  float* rs = reinterpret_cast<float*>(wbase + align256(p.N * p.K * 2));
   uint16_t* xh = nullptr;
   uint32_t* flags = nullptr;
   if (x_dtype != DIMQ_F16) {
-    xh = reinterpret_cast<uint16_t*>(base + align256(p.N * p.K * 2) + align256(p.N * 4));
+    xh = reinterpret_cast<uint16_t*>(decoded ? static_cast<uint8_t*>(ws) : wbase + wbytes);
     flags = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(xh) + align256(p.M * p.K * 2));
   }
   switch (bits) {
-    case 2: launch_prep_bits<2>(p, x_dtype, wd, rs, xh, flags, s); break;
-    case 3: launch_prep_bits<3>(p, x_dtype, wd, rs, xh, flags, s); break;
-    default: launch_prep_bits<4>(p, x_dtype, wd, rs, xh, flags, s); break;
+    case 2: launch_prep_bits<2>(p, x_dtype, decoded == nullptr, wd, rs, xh, flags, s); break;
+    case 3: launch_prep_bits<3>(p, x_dtype, decoded == nullptr, wd, rs, xh, flags, s); break;
+    default: launch_prep_bits<4>(p, x_dtype, decoded == nullptr, wd, rs, xh, flags, s); break;
   }
   const int rc = check_launch("linear_codebook (weight pre-decode)");
   if (rc != DIMQ_OK) return rc;

@@ -16,7 +16,8 @@ unnoticed.
 
 from __future__ import annotations
 
-from typing import Any, Mapping
+from contextlib import contextmanager
+from typing import Any, Iterator, Mapping
 
 import torch
 import torch.nn as nn
@@ -110,6 +111,7 @@ class DIMQCodebookLinear(nn.Module):
         self.in_features = int(in_features)
         self.out_dtype = out_dtype
         self.variant = variant
+        self._decoded: torch.Tensor | None = None  # set by decoded_weights() for the span of one forward
 
     def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None,
                 activation: str | None = None) -> torch.Tensor:
@@ -123,7 +125,8 @@ class DIMQCodebookLinear(nn.Module):
                                                 self.in_features, out_dtype=self.out_dtype, variant=self.variant)
         return ops.dimq_linear_codebook(x, self.packed_weight, self.codebook, self.bits, self.bias,
                                         self.out_features, self.in_features, out_dtype=self.out_dtype,
-                                        variant=self.variant, residual=residual, activation=activation)
+                                        variant=self.variant, residual=residual, activation=activation,
+                                        decoded=self._decoded)
 
     @classmethod
     @torch.no_grad()
@@ -316,6 +319,47 @@ def quantize_model_weight_only(model: nn.Module, bits_for: Any, *, per_channel: 
                                                      codebook_dtype=codebook_dtype, out_dtype=out_dtype)
             parent._modules[leaf] = new
     return model
+
+
+@contextmanager
+def decoded_weights(model: nn.Module, rows: int) -> Iterator[None]:
+    """For the span of the ``with`` block, the model's weight-only codebook
+    Linears run on weights decoded by one batch of launches at entry
+    (``ops.predecode_codebook_weights``) instead of decoding them in every
+    call: same kernels, same results, fewer launches.  ``rows`` is the number
+    of activation rows the Linears will see (batch x tokens); layers whose
+    calls at that size do not take the large-M path (where the per-call
+    decode happens) are left alone, so small batches decode nothing extra.
+    The decode runs at entry on the current stream, so the packed weights and
+    codebooks must not change inside the block; nested use is not supported.
+    Scope it to what the next few calls read: the GEMMs then find the decoded
+    weights still in the GPU's caches.  Measured on ViT-B/16 bs64 (graph
+    replay, same process): one batch per encoder block 4.24 ms per forward,
+    the per-call decode 4.33 ms, one batch for all 48 Linears 4.41 ms (170 MB
+    of decoded weights, mostly evicted before use).
+    No counterpart in the reference, whose LUT kernels decode inside every
+    call (dimq_cuda_backend/csrc/dimq_gemm_lut.cu)."""
+    cands = [m for m in model.modules() if isinstance(m, DIMQCodebookLinear) and m.activation_centers is None
+             and m.packed_weight.is_cuda and m._decoded is None]
+    layers = []
+    if cands:
+        from . import _C
+        for mod in cands:
+            wbytes = _C.lib.dimq_codebook_predecode_bytes(mod.out_features, mod.in_features, mod.bits)
+            # the large-M path of an fp16 call needs exactly the decoded weights as its workspace
+            if wbytes > 0 and _C.lib.dimq_linear_codebook_workspace_bytes(
+                    int(rows), mod.in_features, mod.out_features, mod.bits, _C.F16) == wbytes:
+                layers.append(mod)
+    try:
+        if layers:
+            _, views = ops.predecode_codebook_weights(
+                [(m.packed_weight, m.codebook, m.bits, m.out_features, m.in_features) for m in layers])
+            for mod, v in zip(layers, views):
+                mod._decoded = v
+        yield
+    finally:
+        for mod in layers:
+            mod._decoded = None
 
 
 def _resolve_parent(model: nn.Module, layer_name: str):

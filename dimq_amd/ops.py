@@ -140,17 +140,34 @@ def dimq_linear_codebook(
     variant: str = "auto",
     residual: torch.Tensor | None = None,
     activation: str | None = None,
+    decoded: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """y = act(x @ W_hat^T + bias + residual) with W_hat[n, k] = codebook[n or 0, idx[n, k]].
 
     ``residual`` (output shape) and ``activation`` ("relu" or "gelu", exact erf
     form) are fused into the kernel's store; without them this is the plain
-    weight-only Linear."""
+    weight-only Linear.  ``decoded``: this layer's buffer from
+    ``predecode_codebook_weights`` (same packed weights and codebook), used by
+    the large-M path in place of its own per-call weight decode."""
     require_extension()
     return torch.ops.dimq.linear_codebook(
         x, packed_weight, codebook, int(bits), bias, int(out_features), int(in_features), out_dtype,
-        VARIANTS[variant], residual, ACTIVATIONS[activation],
+        VARIANTS[variant], residual, ACTIVATIONS[activation], decoded,
     )
+
+
+def predecode_codebook_weights(layers):
+    """Decodes the weights of several codebook Linears in one batch of launches.
+
+    ``layers``: (packed_weight, codebook, bits, out_features, in_features)
+    tuples on one GPU.  Returns (buffer, views): views[i] is layer i's decode
+    (None when bits is 8 or in_features % 32 != 0), to pass as
+    ``dimq_linear_codebook(..., decoded=views[i])`` while the packed weights
+    and codebook stay unchanged.  No counterpart in the reference, whose LUT
+    kernels decode inside every call."""
+    require_extension()
+    from . import _C
+    return _C.predecode_codebook_weights_impl(layers)
 
 
 def dimq_conv2d_codebook(

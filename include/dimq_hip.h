@@ -291,15 +291,60 @@ int dimq_linear_codebook_ex(const void* x, int x_dtype, int64_t M, int64_t K, co
  * range over work-groups and keep the fp32 partial sums there (a second,
  * small kernel adds them): more work-groups stream the weights, and for
  * M > 4 the activations are read by 64 columns per work-group instead of 16.
- * Otherwise it is dimq_linear_codebook_ex (x_dtype is not used by the query;
- * the query returns 0 for M > 16).  The workspace is written on `stream`;
- * calls sharing one must be ordered on it. */
+ * Large-M shapes (M >= 2048, bits 2-4, K % 32 == 0, fp16 / bf16 / fp32 x,
+ * 256-byte aligned workspace) decode the weights once per call into the
+ * workspace as fp16 (and convert bf16 / fp32 activations to fp16 there with
+ * per-row range flags), then run an fp16 GEMM on them.  Otherwise it is
+ * dimq_linear_codebook_ex.  The query returns 0 for shapes that use no
+ * workspace.  The workspace is written on `stream`; calls sharing one must
+ * be ordered on it. */
 int64_t dimq_linear_codebook_workspace_bytes(int64_t M, int64_t K, int64_t N, int bits, int x_dtype);
 int dimq_linear_codebook_ex_ws(const void* x, int x_dtype, int64_t M, int64_t K, const uint8_t* packed_w,
                                int64_t packed_numel, int bits, const void* codebook, int cb_dtype, int64_t cb_rows,
                                int64_t cb_size, const void* bias, int bias_dtype, int64_t N, void* y, int y_dtype,
                                const void* residual, int residual_dtype, int activation, int variant, void* workspace,
                                int64_t workspace_bytes, void* stream);
+
+/* Batched weight pre-decode (no counterpart in the reference, whose LUT
+ * kernels decode the packed indices inside every call,
+ * csrc/dimq_gemm_lut.cu): the large-M path of dimq_linear_codebook_ex_ws
+ * decodes one layer's weights per call in a launch of its own; a model
+ * forward can instead decode all its layers' weights in one launch per bit
+ * width and pass each layer its decode.  Job j reads packed_w / codebook as
+ * dimq_linear_codebook_ex (bits 2-4, in_features % 32 == 0) and writes
+ * dimq_codebook_predecode_bytes(out_features, in_features, bits) bytes at
+ * `decoded` (256-byte aligned): W_hat as fp16 rows scaled by a power of two
+ * per row, then the rows' fp32 factors.  The bytes are this library's
+ * private layout, valid for dimq_linear_codebook_predecoded with the same
+ * packed_w and codebook, until either changes. */
+typedef struct {
+  const uint8_t* packed_w;
+  int64_t packed_numel;
+  int bits;
+  const void* codebook;
+  int cb_dtype;
+  int64_t cb_rows;
+  int64_t cb_size;
+  int64_t out_features;
+  int64_t in_features;
+  void* decoded;
+} DimqPredecodeJob;
+int64_t dimq_codebook_predecode_bytes(int64_t out_features, int64_t in_features, int bits);
+int dimq_codebook_predecode_batch(const DimqPredecodeJob* jobs, int count, void* stream);
+
+/* dimq_linear_codebook_ex_ws on weights decoded by
+ * dimq_codebook_predecode_batch (no counterpart in the reference; same
+ * arguments, checks and results as dimq_linear_codebook_ex_ws plus
+ * `decoded`).  When the call takes the large-M path the weights come from
+ * `decoded` and only bf16 / fp32 activations use the workspace (fp16 ones
+ * none); other shapes ignore `decoded` and run as dimq_linear_codebook_ex_ws.
+ * A workspace of dimq_linear_codebook_workspace_bytes always suffices. */
+int dimq_linear_codebook_predecoded(const void* x, int x_dtype, int64_t M, int64_t K, const uint8_t* packed_w,
+                                    int64_t packed_numel, int bits, const void* codebook, int cb_dtype,
+                                    int64_t cb_rows, int64_t cb_size, const void* bias, int bias_dtype, int64_t N,
+                                    void* y, int y_dtype, const void* residual, int residual_dtype, int activation,
+                                    int variant, const void* decoded, void* workspace, int64_t workspace_bytes,
+                                    void* stream);
 
 /* Weight x activation codebook Linear (no kernel counterpart in the
  * reference: its QAT wrapper quantizes activations to activation_centers with

@@ -125,3 +125,87 @@ def test_predecoded_matches_fused_path(gpu):
     assert oracle.rel_err(y_pd.cpu(), ref) <= 2e-3
     assert oracle.rel_err(y_fu.cpu(), ref) <= 2e-3
     assert oracle.rel_err(y_pd.cpu(), y_fu.cpu()) <= 2e-3
+
+
+# ---------------------------------------------------------------- batched weight pre-decode
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16, torch.float32])
+@torch.no_grad()
+def test_predecode_batch_matches_per_call_decode(gpu, xdt):
+    """dimq_codebook_predecode_batch over 38 layers (2, 3 and 4 bits, per-layer and per-channel codebooks,
+    more than one launch's 32 jobs): each layer's Linear on its batch decode gives the same bits as the same
+    call decoding its own weights (same decode, same GEMM), and stays within the bar of the oracle."""
+    from dimq_amd import ops
+    M = 2048
+    announce(f"predecode batch x={xdt}")
+    shapes = [(64, 64, 2 + i % 3, i % 2 == 0) for i in range(34)] + [(352, 96, 3, True), (768, 256, 4, False),
+                                                                      (256, 512, 2, True), (512, 64, 4, True)]
+    layers, cases = [], []
+    for i, (N, K, bits, pc) in enumerate(shapes):
+        cb, packed, x, bias = _case(M, N, K, bits, pc, 100 + i, xdt)
+        cases.append((cb, packed, x, bias, N, K, bits))
+        layers.append((packed.to(gpu), cb.to(gpu), bits, N, K))
+    buf, views = ops.predecode_codebook_weights(layers)
+    assert all(v is not None for v in views) and buf is not None
+    for i, ((cb, packed, x, bias, N, K, bits), (pg, cg, _, _, _)) in enumerate(zip(cases, layers)):
+        xg, bg = x.to(gpu), bias.to(gpu)
+        y_own = ops.dimq_linear_codebook(xg, pg, cg, bits, bg, N, K, out_dtype=torch.float32)
+        y_bat = ops.dimq_linear_codebook(xg, pg, cg, bits, bg, N, K, out_dtype=torch.float32, decoded=views[i])
+        assert torch.equal(y_own, y_bat), (i, N, K, bits)
+        if i in (0, 1, 2, 34, 35, 36, 37):
+            ref = oracle.linear_dequant_reference(x.float(), packed, bits, cb, N, K, bias)
+            assert oracle.rel_err(y_bat.cpu(), ref) <= 2e-3, (i, N, K, bits)
+
+
+@torch.no_grad()
+def test_predecode_batch_epilogues_and_small_m(gpu):
+    """Fused residual / GELU epilogues on decoded weights; a call below the large-M threshold ignores `decoded`
+    and decodes per call as before; layers the batch cannot decode (8 bits, K % 32 != 0) get no view."""
+    from dimq_amd import ops
+    announce("predecode batch epilogues")
+    M, N, K = 4200, 768, 192
+    cb, packed, x, bias = _case(M, N, K, 4, True, 41)
+    pg, cg, xg, bg = packed.to(gpu), cb.to(gpu), x.to(gpu), bias.to(gpu)
+    cb8 = (torch.randn(N, 256) * 0.05).sort(dim=1).values.to(gpu)
+    p8 = torch.randint(0, 256, (N * K,), dtype=torch.uint8).to(gpu)
+    p80 = torch.from_numpy(oracle.pack_bits(torch.randint(0, 16, (N, 80), dtype=torch.uint8), 4)).to(gpu)
+    _, views = ops.predecode_codebook_weights([(pg, cg, 4, N, K), (p8, cb8, 8, N, K), (p80, cg, 4, N, 80)])
+    assert views[0] is not None and views[1] is None and views[2] is None
+    res = (torch.randn(M, N, generator=torch.Generator().manual_seed(42)) * 0.5).bfloat16().to(gpu)
+    for kw in ({"residual": res}, {"activation": "gelu"}):
+        a = ops.dimq_linear_codebook(xg, pg, cg, 4, bg, N, K, out_dtype=torch.bfloat16, **kw)
+        b = ops.dimq_linear_codebook(xg, pg, cg, 4, bg, N, K, out_dtype=torch.bfloat16, decoded=views[0], **kw)
+        assert torch.equal(a, b), kw
+    small = xg[:100]
+    a = ops.dimq_linear_codebook(small, pg, cg, 4, bg, N, K, out_dtype=torch.float32)
+    b = ops.dimq_linear_codebook(small, pg, cg, 4, bg, N, K, out_dtype=torch.float32, decoded=views[0])
+    assert torch.equal(a, b)
+    with pytest.raises(RuntimeError, match="decoded"):
+        ops.dimq_linear_codebook(xg, pg, cg, 4, bg, N, K, decoded=views[0][:1000])
+
+
+@torch.no_grad()
+def test_decoded_weights_context_in_a_model(gpu):
+    """modules.decoded_weights: the ViT blocks' codebook Linears run on one batch decode per forward, with the
+    same outputs as per-call decoding, and the views are dropped when the block ends."""
+    from dimq_amd.bench_models import quantize_vit, ViT
+    from dimq_amd.modules import DIMQCodebookLinear, decoded_weights
+    announce("decoded_weights ViT-small M=2 x 1025")
+    torch.manual_seed(1)
+    m = ViT(image=256, patch=8, dim=128, depth=2, heads=4, mlp=256, classes=10)   # 32x32 patches + cls: 1025 tokens
+    for mod in m.modules():
+        if isinstance(mod, torch.nn.Linear):
+            torch.nn.init.normal_(mod.weight, std=0.02)
+    from tests.test_gpu_models import _cast_float_params
+    m = _cast_float_params(quantize_vit(m.to(gpu), 4, out_dtype=torch.bfloat16), torch.bfloat16).eval()
+    x = torch.randn(2, 3, 256, 256, device=gpu).bfloat16()
+    y_ctx = m(x)                                             # forward uses decoded_weights (M = 2050 rows)
+    lin = [mod for mod in m.modules() if isinstance(mod, DIMQCodebookLinear)]
+    assert all(mod._decoded is None for mod in lin)
+    h = m.embed(x)
+    h = torch.cat([m.class_token.expand(2, -1, -1), h], dim=1) + m.pos_embedding
+    with decoded_weights(m, h.shape[0] * h.shape[1]):
+        assert sum(mod._decoded is not None for mod in lin) == 8
+    for blk in m.blocks:
+        h = blk(h)
+    y_own = m.head(m.ln(h[:, 0]))
+    assert torch.equal(y_ctx, y_own)

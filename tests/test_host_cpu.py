@@ -100,6 +100,35 @@ def test_linear_workspace_sizes_and_act_codebook_errors(capi):
     assert lib.dimq_last_error() == b"activation codebook is required"
 
 
+def test_predecode_sizes_and_job_errors(capi):
+    """Batched weight pre-decode: bytes per layer (fp16 W_hat, then N fp32 row factors, each 256-byte
+    aligned), 0 for layers it cannot decode, and job checks that fail before any launch."""
+    import ctypes
+    lib = capi.lib
+    up = lambda b: (b + 255) // 256 * 256
+    assert lib.dimq_codebook_predecode_bytes(768, 768, 4) == up(768 * 768 * 2) + up(768 * 4)
+    assert lib.dimq_codebook_predecode_bytes(300, 96, 3) == up(300 * 96 * 2) + up(300 * 4)
+    assert lib.dimq_codebook_predecode_bytes(768, 80, 4) == 0      # in_features % 32 != 0
+    assert lib.dimq_codebook_predecode_bytes(768, 768, 8) == 0     # 8-bit codebooks are not pre-decoded
+    # the large-M fp16 path's workspace is exactly the decoded weights
+    assert lib.dimq_linear_codebook_workspace_bytes(12608, 768, 3072, 4, capi.F16) == \
+        lib.dimq_codebook_predecode_bytes(3072, 768, 4)
+    assert lib.dimq_codebook_predecode_batch(None, 0, None) == 0   # nothing to do, no launch
+    job = capi.PredecodeJob(256, 64 * 64, 8, 512, capi.F32, 64, 256, 64, 64, 1024)
+    arr = (capi.PredecodeJob * 1)(job)
+    assert lib.dimq_codebook_predecode_batch(ctypes.cast(arr, ctypes.c_void_p), 1, None) != 0
+    assert b"bits 2-4" in lib.dimq_last_error()
+    arr[0].bits, arr[0].cb_size, arr[0].decoded = 4, 16, 1040
+    assert lib.dimq_codebook_predecode_batch(ctypes.cast(arr, ctypes.c_void_p), 1, None) != 0
+    assert b"256-byte aligned" in lib.dimq_last_error()
+    arr[0].decoded, arr[0].cb_rows = 1024, 3
+    assert lib.dimq_codebook_predecode_batch(ctypes.cast(arr, ctypes.c_void_p), 1, None) != 0
+    assert b"per channel" in lib.dimq_last_error()
+    arr[0].cb_rows, arr[0].packed_numel = 64, 100
+    assert lib.dimq_codebook_predecode_batch(ctypes.cast(arr, ctypes.c_void_p), 1, None) != 0
+    assert b"too small" in lib.dimq_last_error()
+
+
 def test_support_op_argument_errors(capi):
     lib = capi.lib
     assert lib.dimq_layer_norm(None, capi.F32, 4, 768, 768, None, None, capi.F32, 1e-6, None, None) == 1

@@ -284,7 +284,8 @@ def make_vit(dev, rotations):
     m = _cast_float_params(quantize_vit(m, 4, out_dtype=torch.bfloat16), torch.bfloat16)
     return _model_workload(
         "vit_b16", "ViT-B/16 forward, bs64, 3x224x224 N(0,1): qkv/proj/fc1/fc2 4-bit per-output-channel codebooks "
-        "(N(0,0.02) weights); patch embedding, LayerNorm, softmax, attention (SDPA) and head in bf16",
+        "(N(0,0.02) weights); patch embedding, LayerNorm, residual stream and head in bf16, the tensors that only "
+        "feed a codebook GEMM and the qkv -> attention (SDPA) -> proj link in fp16",
         dev, rotations, m, xs_cpu, vit_flops(1), "bf16", torch.contiguous_format,
         {"model": "vit_b16", "image": 224, "bits": 4, "codebook": "per_channel"})
 

@@ -136,9 +136,11 @@ def quantize_vit(model: ViT, bits: int = 4, out_dtype: torch.dtype = torch.bfloa
     the LayerNorms -> DIMQLayerNorm (the HIP LayerNorm kernel, same parameters).
 
     fp16_links: the tensors that only feed a codebook GEMM -- ln_1 -> qkv, ln_2 -> fc1 and fc1 (GELU) -> fc2 --
-    are written in fp16 instead of bf16 (one rounding of the same fp32 result, with three more mantissa bits), so
-    those GEMMs stage their activations without a bf16 -> fp16 conversion; the residual stream, attention and the
-    head stay bf16."""
+    and the qkv output, so attention runs in fp16 and hands proj fp16, are written in fp16 instead of bf16 (one
+    rounding of the same fp32 result, with three more mantissa bits), so those GEMMs stage their activations
+    without a bf16 -> fp16 conversion; the residual stream and the head stay bf16.  The qkv / attention link
+    measured 4.26-4.34 -> 4.10-4.14 ms per bs64 forward, logits' max|err|/max|ref| against the fp32 model
+    1.00e-2 -> 0.92e-2."""
     def pick(name, module):
         leaf = name.rsplit(".", 1)[-1]
         return bits if leaf in ("qkv", "proj", "fc1", "fc2") else None
@@ -154,6 +156,7 @@ def quantize_vit(model: ViT, bits: int = 4, out_dtype: torch.dtype = torch.bfloa
     if fp16_links:
         for blk in model.blocks:
             blk.fc1.out_dtype = torch.float16
+            blk.attn.qkv.out_dtype = torch.float16
     return model
 
 

@@ -78,7 +78,7 @@ def test_w4a4_workspace_sizes(capi):
 def test_linear_workspace_sizes_and_act_codebook_errors(capi):
     lib = capi.lib
     up = lambda b: (b + 255) // 256 * 256
-    # only the decode shapes (M <= 16) use a workspace; every dtype converts inside the tiles
+    # below the large-M path (M >= 2048) only the decode shapes (M <= 16) use a workspace
     ws = lib.dimq_linear_codebook_workspace_bytes
     assert ws(1576, 768, 3072, 4, capi.F32) == 0
     assert ws(1576, 768, 3072, 4, capi.BF16) == 0

@@ -442,8 +442,8 @@ def make_w4a4(dev, rotations, op="linear", chained=False):
 
 
 VIT_LINEARS = {  # name: N, K, activation dtype, epilogue, output dtype (as in the bs64 forward)
-    "qkv": (2304, 768, torch.float16, None, torch.bfloat16),
-    "proj": (768, 768, torch.bfloat16, "residual", torch.bfloat16),
+    "qkv": (2304, 768, torch.float16, None, torch.float16),
+    "proj": (768, 768, torch.float16, "residual", torch.bfloat16),
     "fc1": (3072, 768, torch.float16, "gelu", torch.float16),
     "fc2": (768, 3072, torch.float16, "residual", torch.bfloat16),
 }

@@ -346,54 +346,97 @@ __global__ __launch_bounds__(64 * WGM * WGN, big_min_waves(BITS, MBLK, NBLK, CON
   }
 
   // epilogue: acc[mb][nb][4j + i] = y[m][n], m = block row m0 + wm*MBLK*32 +
-  // mb*32 + col, n = n0 + wn*NBLK*32 + nb*32 + 8j + 4g + i
+  // mb*32 + col, n = n0 + wn*NBLK*32 + nb*32 + 8j + 4g + i.  For j = 2 jp and
+  // 2 jp + 1 the lanes l and l + 32 (g 0 and 1, same row) swap four finished
+  // values, so lane g holds the 8 columns 16 jp + 8 g .. + 7 of its row and
+  // writes them as one 16-byte store (two 8-byte stores per lane before).
   const bool vec = p.ldy % 4 == 0 && p.y_dt != DIMQ_F64;
+  const bool vec8 = p.ldy % 8 == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0 && p.y_dt != DIMQ_F64;
   static_for<NBLK>([&](auto nbc) {
     constexpr int nb = decltype(nbc)::value;
-    // residuals of this column block: all loads out before the first store
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int nl = 8 * j + 4 * g;
-      const int64_t n = n0 + wn * NBLK * 32 + nb * 32 + nl;
+    for (int jp = 0; jp < 2; ++jp) {
+      float sc[2][4], bv[2][4];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int nl = 8 * (2 * jp + h) + 4 * g;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sc[h][i] = __shfl(rscale[nb], nl + i, 32);
+          bv[h][i] = ebias[wn * NBLK * 32 + nb * 32 + nl + i];
+        }
+      }
+      const int64_t n8 = n0 + wn * NBLK * 32 + nb * 32 + 16 * jp + 8 * g;  // this lane's 8 columns
       // 16-bit residuals of this row group: loads out before its stores (a
       // whole-tile prefetch would cost this kernel an occupancy step)
-      ResPairs<4> rr[MBLK];
-      if ((MODE & kEpiRes) && res_pairs(p.epi, vec)) {
+      ResPairs<8> rr[MBLK];
+      if ((MODE & kEpiRes) && res_pairs(p.epi, vec8)) {
 #pragma unroll
         for (int mb = 0; mb < MBLK; ++mb) {
           const int64_t m = m0 + wm * MBLK * 32 + mb * 32 + col;
-          if (m < p.M && n + 4 <= p.N) res_issue<4>(p.epi, m * p.ldy + n, rr[mb]);
+          if (m < p.M && n8 + 8 <= p.N) res_issue<8>(p.epi, m * p.ldy + n8, rr[mb]);
         }
-      }
-      float sc[4], bv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sc[i] = __shfl(rscale[nb], nl + i, 32);
-        bv[i] = ebias[wn * NBLK * 32 + nb * 32 + nl + i];
       }
 #pragma unroll
       for (int mb = 0; mb < MBLK; ++mb) {
         const int64_t m = m0 + wm * MBLK * 32 + mb * 32 + col;
-        if (m >= p.M) continue;
-        float v[4];
+        float va[4], vb[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = acc[mb][nb][4 * j + i] * sc[i] + bv[i];
-        const int64_t off = m * p.ldy + n;
-        if (vec && n + 4 <= p.N) {
-          epi_m<MODE, 4>(p.epi, &rr[mb], off, true, v);
-          if (p.y_dt == DIMQ_F32) {
-            *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.y) + off) = make_float4(v[0], v[1], v[2], v[3]);
+        for (int i = 0; i < 4; ++i) {
+          va[i] = acc[mb][nb][4 * (2 * jp) + i] * sc[0][i] + bv[0][i];
+          vb[i] = acc[mb][nb][4 * (2 * jp + 1) + i] * sc[1][i] + bv[1][i];
+        }
+        if (vec8) {
+          // g 0 keeps va (columns +0..3) and takes the partner's va (+4..7);
+          // g 1 takes the partner's vb (+8..11) and keeps vb (+12..15)
+          float v[8];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float r = __shfl_xor(g ? va[i] : vb[i], 32);
+            v[i] = g ? r : va[i];
+            v[4 + i] = g ? vb[i] : r;
+          }
+          if (m >= p.M) continue;
+          const int64_t off = m * p.ldy + n8;
+          if (n8 + 8 <= p.N) {
+            epi_m<MODE, 8>(p.epi, &rr[mb], off, true, v);
+            if (p.y_dt == DIMQ_F32) {
+              float* yp = reinterpret_cast<float*>(p.y) + off;
+              *reinterpret_cast<float4*>(yp) = make_float4(v[0], v[1], v[2], v[3]);
+              *reinterpret_cast<float4*>(yp + 4) = make_float4(v[4], v[5], v[6], v[7]);
+            } else {
+              uint32_t h[4];
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                h[i] = p.y_dt == DIMQ_F16 ? f16x2_rne(v[2 * i], v[2 * i + 1]) : bf16x2_rne(v[2 * i], v[2 * i + 1]);
+              *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p.y) + off) = make_uint4(h[0], h[1], h[2], h[3]);
+            }
           } else {
-            uint32_t h[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) h[i] = p.y_dt == DIMQ_F16 ? float_to_f16_bits(v[i]) : float_to_bf16_bits(v[i]);
-            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.y) + off) =
-                make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+            for (int i = 0; i < 8; ++i)
+              if (n8 + i < p.N) store_from_float(p.y, p.y_dt, off + i, epi1_m<MODE>(p.epi, off + i, v[i]));
           }
         } else {
+          if (m >= p.M) continue;
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (n + i < p.N) store_from_float(p.y, p.y_dt, off + i, epi1_m<MODE>(p.epi, off + i, v[i]));
+          for (int h = 0; h < 2; ++h) {
+            const float* vv = h ? vb : va;
+            const int64_t n = n0 + wn * NBLK * 32 + nb * 32 + 8 * (2 * jp + h) + 4 * g;
+            const int64_t off = m * p.ldy + n;
+            float v[4] = {vv[0], vv[1], vv[2], vv[3]};
+            if (vec && n + 4 <= p.N) {
+              epi_m<MODE, 4>(p.epi, nullptr, off, true, v);
+              if (p.y_dt == DIMQ_F32) {
+                *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.y) + off) = make_float4(v[0], v[1], v[2], v[3]);
+              } else {
+                const uint32_t h0 = p.y_dt == DIMQ_F16 ? f16x2_rne(v[0], v[1]) : bf16x2_rne(v[0], v[1]);
+                const uint32_t h1 = p.y_dt == DIMQ_F16 ? f16x2_rne(v[2], v[3]) : bf16x2_rne(v[2], v[3]);
+                *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.y) + off) = make_uint2(h0, h1);
+              }
+            } else {
+              for (int i = 0; i < 4; ++i)
+                if (n + i < p.N) store_from_float(p.y, p.y_dt, off + i, epi1_m<MODE>(p.epi, off + i, v[i]));
+            }
+          }
         }
       }
     }

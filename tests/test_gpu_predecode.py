@@ -209,3 +209,42 @@ def test_decoded_weights_context_in_a_model(gpu):
         h = blk(h)
     y_own = m.head(m.ln(h[:, 0]))
     assert torch.equal(y_ctx, y_own)
+
+
+@torch.no_grad()
+def test_predecoded_paths_under_graph_replay(gpu):
+    """The pre-decoded Linear (fp16 x; bf16 x with its conversion and range flags; GELU) and the batched
+    decode captured in a HIP graph: every replay, with unrelated eager work between replays, gives the eager
+    result bit for bit (bench.py times these paths as graph replays)."""
+    from dimq_amd import ops
+    announce("predecode graph replay M=2304")
+    M, N, K = 2304, 512, 256
+    cb, packed, x, bias = _case(M, N, K, 4, True, 77)
+    pg, cg, bg, xg = packed.to(gpu), cb.to(gpu), bias.to(gpu), x.to(gpu)
+    xbg = x.bfloat16().to(gpu)
+
+    def run():
+        y1 = ops.dimq_linear_codebook(xg, pg, cg, 4, bg, N, K, out_dtype=torch.float32)
+        y2 = ops.dimq_linear_codebook(xbg, pg, cg, 4, bg, N, K, out_dtype=torch.bfloat16, activation="gelu")
+        _, views = ops.predecode_codebook_weights([(pg, cg, 4, N, K)])
+        y3 = ops.dimq_linear_codebook(xg, pg, cg, 4, bg, N, K, out_dtype=torch.float32, decoded=views[0])
+        return y1, y2, y3
+
+    eager = run()
+    assert torch.equal(eager[0], eager[2])
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = run()
+    for r in range(3):
+        for o in outs:
+            o.zero_()
+        _ = (xg * 2).sum()  # unrelated eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o, e), f"replay {r}"

@@ -236,8 +236,11 @@ def _cast_float_params(model, dtype):
     return model
 
 
-def _model_workload(name, workload, dev, rotations, qmodel, xs_cpu, flops_per_image, dtype_name, mf, extra):
-    """Shared plumbing of the end-to-end model workloads: graph-replayed forward, images/s."""
+def _model_workload(name, workload, dev, rotations, qmodel, xs_cpu, flops_per_image, dtype_name, mf, extra,
+                    check_images=2):
+    """Shared plumbing of the end-to-end model workloads: graph-replayed forward, images/s.  The parity check
+    runs the first ``check_images`` images on both sides; enough for the timed kernel paths to be the checked
+    ones (the ViT's Linears take the pre-decoded path from 2048 rows on)."""
     batch = xs_cpu.shape[0]
     xdt = torch.bfloat16 if dtype_name == "bf16" else torch.float16
     xs = [xs_cpu.to(dev).to(xdt).contiguous(memory_format=mf) for _ in range(rotations)]
@@ -260,7 +263,7 @@ def _model_workload(name, workload, dev, rotations, qmodel, xs_cpu, flops_per_im
     @torch.no_grad()
     def check():
         import oracle
-        n = 2
+        n = check_images
         ref = cpu_model()(xs_cpu[:n].float())
         out = qmodel(xs[0][:n]).float().cpu()
         return oracle.rel_err(out, ref)
@@ -287,7 +290,8 @@ def make_vit(dev, rotations):
         "(N(0,0.02) weights); patch embedding, LayerNorm, residual stream and head in bf16, the tensors that only "
         "feed a codebook GEMM and the qkv -> attention (SDPA) -> proj link in fp16",
         dev, rotations, m, xs_cpu, vit_flops(1), "bf16", torch.contiguous_format,
-        {"model": "vit_b16", "image": 224, "bits": 4, "codebook": "per_channel"})
+        {"model": "vit_b16", "image": 224, "bits": 4, "codebook": "per_channel", "parity_images": 11},
+        check_images=11)  # 11 x 197 = 2167 rows: the pre-decoded path and batched decode the timed forward takes
 
 
 def make_resnet18(dev, rotations):

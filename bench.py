@@ -137,6 +137,9 @@ def make_cfg1(dev, rotations, variant="auto"):
     )
 
 
+_QUANT_CACHE = {}
+
+
 def make_cfg5(dev, rotations, M=16, variant="auto"):
     from dimq_amd import ops
     from dimq_amd.codebook import assign_indices, init_centers_per_channel
@@ -144,10 +147,13 @@ def make_cfg5(dev, rotations, M=16, variant="auto"):
 
     g = torch.Generator().manual_seed(4)
     w = torch.randn(4096, 4096, generator=g) * 0.02
-    centers = init_centers_per_channel(w, 8)
+    if "cfg5" not in _QUANT_CACHE:  # the same seeded weights for every M: quantize once per process
+        c = init_centers_per_channel(w, 8)
+        _QUANT_CACHE["cfg5"] = (c, pack_indices(assign_indices(w, c), 3).cpu())
+    centers, packed_cpu = _QUANT_CACHE["cfg5"]
     cb = centers.to(dev)
     # weights rotate too (6.3 MB packed each) so that repeats stream from HBM
-    packs = [pack_indices(assign_indices(w, centers), 3).to(dev)]
+    packs = [packed_cpu.to(dev)]
     for _ in range(rotations - 1):
         packs.append(packs[0].clone())
     xs = [torch.randn(M, 4096, generator=g).bfloat16().to(dev) for _ in range(rotations)]
@@ -220,7 +226,9 @@ def make_codec(dev, rotations, direction="unpack"):
         step=step, flops=0.0, alg_bytes=alg_bytes, bound="hbm", dtype="u8",
         unit="GB/s", per_step_units=alg_bytes / 1e9, cpu_step=cpu_step, cpu_full_batch=n, check=check,
         extra_config={"numel": n, "bits": 3},
-        per_set_bytes=alg_bytes,
+        per_set_bytes=alg_bytes, cpu_cores=1,
+        cpu_desc="the oracle's C LSB-first bit packer/unpacker (one thread; the reference's CPU codec is "
+                 "torch slicing, dimq_backend/export.py:38-78)",
     )
 
 
@@ -542,8 +550,9 @@ def time_gpu(wl, rotations, steps, warmup):
     with torch.cuda.graph(graph):
         for i in range(rotations):
             step(i)
-    replays = max(1, steps // rotations)
-    rem = steps - replays * rotations
+    # exactly `steps` timed steps: whole replays of the rotation graph, then a graph of the first `rem` sets
+    # (the sets the warm-up touched longest ago when steps < rotations)
+    replays, rem = divmod(steps, rotations)
     graph_rem = None
     if rem:
         graph_rem = torch.cuda.CUDAGraph()
@@ -562,8 +571,8 @@ def time_gpu(wl, rotations, steps, warmup):
         graph_rem.replay()
     end.record()
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / (replays * rotations + rem)
-    return ms, replays * rotations + rem
+    ms = start.elapsed_time(end) / steps
+    return ms, steps
 
 
 def time_cpu(wl, budget_s=15.0):
@@ -595,13 +604,37 @@ def time_cpu(wl, budget_s=15.0):
     med = times[len(times) // 2]
     frac = sample / full
     value = wl["per_step_units"] * frac / med
-    try:
-        model = [l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name")][0]
-    except Exception:
-        model = "unknown"
-    return dict(value=value, unit=wl["unit"], cores=wl.get("cpu_cores", threads), kind="port",
+    used = wl.get("cpu_cores", torch.get_num_threads())
+    return dict(value=value, unit=wl["unit"], cores=used, kind="port",
                 sample=f"{sample}/{full} of one step ({wl['name']}), median of {len(times)} runs after 3 warm-ups; "
-                       f"{wl.get('cpu_desc', 'oracle dequantize + torch CPU fp32')}; {model}")
+                       f"{wl.get('cpu_desc', 'oracle dequantize + torch CPU fp32')}",
+                cpu_model=host_cpu_model(), threads_used=used, cpus_available=threads,
+                host=host_id())
+
+
+def host_cpu_model():
+    """Full CPU model string of the host that ran the baseline (/proc/cpuinfo)."""
+    try:
+        info = {}
+        n = 0
+        for line in open("/proc/cpuinfo"):
+            if ":" not in line:
+                continue
+            k, v = (t.strip() for t in line.split(":", 1))
+            n += k == "processor"
+            info.setdefault(k, v)
+        return (f"{info.get('model name', '?')}, family {info.get('cpu family', '?')} model {info.get('model', '?')} "
+                f"stepping {info.get('stepping', '?')}, {info.get('cache size', '?')} cache, "
+                f"{info.get('cpu MHz', '?')} MHz ({n} logical CPUs visible)")
+    except OSError:
+        return "unknown"
+
+
+def host_id():
+    """The machine's hostname and the GPU's name, so baselines of different rounds can be told apart."""
+    import socket
+    gpu = torch.cuda.get_device_name(0) if torch.cuda.is_available() else "none"
+    return f"{socket.gethostname()} / {gpu}"
 
 
 def run_workload(args, config, dev, steps, warmup, cpu_budget_s=15.0):
@@ -709,13 +742,34 @@ def main():
         out = run_workload(args, args.config, dev, args.steps, args.warmup)
     else:
         out = run_workload(args, "cfg2", dev, args.steps, args.warmup)
+        keep = ("value", "unit", "ms_per_step", "steps", "dtype", "config", "roofline", "cpu_baseline")
         # second half of the metric: the ViT-B/16 bs64 forward (a few graph replays of the whole forward)
         vit = run_workload(args, "vit", dev, max(4, min(args.steps, 40)), max(1, min(args.warmup, 8)),
                            cpu_budget_s=12.0)
-        out["models"] = {"vit_b16": {k: vit[k] for k in ("metric_part", "value", "unit", "ms_per_step", "steps",
-                                                         "dtype", "config", "roofline", "cpu_baseline")}}
+        out["models"] = {"vit_b16": {"metric_part": vit["metric_part"], **{k: vit[k] for k in keep}}}
+        # every other BASELINE config on the same line, each with its own roofline and CPU baseline
+        out["configs"] = {}
+        for name, config, kw, steps in DEFAULT_EXTRA:
+            sub = argparse.Namespace(**{**vars(args), **kw})
+            n = steps(args.steps)
+            print(f"[bench] {name}: {n} steps", file=sys.stderr, flush=True)
+            r = run_workload(sub, config, dev, n, max(args.warmup, 2), cpu_budget_s=6.0)
+            out["configs"][name] = {k: r[k] for k in keep}
     out.pop("metric_part", None)
     print(json.dumps(out), flush=True)
+
+
+# the default line's "configs" map: name, workload, its options, timed steps as a function of --steps (the
+# kernel-sized configs time at least 200 launches so that one event pair brackets >= ~1 ms of GPU work)
+DEFAULT_EXTRA = [
+    ("cfg1", "cfg1", {}, lambda k: max(k, 200)),
+    ("cfg5_m1", "cfg5", {"m": 1}, lambda k: max(k, 200)),
+    ("cfg5_m4", "cfg5", {"m": 4}, lambda k: max(k, 200)),
+    ("cfg5_m16", "cfg5", {"m": 16}, lambda k: max(k, 200)),
+    ("codec_pack", "codec", {"direction": "pack"}, lambda k: max(k, 40)),
+    ("codec_unpack", "codec", {"direction": "unpack"}, lambda k: max(k, 40)),
+    ("resnet18", "resnet18", {}, lambda k: max(4, min(k, 40))),
+]
 
 
 if __name__ == "__main__":

@@ -798,6 +798,18 @@ def _register() -> torch.library.Library:
 _LIBRARY = _register()
 
 
+# The reference extension's module-level functions (csrc/dimq_ops.cpp:55-62,
+# its PYBIND11_MODULE block): the same six names and positional arguments as
+# the registered ops, callable as dimq_backend._C.linear_lut(...) without the
+# dispatcher.  They are the op implementations themselves.
+pack_u4 = pack_u4_impl
+unpack_u4 = unpack_u4_impl
+quantize_activation_u4 = quantize_activation_u4_impl
+build_product_table = build_product_table_impl
+linear_lut = linear_lut_impl
+conv2d_lut = conv2d_lut_impl
+
+
 # ---------------------------------------------------------------------------
 # QAT kernels (quant/dimq.py:197-296): host wrappers used by dimq_amd.qat
 def _qat_inputs(w, centers):

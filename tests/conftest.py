@@ -26,3 +26,12 @@ def gpu():
 def announce(name: str) -> None:
     """Print and flush the case name before a GPU step, so a crash names its case."""
     print(f"[case] {name}", flush=True)
+
+
+def out_tol(dtype) -> float:
+    """Parity bar of a weight-only GEMM/conv output in `dtype`: max|err| / max|ref| <= 2e-3 (fp32
+    accumulation) plus the one rounding of the result to a 16-bit output, which alone moves an element by up
+    to 2^-9 (bf16) or 2^-11 (fp16) of its magnitude."""
+    import torch
+
+    return 2e-3 + {torch.bfloat16: 2.0 ** -9, torch.float16: 2.0 ** -11}.get(dtype, 0.0)

@@ -2,8 +2,9 @@
 against the dequantize-then-float CPU model (oracle.dequantized_model).
 
 Activations run in bf16 (ViT) / fp16 (ResNet) on the GPU and in fp32 on the
-CPU, so the bound is looser than the single-layer 2e-3: max|err|/max|ref| of
-the logits <= 3e-2."""
+CPU, and every layer's output is rounded to 16 bits before the next layer
+reads it, so the bound is looser than the single-layer one: max|err|/max|ref|
+of the logits <= 1.5e-2 (LOGITS_TOL)."""
 
 from __future__ import annotations
 
@@ -11,9 +12,11 @@ import pytest
 import torch
 
 import oracle
-from tests.conftest import announce
+from tests.conftest import announce, out_tol
 
 pytestmark = pytest.mark.gpu
+
+LOGITS_TOL = 1.5e-2
 
 
 def _cast_float_params(model, dtype):
@@ -43,7 +46,7 @@ def test_vit_small_forward_vs_dequant_reference(gpu):
     x = torch.randn(3, 3, 32, 32)
     y = m(x.cuda().bfloat16()).float().cpu()
     ref = oracle.dequantized_model(m)(x)
-    assert oracle.rel_err(y, ref) <= 3e-2
+    assert oracle.rel_err(y, ref) <= LOGITS_TOL, oracle.rel_err(y, ref)
 
 
 @torch.no_grad()
@@ -59,7 +62,29 @@ def test_resnet18_forward_vs_dequant_reference(gpu):
     x = torch.randn(2, 3, 64, 64)
     y = m(x.cuda().half().contiguous(memory_format=torch.channels_last)).float().cpu()
     ref = oracle.dequantized_model(m)(x)
-    assert oracle.rel_err(y, ref) <= 3e-2
+    assert oracle.rel_err(y, ref) <= LOGITS_TOL, oracle.rel_err(y, ref)
+
+
+@torch.no_grad()
+def test_resnet18_bs128_forward_vs_dequant_reference(gpu):
+    """BASELINE cfg3 at its workload: ResNet-18, batch 128, 224x224, BN folded, 8-bit stem and fc, 2-bit 3x3,
+    4-bit 1x1 downsample, fp16 channels-last activations (the kernels, grid sizes and tile choices of the timed
+    forward: parts per image, tile rounds, the 8-bit fc's tile pick at M 128), against the dequantized fp32
+    model on the CPU (quant/dimq_wrapper.py:189-197,237-240).  Checked over the whole batch, and the first
+    images also per image, so that a wrong image offset cannot hide under the batch maximum."""
+    from dimq_amd.bench_models import quantize_resnet18, resnet18
+    announce("resnet18 forward 128x3x224x224")
+    m = resnet18().cuda().to(memory_format=torch.channels_last)
+    m = _cast_float_params(quantize_resnet18(m, out_dtype=torch.float16), torch.float16).eval()
+    x = torch.randn(128, 3, 224, 224, generator=torch.Generator().manual_seed(2))
+    y = m(x.cuda().half().contiguous(memory_format=torch.channels_last)).float().cpu()
+    assert y.shape == (128, 1000)
+    ref = oracle.dequantized_model(m)(x)
+    err = oracle.rel_err(y, ref)
+    print(f"resnet18 bs128 logits rel err {err:.3e}", flush=True)
+    assert err <= LOGITS_TOL, err
+    for i in (0, 63, 127):
+        assert oracle.rel_err(y[i], ref[i]) <= 2 * LOGITS_TOL, (i, oracle.rel_err(y[i], ref[i]))
 
 
 # ---------------------------------------------------------------- BASELINE cfg4 at its real shapes
@@ -95,7 +120,7 @@ def test_vit_linear_shapes_full_size(gpu, name, N, K, epi, out, xdt):
         ref = ref + res.float()
     elif epi == "gelu":
         ref = torch.nn.functional.gelu(ref)
-    tol = {torch.float32: 2e-3, torch.float16: 2e-3}.get(out, 8e-3)  # a bf16 output alone rounds at 2^-9 relative
+    tol = out_tol(out)
     err = oracle.rel_err(y.float().cpu(), ref)
     assert err <= tol, err
 
@@ -112,4 +137,4 @@ def test_vit_b16_bs64_forward_vs_dequant_reference(gpu):
     x = torch.randn(64, 3, 224, 224, generator=torch.Generator().manual_seed(3))
     y = m(x.to(gpu).bfloat16()).float().cpu()
     ref = oracle.dequantized_model(m)(x)
-    assert oracle.rel_err(y, ref) <= 3e-2, oracle.rel_err(y, ref)
+    assert oracle.rel_err(y, ref) <= LOGITS_TOL, oracle.rel_err(y, ref)

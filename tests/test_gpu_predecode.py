@@ -13,7 +13,7 @@ import pytest
 import torch
 
 import oracle
-from tests.conftest import announce
+from tests.conftest import announce, out_tol
 
 pytestmark = pytest.mark.gpu
 
@@ -87,7 +87,7 @@ def test_predecoded_linear_epilogues(gpu, M, N, K, epi, out, xdt):
         ref = torch.nn.functional.gelu(ref)
     elif epi == "relu":
         ref = torch.relu(ref)
-    tol = 8e-3 if out == torch.bfloat16 else 2e-3
+    tol = out_tol(out)
     assert oracle.rel_err(y.float().cpu(), ref) <= tol
 
 

@@ -180,6 +180,19 @@ def test_reference_schemas_registered_verbatim(capi):
         assert got.replace("dimq::", "") == schema
 
 
+def test_extension_module_functions_match_the_schemas(capi):
+    """csrc/dimq_ops.cpp:55-62: the extension also exposes the six ops as module-level functions taking the
+    schema's arguments in order; a CPU tensor gets the CUDA-only error, as from the compiled extension."""
+    import inspect
+    for name in ("pack_u4", "unpack_u4", "quantize_activation_u4", "build_product_table", "linear_lut",
+                 "conv2d_lut"):
+        fn = getattr(capi, name)
+        schema = getattr(torch.ops.dimq, name).default._schema
+        assert list(inspect.signature(fn).parameters) == [a.name for a in schema.arguments], name
+    with pytest.raises(RuntimeError, match="pack_u4 expects a CUDA tensor"):
+        capi.pack_u4(torch.zeros(4, dtype=torch.uint8))
+
+
 # ---------------------------------------------------------------------------
 # codebook initialisation (host)
 # ---------------------------------------------------------------------------

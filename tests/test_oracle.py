@@ -306,3 +306,60 @@ def test_qat_oracle_finite_differences():
         assert torch.autograd.gradcheck(lambda a, b: qat.soft_dequantize(a, b, tau), (w, c))
     cs = torch.tensor([0.0, 0.01, 0.015, 0.3], dtype=torch.float64, requires_grad=True)
     assert torch.autograd.gradcheck(lambda b: qat.separation_loss(w.detach(), b, 2.0), (cs,))
+
+
+# ---------------------------------------------------------------- end-to-end model reference
+def _bit_list_pack(idx, bits):
+    """LSB-first bitstream written bit by bit (the packed format of dimq_backend/export.py:38-55, generalised)."""
+    flat = [int(v) for v in np.asarray(idx).reshape(-1)]
+    out = bytearray((len(flat) * bits + 7) // 8)
+    for i, v in enumerate(flat):
+        for b in range(bits):
+            if (v >> b) & 1:
+                out[(i * bits + b) // 8] |= 1 << ((i * bits + b) % 8)
+    return torch.tensor(list(out), dtype=torch.uint8)
+
+
+@torch.no_grad()
+def test_dequantized_model_matches_gathered_float_layers():
+    """oracle.dequantized_model (the CPU reference of the end-to-end forwards) against a model written out by
+    hand: W_hat gathered with torch indexing from the indices (C[n, idx[n, k]], reference.py:47-56), then
+    F.conv2d / F.linear in fp32 (quant/dimq_wrapper.py:189-197,237-240), torch's LayerNorm and max pool for the
+    HIP support layers.  Covers a strided, padded, dilated, grouped conv with a per-channel codebook, a Linear
+    with a per-layer codebook and no bias, 2/3/8-bit indices, and the layers' order and hyper-parameters."""
+    from dimq_amd.modules import DIMQCodebookConv2d, DIMQCodebookLinear, DIMQLayerNorm, DIMQMaxPool2d
+
+    g = torch.Generator().manual_seed(11)
+    shape = (8, 3, 3, 2)                        # OC 8, groups 2 -> 3 input channels per group, 3x2 kernel
+    cidx = torch.randint(0, 4, shape, generator=g, dtype=torch.uint8)
+    ccb = torch.randn(8, 4, generator=g).sort(dim=1).values
+    cbias = torch.randn(8, generator=g)
+    conv = DIMQCodebookConv2d(_bit_list_pack(cidx, 2), ccb, 2, shape, cbias, stride=(2, 1), padding=(1, 2),
+                              dilation=(1, 2), groups=2)
+    x = torch.randn(2, 6, 9, 8, generator=g)
+    conv_out = F.conv2d(x, ccb[torch.arange(8)[:, None], cidx.reshape(8, -1).long()].reshape(shape), cbias, (2, 1),
+                        (1, 2), (1, 2), 2)
+    pooled = F.max_pool2d(conv_out, 2, 2, 0)
+    D = pooled[0].numel()
+    lidx = torch.randint(0, 8, (5, D), generator=g, dtype=torch.uint8)
+    lcb = torch.randn(1, 8, generator=g).sort(dim=1).values
+    lin = DIMQCodebookLinear(_bit_list_pack(lidx, 3), lcb, 3, 5, D, None)
+    ln = DIMQLayerNorm(5)
+    ln.weight.data = torch.randn(5, generator=g)
+    ln.bias.data = torch.randn(5, generator=g)
+    hidx = torch.randint(0, 256, (4, 5), generator=g, dtype=torch.uint8)
+    hcb = torch.randn(4, 256, generator=g)
+    hbias = torch.randn(4, generator=g)
+    head = DIMQCodebookLinear(_bit_list_pack(hidx, 8), hcb, 8, 4, 5, hbias)
+    model = torch.nn.Sequential(conv, DIMQMaxPool2d(2, 2, 0), torch.nn.Flatten(), lin, ln, head)
+
+    got = oracle.dequantized_model(model)(x)
+    h = pooled.flatten(1) @ lcb[0][lidx.long()].T
+    h = F.layer_norm(h, (5,), ln.weight, ln.bias, ln.eps)
+    want = F.linear(h, hcb[torch.arange(4)[:, None], hidx.long()], hbias)
+    torch.testing.assert_close(got, want, rtol=1e-6, atol=1e-6)
+    # a planted mistake: the conv's codebook rows taken in reverse order
+    bad = oracle.dequantized_model(torch.nn.Sequential(
+        DIMQCodebookConv2d(_bit_list_pack(cidx, 2), ccb.flip(0), 2, shape, cbias, stride=(2, 1), padding=(1, 2),
+                           dilation=(1, 2), groups=2)))(x)
+    assert not torch.allclose(bad, conv_out, rtol=1e-3, atol=1e-3)

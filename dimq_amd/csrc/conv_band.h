@@ -16,8 +16,11 @@
 //   2. stage A is transposed NCHW -> [row][col][channel] fp16 into LDS
 //      (8x8 transposes in registers), barrier, the loads of stage B (the
 //      remaining rows) go out, round 0 runs (one block-half per wave), stage B
-//      is committed, barrier, the remaining blocks run two accumulator chains
-//      per wave;
+//      is committed, barrier, round 0's blocks are stored, the remaining
+//      blocks run two accumulator chains per wave.  Round 0's stores leave
+//      after stage B's commit because vmcnt counts loads and stores in issue
+//      order: stores issued before the commit would make its wait for stage B
+//      also wait for them to complete;
 //   3. each finished 32x32 block goes through a wave-private LDS area and
 //      leaves as non-temporal 16-byte stores, 8 channels x 128 bytes per
 //      instruction: the output is written once and never re-read here, and
@@ -96,9 +99,9 @@ __device__ __forceinline__ void band_commit(const HaloArgs& p, int r0, int t, in
   for (int j = 0; j < 8; ++j) {
     // pixel j: channels 2w, 2w+1 from half (j & 1) of word j / 2 of rows 2w, 2w+1
     const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-    const uint4 o = tk.live ? make_uint4(perm(in[1][j >> 1], in[0][j >> 1], sel), perm(in[3][j >> 1], in[2][j >> 1], sel),
-                                         perm(in[5][j >> 1], in[4][j >> 1], sel), perm(in[7][j >> 1], in[6][j >> 1], sel))
-                            : make_uint4(0, 0, 0, 0);
+    const uint32_t m = tk.live ? 0xffffffffu : 0u;  // rows outside the image: zeros (a mask, not a branch)
+    const uint4 o = make_uint4(perm(in[1][j >> 1], in[0][j >> 1], sel) & m, perm(in[3][j >> 1], in[2][j >> 1], sel) & m,
+                               perm(in[5][j >> 1], in[4][j >> 1], sel) & m, perm(in[7][j >> 1], in[6][j >> 1], sel) & m);
     *reinterpret_cast<uint4*>(&halo[(r * p.IW_t + 8 * q + j + 1) * CP + 8 * co]) = o;
   }
 }
@@ -264,18 +267,18 @@ __global__ __launch_bounds__(kBandThreads, 1) void conv_band_kernel(const HaloAr
       }
     }
   };
-  // round 0: one block-half per wave, reading stage A only
+  // round 0: one block-half per wave, reading stage A only; its stores leave after stage B's commit
   {
     const int mb = bp.blk0 + wq;
+    floatx16 acc[2];
     if (mb < bp.blk1) {
-      floatx16 acc[2];
       const int mbs[2] = {mb, mb};
       compute(1, mbs, acc);
-      band_store<MODE>(p, acc[0], b, bp.px1, mb, col, g, oc0 + 32 * wn, lane, scale, bv, park);
     }
+    band_commit(p, bp.ra, tid, tB, tkb, halo);
+    lds_barrier();
+    if (mb < bp.blk1) band_store<MODE>(p, acc[0], b, bp.px1, mb, col, g, oc0 + 32 * wn, lane, scale, bv, park);
   }
-  band_commit(p, bp.ra, tid, tB, tkb, halo);
-  lds_barrier();
   for (int mb = bp.blk0 + wq + kBandBlocksPerRound; mb < bp.blk1; mb += 2 * kBandBlocksPerRound) {
     const bool two = mb + kBandBlocksPerRound < bp.blk1;
     const int mbs[2] = {mb, mb + kBandBlocksPerRound};

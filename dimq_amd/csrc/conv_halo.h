@@ -21,7 +21,7 @@
 // row's packed indices and codebook byte planes in VGPRs for the whole tile.
 #pragma once
 
-#include "conv_band.h"
+#include "conv_common.h"
 
 #include <algorithm>
 

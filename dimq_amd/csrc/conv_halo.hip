@@ -1,6 +1,7 @@
 // Host side of the LDS-halo conv kernels (conv_halo.h): weight preparation
 // into the kernel layout, shape eligibility, launch.
 #include "conv_halo.h"
+#include "conv_band.h"
 
 namespace dimq {
 namespace {

@@ -32,7 +32,7 @@ int gemm_fast_tile(int tile, const GemmArgs& p, int bits) {
 
 // Large-tile kernels (gemm_big.h) for Linear shapes with M > 64, K % 64 == 0
 // and aligned rows/streams.  Measured on the ViT-B/16 shapes (M = 12,608) and
-// cfg1: the deep-pipeline 128x128 tile (7) is fastest for K < 2048, the 2x2
+// cfg1: the deep-pipeline tile (7, 64x128) is fastest for K < 2048, the 2x2
 // 128x128 tile (2) for K >= 2048.  Returns -1 when the shape does not qualify.
 int gemm_big_tile(const GemmArgs& p, int bits, int x_dtype, int variant) {
   if (variant == DIMQ_VARIANT_SMALL_M || p.conv || !(bits == 2 || bits == 3 || bits == 4)) return -1;

@@ -703,7 +703,13 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_lds_kernel(const GemmArgs
 
 typedef __attribute__((address_space(3))) void lds_void_g;
 
-// Deep-pipeline variant for one wave per SIMD: 4 waves side by side in n
+// Row blocks (32 rows each) of the deep-pipeline tile: 64 x 128 tiles.  At the
+// cfg1 shape (M 1576, N 3072, K 768, fp32 x) 64-row tiles (624 of them)
+// measured 25.9 us against 28.1 us for 128-row tiles (312, two rounds on 256
+// CUs, the second a fifth full) and 31.0 us for 192-row tiles (216).
+constexpr int kDeepMblk = 2;
+
+// Deep-pipeline variant: 4 waves side by side in n
 // (wave tile (MBLK*32) x 32), activations two stages ahead in registers,
 // packed weights through a 3-stage LDS ring filled with global_load_lds
 // (no registers held by the weight loads).
@@ -724,6 +730,7 @@ __global__ __launch_bounds__(256) void gemm_deep_kernel(const GemmArgs p) {
   __shared__ __attribute__((aligned(16))) uint8_t Bs[RING][BSTAGE];
   __shared__ float cbs[BN * E];
   __shared__ float ebias[BN];  // the tile's bias, staged once (the epilogue's loads would serialise)
+  __shared__ float escale[BN];  // the tile's column factors acc_scale * 2^-e (parked epilogue)
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -790,9 +797,19 @@ __global__ __launch_bounds__(256) void gemm_deep_kernel(const GemmArgs p) {
 #pragma unroll
     for (int d = 0; d < DPT; ++d) {
       const void* src = reinterpret_cast<const void*>(bsrc[d] + kb);
-      lds_void_g* dst = (lds_void_g*)(&Bs[slot][(wave * 64 + 256 * d) * DSZ]);
-      if constexpr (DSZ == 16) __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
-      else __builtin_amdgcn_global_load_lds(src, dst, 4, 0, 0);
+      // Inline assembly rather than the builtin: the compiler cannot tell the
+      // ring's slots apart, so with the builtin it put s_waitcnt vmcnt(0) in
+      // front of every stage's weight reads, waiting for all loads in flight
+      // (measured at the cfg1 shape: 32.1 -> 28.4 us).  The wait is the
+      // activations' own: stage s's DMA is issued before stage s's activation
+      // loads, so the commit's wait for those (vmcnt retires in issue order)
+      // covers it, and the barrier after the commit publishes both.
+      const uint32_t la =
+          static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_g*)(&Bs[slot][(wave * 64 + 256 * d) * DSZ])));
+      if constexpr (DSZ == 16)
+        asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(la)) : "memory");
+      else
+        asm volatile("global_load_lds_dword %0, off" ::"v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(la)) : "memory");
     }
   };
   auto compute = [&](int buf, int slot) {
@@ -831,6 +848,7 @@ __global__ __launch_bounds__(256) void gemm_deep_kernel(const GemmArgs p) {
     const int rl = (p.cb_rows == 1) ? 0 : nl;
     const int e = planes_from_lds<BITS, false>(cbs + rl * E, cb, cb);
     rscale = ldexpf(p.acc_scale, -e);
+    if (g == 0) escale[nl] = rscale;
   }
   commit_a(0, ra0, true);  // waits for stage 0 (and the weight stages before it); range guard
   issue_a(2, ra0);
@@ -865,6 +883,57 @@ __global__ __launch_bounds__(256) void gemm_deep_kernel(const GemmArgs p) {
       exact_tile_out(p, XT, BITS, m0, m0 + BM, n0, n0 + BN, 0);
       return;
     }
+  }
+
+  // Parked epilogue (fp32 y, epilogues without a residual or quantization):
+  // two passes of MBLK/2 row blocks through LDS (the activation buffers are
+  // free now), then each store instruction writes two whole 512-byte row runs
+  // of the tile.  Stored straight from the accumulators, each instruction
+  // covered 32 bytes of 32 rows, and the partly written lines doubled the HBM
+  // write traffic (cfg1: 37.8 MB written for a 19.4 MB output; the kernel
+  // measured 33.3 -> 32.1 us with the parked stores).
+  constexpr bool kPark = (MODE & (kEpiRes | kEpiQuant)) == 0 && MBLK % 2 == 0;
+  if (kPark && p.y_dt == DIMQ_F32 && p.ldy % 4 == 0) {
+    constexpr int PR = MBLK / 2 * 32;  // rows per pass
+    constexpr int PP = BN + 4;         // park pitch (floats)
+    static_assert(!kPark || PR * PP * 4 <= (int)sizeof(As), "a pass fits in the activation buffers");
+    float* park = reinterpret_cast<float*>(&As[0][0]);
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+      __syncthreads();  // the last stage's (pass 1: the previous pass's) readers are done
+#pragma unroll
+      for (int mbl = 0; mbl < MBLK / 2; ++mbl) {
+        const int mb = pass * (MBLK / 2) + mbl;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          *reinterpret_cast<float4*>(park + (mbl * 32 + col) * PP + wave * 32 + 8 * j + 4 * g) =
+              make_float4(acc[mb][4 * j], acc[mb][4 * j + 1], acc[mb][4 * j + 2], acc[mb][4 * j + 3]);
+      }
+      __syncthreads();
+      constexpr int CH = PR * BN / 4;  // 16-byte chunks of a pass
+#pragma unroll
+      for (int u = 0; u < CH / 256; ++u) {
+        const int c = tid + 256 * u;
+        const int r = c / (BN / 4), c4 = c % (BN / 4);
+        const int64_t m = m0 + pass * PR + r;
+        const int64_t n = n0 + 4 * c4;
+        if (m >= p.M) continue;
+        const float4 a = *reinterpret_cast<const float4*>(park + r * PP + 4 * c4);
+        const float4 sc = *reinterpret_cast<const float4*>(escale + 4 * c4);
+        const float4 bb = *reinterpret_cast<const float4*>(ebias + 4 * c4);
+        float v[4] = {a.x * sc.x + bb.x, a.y * sc.y + bb.y, a.z * sc.z + bb.z, a.w * sc.w + bb.w};
+        const int64_t off = m * p.ldy + n;
+        if (n + 4 <= p.N) {
+          epi_m<MODE, 4>(p.epi, nullptr, off, true, v);
+          *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.y) + off) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (n + i < p.N) store_from_float(p.y, p.y_dt, off + i, epi1_m<MODE>(p.epi, off + i, v[i]));
+        }
+      }
+    }
+    return;
   }
 
   // epilogue: acc[mb][4j + i] = y[m][n], m = m0 + mb*32 + col, n = n0 + 32*wave + 8j + 4g + i
@@ -983,7 +1052,7 @@ int launch_big_conv_bits(const GemmArgs& p, int xt, int tile, hipStream_t s) {
 }
 
 // Linear tile ids (WGM x WGN waves of (MBLK*32) x (NBLK*32)):
-//   2: 128x128 (2x2, 64x64)   7: 128x128 deep pipeline
+//   2: 128x128 (2x2, 64x64)   7: 64x128 deep pipeline (kDeepMblk)
 //  10: 256x256 shared decode (4x2, 64x128), next stage's decode woven between the MFMAs
 // Epilogue modes: none / relu / gelu / residual on each; for fp16 inputs (the
 // W4A4 activation codes) also none / relu / gelu with the next layer's
@@ -996,7 +1065,7 @@ int launch_big_linear_modes(const GemmArgs& p, int tile, int mode, hipStream_t s
 #define DIMQ_QMODE(M)                                                                \
   case M:                                                                            \
     if (tile == 10) return launch_lds<BITS, XT, 4, 2, 2, 4, M, 8>(p, s);             \
-    if (tile == 7) return launch_deep<BITS, XT, 4, M>(p, s);                         \
+    if (tile == 7) return launch_deep<BITS, XT, kDeepMblk, M>(p, s);                         \
     return launch_big<BITS, XT, 2, 2, 2, 2, false, M>(p, s);
         DIMQ_QMODE(kEpiQuant)
         DIMQ_QMODE(kEpiRelu | kEpiQuant)
@@ -1015,10 +1084,10 @@ int launch_big_linear_modes(const GemmArgs& p, int tile, int mode, hipStream_t s
   }
   if (tile == 7) {
     switch (mode) {
-      case kEpiRelu: return launch_deep<BITS, XT, 4, kEpiRelu>(p, s);
-      case kEpiGelu: return launch_deep<BITS, XT, 4, kEpiGelu>(p, s);
-      case kEpiRes: return launch_deep<BITS, XT, 4, kEpiRes>(p, s);
-      default: return launch_deep<BITS, XT, 4, kEpiNone>(p, s);
+      case kEpiRelu: return launch_deep<BITS, XT, kDeepMblk, kEpiRelu>(p, s);
+      case kEpiGelu: return launch_deep<BITS, XT, kDeepMblk, kEpiGelu>(p, s);
+      case kEpiRes: return launch_deep<BITS, XT, kDeepMblk, kEpiRes>(p, s);
+      default: return launch_deep<BITS, XT, kDeepMblk, kEpiNone>(p, s);
     }
   }
   switch (mode) {

@@ -143,6 +143,13 @@ int linear_codebook_impl(const void* x, int x_dtype, int64_t M, int64_t K, int64
   // (ResNet-18 fc, M 128 x N 1000: 32 work-groups on 64-row tiles, 128 on
   // 16-row tiles; measured 28.9 -> 23.4 us per call)
   if (bits == 8 && tile == kTile64x32 && ((M + 63) / 64) * ((N + 63) / 64) < kCUs / 2) tile = kTile16x16;
+  if (tile == kTileGemv && gemv_direct_ok(p, bits, x_dtype)) {
+    switch (bits) {
+      case 2: return launch_gemv_direct<2>(p, s);
+      case 3: return launch_gemv_direct<3>(p, s);
+      default: return launch_gemv_direct<4>(p, s);
+    }
+  }
   if (tile == kTileGemv) {
     const bool ws_ok = workspace != nullptr && aligned(workspace, 16);
     GemvPlan pl;
@@ -190,6 +197,7 @@ extern "C" int64_t dimq_linear_codebook_workspace_bytes(int64_t M, int64_t K, in
   p.K = K;
   p.N = N;
   p.fast_b = p.vec_a = true;
+  if (gemv_direct_ok(p, bits, x_dtype)) return 0;  // no split k
   GemvPlan pl;
   if (!gemv_plan(p, bits, true, pl)) return 0;
   return (gemv_partial_bytes(p, pl) + 255) / 256 * 256;

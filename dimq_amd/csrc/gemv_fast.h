@@ -20,6 +20,7 @@
 //            16 columns).  With KS > 1 the work-groups of one column block
 //            write fp32 partial sums into the caller's workspace and
 //            gemv_reduce_kernel adds them (bias and epilogue there).
+// bf16 activations with 4 < M <= 16 take gemv_direct_kernel (below) instead.
 #pragma once
 
 #include "gemm_big.h"
@@ -201,6 +202,166 @@ __global__ __launch_bounds__(256) void gemv_reduce_kernel(const GemmArgs p, int 
   store_from_float(p.y, p.y_dt, off, epi1(p.epi, off, v));
 }
 
+// ---- bf16 activations, 4 < M <= 16: direct A operand, bf16 hi + lo weights --
+//
+// For bf16 activations the MFMA can take x as it is (v_mfma_f32_16x16x32_bf16),
+// with each weight split into two bf16 parts, hi = bf16(c) and lo = bf16(c -
+// hi), whose sum carries 16 significant bits (two MFMAs per 8 indices).  The
+// activations then need no conversion, no LDS staging and no range guard
+// (bf16 has fp32's exponent range), so a work-group can own 16 columns over
+// the whole k range without the 128 KB of staged fp16 rows per work-group
+// that M = 16 costs the staged kernel, and the split-k partial sums and their
+// second launch go away: each lane loads its A fragments (8 consecutive x of
+// row lane % 16) straight from global memory, one 32-index chunk ahead.
+// Work-group = 4 waves on 16 columns; wave w takes the k quarter w, lane
+// (col, g) the run of R = K / 16 indices 4w + g of its column; the four waves'
+// 16 x 16 partial tiles are added through LDS.  Measured at cfg5 M = 16 (X
+// bf16 [16, 4096], 3-bit): 9.4 against 10.1 us for the staged split-k kernel
+// and its reduction; at M <= 4 the staged kernel stays faster (5.9 against
+// 6.5 us at M = 1), whose rows past M cost nothing.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// 8-index field word of sub-step s of a 32-index chunk (slot order of decode_sub).
+template <int BITS>
+__device__ __forceinline__ uint32_t chunk_word(const uint32_t (&c)[BITS], int s) {
+  if constexpr (BITS == 4) {
+    return c[s];
+  } else if constexpr (BITS == 2) {
+    return c[s >> 1] >> (4 * (s & 1));
+  } else {
+    if (s == 0) return c[0];
+    if (s == 1) return __builtin_amdgcn_alignbit(c[1], c[0], 24);
+    if (s == 2) return __builtin_amdgcn_alignbit(c[2], c[1], 16);
+    return c[2] >> 8;
+  }
+}
+
+// Eight indices -> their hi and lo bf16 weights (slot order), one selector pass for both.
+template <int BITS>
+__device__ __forceinline__ void decode_hilo(uint32_t G, const CodebookRegs<BITS>& ch, const CodebookRegs<BITS>& cl,
+                                            bf16x8& wh, bf16x8& wl) {
+  uint32_t D0, D1;
+  if constexpr (BITS == 4) {
+    D0 = G & 0x0f0f0f0fu;
+    D1 = (G >> 4) & 0x0f0f0f0fu;
+  } else if constexpr (BITS == 2) {
+    D0 = G & 0x03030303u;
+    D1 = (G >> 2) & 0x03030303u;
+  } else {
+    D0 = spread3x4(G & 0xfffu);
+    D1 = spread3x4((G >> 12) & 0xfffu);
+  }
+  uint32_t h[4], l[4];
+  lookup4<BITS>(ch, D0, h[0], h[1]);
+  lookup4<BITS>(ch, D1, h[2], h[3]);
+  lookup4<BITS>(cl, D0, l[0], l[1]);
+  lookup4<BITS>(cl, D1, l[2], l[3]);
+  const u32x4 hv = {h[0], h[1], h[2], h[3]}, lv = {l[0], l[1], l[2], l[3]};
+  wh = __builtin_bit_cast(bf16x8, hv);
+  wl = __builtin_bit_cast(bf16x8, lv);
+}
+
+// A fragment of sub-step s of a 32-index chunk in the weight decoder's slot
+// order (kperm16), from the chunk's 32 activations in natural order (x[4]
+// holds k 8j .. 8j + 7 in x[j]): 3-bit slots are natural; 4-bit slots hold the
+// even k of a group of 8, then the odd k; 2-bit sub-steps 2h, 2h + 1 take k
+// {0,4,8,12,1,5,9,13} and {2,6,10,14,3,7,11,15} of the chunk's 16-group h.
+template <int BITS>
+__device__ __forceinline__ uint4 a_slots(const uint4 (&x)[4], int s) {
+  constexpr uint32_t LO = 0x05040100u, HI = 0x07060302u;  // low / high halves of two dwords
+  if constexpr (BITS == 3) {
+    return x[s];
+  } else if constexpr (BITS == 4) {
+    const uint4 v = x[s];
+    return make_uint4(perm(v.y, v.x, LO), perm(v.w, v.z, LO), perm(v.y, v.x, HI), perm(v.w, v.z, HI));
+  } else {
+    const uint4 a = x[2 * (s >> 1)], b = x[2 * (s >> 1) + 1];  // dwords d0..d3, d4..d7 of the 16-group
+    if ((s & 1) == 0)
+      return make_uint4(perm(a.z, a.x, LO), perm(b.z, b.x, LO), perm(a.z, a.x, HI), perm(b.z, b.x, HI));
+    return make_uint4(perm(a.w, a.y, LO), perm(b.w, b.y, LO), perm(a.w, a.y, HI), perm(b.w, b.y, HI));
+  }
+}
+
+template <int BITS, int R>
+__global__ __launch_bounds__(256) void gemv_direct_kernel(const GemmArgs p) {
+  constexpr int E = 1 << BITS;
+  constexpr int NW = R / 32 * BITS;  // packed words of a run
+  constexpr int CH = R / 32;         // 32-index chunks of a run
+  __shared__ floatx4 red[4][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, col = lane & 15, g = lane >> 4;
+  const int64_t n0 = (int64_t)blockIdx.x * 16;
+  const int64_t n = n0 + col < p.N ? n0 + col : p.N - 1;
+  const int64_t k0 = (int64_t)(4 * wave + g) * R;
+  float cbv[E];
+  load_cb_row<E>(p.cb, p.cb_dt, p.cb_rows == 1 ? 0 : n, p.cb_size, cbv);
+  uint32_t bw[NW];
+  {
+    const uint4* src = reinterpret_cast<const uint4*>(p.w + (((n * p.K + k0) * BITS) >> 3));
+#pragma unroll
+    for (int q = 0; q < NW / 4; ++q) {
+      const uint4 t = src[q];
+      bw[4 * q] = t.x; bw[4 * q + 1] = t.y; bw[4 * q + 2] = t.z; bw[4 * q + 3] = t.w;
+    }
+  }
+  const bool live = col < p.M;  // A row col; rows >= M are zero (and load row 0)
+  const uint4* xa =
+      reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p.x) + (live ? col : 0) * p.ldx + k0);
+  CodebookRegs<BITS> ch, cl;
+  {
+    uint32_t hb[E], lb[E];
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      hb[j] = float_to_bf16_bits(cbv[j]);
+      lb[j] = float_to_bf16_bits(cbv[j] - bf16_bits_to_float(hb[j]));
+    }
+    set_planes<BITS>(ch, hb);
+    set_planes<BITS>(cl, lb);
+  }
+  floatx4 acc = floatx4{0.0f, 0.0f, 0.0f, 0.0f}, acc2 = acc;
+  uint4 xr[2][4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) xr[0][s] = xa[s];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    if (c + 1 < CH) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) xr[(c + 1) & 1][s] = xa[4 * (c + 1) + s];
+    }
+    uint32_t chunk[BITS];
+#pragma unroll
+    for (int w = 0; w < BITS; ++w) chunk[w] = bw[c * BITS + w];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      bf16x8 wh, wl;
+      decode_hilo<BITS>(chunk_word<BITS>(chunk, s), ch, cl, wh, wl);
+      const uint4 xv = live ? a_slots<BITS>(xr[c & 1], s) : make_uint4(0, 0, 0, 0);
+      const bf16x8 a = __builtin_bit_cast(bf16x8, xv);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, wh, acc, 0, 0, 0);
+      acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, wl, acc2, 0, 0, 0);
+    }
+  }
+  red[wave][lane] = acc + acc2;
+  __syncthreads();
+  if (wave != 0) return;
+  acc = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];  // acc[i] = y[4g + i][n0 + col]
+  if (n0 + col >= p.N) return;
+  const float b = p.bias ? load_as_float(p.bias, p.bias_dt, n0 + col) : 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t m = 4 * g + i;
+    if (m < p.M) {
+      const int64_t off = m * p.ldy + n0 + col;
+      store_from_float(p.y, p.y_dt, off, epi1(p.epi, off, acc[i] * p.acc_scale + b));
+    }
+  }
+}
+
+// The direct kernel's shapes: bf16 x, 4 < M <= 16, K = 16 R with R in {64, 128, 256}.
+inline bool gemv_direct_ok(const GemmArgs& p, int bits, int xt) {
+  return xt == DIMQ_BF16 && p.M > 4 && p.M <= 16 && !p.conv && (bits == 2 || bits == 3 || bits == 4) && p.fast_b &&
+         p.vec_a && (p.K == 1024 || p.K == 2048 || p.K == 4096);
+}
+
 // Split of a GEMV call: column blocks per work-group (NCB) and k splits (KS);
 // every lane streams one run of kGemvRun indices.  False when the shape does
 // not fit the kernel (other M <= 16 shapes take gemv_cb_kernel).
@@ -247,6 +408,17 @@ int launch_gemv_stream_k(const GemmArgs& p, const GemvPlan& pl, float* partial, 
 }
 
 }  // namespace
+
+template <int BITS>
+int launch_gemv_direct(const GemmArgs& p, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((p.N + 15) / 16));
+  switch (p.K) {
+    case 1024: hipLaunchKernelGGL((gemv_direct_kernel<BITS, 64>), grid, dim3(256), 0, s, p); break;
+    case 2048: hipLaunchKernelGGL((gemv_direct_kernel<BITS, 128>), grid, dim3(256), 0, s, p); break;
+    default: hipLaunchKernelGGL((gemv_direct_kernel<BITS, 256>), grid, dim3(256), 0, s, p); break;
+  }
+  return check_launch("linear_codebook (gemv, bf16)");
+}
 
 // Runs a planned GEMV; `partial` holds gemv_partial_bytes when pl.ks > 1.
 template <int BITS>

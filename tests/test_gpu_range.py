@@ -56,7 +56,8 @@ def _scaled(x, mode, g):
 LINEAR_CASES = [
     # id, M, N, K, bits; the ops entry allocates the workspace its query asks for
     ("gemv_stream", 1, 256, 4096, 3),
-    ("gemv_stream_splitk_4col", 8, 128, 2048, 4),
+    ("gemv_stream_splitk_4col", 8, 128, 2048, 4),  # bf16: the direct bf16 kernel
+    ("gemv_direct_k1024", 5, 64, 1024, 2),
     ("gemv_cb", 5, 77, 1000, 3),
     ("gemm_fast", 40, 256, 512, 4),
     ("gemm_cb", 40, 100, 100, 2),

@@ -291,6 +291,9 @@ int dimq_linear_codebook_ex(const void* x, int x_dtype, int64_t M, int64_t K, co
  * range over work-groups and keep the fp32 partial sums there (a second,
  * small kernel adds them): more work-groups stream the weights, and for
  * M > 4 the activations are read by 64 columns per work-group instead of 16.
+ * bf16 activations with 4 < M <= 16 and K in {1024, 2048, 4096} need no
+ * workspace: one launch multiplies them as they are with bf16 hi + lo
+ * weights.
  * Large-M shapes (M >= 2048, bits 2-4, K % 32 == 0, fp16 / bf16 / fp32 x,
  * 256-byte aligned workspace) decode the weights once per call into the
  * workspace as fp16 (and convert bf16 / fp32 activations to fp16 there with

@@ -83,9 +83,12 @@ def test_linear_workspace_sizes_and_act_codebook_errors(capi):
     assert ws(1576, 768, 3072, 4, capi.F32) == 0
     assert ws(1576, 768, 3072, 4, capi.BF16) == 0
     assert ws(17, 4096, 4096, 3, capi.BF16) == 0
-    # decode GEMV, 4 < M <= 16: fp32 partial sums of the k splits (k ranges of 1024)
-    assert ws(16, 4096, 4096, 3, capi.BF16) == up(4 * 16 * 4096 * 4)
+    # decode GEMV, 4 < M <= 16: bf16 x with K in {1024, 2048, 4096} takes the one-launch bf16 kernel (no
+    # workspace); other shapes keep fp32 partial sums of the k splits (k ranges of 1024)
+    assert ws(16, 4096, 4096, 3, capi.BF16) == 0
+    assert ws(16, 4096, 4096, 3, capi.F16) == up(4 * 16 * 4096 * 4)
     assert ws(9, 8192, 192, 2, capi.F16) == up(8 * 9 * 192 * 4)
+    assert ws(9, 8192, 192, 2, capi.BF16) == up(8 * 9 * 192 * 4)
     assert ws(16, 4096, 4000, 3, capi.BF16) == 0   # N % 64 != 0: one k range per work-group
     assert ws(4, 4096, 4096, 3, capi.BF16) == 0    # M <= 4, K 4096: one k range per work-group
     assert ws(4, 8192, 4096, 3, capi.BF16) == up(2 * 4 * 4096 * 4)  # M <= 4: k ranges of 4096

@@ -218,9 +218,15 @@ __global__ __launch_bounds__(64 * WGM * WGN, big_min_waves(BITS, MBLK, NBLK, CON
 
   const int64_t nk = p.K / kBigKS;
   RawA<XT> ra[A_TASKS];
+  bool avalid[A_TASKS];  // CONV: the task's tap lies inside the image (else its group reads as zeros)
   uint32_t b0[NBLK][2 * BITS], b1[NBLK][2 * BITS];
   uint32_t trk = 0;
 
+  // CONV taps in the padding still issue their load (pixel (0, 0) of the
+  // row's image) and are zeroed at commit: with a branch around the load the
+  // compiler cannot count the loads in flight, and its wait for the stage
+  // being computed then also waited for part of the next stage's loads,
+  // issued just before (a full memory latency per 64-k stage).
   auto issue_a = [&](int64_t kt) {
     const int64_t k = (kt < nk ? kt : nk - 1) * kBigKS;
     if constexpr (CONV) {
@@ -232,13 +238,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, big_min_waves(BITS, MBLK, NBLK, CON
       for (int i = 0; i < A_TASKS; ++i) {
         const int ih = aih[i] + kh * p.cdh;
         const int iw = aiw[i] + kw * p.cdw;
-        if (static_cast<unsigned>(ih) < static_cast<unsigned>(p.cH) &&
-            static_cast<unsigned>(iw) < static_cast<unsigned>(p.cW)) {
-          issue_a16<XT>(p.x, aoff[i] + (static_cast<int64_t>(ih) * p.cW + iw) * p.cC + c0, ra[i]);
-        } else {
-#pragma unroll
-          for (int w = 0; w < RawA<XT>::kWords; ++w) ra[i].w[w] = 0u;
-        }
+        avalid[i] = static_cast<unsigned>(ih) < static_cast<unsigned>(p.cH) &&
+                    static_cast<unsigned>(iw) < static_cast<unsigned>(p.cW);
+        const int64_t pix = avalid[i] ? static_cast<int64_t>(ih) * p.cW + iw : 0;
+        issue_a16<XT>(p.x, aoff[i] + pix * p.cC + c0, ra[i]);
       }
     } else {
 #pragma unroll
@@ -250,6 +253,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, big_min_waves(BITS, MBLK, NBLK, CON
     for (int i = 0; i < A_TASKS; ++i) {
       uint32_t o[8];
       convert_a16_big<BITS, XT>(ra[i], o);
+      if constexpr (CONV) {
+        const uint32_t m = avalid[i] ? 0xffffffffu : 0u;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) o[w] &= m;
+      }
       if (range_guarded<XT>() && track) trk = range_track(trk, o);
       uint4* dst = reinterpret_cast<uint4*>(&As[buf][alds[i]]);
       dst[0] = make_uint4(o[0], o[1], o[2], o[3]);

@@ -96,11 +96,13 @@ __device__ __forceinline__ uint32_t stage_word(const uint32_t (&c)[2 * BITS], in
 }
 
 // 16 raw activations -> 8 dwords of fp16 pairs in the slot order of BITS
-// (bf16: one round-to-nearest v_cvt_pk_f16_f32 per pair).
+// (fp32, bf16: one round-to-nearest v_cvt_pk_f16_f32 per pair).
 template <int BITS, int XT>
 __device__ __forceinline__ void convert_a16_big(const RawA<XT>& r, uint32_t out[8]) {
   if constexpr (XT == DIMQ_F32) {
-    convert_a16<BITS, XT, false>(r, 1.0f, 0, out);
+#pragma unroll
+    for (int d = 0; d < 8; ++d)
+      out[d] = f16x2_rne(__uint_as_float(r.w[kperm16(BITS, 2 * d)]), __uint_as_float(r.w[kperm16(BITS, 2 * d + 1)]));
   } else {
     uint32_t w[8];
 #pragma unroll

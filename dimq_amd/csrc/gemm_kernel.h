@@ -287,18 +287,16 @@ __device__ __forceinline__ void load_a_group(const GemmArgs& p, int64_t gm, int6
 #pragma unroll
     for (int j = 0; j < 16; ++j) v[j] = 0.0f;
   }
-  uint32_t h[16];
+  if constexpr (A4) {
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    float t = v[j];
-    if constexpr (A4) {
+    for (int j = 0; j < 16; ++j) {
       const bool live = (gm < p.M) && (k0 + j < p.K);
-      t = live ? (float)(quantize_u4(t, p.act_scale, p.act_zp) - p.act_zp) : 0.0f;
+      v[j] = live ? (float)(quantize_u4(v[j], p.act_scale, p.act_zp) - p.act_zp) : 0.0f;
     }
-    h[j] = float_to_f16_bits(t);
   }
+  // one round-to-nearest v_cvt_pk_f16_f32 per pair of slots
 #pragma unroll
-  for (int d = 0; d < 8; ++d) out[d] = h[kperm16(BITS, 2 * d)] | (h[kperm16(BITS, 2 * d + 1)] << 16);
+  for (int d = 0; d < 8; ++d) out[d] = f16x2_rne(v[kperm16(BITS, 2 * d)], v[kperm16(BITS, 2 * d + 1)]);
   if constexpr (range_guarded<XT, A4>()) {
 #pragma unroll
     for (int d = 0; d < 8; ++d) trk |= out[d];
@@ -823,20 +821,19 @@ __device__ __forceinline__ void issue_a16(const void* x, int64_t off, RawA<XT>& 
 // 16 raw activations -> 8 dwords of fp16 pairs in the slot order of BITS.
 template <int BITS, int XT, bool A4>
 __device__ __forceinline__ void convert_a16(const RawA<XT>& r, float s, int zp, uint32_t out[8]) {
-  uint32_t h[16];
+  float v[16];
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
-    float v;
-    if constexpr (XT == DIMQ_F32) v = __uint_as_float(r.w[j]);
+    if constexpr (XT == DIMQ_F32) v[j] = __uint_as_float(r.w[j]);
     else {
       const uint32_t bits = (r.w[j >> 1] >> (16 * (j & 1))) & 0xffffu;
-      v = (XT == DIMQ_F16) ? f16_bits_to_float(bits) : bf16_bits_to_float(bits);
+      v[j] = (XT == DIMQ_F16) ? f16_bits_to_float(bits) : bf16_bits_to_float(bits);
     }
-    if constexpr (A4) v = (float)(quantize_u4(v, s, zp) - zp);
-    h[j] = float_to_f16_bits(v);
+    if constexpr (A4) v[j] = (float)(quantize_u4(v[j], s, zp) - zp);
   }
+  // one round-to-nearest v_cvt_pk_f16_f32 per pair of slots
 #pragma unroll
-  for (int d = 0; d < 8; ++d) out[d] = h[kperm16(BITS, 2 * d)] | (h[kperm16(BITS, 2 * d + 1)] << 16);
+  for (int d = 0; d < 8; ++d) out[d] = f16x2_rne(v[kperm16(BITS, 2 * d)], v[kperm16(BITS, 2 * d + 1)]);
 }
 
 template <int BITS>

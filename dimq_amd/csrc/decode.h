@@ -79,8 +79,14 @@ __device__ __forceinline__ void lookup4(const CodebookRegs<BITS>& cb, uint32_t D
     hi = perm(cb.H[1], cb.H[0], D);
   } else {
     const uint32_t s = D & 0x07070707u;
-    // byte i of sel2 = i + 4 * bit3(D.byte_i): picks the upper half table
-    const uint32_t sel2 = ((D >> 1) & 0x04040404u) | 0x03020100u;
+    // byte i of sel2 = i + 4 * bit3(D.byte_i): picks the upper half table.
+    // The two masks come from registers so that the and + or is one
+    // v_and_or_b32 (a VOP3 instruction takes no literal on gfx9); as
+    // literals they cost a v_and_b32 and a v_or_b32.
+    uint32_t k4, k3210;
+    asm("s_mov_b32 %0, 0x4040404" : "=s"(k4));
+    asm("v_mov_b32 %0, 0x3020100" : "=v"(k3210));
+    const uint32_t sel2 = ((D >> 1) & k4) | k3210;
     const uint32_t la = perm(cb.L[1], cb.L[0], s), lb = perm(cb.L[3], cb.L[2], s);
     const uint32_t ha = perm(cb.H[1], cb.H[0], s), hb = perm(cb.H[3], cb.H[2], s);
     lo = perm(lb, la, sel2);

@@ -822,12 +822,25 @@ __global__ __launch_bounds__(256) void gemm_deep_kernel(const GemmArgs p) {
         asm volatile("global_load_lds_dword %0, off" ::"v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(la)) : "memory");
     }
   };
+  // 4-bit: k16 step s pairs 8-k chunk s (lane group 0) with chunk s + 4
+  // (lane group 1) instead of chunks 2s and 2s + 1, so a lane's four packed
+  // words of the stage are consecutive (one 16-byte LDS read, no per-lane
+  // select) and its activation fragments are the 16-byte chunks s + 4g of
+  // the row (the MFMA sums the 16 slots of both lane groups, so any pairing
+  // of the stage's eight chunks gives the same products).
+  constexpr bool kChunkPairs = BITS == 4;
   auto compute = [&](int buf, int slot) {
     uint32_t bq[2 * BITS];
     const uint32_t* brow = reinterpret_cast<const uint32_t*>(&Bs[slot][nl * RB]);
+    if constexpr (kChunkPairs) {
+      const uint4 q = *reinterpret_cast<const uint4*>(brow + 4 * g);
+      bq[0] = q.x; bq[1] = q.y; bq[2] = q.z; bq[3] = q.w;
+    } else {
 #pragma unroll
-    for (int w = 0; w < 2 * BITS; ++w) bq[w] = brow[w];
-    const uint16_t* arow = &As[buf][col * kBigLDA + 8 * g];
+      for (int w = 0; w < 2 * BITS; ++w) bq[w] = brow[w];
+    }
+    constexpr int AS = kChunkPairs ? 8 : 16;  // halves between the fragments of consecutive steps
+    const uint16_t* arow = &As[buf][col * kBigLDA + (kChunkPairs ? 32 : 8) * g];
     half8 xf[2][MBLK];
 #pragma unroll
     for (int mb = 0; mb < MBLK; ++mb) xf[0][mb] = *reinterpret_cast<const half8*>(arow + mb * 32 * kBigLDA);
@@ -836,9 +849,9 @@ __global__ __launch_bounds__(256) void gemm_deep_kernel(const GemmArgs p) {
       if (s + 1 < kBigKS / 16) {
 #pragma unroll
         for (int mb = 0; mb < MBLK; ++mb)
-          xf[(s + 1) & 1][mb] = *reinterpret_cast<const half8*>(arow + mb * 32 * kBigLDA + 16 * (s + 1));
+          xf[(s + 1) & 1][mb] = *reinterpret_cast<const half8*>(arow + mb * 32 * kBigLDA + AS * (s + 1));
       }
-      const half8 wf = decode_word<BITS>(stage_word<BITS>(bq, s, g), cb);
+      const half8 wf = decode_word<BITS>(kChunkPairs ? bq[s] : stage_word<BITS>(bq, s, g), cb);
 #pragma unroll
       for (int mb = 0; mb < MBLK; ++mb) acc[mb] = mfma32(wf, xf[s & 1][mb], acc[mb]);
     }

@@ -156,6 +156,53 @@ def test_predecode_batch_matches_per_call_decode(gpu, xdt):
             assert oracle.rel_err(y_bat.cpu(), ref) <= 2e-3, (i, N, K, bits)
 
 
+def _scaled_decode_cpu(packed, bits, cb, N, K):
+    """The decode's contract on the CPU: W_hat[n] = fp16(C[idx] * 2^e_n) (round to nearest even), with e_n =
+    clamp(15 - ex, -100, 100) for max|C_n| = m * 2^ex, m in [0.5, 1) (e_n = 0 for an all-zero row), and the
+    row factor 2^-e_n; C[idx] from the oracle's dequantize (reference.py:47-56)."""
+    import numpy as np
+    w = oracle.dequantize(packed, bits, cb, N, K).astype(np.float32)
+    c = cb.float().numpy().reshape(-1 if cb.shape[0] != 1 else 1, cb.shape[-1])
+    mx = np.abs(c).max(axis=1)
+    ex = np.frexp(mx)[1]
+    e = np.where(mx > 0, np.clip(15 - ex, -100, 100), 0).astype(np.int32)
+    e = np.broadcast_to(e, (N,)) if e.shape[0] == 1 else e
+    w_hat = np.ldexp(w, e[:, None]).astype(np.float32).astype(np.float16)
+    return w_hat, np.ldexp(np.float32(1.0), -e).astype(np.float32)
+
+
+@torch.no_grad()
+def test_predecode_batch_is_the_scaled_dequantized_weight(gpu):
+    """The decoded fp16 rows and their factors, bit for bit, against the CPU statement of the decode: 2, 3 and
+    4 bits, per-layer and per-channel codebooks, a codebook with fewer entries than 2^bits, an all-zero row,
+    centres near fp16's subnormals and near its largest values (the exponent clamp), K past one lane pass."""
+    import numpy as np
+    from dimq_amd import ops
+    announce("predecode decode bits")
+    cases = []
+    for i, (N, K, bits, rows, size) in enumerate([(37, 64, 2, 37, 4), (64, 96, 3, 1, 8), (130, 768, 4, 130, 16),
+                                                  (16, 4608, 4, 16, 16), (33, 128, 4, 33, 10), (24, 3072, 3, 24, 8)]):
+        g = torch.Generator().manual_seed(300 + i)
+        cb = (torch.randn(rows, size, generator=g) * 0.05).sort(dim=1).values
+        if rows > 2:
+            cb[0] = 0.0                   # all-zero row: e = 0
+            cb[1] *= 1e-30                # e clamped at +100
+            cb[2] = cb[2] * 1e4           # largest entries near 2^15 after scaling
+        idx = torch.randint(0, size, (N, K), generator=g, dtype=torch.uint8)
+        packed = torch.from_numpy(oracle.pack_bits(idx, bits))
+        cases.append((packed, cb, bits, N, K))
+    layers = [(p.to(gpu), c.to(gpu), b, n, k) for p, c, b, n, k in cases]
+    buf, views = ops.predecode_codebook_weights(layers)
+    for (packed, cb, bits, N, K), v in zip(cases, views):
+        got = v.cpu().numpy()
+        w_gpu = got[: N * K * 2].view(np.float16).reshape(N, K)
+        off = (N * K * 2 + 255) // 256 * 256
+        rs_gpu = got[off: off + 4 * N].view(np.float32)
+        w_ref, rs_ref = _scaled_decode_cpu(packed, bits, cb, N, K)
+        assert np.array_equal(w_gpu.view(np.uint16), w_ref.view(np.uint16)), (N, K, bits)
+        assert np.array_equal(rs_gpu, rs_ref), (N, K, bits)
+
+
 @torch.no_grad()
 def test_predecode_batch_epilogues_and_small_m(gpu):
     """Fused residual / GELU epilogues on decoded weights; a call below the large-M threshold ignores `decoded`

@@ -295,12 +295,21 @@ __global__ __launch_bounds__(256) void gemv_direct_kernel(const GemmArgs p) {
   float cbv[E];
   load_cb_row<E>(p.cb, p.cb_dt, p.cb_rows == 1 ? 0 : n, p.cb_size, cbv);
   uint32_t bw[NW];
-  {
+  if constexpr (NW % 4 == 0) {
     const uint4* src = reinterpret_cast<const uint4*>(p.w + (((n * p.K + k0) * BITS) >> 3));
 #pragma unroll
     for (int q = 0; q < NW / 4; ++q) {
       const uint4 t = src[q];
       bw[4 * q] = t.x; bw[4 * q + 1] = t.y; bw[4 * q + 2] = t.z; bw[4 * q + 3] = t.w;
+    }
+  } else {
+    // 3-bit runs of 64 indices: 24 bytes, 8-byte aligned
+    static_assert(NW % 2 == 0, "a run is a whole number of 8-byte pieces");
+    const uint2* src = reinterpret_cast<const uint2*>(p.w + (((n * p.K + k0) * BITS) >> 3));
+#pragma unroll
+    for (int q = 0; q < NW / 2; ++q) {
+      const uint2 t = src[q];
+      bw[2 * q] = t.x; bw[2 * q + 1] = t.y;
     }
   }
   const bool live = col < p.M;  // A row col; rows >= M are zero (and load row 0)

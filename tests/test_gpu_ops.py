@@ -471,11 +471,13 @@ def test_linear_codebook_large_tiles(gpu, bits, M, N, K, xdt):
                                        (5, 77, 4096, torch.float16), (9, 200, 8192, torch.bfloat16),
                                        (16, 48, 12288, torch.float32), (16, 256, 4096, torch.bfloat16),
                                        (8, 128, 2048, torch.float32), (12, 64, 1024, torch.float16),
-                                       (16, 4096, 4096, torch.bfloat16)])
+                                       (16, 4096, 4096, torch.bfloat16), (8, 96, 1024, torch.bfloat16),
+                                       (6, 80, 2048, torch.bfloat16)])
 def test_linear_codebook_gemv_fast(gpu, bits, M, N, K, xdt):
     """Decode-shape GEMVs (streamed weight runs; 16-column work-groups with the k range split over waves, or
-    64-column work-groups with k split over work-groups and the partial sums added by a second kernel),
-    N tails, per-layer and per-channel codebooks, fp32 / fp16 / bf16 activations."""
+    64-column work-groups with k split over work-groups and the partial sums added by a second kernel; bf16
+    activations with 4 < M <= 16 and K 1024 / 2048 / 4096 the direct kernel, whose lane runs are 64 / 128 /
+    256 indices), N tails, per-layer and per-channel codebooks, fp32 / fp16 / bf16 activations."""
     ops = _ops()
     for per_channel in (True, False):
         announce(f"linear_codebook gemv bits={bits} M={M} N={N} K={K} {xdt} pc={per_channel}")

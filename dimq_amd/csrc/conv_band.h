@@ -1,6 +1,9 @@
-// Banded direct 3x3 convolution for NCHW fp16 activations with NCHW output:
-// fp32 (the reference op's layout: BASELINE cfg2, the W4A4 conv2d_lut path)
-// or fp16 (also the next layer's W4A4 codes from the quantizing epilogue).
+// Banded direct 3x3 convolution of fp16 activations, C = 64, stride 1, pad 1:
+//   NCHW in and out, fp32 (the reference op's layout: BASELINE cfg2, the
+//   W4A4 conv2d_lut path) or fp16 (also the next layer's W4A4 codes from the
+//   quantizing epilogue);
+//   NHWC in and out (ResNet-18's layer1 in channels_last), fp32 or fp16, the
+//   residual and ReLU of a basic block's second conv fused.
 //
 // One 512-thread work-group (8 waves, two per SIMD) owns a contiguous run of
 // 32-pixel blocks of one image (the image's OH*OW output pixels, flattened
@@ -13,8 +16,8 @@
 //      first round of blocks), then each lane loads its output channel's
 //      packed weights and codebook row and decodes its 36 weight fragments
 //      into VGPRs (resident for the whole work-group) while the rows land;
-//   2. stage A is transposed NCHW -> [row][col][channel] fp16 into LDS
-//      (8x8 transposes in registers), barrier, the loads of stage B (the
+//   2. stage A is written into LDS as [row][col][channel] fp16 (NCHW: 8x8
+//      transposes in registers; NHWC: as it is), barrier, the loads of stage B (the
 //      remaining rows) go out, round 0 runs (one block-half per wave), stage B
 //      is committed, barrier, round 0's blocks are stored, the remaining
 //      blocks run two accumulator chains per wave.  Round 0's stores leave
@@ -22,10 +25,12 @@
 //      order: stores issued before the commit would make its wait for stage B
 //      also wait for them to complete;
 //   3. each finished 32x32 block goes through a wave-private LDS area and
-//      leaves as non-temporal 16-byte stores, 8 channels x 128 bytes per
-//      instruction: the output is written once and never re-read here, and
-//      streaming it past the L2 keeps the 25 MB fp32 output of a cfg2 call
-//      from evicting the input rows other work-groups still read.
+//      leaves as 16-byte stores: NCHW fp32 non-temporal, 8 channels x 128
+//      bytes per instruction (the output is written once and never re-read
+//      here, and streaming it past the L2 keeps the 25 MB fp32 output of a
+//      cfg2 call from evicting the input rows other work-groups still read);
+//      NHWC each pixel's 32 channels as one run of 64 (fp16) or 128 (fp32)
+//      bytes, through the L2.
 #pragma once
 
 #include "conv_common.h"
@@ -106,6 +111,49 @@ __device__ __forceinline__ void band_commit(const HaloArgs& p, int r0, int t, in
   }
 }
 
+// NHWC input: the same tasks (channel octet co, stage row r, 8 columns q),
+// each eight 16-byte loads of the octet's channels of one pixel (128-byte
+// pixel runs, C = 64), written to the halo as they are: the pixel-major layout
+// needs no transpose.
+__device__ __forceinline__ void band_issue_nhwc(const HaloArgs& p, int b, int ih_first, int t, int tasks,
+                                                BandTask& tk) {
+  const int qn = p.W >> 3;
+  const int tt = t < tasks ? t : 0;
+  const int co = tt & 7, rest = tt >> 3, q = rest % qn, r = rest / qn;
+  const int ih = ih_first + r;
+  tk.live = t < tasks && ih >= 0 && ih < p.H;
+  const int ihc = tk.live ? ih : 0;
+  const uint16_t* src = reinterpret_cast<const uint16_t*>(p.x) + (((int64_t)b * p.H + ihc) * p.W + 8 * q) * 64 + 8 * co;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) tk.v[j] = *reinterpret_cast<const uint4*>(src + 64 * j);
+}
+
+__device__ __forceinline__ void band_commit_nhwc(const HaloArgs& p, int r0, int t, int tasks, const BandTask& tk,
+                                                 uint16_t* halo) {
+  if (t >= tasks) return;
+  constexpr int CP = 72;
+  const int qn = p.W >> 3;
+  const int co = t & 7, rest = t >> 3, q = rest % qn, r = r0 + rest / qn;
+  const uint32_t m = tk.live ? 0xffffffffu : 0u;  // rows outside the image: zeros
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    *reinterpret_cast<uint4*>(&halo[(r * p.IW_t + 8 * q + j + 1) * CP + 8 * co]) =
+        make_uint4(tk.v[j].x & m, tk.v[j].y & m, tk.v[j].z & m, tk.v[j].w & m);
+}
+
+// NHWC output with a residual (16-bit, in y's layout): the two 8-channel
+// pieces lane l stores for a block, requested before the block's (and the
+// previous blocks') stores so that waiting for them does not wait for those
+// stores too (vmcnt counts loads and stores in issue order).  Past the last
+// pixel of the part the address is clamped (the value is not stored).
+__device__ __forceinline__ void band_res_issue_nhwc(const HaloArgs& p, int b, int px1, int mb, int ocr, int lane,
+                                                    ResPairs<8> (&rr)[2]) {
+  const int pix = min(mb * 32 + (lane & 31), px1 - 1);
+  const int64_t off = ((int64_t)b * p.OH * p.OW + pix) * p.OC + min(ocr, p.OC - 32) + 8 * (lane >> 5);
+#pragma unroll
+  for (int it = 0; it < 2; ++it) res_issue<8>(p.epi, off + 16 * it, rr[it]);
+}
+
 // One 32-pixel x 32-channel block (lane (col, g) holds channel col's pixels
 // 8j + 4g + i), after the epilogue (ReLU, the next layer's activation
 // quantization), -> wave-private LDS, channel-major, then
@@ -114,13 +162,14 @@ __device__ __forceinline__ void band_commit(const HaloArgs& p, int r0, int t, in
 //   fp16 y: 16-byte stores of 16 channels x 64 bytes (a channel's 32 pixels)
 //           per instruction, through the L2, which joins the two 64-byte
 //           halves of a line written by neighbouring blocks.
-template <int MODE>
+template <int MODE, bool NHWC>
 __device__ __forceinline__ void band_store(const HaloArgs& p, const floatx16& acc, int b, int px1, int mb, int col,
-                                           int g, int ocr, int lane, float scale, float bv, float* park) {
+                                           int g, int ocr, int lane, float scale, float bv, float* park,
+                                           const ResPairs<8> (&rr)[2]) {
   float v[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) v[i] = acc[i] * scale + bv;
-  epi_m<MODE, 16>(p.epi, nullptr, 0, false, v);
+  if constexpr (!NHWC) epi_m<MODE, 16>(p.epi, nullptr, 0, false, v);  // NHWC: per stored piece, below
 #pragma unroll
   for (int j = 0; j < 4; ++j)
     *reinterpret_cast<float4*>(park + col * kParkPitch + 8 * j + 4 * g) =
@@ -130,7 +179,52 @@ __device__ __forceinline__ void band_store(const HaloArgs& p, const floatx16& ac
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   typedef float f4v __attribute__((ext_vector_type(4)));
   const int64_t ohw = (int64_t)p.OH * p.OW;
-  if (p.y_dt == DIMQ_F32) {
+  if constexpr (NHWC) {
+    // lane l: pixel l % 32 of the block, channels 8 (l / 32) + 16 it (fp16) or
+    // 4 (l / 32) + 8 it (fp32): each pixel's 32 channels are one 64- or
+    // 128-byte run; the residual pieces were requested by band_res_issue_nhwc
+    const int px = lane & 31;
+    const int pix = mb * 32 + px;
+    const bool live = pix < px1 && ocr < p.OC;  // OC % 32 == 0 (setup)
+    const int64_t obase = ((int64_t)b * ohw + pix) * p.OC + ocr;
+    if (p.y_dt == DIMQ_F16) {
+#pragma unroll
+      for (int it = 0; it < 2; ++it) {
+        const int c8 = 8 * (lane >> 5) + 16 * it;
+        float w[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) w[j] = park[(c8 + j) * kParkPitch + px];
+        if constexpr ((MODE & kEpiRes) != 0) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const uint32_t h = (rr[it].w[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+            w[j] += p.epi.res_dt == DIMQ_F16 ? f16_bits_to_float(h) : bf16_bits_to_float(h);
+          }
+        }
+        if constexpr ((MODE & 3) == kEpiRelu) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) w[j] = w[j] < 0.0f ? 0.0f : w[j];
+        }
+        const uint4 h = make_uint4(f16x2_rne(w[0], w[1]), f16x2_rne(w[2], w[3]), f16x2_rne(w[4], w[5]),
+                                   f16x2_rne(w[6], w[7]));
+        if (live) *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p.y) + obase + c8) = h;
+      }
+    } else {  // fp32 y (no residual: setup)
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int c4 = 4 * (lane >> 5) + 8 * it;
+        float w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[j] = park[(c4 + j) * kParkPitch + px];
+        if constexpr ((MODE & 3) == kEpiRelu) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) w[j] = w[j] < 0.0f ? 0.0f : w[j];
+        }
+        // through the L2 (not non-temporal): a 128-byte line is four pieces of two lanes
+        if (live) *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.y) + obase + c4) = make_float4(w[0], w[1], w[2], w[3]);
+      }
+    }
+  } else if (p.y_dt == DIMQ_F32) {
     const int p4 = 4 * (lane & 7);
     const int pix0 = mb * 32 + p4;
 #pragma unroll
@@ -164,8 +258,9 @@ __device__ __forceinline__ void band_store(const HaloArgs& p, const floatx16& ac
 
 // Waves: wn = wave & 1 owns output channels oc0 + [32 wn, 32 wn + 32), wq =
 // wave >> 1 the blocks blk0 + wq + 4i.  KH = KW = 3, stride 1, pad 1, C = 64.
-template <int BITS, int MODE>
+template <int BITS, int MODE, bool NHWC>
 __global__ __launch_bounds__(kBandThreads, 1) void conv_band_kernel(const HaloArgs p) {
+  constexpr bool RES = NHWC && (MODE & kEpiRes) != 0;
   constexpr int T = 36, WPL = 9 * BITS, CP = 72, E = 1 << BITS;
   extern __shared__ __attribute__((aligned(16))) uint16_t halo[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, col = lane & 31, g = lane >> 5;
@@ -185,7 +280,15 @@ __global__ __launch_bounds__(kBandThreads, 1) void conv_band_kernel(const HaloAr
   // starts 1.5-2 us later.
   const int tA = bp.ra * p.W, tB = (bp.IH - bp.ra) * p.W;  // 8 * rows * W / 8
   BandTask tka, tkb;
-  band_issue(p, b, ih_first, tid, tA, tka);
+  auto issue = [&](int ih0, int tasks, BandTask& tk) {
+    if constexpr (NHWC) band_issue_nhwc(p, b, ih0, tid, tasks, tk);
+    else band_issue(p, b, ih0, tid, tasks, tk);
+  };
+  auto commit = [&](int r0, int tasks, const BandTask& tk) {
+    if constexpr (NHWC) band_commit_nhwc(p, r0, tid, tasks, tk, halo);
+    else band_commit(p, r0, tid, tasks, tk, halo);
+  };
+  issue(ih_first, tA, tka);
   CbRaw<E> cbraw;
   cb_row_issue<E>(p.cb, p.cb_dt, p.cb_rows == 1 ? 0 : min(ocl, p.OC - 1), p.cb_size, cbraw);
   const bool has_bias = p.bias && ocl < p.OC;
@@ -213,13 +316,13 @@ __global__ __launch_bounds__(kBandThreads, 1) void conv_band_kernel(const HaloAr
     for (int w = 0; w < BITS; ++w) chunk[w] = wreg[(t >> 2) * BITS + w];
     wf[t] = decode_sub<BITS>(chunk, t & 3, cbr);
   }
-  band_commit(p, 0, tid, tA, tka, halo);
+  commit(0, tA, tka);
   for (int t = tid; t < bp.IH * 16; t += kBandThreads) {  // left and right padding columns
     const int co = t & 7, side = (t >> 3) & 1, r = t >> 4;
     *reinterpret_cast<uint4*>(&halo[(r * p.IW_t + (side ? p.IW_t - 1 : 0)) * CP + 8 * co]) = make_uint4(0, 0, 0, 0);
   }
   lds_barrier();
-  band_issue(p, b, ih_first + bp.ra, tid, tB, tkb);  // in flight through round 0
+  issue(ih_first + bp.ra, tB, tkb);  // in flight through round 0
 
   const int row_step = p.IW_t * CP;
   // nq = 1 or 2 blocks (independent accumulator chains) of this wave
@@ -268,36 +371,52 @@ __global__ __launch_bounds__(kBandThreads, 1) void conv_band_kernel(const HaloAr
     }
   };
   // round 0: one block-half per wave, reading stage A only; its stores leave after stage B's commit
+  const int ocr = oc0 + 32 * wn;
+  ResPairs<8> rr[2][2];  // NHWC residual pieces of this wave's (up to two) blocks
   {
     const int mb = bp.blk0 + wq;
     floatx16 acc[2];
     if (mb < bp.blk1) {
       const int mbs[2] = {mb, mb};
       compute(1, mbs, acc);
+      if constexpr (RES) band_res_issue_nhwc(p, b, bp.px1, mb, ocr, lane, rr[0]);
     }
-    band_commit(p, bp.ra, tid, tB, tkb, halo);
+    commit(bp.ra, tB, tkb);
     lds_barrier();
-    if (mb < bp.blk1) band_store<MODE>(p, acc[0], b, bp.px1, mb, col, g, oc0 + 32 * wn, lane, scale, bv, park);
+    if (mb < bp.blk1) band_store<MODE, NHWC>(p, acc[0], b, bp.px1, mb, col, g, ocr, lane, scale, bv, park, rr[0]);
   }
   for (int mb = bp.blk0 + wq + kBandBlocksPerRound; mb < bp.blk1; mb += 2 * kBandBlocksPerRound) {
     const bool two = mb + kBandBlocksPerRound < bp.blk1;
     const int mbs[2] = {mb, mb + kBandBlocksPerRound};
     floatx16 acc[2];
     compute(two ? 2 : 1, mbs, acc);
-    band_store<MODE>(p, acc[0], b, bp.px1, mb, col, g, oc0 + 32 * wn, lane, scale, bv, park);
-    if (two) band_store<MODE>(p, acc[1], b, bp.px1, mb + kBandBlocksPerRound, col, g, oc0 + 32 * wn, lane, scale, bv,
-                              park);
+    if constexpr (RES) {
+      band_res_issue_nhwc(p, b, bp.px1, mb, ocr, lane, rr[0]);
+      if (two) band_res_issue_nhwc(p, b, bp.px1, mb + kBandBlocksPerRound, ocr, lane, rr[1]);
+    }
+    band_store<MODE, NHWC>(p, acc[0], b, bp.px1, mb, col, g, ocr, lane, scale, bv, park, rr[0]);
+    if (two)
+      band_store<MODE, NHWC>(p, acc[1], b, bp.px1, mb + kBandBlocksPerRound, col, g, ocr, lane, scale, bv, park, rr[1]);
   }
 }
 
 template <int BITS>
 int launch_band_bits(const HaloArgs& p, int mode, hipStream_t s) {
-  auto k = conv_band_kernel<BITS, kEpiNone>;
-  switch (mode) {
-    case kEpiRelu: k = conv_band_kernel<BITS, kEpiRelu>; break;
-    case kEpiQuant: k = conv_band_kernel<BITS, kEpiQuant>; break;
-    case kEpiRelu | kEpiQuant: k = conv_band_kernel<BITS, kEpiRelu | kEpiQuant>; break;
-    default: break;
+  auto k = conv_band_kernel<BITS, kEpiNone, false>;
+  if (p.x_layout == DIMQ_NHWC) {
+    switch (mode) {
+      case kEpiRelu: k = conv_band_kernel<BITS, kEpiRelu, true>; break;
+      case kEpiRes: k = conv_band_kernel<BITS, kEpiRes, true>; break;
+      case kEpiResRelu: k = conv_band_kernel<BITS, kEpiResRelu, true>; break;
+      default: k = conv_band_kernel<BITS, kEpiNone, true>; break;
+    }
+  } else {
+    switch (mode) {
+      case kEpiRelu: k = conv_band_kernel<BITS, kEpiRelu, false>; break;
+      case kEpiQuant: k = conv_band_kernel<BITS, kEpiQuant, false>; break;
+      case kEpiRelu | kEpiQuant: k = conv_band_kernel<BITS, kEpiRelu | kEpiQuant, false>; break;
+      default: break;
+    }
   }
   const size_t lds = (size_t)p.IH_t * p.IW_t * 72 * sizeof(uint16_t) + (size_t)8 * kParkFloats * sizeof(float);
   const hipError_t e =

@@ -64,18 +64,30 @@ __global__ void prepare_kernel(const uint8_t* __restrict__ src, int OC, int C, i
 
 }  // namespace
 
-// Band kernel (conv_band.h) for a halo call: NCHW in and fp32 or fp16 NCHW
-// out (fp16: OH*OW % 8 == 0), C = 64, 3x3, stride 1, pad 1, epilogue none /
-// ReLU, either with the next layer's activation quantization (fp16 out).  Picks the parts per image (about one work-group
-// per CU, at most 13 blocks of 32 pixels per part) and checks that every
-// part's stages fit one task per thread and its halo fits in LDS; fills
-// p.parts, p.nblk, p.IH_t, p.IW_t.  False: the call takes the tile kernels.
+// Band kernel (conv_band.h) for a halo call: C = 64, 3x3, stride 1, pad 1,
+// fp32 or fp16 output, and either
+//   NCHW in and out (fp16: OH*OW % 8 == 0), epilogue none / ReLU, either with
+//   the next layer's activation quantization (fp16 out), or
+//   NHWC in and out (OC % 32 == 0), epilogue none / ReLU, or a 16-bit
+//   16-byte aligned residual (+ ReLU) with an fp16 output.
+// Picks the parts per image (about one work-group per CU, at most 13 blocks
+// of 32 pixels per part) and checks that every part's stages fit one task per
+// thread and its halo fits in LDS; fills p.parts, p.nblk, p.IH_t, p.IW_t.
+// False: the call takes the tile kernels.
 static bool band_setup(HaloArgs& p, int stride, int mode) {
-  if (p.x_layout != DIMQ_NCHW || p.y_layout != DIMQ_NCHW || !(p.y_dt == DIMQ_F32 || p.y_dt == DIMQ_F16)) return false;
+  if (!(p.y_dt == DIMQ_F32 || p.y_dt == DIMQ_F16)) return false;
   if (p.C != 64 || p.KH != 3 || p.KW != 3 || stride != 1 || p.pad_h != 1 || p.pad_w != 1) return false;
-  if (!(mode == kEpiNone || mode == kEpiRelu || mode == kEpiQuant || mode == (kEpiRelu | kEpiQuant))) return false;
-  if ((mode & kEpiQuant) != 0 && p.y_dt != DIMQ_F16) return false;
-  if (p.y_dt == DIMQ_F16 && ((int64_t)p.OH * p.OW) % 8 != 0) return false;  // 16-byte fp16 stores of 8 pixels
+  if (p.x_layout == DIMQ_NHWC) {
+    if (p.y_layout != DIMQ_NHWC || p.OC % 32 != 0) return false;
+    const bool res16 = p.epi.res_vec && (p.epi.res_dt == DIMQ_F16 || p.epi.res_dt == DIMQ_BF16) &&
+                       p.y_dt == DIMQ_F16;
+    if (!(mode == kEpiNone || mode == kEpiRelu || ((mode == kEpiRes || mode == kEpiResRelu) && res16))) return false;
+  } else {
+    if (p.x_layout != DIMQ_NCHW || p.y_layout != DIMQ_NCHW) return false;
+    if (!(mode == kEpiNone || mode == kEpiRelu || mode == kEpiQuant || mode == (kEpiRelu | kEpiQuant))) return false;
+    if ((mode & kEpiQuant) != 0 && p.y_dt != DIMQ_F16) return false;
+    if (p.y_dt == DIMQ_F16 && ((int64_t)p.OH * p.OW) % 8 != 0) return false;  // 16-byte fp16 stores of 8 pixels
+  }
   if (p.W % 8 != 0 || p.OW != p.W || p.OH != p.H || ((int64_t)p.OH * p.OW) % 4 != 0) return false;
   if (!aligned(p.y, 16)) return false;
   const int64_t npx = (int64_t)p.OH * p.OW;

@@ -839,27 +839,41 @@ def test_conv2d_halo_prepared_vs_oracle(gpu, case, layout):
     dict(B=16, H=28, W=32, OC=128, bits=4, act=None, bias=False, pc=True, out=torch.float32),  # 2 channel blocks
     dict(B=8, H=56, W=56, OC=64, bits=2, act="relu", bias=True, pc=True, out=torch.float16),   # fp16 output
     dict(B=3, H=7, W=8, OC=96, bits=3, act=None, bias=True, pc=False, out=torch.float16),      # fp16, partial block
+    # NHWC only (ResNet-18 layer1's second conv): a 16-bit residual, then ReLU
+    dict(B=4, H=56, W=56, OC=64, bits=2, act="relu", bias=True, pc=True, out=torch.float16, res=True),
+    dict(B=3, H=7, W=8, OC=96, bits=3, act=None, bias=True, pc=False, out=torch.float16, res=True),
 ])
-def test_conv2d_band_kernel(gpu, case):
-    """NCHW fp16 3x3 stride-1 C 64 convs with fp32 or fp16 NCHW output (the band kernel: runs of 32-pixel
-    blocks per work-group, two-stage halo, stores through a wave-private LDS transpose) against the oracle,
-    with bias / ReLU, partial blocks, channel tails, 2/3/4-bit, per-layer and per-channel codebooks."""
+@pytest.mark.parametrize("layout", ["nchw", "nhwc"])
+def test_conv2d_band_kernel(gpu, case, layout):
+    """fp16 3x3 stride-1 C 64 convs with fp32 or fp16 output in the input's layout (the band kernel: runs of
+    32-pixel blocks per work-group, two-stage halo, stores through a wave-private LDS area; NCHW input
+    transposed into the pixel-major halo, NHWC input copied as it is) against the oracle, with bias / ReLU,
+    NHWC residuals, partial blocks, channel tails, 2/3/4-bit, per-layer and per-channel codebooks."""
     ops = _ops()
-    announce(f"conv band {case}")
+    if case.get("res") and layout == "nchw":
+        pytest.skip("the residual cases are NHWC (ResNet's layout); NCHW residuals take the halo tiles")
+    announce(f"conv band {case} {layout}")
     g = _gen(case["H"] * 7 + case["W"] + case["OC"] + case["bits"])
     shape = (case["OC"], 64, 3, 3)
     x = torch.relu(torch.randn(case["B"], 64, case["H"], case["W"], generator=g)).half()
     cb, idx, packed = _codebook_case(case["OC"], 576, case["bits"], case["pc"], g)
     bias = torch.randn(case["OC"], generator=g) * 0.1 if case["bias"] else None
+    res = (torch.randn(case["B"], case["OC"], case["H"], case["W"], generator=g) * 0.5).half() if case.get("res") \
+        else None
+    fmt = torch.channels_last if layout == "nhwc" else torch.contiguous_format
     pd = packed.to(gpu)
     prep = ops.prepare_conv_weight(pd, case["bits"], shape)
-    y = ops.dimq_conv2d_codebook(x.to(gpu), pd, cb.to(gpu), case["bits"], None if bias is None else bias.to(gpu),
-                                 shape, (1, 1), (1, 1), (1, 1), 1, out_dtype=case["out"], prepared_weight=prep,
-                                 activation=case["act"])
+    y = ops.dimq_conv2d_codebook(x.to(gpu).to(memory_format=fmt), pd, cb.to(gpu), case["bits"],
+                                 None if bias is None else bias.to(gpu), shape, (1, 1), (1, 1), (1, 1), 1,
+                                 out_dtype=case["out"], prepared_weight=prep, activation=case["act"],
+                                 residual=None if res is None else res.to(gpu).to(memory_format=fmt))
     ref = oracle.conv2d_dequant_reference(x.float(), packed, case["bits"], cb, shape, bias, 1, 1, 1, 1)
+    if res is not None:
+        ref = ref + res.float()
     if case["act"] == "relu":
         ref = torch.relu(ref)
     assert y.shape == ref.shape and y.dtype == case["out"]
+    assert y.is_contiguous(memory_format=fmt)
     tol = out_tol(case["out"])
     assert oracle.rel_err(y.float(), ref) <= tol, oracle.rel_err(y.float(), ref)
 

@@ -112,14 +112,70 @@ __device__ __forceinline__ uint4 stem_load_pair(const StemArgs& p, int b, int ih
   return make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
 }
 
-// Index `flat` of the LSB-first packed stream.
-__device__ __forceinline__ int stem_index(const StemArgs& p, int64_t flat) {
-  const int64_t bit = flat * p.bits;
-  const int64_t byte = bit >> 3;
-  const int sh = static_cast<int>(bit & 7);
-  uint32_t v = p.w[byte];
-  if (sh + p.bits > 8 && byte + 1 < p.w_bytes) v |= static_cast<uint32_t>(p.w[byte + 1]) << 8;
-  return static_cast<int>((v >> sh) & ((1u << p.bits) - 1u));
+// Staging of NHWC input with C in {3, 4}, W and padc even (the ResNet stem):
+// every pair lies wholly inside a row or wholly in the padding, and is one
+// 12- or 16-byte load, so kStemPairs of a thread's pairs are requested
+// without a branch, in one round trip, before any is written to LDS; `live`
+// has bit u set for pair u inside the image (outside pairs re-read pixel 0 and
+// are written as zeros). A whole band per thread at once (10 pairs), or
+// holding it through the previous band's MFMAs, needs more VGPRs than the 7x7
+// kernel has left at two waves per SIMD beside its weight fragments (it spills
+// 7 and 84).
+constexpr int kStemPairs = 5;
+struct StemStage {
+  uint4 v[kStemPairs];
+  uint32_t live;
+};
+
+__device__ __forceinline__ bool stem_fast_nhwc(const StemArgs& p) {
+  return p.x_layout == DIMQ_NHWC && (p.C == 3 || p.C == 4) && p.W % 2 == 0 && p.padc % 2 == 0;
+}
+
+// Pairs base + u * kStemThreads, u < kStemPairs, of the band at (b, ih0).
+__device__ __forceinline__ void stem_issue_band(const StemArgs& p, int b, int ih0, int base, int units, StemStage& st) {
+  st.live = 0u;
+#pragma unroll
+  for (int u = 0; u < kStemPairs; ++u) {
+    const int i = base + u * kStemThreads;
+    const int r = i / p.npairs;
+    const int j = i - r * p.npairs;
+    const int ih = ih0 + r, iw0 = 2 * j - p.padc;
+    const bool live = i < units && ih >= 0 && ih < p.H && iw0 >= 0 && iw0 < p.W;
+    const int64_t pix = live ? ((int64_t)b * p.H + ih) * p.W + iw0 : 0;
+    const uint16_t* src = reinterpret_cast<const uint16_t*>(p.x) + pix * p.C;
+    if (p.C == 4) {
+      st.v[u] = *reinterpret_cast<const uint4*>(src);
+    } else {
+      const uint3 t = *reinterpret_cast<const uint3*>(src);
+      st.v[u] = make_uint4(t.x, t.y, t.z, 0u);
+    }
+    st.live |= live ? (1u << u) : 0u;
+  }
+}
+
+__device__ __forceinline__ void stem_commit_band(int base, int units, const StemStage& st, uint4* xs) {
+#pragma unroll
+  for (int u = 0; u < kStemPairs; ++u) {
+    const int i = base + u * kStemThreads;
+    if (i >= units) break;
+    const uint32_t m = (st.live >> u) & 1u ? 0xffffffffu : 0u;
+    xs[i] = make_uint4(st.v[u].x & m, st.v[u].y & m, st.v[u].z & m, st.v[u].w & m);
+  }
+}
+
+// The two stream bytes holding index `flat` of the LSB-first packed stream
+// (the second clamped to the stream), loaded without a branch so that a
+// thread's loads all go out before the first is used; stem_index_of decodes.
+// (32-bit arithmetic: a stem's OC x C x KH x KW x bits is far below 2^31.)
+__device__ __forceinline__ uint32_t stem_index_bytes(const StemArgs& p, int flat) {
+  const int byte = (flat * p.bits) >> 3;
+  const int next = byte + 1 < p.w_bytes ? byte + 1 : byte;
+  return static_cast<uint32_t>(p.w[byte]) | (static_cast<uint32_t>(p.w[next]) << 8);
+}
+
+__device__ __forceinline__ int stem_index_of(const StemArgs& p, int flat, uint32_t bytes) {
+  const int sh = (flat * p.bits) & 7;
+  return static_cast<int>((bytes >> sh) & ((1u << p.bits) - 1u));
 }
 
 template <int KH, int NP, int MODE>
@@ -147,24 +203,69 @@ __global__ __launch_bounds__(kStemThreads, 2) void conv_stem_kernel(const StemAr
     const int oc = item / NP;
     const int o = item - oc * NP;
     const bool ocv = oc < p.OC;
-    const int64_t row = (p.cb_rows == 1) ? 0 : oc;
-    float v[KH][8];
-    float mx = 0.0f;
+    const int row = (p.cb_rows == 1) ? 0 : oc;
+    // every index's stream bytes, then every codebook entry, each set issued
+    // before any of it is used (taps outside the kernel read index 0 and are
+    // zeroed by a select): a branch around each load made the weight decode
+    // a chain of KH x 8 dependent round trips (~20 us per work-group at the
+    // ResNet stem)
+    int flat[KH][8];
+    bool tap[KH][8];
+    uint32_t ib[KH][8];
 #pragma unroll
     for (int kh = 0; kh < KH; ++kh) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        v[kh][e] = 0.0f;
         const int px = e >= p.C ? 1 : 0;
         const int c = e - px * p.C;
         const int kw = 2 * o + px - p.par;
-        if (ocv && e < 2 * p.C && kw >= 0 && kw < p.KW) {
-          const int idx = stem_index(p, (((int64_t)oc * p.C + c) * KH + kh) * p.KW + kw);
-          if (idx < p.cb_size) v[kh][e] = load_as_float(p.cb, p.cb_dt, row * p.cb_size + idx);
-        }
-        mx = fmaxf(mx, fabsf(v[kh][e]));
+        tap[kh][e] = ocv && e < 2 * p.C && kw >= 0 && kw < p.KW;
+        flat[kh][e] = tap[kh][e] ? ((oc * p.C + c) * KH + kh) * p.KW + kw : 0;
+        ib[kh][e] = stem_index_bytes(p, flat[kh][e]);
       }
     }
+    int idx[KH][8];
+#pragma unroll
+    for (int kh = 0; kh < KH; ++kh)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int i = stem_index_of(p, flat[kh][e], ib[kh][e]);
+        tap[kh][e] = tap[kh][e] && i < p.cb_size;
+        idx[kh][e] = tap[kh][e] ? i : 0;
+      }
+    float v[KH][8];
+    if (p.cb_dt == DIMQ_F32) {
+      const float* cbf = reinterpret_cast<const float*>(p.cb) + row * p.cb_size;
+#pragma unroll
+      for (int kh = 0; kh < KH; ++kh)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[kh][e] = cbf[idx[kh][e]];
+    } else if (p.cb_dt == DIMQ_F16 || p.cb_dt == DIMQ_BF16) {
+      const uint16_t* cbh = reinterpret_cast<const uint16_t*>(p.cb) + row * p.cb_size;
+      uint32_t h[KH][8];
+#pragma unroll
+      for (int kh = 0; kh < KH; ++kh)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h[kh][e] = cbh[idx[kh][e]];
+#pragma unroll
+      for (int kh = 0; kh < KH; ++kh)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          v[kh][e] = p.cb_dt == DIMQ_F16 ? f16_bits_to_float(h[kh][e]) : bf16_bits_to_float(h[kh][e]);
+    } else {
+#pragma unroll
+      for (int kh = 0; kh < KH; ++kh)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[kh][e] = load_as_float(p.cb, p.cb_dt, row * p.cb_size + idx[kh][e]);
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int kh = 0; kh < KH; ++kh)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v[kh][e] = tap[kh][e] ? v[kh][e] : 0.0f;
+        mx = fmaxf(mx, fabsf(v[kh][e]));
+      }
     // the NP threads of one channel are NP consecutive lanes of one wave
 #pragma unroll
     for (int d = 1; d < NP; d <<= 1) mx = fmaxf(mx, __shfl_xor(mx, d, 64));
@@ -209,30 +310,40 @@ __global__ __launch_bounds__(kStemThreads, 2) void conv_stem_kernel(const StemAr
   const int64_t ohw = (int64_t)p.OH * p.OW;
   const bool vec_nchw = (ohw % 8 == 0) && (p.OW % 8 == 0 || p.TH * p.OW % 8 == 0);
 
+  const bool fast = stem_fast_nhwc(p);
   for (int band = xcd * p.per_xcd + local; band < band_end; band += gx) {
     const int b = band / p.bands_h;
     const int oh0 = (band - b * p.bands_h) * p.TH;
     const int ih0 = 2 * oh0 - p.pad_h;
-    // stage IR rows x npairs pairs, four loads in flight per thread
-    for (int base = tid; base < xs_units; base += 4 * kStemThreads) {
-      uint4 v[4];
+    if (fast) {
+      for (int base = tid; base < xs_units; base += kStemPairs * kStemThreads) {
+        StemStage stage;
+        stem_issue_band(p, b, ih0, base, xs_units, stage);
+        stem_commit_band(base, xs_units, stage, xs);
+      }
+      __syncthreads();
+    } else {
+      // stage IR rows x npairs pairs, four loads in flight per thread
+      for (int base = tid; base < xs_units; base += 4 * kStemThreads) {
+        uint4 v[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int i = base + u * kStemThreads;
-        v[u] = make_uint4(0u, 0u, 0u, 0u);
-        if (i < xs_units) {
-          const int r = i / p.npairs;
-          const int j = i - r * p.npairs;
-          v[u] = stem_load_pair(p, b, ih0 + r, 2 * j - p.padc);
+        for (int u = 0; u < 4; ++u) {
+          const int i = base + u * kStemThreads;
+          v[u] = make_uint4(0u, 0u, 0u, 0u);
+          if (i < xs_units) {
+            const int r = i / p.npairs;
+            const int j = i - r * p.npairs;
+            v[u] = stem_load_pair(p, b, ih0 + r, 2 * j - p.padc);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int i = base + u * kStemThreads;
+          if (i < xs_units) xs[i] = v[u];
         }
       }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int i = base + u * kStemThreads;
-        if (i < xs_units) xs[i] = v[u];
-      }
+      __syncthreads();
     }
-    __syncthreads();
 
     const int P = min(p.TH, p.OH - oh0) * p.OW;
     const int nblk = (P + 31) / 32;

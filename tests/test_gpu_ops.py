@@ -723,6 +723,7 @@ def test_conv2d_prepared_variants_agree(gpu, variant):
     dict(B=3, C=3, H=37, W=37, OC=32, K=7, p=3, bits=4, dt=torch.bfloat16, out=torch.float32, pc=True),   # W*C odd
     dict(B=2, C=4, H=40, W=34, OC=64, K=7, p=2, bits=3, dt=torch.float16, out=torch.bfloat16, pc=True),   # even pad
     dict(B=2, C=3, H=50, W=50, OC=24, K=3, p=1, bits=2, dt=torch.float16, out=torch.float16, pc=True),    # 3x3/2 stem
+    dict(B=2, C=3, H=33, W=35, OC=32, K=7, p=3, bits=4, dt=torch.float16, out=torch.float16, pc=True),    # odd W
     dict(B=1, C=1, H=31, W=29, OC=16, K=3, p=0, bits=8, dt=torch.float32, out=torch.float32, pc=True),    # fp32 input
     dict(B=2, C=2, H=20, W=18, OC=40, K=7, p=3, bits=8, dt=torch.float16, out=torch.float16, pc=True, cbn=200),
 ])

@@ -214,7 +214,7 @@ __global__ __launch_bounds__(256) void gemv_reduce_kernel(const GemmArgs p, int 
 // the whole k range without the 128 KB of staged fp16 rows per work-group
 // that M = 16 costs the staged kernel, and the split-k partial sums and their
 // second launch go away: each lane loads its A fragments (8 consecutive x of
-// row lane % 16) straight from global memory, one 32-index chunk ahead.
+// row lane % 16) straight from global memory, two 32-index chunks ahead.
 // Work-group = 4 waves on 16 columns; wave w takes the k quarter w, lane
 // (col, g) the run of R = K / 16 indices 4w + g of its column; the four waves'
 // 16 x 16 partial tiles are added through LDS.  Measured at cfg5 M = 16 (X
@@ -320,9 +320,17 @@ __global__ __launch_bounds__(256) void gemv_direct_kernel(const GemmArgs p) {
   const bool live = col < p.M;  // A row col; rows >= M are zero (and load row 0)
   const uint4* xa =
       reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p.x) + (live ? col : 0) * p.ldx + k0);
-  uint4 xr[2][4];
+  // Activation chunks held: the chunk computed and the next two in flight
+  // (cfg5 M = 16, same process: 8.51 us one ahead, 8.35 two, 8.42 three,
+  // 8.69 four; a chunk's ~550 cycles of decode and MFMAs are shorter than its
+  // activations' load latency).
+  constexpr int XD = 3;
+  uint4 xr[XD][4];
+  // the first chunks' activations, before the codebook's wait
 #pragma unroll
-  for (int s = 0; s < 4; ++s) xr[0][s] = xa[s];  // the first chunk's activations, before the codebook's wait
+  for (int j = 0; j < XD - 1 && j < CH; ++j)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) xr[j][s] = xa[4 * j + s];
   float cbv[E];
   cb_row_finish<E>(cbraw, p.cb_dt, p.cb_size, cbv);
   CodebookRegs<BITS> ch, cl;
@@ -339,9 +347,9 @@ __global__ __launch_bounds__(256) void gemv_direct_kernel(const GemmArgs p) {
   floatx4 acc = floatx4{0.0f, 0.0f, 0.0f, 0.0f}, acc2 = acc;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    if (c + 1 < CH) {
+    if (c + XD - 1 < CH) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) xr[(c + 1) & 1][s] = xa[4 * (c + 1) + s];
+      for (int s = 0; s < 4; ++s) xr[(c + XD - 1) % XD][s] = xa[4 * (c + XD - 1) + s];
     }
     uint32_t chunk[BITS];
 #pragma unroll
@@ -350,7 +358,7 @@ __global__ __launch_bounds__(256) void gemv_direct_kernel(const GemmArgs p) {
     for (int s = 0; s < 4; ++s) {
       bf16x8 wh, wl;
       decode_hilo<BITS>(chunk_word<BITS>(chunk, s), ch, cl, wh, wl);
-      const uint4 xv = live ? a_slots<BITS>(xr[c & 1], s) : make_uint4(0, 0, 0, 0);
+      const uint4 xv = live ? a_slots<BITS>(xr[c % XD], s) : make_uint4(0, 0, 0, 0);
       const bf16x8 a = __builtin_bit_cast(bf16x8, xv);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, wh, acc, 0, 0, 0);
       acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, wl, acc2, 0, 0, 0);

@@ -362,10 +362,32 @@ __global__ __launch_bounds__(64 * WGM * WGN, big_min_waves(BITS, MBLK, NBLK, CON
   // writes them as one 16-byte store (two 8-byte stores per lane before).
   const bool vec = p.ldy % 4 == 0 && p.y_dt != DIMQ_F64;
   const bool vec8 = p.ldy % 8 == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0 && p.y_dt != DIMQ_F64;
+  // 16-bit residuals of row group gi = 2 nb + jp, requested one group ahead
+  // of its stores (two register sets; a whole-tile prefetch would cost this
+  // kernel an occupancy step), so each group's loads land during the
+  // previous group's stores: requested right before their own stores, their
+  // latency added to every group (ResNet-18 bs128, the residual layers)
+  const bool rpair = (MODE & kEpiRes) && res_pairs(p.epi, vec8);
+  ResPairs<8> rbuf[2][MBLK];
+  auto res_group = [&](int gi, ResPairs<8> (&rr)[MBLK]) {
+    const int64_t n8 = n0 + wn * NBLK * 32 + (gi >> 1) * 32 + 16 * (gi & 1) + 8 * g;
+#pragma unroll
+    for (int mb = 0; mb < MBLK; ++mb) {
+      const int64_t m = m0 + wm * MBLK * 32 + mb * 32 + col;
+      if (m < p.M && n8 + 8 <= p.N) res_issue<8>(p.epi, m * p.ldy + n8, rr[mb]);
+    }
+  };
+  if constexpr ((MODE & kEpiRes) != 0) {
+    if (rpair) res_group(0, rbuf[0]);
+  }
   static_for<NBLK>([&](auto nbc) {
     constexpr int nb = decltype(nbc)::value;
 #pragma unroll
     for (int jp = 0; jp < 2; ++jp) {
+      const int gi = 2 * nb + jp;
+      if constexpr ((MODE & kEpiRes) != 0) {
+        if (rpair && gi + 1 < 2 * NBLK) res_group(gi + 1, rbuf[(gi + 1) & 1]);
+      }
       float sc[2][4], bv[2][4];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
@@ -377,16 +399,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, big_min_waves(BITS, MBLK, NBLK, CON
         }
       }
       const int64_t n8 = n0 + wn * NBLK * 32 + nb * 32 + 16 * jp + 8 * g;  // this lane's 8 columns
-      // 16-bit residuals of this row group: loads out before its stores (a
-      // whole-tile prefetch would cost this kernel an occupancy step)
-      ResPairs<8> rr[MBLK];
-      if ((MODE & kEpiRes) && res_pairs(p.epi, vec8)) {
-#pragma unroll
-        for (int mb = 0; mb < MBLK; ++mb) {
-          const int64_t m = m0 + wm * MBLK * 32 + mb * 32 + col;
-          if (m < p.M && n8 + 8 <= p.N) res_issue<8>(p.epi, m * p.ldy + n8, rr[mb]);
-        }
-      }
+      ResPairs<8>(&rr)[MBLK] = rbuf[gi & 1];
 #pragma unroll
       for (int mb = 0; mb < MBLK; ++mb) {
         const int64_t m = m0 + wm * MBLK * 32 + mb * 32 + col;

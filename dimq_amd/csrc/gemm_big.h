@@ -152,6 +152,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, big_min_waves(BITS, MBLK, NBLK, CON
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kBigLDA];
   __shared__ float cbs[BN * E];
   __shared__ float ebias[BN];  // the tile's bias, staged once (the epilogue's loads would serialise)
+  __shared__ float escale[BN];  // the tile's column factors acc_scale 2^-e (parked epilogue)
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -173,11 +174,14 @@ __global__ __launch_bounds__(64 * WGM * WGN, big_min_waves(BITS, MBLK, NBLK, CON
   int64_t brow[NBLK];
 #pragma unroll
   for (int nb = 0; nb < NBLK; ++nb) {
-    const int nl = wn * NBLK * 32 + nb * 32 + col;
+    // column block nb of wave column wn: tile columns (nb WGN + wn) 32 ..,
+    // so that the epilogue's pass nb covers WGN * 32 contiguous columns
+    const int nl = (nb * WGN + wn) * 32 + col;
     brow[nb] = n0 + nl < p.N ? n0 + nl : p.N - 1;
     const int rl = (p.cb_rows == 1) ? 0 : nl;
     const int e = planes_from_lds<BITS, false>(cbs + rl * E, cb[nb], cb[nb]);
     rscale[nb] = ldexpf(p.acc_scale, -e);
+    if (g == 0) escale[nl] = rscale[nb];
   }
 
   // activation tasks: (row m, 16-wide group kg) per thread, 4 groups per row
@@ -355,115 +359,224 @@ __global__ __launch_bounds__(64 * WGM * WGN, big_min_waves(BITS, MBLK, NBLK, CON
     }
   }
 
-  // epilogue: acc[mb][nb][4j + i] = y[m][n], m = block row m0 + wm*MBLK*32 +
-  // mb*32 + col, n = n0 + wn*NBLK*32 + nb*32 + 8j + 4g + i.  For j = 2 jp and
-  // 2 jp + 1 the lanes l and l + 32 (g 0 and 1, same row) swap four finished
-  // values, so lane g holds the 8 columns 16 jp + 8 g .. + 7 of its row and
-  // writes them as one 16-byte store (two 8-byte stores per lane before).
-  const bool vec = p.ldy % 4 == 0 && p.y_dt != DIMQ_F64;
-  const bool vec8 = p.ldy % 8 == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0 && p.y_dt != DIMQ_F64;
-  // 16-bit residuals of row group gi = 2 nb + jp, requested one group ahead
-  // of its stores (two register sets; a whole-tile prefetch would cost this
-  // kernel an occupancy step), so each group's loads land during the
-  // previous group's stores: requested right before their own stores, their
-  // latency added to every group (ResNet-18 bs128, the residual layers)
-  const bool rpair = (MODE & kEpiRes) && res_pairs(p.epi, vec8);
-  ResPairs<8> rbuf[2][MBLK];
-  auto res_group = [&](int gi, ResPairs<8> (&rr)[MBLK]) {
-    const int64_t n8 = n0 + wn * NBLK * 32 + (gi >> 1) * 32 + 16 * (gi & 1) + 8 * g;
+  // Parked epilogue where a pass of WGN * 32 columns fits in the activation
+  // buffers; otherwise (64 x 128 tiles) stores straight from the accumulators.
+  constexpr bool kParked = BM * (WGN * 32 + 4) * 4 <= 2 * BM * kBigLDA * 2;
+  if constexpr (kParked) {
+    // Epilogue through LDS, in NBLK passes: pass nb parks every wave's column
+    // block nb (acc[mb][nb][4j + i] = tile row wm*MBLK*32 + mb*32 + col, tile
+    // column (nb WGN + wn) 32 + 8j + 4g + i) as fp32 in the activation
+    // buffers, then the work-group stores the pass's WGN * 32 contiguous
+    // columns as 8-column chunks: 8 consecutive lanes write a row's whole run
+    // (128 bytes of fp16 at WGN 2), stored non-temporally.  Stored straight
+    // from the accumulators, each instruction wrote 32-byte pieces of 32 rows
+    // (ResNet-18 3x3 convs at bs128, same process: layer2 57.8 -> 54.9 us,
+    // with the residual 64.2 -> 58.4; layer3 53.2 -> 50.3, 55.1 -> 52.4; the
+    // parked layout with ordinary stores took about half of those gains).
+    // 16-bit residuals: pass 0's requested before the first park, pass nb + 1's
+    // before pass nb's stores.
+    constexpr int PW = WGN * 32;          // columns per pass
+    constexpr int OTP = PW + 4;           // fp32 row pitch of the parked pass
+    static_assert(BM * OTP * 4 <= 2 * BM * kBigLDA * 2, "a parked pass fits in the activation buffers");
+    constexpr int CH = BM * PW / 8;       // 8-column chunks per pass
+    constexpr int CPT = (CH + NT - 1) / NT;  // chunks per thread
+    static_assert(NT % (PW / 8) == 0, "a thread's chunks share one column group");
+    float* ot = reinterpret_cast<float*>(&As[0][0]);
+    const bool vec8 = p.ldy % 8 == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0 && p.y_dt != DIMQ_F64;
+    const int qg = tid % (PW / 8);  // this thread's 8-column group of every pass
+    const bool rpair = (MODE & kEpiRes) && res_pairs(p.epi, vec8);
+    auto res_load = [&](int nb, ResPairs<8> (&rr)[CPT]) {
 #pragma unroll
-    for (int mb = 0; mb < MBLK; ++mb) {
-      const int64_t m = m0 + wm * MBLK * 32 + mb * 32 + col;
-      if (m < p.M && n8 + 8 <= p.N) res_issue<8>(p.epi, m * p.ldy + n8, rr[mb]);
-    }
-  };
-  if constexpr ((MODE & kEpiRes) != 0) {
-    if (rpair) res_group(0, rbuf[0]);
-  }
-  static_for<NBLK>([&](auto nbc) {
-    constexpr int nb = decltype(nbc)::value;
-#pragma unroll
-    for (int jp = 0; jp < 2; ++jp) {
-      const int gi = 2 * nb + jp;
-      if constexpr ((MODE & kEpiRes) != 0) {
-        if (rpair && gi + 1 < 2 * NBLK) res_group(gi + 1, rbuf[(gi + 1) & 1]);
+      for (int u = 0; u < CPT; ++u) {
+        const int c = tid + u * NT;
+        const int64_t m = m0 + c / (PW / 8);
+        const int64_t n = n0 + nb * PW + 8 * qg;
+        if (c < CH && m < p.M && n + 8 <= p.N) res_issue<8>(p.epi, m * p.ldy + n, rr[u]);
       }
-      float sc[2][4], bv[2][4];
+    };
+    ResPairs<8> rr[CPT], rn[CPT];
+    if constexpr ((MODE & kEpiRes) != 0) {
+      if (rpair) res_load(0, rr);
+    }
+    __syncthreads();  // every wave is done reading the activation buffers
+    static_for<NBLK>([&](auto nbc) {
+      constexpr int nb = decltype(nbc)::value;
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int nl = 8 * (2 * jp + h) + 4 * g;
+      for (int mb = 0; mb < MBLK; ++mb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          sc[h][i] = __shfl(rscale[nb], nl + i, 32);
-          bv[h][i] = ebias[wn * NBLK * 32 + nb * 32 + nl + i];
+        for (int j = 0; j < 4; ++j)
+          *reinterpret_cast<float4*>(ot + (wm * MBLK * 32 + mb * 32 + col) * OTP + wn * 32 + 8 * j + 4 * g) =
+              make_float4(acc[mb][nb][4 * j], acc[mb][nb][4 * j + 1], acc[mb][nb][4 * j + 2], acc[mb][nb][4 * j + 3]);
+      __syncthreads();
+      if constexpr ((MODE & kEpiRes) != 0) {
+        if (rpair && nb + 1 < NBLK) res_load(nb + 1, rn);
+      }
+      const int nlg = nb * PW + 8 * qg;  // tile column of this thread's chunks
+      const float4 s0 = reinterpret_cast<const float4*>(escale)[nlg / 4];
+      const float4 s1 = reinterpret_cast<const float4*>(escale)[nlg / 4 + 1];
+      const float4 b0 = reinterpret_cast<const float4*>(ebias)[nlg / 4];
+      const float4 b1 = reinterpret_cast<const float4*>(ebias)[nlg / 4 + 1];
+      float v[CPT][8];
+#pragma unroll
+      for (int u = 0; u < CPT; ++u) {
+        const int r = (tid + u * NT < CH ? tid + u * NT : CH - 1) / (PW / 8);
+        const float4* a4 = reinterpret_cast<const float4*>(ot + r * OTP) + 2 * qg;
+        const float4 a0 = a4[0], a1 = a4[1];
+        v[u][0] = a0.x * s0.x + b0.x; v[u][1] = a0.y * s0.y + b0.y;
+        v[u][2] = a0.z * s0.z + b0.z; v[u][3] = a0.w * s0.w + b0.w;
+        v[u][4] = a1.x * s1.x + b1.x; v[u][5] = a1.y * s1.y + b1.y;
+        v[u][6] = a1.z * s1.z + b1.z; v[u][7] = a1.w * s1.w + b1.w;
+      }
+      typedef float f4v __attribute__((ext_vector_type(4)));
+#pragma unroll
+      for (int u = 0; u < CPT; ++u) {
+        const int c = tid + u * NT;
+        if (CH % NT != 0 && c >= CH) break;
+        const int64_t m = m0 + c / (PW / 8);
+        const int64_t n = n0 + nlg;
+        if (m >= p.M) continue;
+        const int64_t off = m * p.ldy + n;
+        if (vec8 && n + 8 <= p.N) {
+          epi_m<MODE, 8>(p.epi, &rr[u], off, true, v[u]);
+          if (p.y_dt == DIMQ_F32) {
+            f4v* yp = reinterpret_cast<f4v*>(reinterpret_cast<float*>(p.y) + off);
+            const f4v lo = {v[u][0], v[u][1], v[u][2], v[u][3]}, hi = {v[u][4], v[u][5], v[u][6], v[u][7]};
+            __builtin_nontemporal_store(lo, yp);
+            __builtin_nontemporal_store(hi, yp + 1);
+          } else {
+            u32x4 h;
+            if (p.y_dt == DIMQ_F16) {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) h[i] = f16x2_rne(v[u][2 * i], v[u][2 * i + 1]);
+            } else {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) h[i] = bf16x2_rne(v[u][2 * i], v[u][2 * i + 1]);
+            }
+            u32x4* yp = reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(p.y) + off);
+            __builtin_nontemporal_store(h, yp);
+          }
+        } else {
+          for (int i = 0; i < 8; ++i)
+            if (n + i < p.N) store_from_float(p.y, p.y_dt, off + i, epi1_m<MODE>(p.epi, off + i, v[u][i]));
         }
       }
-      const int64_t n8 = n0 + wn * NBLK * 32 + nb * 32 + 16 * jp + 8 * g;  // this lane's 8 columns
-      ResPairs<8>(&rr)[MBLK] = rbuf[gi & 1];
+      __syncthreads();  // the next pass overwrites the parked values
+      if constexpr ((MODE & kEpiRes) != 0) {
+#pragma unroll
+        for (int u = 0; u < CPT; ++u) rr[u] = rn[u];
+      }
+    });
+  } else {
+    // epilogue: acc[mb][nb][4j + i] = y[m][n], m = block row m0 + wm*MBLK*32 +
+    // mb*32 + col, n = n0 + (nb*WGN + wn)*32 + 8j + 4g + i.  For j = 2 jp and
+    // 2 jp + 1 the lanes l and l + 32 (g 0 and 1, same row) swap four finished
+    // values, so lane g holds the 8 columns 16 jp + 8 g .. + 7 of its row and
+    // writes them as one 16-byte store (two 8-byte stores per lane before).
+    const bool vec = p.ldy % 4 == 0 && p.y_dt != DIMQ_F64;
+    const bool vec8 = p.ldy % 8 == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0 && p.y_dt != DIMQ_F64;
+    // 16-bit residuals of row group gi = 2 nb + jp, requested one group ahead
+    // of its stores (two register sets; a whole-tile prefetch would cost this
+    // kernel an occupancy step), so each group's loads land during the
+    // previous group's stores: requested right before their own stores, their
+    // latency added to every group (ResNet-18 bs128, the residual layers)
+    const bool rpair = (MODE & kEpiRes) && res_pairs(p.epi, vec8);
+    ResPairs<8> rbuf[2][MBLK];
+    auto res_group = [&](int gi, ResPairs<8> (&rr)[MBLK]) {
+      const int64_t n8 = n0 + ((gi >> 1) * WGN + wn) * 32 + 16 * (gi & 1) + 8 * g;
 #pragma unroll
       for (int mb = 0; mb < MBLK; ++mb) {
         const int64_t m = m0 + wm * MBLK * 32 + mb * 32 + col;
-        float va[4], vb[4];
+        if (m < p.M && n8 + 8 <= p.N) res_issue<8>(p.epi, m * p.ldy + n8, rr[mb]);
+      }
+    };
+    if constexpr ((MODE & kEpiRes) != 0) {
+      if (rpair) res_group(0, rbuf[0]);
+    }
+    static_for<NBLK>([&](auto nbc) {
+      constexpr int nb = decltype(nbc)::value;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          va[i] = acc[mb][nb][4 * (2 * jp) + i] * sc[0][i] + bv[0][i];
-          vb[i] = acc[mb][nb][4 * (2 * jp + 1) + i] * sc[1][i] + bv[1][i];
+      for (int jp = 0; jp < 2; ++jp) {
+        const int gi = 2 * nb + jp;
+        if constexpr ((MODE & kEpiRes) != 0) {
+          if (rpair && gi + 1 < 2 * NBLK) res_group(gi + 1, rbuf[(gi + 1) & 1]);
         }
-        if (vec8) {
-          // g 0 keeps va (columns +0..3) and takes the partner's va (+4..7);
-          // g 1 takes the partner's vb (+8..11) and keeps vb (+12..15)
-          float v[8];
+        float sc[2][4], bv[2][4];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int nl = 8 * (2 * jp + h) + 4 * g;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float r = __shfl_xor(g ? va[i] : vb[i], 32);
-            v[i] = g ? r : va[i];
-            v[4 + i] = g ? vb[i] : r;
+            sc[h][i] = __shfl(rscale[nb], nl + i, 32);
+            bv[h][i] = ebias[(nb * WGN + wn) * 32 + nl + i];
           }
-          if (m >= p.M) continue;
-          const int64_t off = m * p.ldy + n8;
-          if (n8 + 8 <= p.N) {
-            epi_m<MODE, 8>(p.epi, &rr[mb], off, true, v);
-            if (p.y_dt == DIMQ_F32) {
-              float* yp = reinterpret_cast<float*>(p.y) + off;
-              *reinterpret_cast<float4*>(yp) = make_float4(v[0], v[1], v[2], v[3]);
-              *reinterpret_cast<float4*>(yp + 4) = make_float4(v[4], v[5], v[6], v[7]);
-            } else {
-              uint32_t h[4];
+        }
+        const int64_t n8 = n0 + (nb * WGN + wn) * 32 + 16 * jp + 8 * g;  // this lane's 8 columns
+        ResPairs<8>(&rr)[MBLK] = rbuf[gi & 1];
 #pragma unroll
-              for (int i = 0; i < 4; ++i)
-                h[i] = p.y_dt == DIMQ_F16 ? f16x2_rne(v[2 * i], v[2 * i + 1]) : bf16x2_rne(v[2 * i], v[2 * i + 1]);
-              *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p.y) + off) = make_uint4(h[0], h[1], h[2], h[3]);
+        for (int mb = 0; mb < MBLK; ++mb) {
+          const int64_t m = m0 + wm * MBLK * 32 + mb * 32 + col;
+          float va[4], vb[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            va[i] = acc[mb][nb][4 * (2 * jp) + i] * sc[0][i] + bv[0][i];
+            vb[i] = acc[mb][nb][4 * (2 * jp + 1) + i] * sc[1][i] + bv[1][i];
+          }
+          if (vec8) {
+            // g 0 keeps va (columns +0..3) and takes the partner's va (+4..7);
+            // g 1 takes the partner's vb (+8..11) and keeps vb (+12..15)
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float r = __shfl_xor(g ? va[i] : vb[i], 32);
+              v[i] = g ? r : va[i];
+              v[4 + i] = g ? vb[i] : r;
             }
-          } else {
-            for (int i = 0; i < 8; ++i)
-              if (n8 + i < p.N) store_from_float(p.y, p.y_dt, off + i, epi1_m<MODE>(p.epi, off + i, v[i]));
-          }
-        } else {
-          if (m >= p.M) continue;
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const float* vv = h ? vb : va;
-            const int64_t n = n0 + wn * NBLK * 32 + nb * 32 + 8 * (2 * jp + h) + 4 * g;
-            const int64_t off = m * p.ldy + n;
-            float v[4] = {vv[0], vv[1], vv[2], vv[3]};
-            if (vec && n + 4 <= p.N) {
-              epi_m<MODE, 4>(p.epi, nullptr, off, true, v);
+            if (m >= p.M) continue;
+            const int64_t off = m * p.ldy + n8;
+            if (n8 + 8 <= p.N) {
+              epi_m<MODE, 8>(p.epi, &rr[mb], off, true, v);
               if (p.y_dt == DIMQ_F32) {
-                *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.y) + off) = make_float4(v[0], v[1], v[2], v[3]);
+                float* yp = reinterpret_cast<float*>(p.y) + off;
+                *reinterpret_cast<float4*>(yp) = make_float4(v[0], v[1], v[2], v[3]);
+                *reinterpret_cast<float4*>(yp + 4) = make_float4(v[4], v[5], v[6], v[7]);
               } else {
-                const uint32_t h0 = p.y_dt == DIMQ_F16 ? f16x2_rne(v[0], v[1]) : bf16x2_rne(v[0], v[1]);
-                const uint32_t h1 = p.y_dt == DIMQ_F16 ? f16x2_rne(v[2], v[3]) : bf16x2_rne(v[2], v[3]);
-                *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.y) + off) = make_uint2(h0, h1);
+                uint32_t h[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                  h[i] = p.y_dt == DIMQ_F16 ? f16x2_rne(v[2 * i], v[2 * i + 1]) : bf16x2_rne(v[2 * i], v[2 * i + 1]);
+                *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p.y) + off) = make_uint4(h[0], h[1], h[2], h[3]);
               }
             } else {
-              for (int i = 0; i < 4; ++i)
-                if (n + i < p.N) store_from_float(p.y, p.y_dt, off + i, epi1_m<MODE>(p.epi, off + i, v[i]));
+              for (int i = 0; i < 8; ++i)
+                if (n8 + i < p.N) store_from_float(p.y, p.y_dt, off + i, epi1_m<MODE>(p.epi, off + i, v[i]));
+            }
+          } else {
+            if (m >= p.M) continue;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const float* vv = h ? vb : va;
+              const int64_t n = n0 + (nb * WGN + wn) * 32 + 8 * (2 * jp + h) + 4 * g;
+              const int64_t off = m * p.ldy + n;
+              float v[4] = {vv[0], vv[1], vv[2], vv[3]};
+              if (vec && n + 4 <= p.N) {
+                epi_m<MODE, 4>(p.epi, nullptr, off, true, v);
+                if (p.y_dt == DIMQ_F32) {
+                  *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.y) + off) = make_float4(v[0], v[1], v[2], v[3]);
+                } else {
+                  const uint32_t h0 = p.y_dt == DIMQ_F16 ? f16x2_rne(v[0], v[1]) : bf16x2_rne(v[0], v[1]);
+                  const uint32_t h1 = p.y_dt == DIMQ_F16 ? f16x2_rne(v[2], v[3]) : bf16x2_rne(v[2], v[3]);
+                  *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.y) + off) = make_uint2(h0, h1);
+                }
+              } else {
+                for (int i = 0; i < 4; ++i)
+                  if (n + i < p.N) store_from_float(p.y, p.y_dt, off + i, epi1_m<MODE>(p.epi, off + i, v[i]));
+              }
             }
           }
         }
       }
-    }
-  });
+    });
+  }
 }
 
 // Shared-decode variant: the work-group decodes each 64-wide k stage of its

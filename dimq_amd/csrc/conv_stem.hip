@@ -424,20 +424,17 @@ __global__ __launch_bounds__(kStemThreads, 2) void conv_stem_kernel(const StemAr
             if (pb + px >= P || ch * 8 >= p.OC) continue;
             const int64_t off = (gp0 + px) * p.OC + ch * 8;
             epi_m<MODE, 8>(p.epi, nullptr, off, true, v);
-            // non-temporal: an instruction writes 8 pixels' whole channel runs
-            typedef float f4v __attribute__((ext_vector_type(4)));
             if (p.y_dt == DIMQ_F32) {
-              f4v* yp = reinterpret_cast<f4v*>(reinterpret_cast<float*>(p.y) + off);
-              const f4v lo = {v[0], v[1], v[2], v[3]}, hi = {v[4], v[5], v[6], v[7]};
-              __builtin_nontemporal_store(lo, yp);
-              __builtin_nontemporal_store(hi, yp + 1);
+              float* yp = reinterpret_cast<float*>(p.y) + off;
+              *reinterpret_cast<float4*>(yp) = make_float4(v[0], v[1], v[2], v[3]);
+              *reinterpret_cast<float4*>(yp + 4) = make_float4(v[4], v[5], v[6], v[7]);
             } else {
               uint32_t h[8];
 #pragma unroll
               for (int u = 0; u < 8; ++u)
                 h[u] = p.y_dt == DIMQ_F16 ? float_to_f16_bits(v[u]) : float_to_bf16_bits(v[u]);
-              const u32x4 hv = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
-              __builtin_nontemporal_store(hv, reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(p.y) + off));
+              *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p.y) + off) =
+                  make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
             }
           }
         } else {

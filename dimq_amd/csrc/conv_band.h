@@ -170,11 +170,13 @@ __device__ __forceinline__ void band_res_issue_nhwc(const HaloArgs& p, int b, in
 //           (the wave's 32 channels) per instruction: cfg2 NHWC, same
 //           process, 16.89 -> 12.97 us against 32-byte pieces of 32 pixels
 //           per instruction through the L2;
-//   NHWC fp16 y: non-temporal 16-byte stores of 16 pixels' 64-byte runs
-//           per instruction (a pixel's 32 channels; the other half of its
-//           line is the other channel half's wave): ResNet-18 layer1 shape,
-//           bs128, same process, 52.6 -> 47.2 us (ReLU) against 32-byte
-//           pieces of 32 pixels per instruction through the L2.
+//   NHWC fp16 y: 16-byte stores of 16 pixels' 64-byte runs per instruction
+//           (a pixel's 32 channels; the other half of its line is the other
+//           channel half's wave), through the L2: the next layer reads them
+//           back.  ResNet-18 layer1 shape, bs128, one conv timed alone over
+//           rotated buffers: 52.6 -> 47.2 us (ReLU) non-temporal against
+//           32-byte pieces of 32 pixels per instruction; in the bs128
+//           forward the non-temporal form was no faster than this one.
 template <int MODE, bool NHWC>
 __device__ __forceinline__ void band_store(const HaloArgs& p, const floatx16& acc, int b, int px1, int mb, int col,
                                            int g, int ocr, int lane, float scale, float bv, float* park,
@@ -219,8 +221,7 @@ __device__ __forceinline__ void band_store(const HaloArgs& p, const floatx16& ac
         }
         const u32x4 h = {f16x2_rne(w[0], w[1]), f16x2_rne(w[2], w[3]), f16x2_rne(w[4], w[5]), f16x2_rne(w[6], w[7])};
         if (pixs < px1 && ocr < p.OC)
-          __builtin_nontemporal_store(h, reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(p.y) +
-                                                                  ((int64_t)b * ohw + pixs) * p.OC + ocr + c8));
+          *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(p.y) + ((int64_t)b * ohw + pixs) * p.OC + ocr + c8) = h;
       }
     } else {  // fp32 y (no residual: setup)
       // lane l: pixel l / 8 + 8 it, channels 4 (l % 8) .. + 3, so that an

@@ -368,11 +368,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, big_min_waves(BITS, MBLK, NBLK, CON
     // column (nb WGN + wn) 32 + 8j + 4g + i) as fp32 in the activation
     // buffers, then the work-group stores the pass's WGN * 32 contiguous
     // columns as 8-column chunks: 8 consecutive lanes write a row's whole run
-    // (128 bytes of fp16 at WGN 2), stored non-temporally.  Stored straight
-    // from the accumulators, each instruction wrote 32-byte pieces of 32 rows
-    // (ResNet-18 3x3 convs at bs128, same process: layer2 57.8 -> 54.9 us,
-    // with the residual 64.2 -> 58.4; layer3 53.2 -> 50.3, 55.1 -> 52.4; the
-    // parked layout with ordinary stores took about half of those gains).
+    // (128 bytes of fp16 at WGN 2).  Stored straight from the accumulators,
+    // each instruction wrote 32-byte pieces of 32 rows.  One conv timed alone
+    // over rotated buffers (ResNet-18 3x3 at bs128, same process), stored
+    // non-temporally: layer2 57.8 -> 54.9 us, with the residual 64.2 -> 58.4;
+    // layer3 53.2 -> 50.3, 55.1 -> 52.4 (ordinary stores took about half of
+    // that).  In the bs128 forward, where the next layer reads the output
+    // back, ordinary stores were as fast or faster, so they are kept.
     // 16-bit residuals: pass 0's requested before the first park, pass nb + 1's
     // before pass nb's stores.
     constexpr int PW = WGN * 32;          // columns per pass
@@ -441,8 +443,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, big_min_waves(BITS, MBLK, NBLK, CON
           if (p.y_dt == DIMQ_F32) {
             f4v* yp = reinterpret_cast<f4v*>(reinterpret_cast<float*>(p.y) + off);
             const f4v lo = {v[u][0], v[u][1], v[u][2], v[u][3]}, hi = {v[u][4], v[u][5], v[u][6], v[u][7]};
-            __builtin_nontemporal_store(lo, yp);
-            __builtin_nontemporal_store(hi, yp + 1);
+            yp[0] = lo;
+            yp[1] = hi;
           } else {
             u32x4 h;
             if (p.y_dt == DIMQ_F16) {
@@ -453,7 +455,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, big_min_waves(BITS, MBLK, NBLK, CON
               for (int i = 0; i < 4; ++i) h[i] = bf16x2_rne(v[u][2 * i], v[u][2 * i + 1]);
             }
             u32x4* yp = reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(p.y) + off);
-            __builtin_nontemporal_store(h, yp);
+            *yp = h;
           }
         } else {
           for (int i = 0; i < 8; ++i)

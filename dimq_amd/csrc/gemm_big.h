@@ -1045,7 +1045,9 @@ __global__ __launch_bounds__(256) void gemm_deep_kernel(const GemmArgs p) {
   // measured 33.3 -> 32.1 us with the parked stores).  The stores are
   // non-temporal: the output streaming through the L2 evicted the activation
   // rows and packed weights that the other column and row tiles still read
-  // (cfg1, same process: 26.08 -> 21.89 us).
+  // (cfg1, same process: 26.0 -> 22.2 us with the output rotated over 22
+  // buffers, 26.6 -> 25.0 us through bench.py, whose op reuses one output
+  // allocation).
   constexpr bool kPark = (MODE & (kEpiRes | kEpiQuant)) == 0 && MBLK % 2 == 0;
   if (kPark && p.y_dt == DIMQ_F32 && p.ldy % 4 == 0) {
     constexpr int PR = MBLK / 2 * 32;  // rows per pass

@@ -65,36 +65,56 @@ __host__ __device__ inline BandPart band_part(int nblk, int parts, int part, int
   return q;
 }
 
-// Staging task: (channel octet co, input row r of the stage, 8 columns q):
-// eight 16-byte loads, one per channel of the octet.  A row outside the image
-// loads row 0 and is written as zeros at commit (zeroing the registers here
-// would make every stage wait for its loads before the next is issued).
+// Staging task: (channel octet co, piece lp of the stage), the stage's rows
+// cut into 16-byte pieces of 8 columns, row-major (qn = W / 8 per row): eight
+// 16-byte loads, one per channel of the octet.  A row outside the image
+// loads a clamped piece of the plane and is written as zeros at commit
+// (zeroing the registers here would make every stage wait for its loads
+// before the next is issued).
 struct BandTask {
   uint4 v[8];
   bool live;
 };
 
-__device__ __forceinline__ void band_issue(const HaloArgs& p, int b, int ih_first, int t, int tasks, BandTask& tk) {
+// NCHW: lanes 8j .. 8j + 7 of a wave load 8 consecutive pieces of each
+// channel of the octet, so one load instruction reads 8 channels' 128-byte
+// runs.  When those runs can start on 128-byte lines (the planes are whole
+// lines apart and x is line-aligned), the stage's pieces are shifted by the
+// returned lead-in s0 (< 8 pieces, taken from the row before the stage and
+// not committed), so that every run is one whole line: unshifted, a run of
+// a row that starts mid-line spans two lines, each requested by two load
+// instructions.  0 when the shift does not apply or the lead-in tasks would
+// not fit one per thread.
+__device__ __forceinline__ int band_shift(const HaloArgs& p, int ih0, int tasks) {
+  const int s0 = (ih0 * (p.W >> 3)) & 7;  // the stage's first piece within its line (two's complement & 7: ih0 may be -1)
+  const bool ok = ((p.H * p.W) & 63) == 0 && (reinterpret_cast<uintptr_t>(p.x) & 127) == 0 &&
+                  tasks + 8 * s0 <= kBandThreads;
+  return ok ? s0 : 0;
+}
+
+__device__ __forceinline__ void band_issue(const HaloArgs& p, int b, int ih_first, int t, int tasks, int s0,
+                                           BandTask& tk) {
   const int qn = p.W >> 3;
-  const int tt = t < tasks ? t : 0;
-  const int co = tt & 7, rest = tt >> 3, q = rest % qn, r = rest / qn;
-  const int ih = ih_first + r;
-  tk.live = t < tasks && ih >= 0 && ih < p.H;
-  const int ihc = tk.live ? ih : 0;
-  const uint16_t* src =
-      reinterpret_cast<const uint16_t*>(p.x) + (((int64_t)b * p.C + 8 * co) * p.H + ihc) * p.W + 8 * q;
+  const int n = tasks + 8 * s0;  // with the lead-in
+  const int tt = t < n ? t : 0;
+  const int co = tt & 7, lp = (tt >> 3) - s0;
+  const int ih = ih_first + (lp >= 0 ? lp / qn : -1);
+  tk.live = t < n && lp >= 0 && ih >= 0 && ih < p.H;
+  const int a = min(max(ih_first * qn + lp, 0), p.H * qn - 1);  // piece of the plane, clamped into it
+  const uint16_t* src = reinterpret_cast<const uint16_t*>(p.x) + ((int64_t)b * p.C + 8 * co) * p.H * p.W + 8 * a;
 #pragma unroll
   for (int c = 0; c < 8; ++c) tk.v[c] = *reinterpret_cast<const uint4*>(src + (int64_t)c * p.H * p.W);
 }
 
 // Halo row r0 + r of task t: pixels 8q .. 8q + 7 (halo columns + 1 for the
 // left padding column), channels 8co .. 8co + 7, as fp16.
-__device__ __forceinline__ void band_commit(const HaloArgs& p, int r0, int t, int tasks, const BandTask& tk,
+__device__ __forceinline__ void band_commit(const HaloArgs& p, int r0, int t, int tasks, int s0, const BandTask& tk,
                                             uint16_t* halo) {
-  if (t >= tasks) return;
+  const int lp = (t >> 3) - s0;
+  if (t >= tasks + 8 * s0 || lp < 0) return;
   constexpr int CP = 72;
   const int qn = p.W >> 3;
-  const int co = t & 7, rest = t >> 3, q = rest % qn, r = r0 + rest / qn;
+  const int co = t & 7, q = lp % qn, r = r0 + lp / qn;
   uint32_t in[8][4];
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
@@ -299,15 +319,16 @@ __global__ __launch_bounds__(kBandThreads, 1) void conv_band_kernel(const HaloAr
   // starts 1.5-2 us later.
   const int tA = bp.ra * p.W, tB = (bp.IH - bp.ra) * p.W;  // 8 * rows * W / 8
   BandTask tka, tkb;
-  auto issue = [&](int ih0, int tasks, BandTask& tk) {
+  const int sA = NHWC ? 0 : band_shift(p, ih_first, tA), sB = NHWC ? 0 : band_shift(p, ih_first + bp.ra, tB);
+  auto issue = [&](int ih0, int tasks, int s0, BandTask& tk) {
     if constexpr (NHWC) band_issue_nhwc(p, b, ih0, tid, tasks, tk);
-    else band_issue(p, b, ih0, tid, tasks, tk);
+    else band_issue(p, b, ih0, tid, tasks, s0, tk);
   };
-  auto commit = [&](int r0, int tasks, const BandTask& tk) {
+  auto commit = [&](int r0, int tasks, int s0, const BandTask& tk) {
     if constexpr (NHWC) band_commit_nhwc(p, r0, tid, tasks, tk, halo);
-    else band_commit(p, r0, tid, tasks, tk, halo);
+    else band_commit(p, r0, tid, tasks, s0, tk, halo);
   };
-  issue(ih_first, tA, tka);
+  issue(ih_first, tA, sA, tka);
   CbRaw<E> cbraw;
   cb_row_issue<E>(p.cb, p.cb_dt, p.cb_rows == 1 ? 0 : min(ocl, p.OC - 1), p.cb_size, cbraw);
   const bool has_bias = p.bias && ocl < p.OC;
@@ -335,13 +356,13 @@ __global__ __launch_bounds__(kBandThreads, 1) void conv_band_kernel(const HaloAr
     for (int w = 0; w < BITS; ++w) chunk[w] = wreg[(t >> 2) * BITS + w];
     wf[t] = decode_sub<BITS>(chunk, t & 3, cbr);
   }
-  commit(0, tA, tka);
+  commit(0, tA, sA, tka);
   for (int t = tid; t < bp.IH * 16; t += kBandThreads) {  // left and right padding columns
     const int co = t & 7, side = (t >> 3) & 1, r = t >> 4;
     *reinterpret_cast<uint4*>(&halo[(r * p.IW_t + (side ? p.IW_t - 1 : 0)) * CP + 8 * co]) = make_uint4(0, 0, 0, 0);
   }
   lds_barrier();
-  issue(ih_first + bp.ra, tB, tkb);  // in flight through round 0
+  issue(ih_first + bp.ra, tB, sB, tkb);  // in flight through round 0
 
   const int row_step = p.IW_t * CP;
   // nq = 1 or 2 blocks (independent accumulator chains) of this wave
@@ -400,7 +421,7 @@ __global__ __launch_bounds__(kBandThreads, 1) void conv_band_kernel(const HaloAr
       if constexpr (RES) band_res_issue_nhwc(p, b, bp.px1, mb, ocr, lane, rr[0]);  // in flight through the MFMAs
       compute(1, mbs, acc);
     }
-    commit(bp.ra, tB, tkb);
+    commit(bp.ra, tB, sB, tkb);
     lds_barrier();
     if (mb < bp.blk1) band_store<MODE, NHWC>(p, acc[0], b, bp.px1, mb, col, g, ocr, lane, scale, bv, park, rr[0]);
   }

@@ -298,6 +298,57 @@ __device__ __forceinline__ void u4_codes(float (&v)[N], float s, int zp) {
   for (int i = 0; i < N; ++i) v[i] = c[i];
 }
 
+// Groups of 8 activations per thread in the W4A4 quantization launches.
+constexpr int kQa4Groups = 4;
+
+// The W4A4 input form (fp16 integers q - zp, u4_codes) of U groups of 8
+// activations: group u of the calling thread holds elements 8 (g0 + u gstride)
+// .. + 7.  Every full group's load is issued before the first is converted,
+// so a thread has U 16-byte (fp16 / bf16) or 32-byte (fp32) loads in flight;
+// each full group leaves as one 16-byte store, a partial last group element
+// by element.  VEC: x is 16-byte aligned.
+template <int XT, bool VEC, int U>
+__device__ __forceinline__ void quantize_a4_f16_groups(const void* __restrict__ x, int64_t n, float s, int zp,
+                                                       uint16_t* __restrict__ out, int64_t g0, int64_t gstride) {
+  float v[U][8];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t base = (g0 + u * gstride) * 8;
+    if (base + 8 > n) continue;
+    if constexpr (VEC && XT == DIMQ_F32) {
+      const float4 a = reinterpret_cast<const float4*>(static_cast<const float*>(x) + base)[0];
+      const float4 b = reinterpret_cast<const float4*>(static_cast<const float*>(x) + base)[1];
+      v[u][0] = a.x; v[u][1] = a.y; v[u][2] = a.z; v[u][3] = a.w;
+      v[u][4] = b.x; v[u][5] = b.y; v[u][6] = b.z; v[u][7] = b.w;
+    } else if constexpr (VEC && (XT == DIMQ_F16 || XT == DIMQ_BF16)) {
+      const uint4 a = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + base);
+      const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[u][2 * j] = XT == DIMQ_F16 ? f16_bits_to_float(w[j] & 0xffffu) : bf16_bits_to_float(w[j] & 0xffffu);
+        v[u][2 * j + 1] = XT == DIMQ_F16 ? f16_bits_to_float(w[j] >> 16) : bf16_bits_to_float(w[j] >> 16);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[u][j] = load_as_float(x, XT, base + j);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t base = (g0 + u * gstride) * 8;
+    if (base + 8 <= n) {
+      u4_codes<8>(v[u], s, zp);
+      uint32_t h[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) h[j] = f16x2_rne(v[u][2 * j], v[u][2 * j + 1]);
+      *reinterpret_cast<uint4*>(out + base) = make_uint4(h[0], h[1], h[2], h[3]);
+    } else {
+      for (int64_t i = base; i < n; ++i)
+        out[i] = (uint16_t)float_to_f16_bits((float)(quantize_u4(load_as_float(x, XT, i), s, zp) - zp));
+    }
+  }
+}
+
 template <int N>
 __device__ __forceinline__ void epi_quant_n(const Epi& e, float (&v)[N]) {
   u4_codes<N>(v, e.qs, e.qzp);

@@ -240,18 +240,20 @@ extern "C" int dimq_conv2d_lut_ws(const void* x, int x_dtype, int64_t B, int64_t
   if (workspace != nullptr && need > 0 && workspace_bytes >= need && aligned(workspace, 16)) {
     const float sc = static_cast<float>(act_scale);
     uint16_t* q = static_cast<uint16_t*>(workspace);
-    int r = launch_quantize_a4_f16(x, x_dtype, s.B * s.C * s.H * s.W, sc, static_cast<int>(act_zp), q, st);
-    if (r != DIMQ_OK) return r;
     const int64_t hw = (s.groups == 1) ? halo_part_words(s.OC, s.C, s.KH, s.KW, 4) : 0;
     if (hw > 0 && halo_eligible(s.C, s.KH, s.KW, s.sh, s.sw, s.dh, s.dw, s.groups, s.OH, s.OW, 4, DIMQ_F16,
                                 kEpiNone, DIMQ_NCHW)) {
+      // the weight layout and the quantized activations in one launch
       uint32_t* kw = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(workspace) + lut_act_bytes(s.B, s.C, s.H, s.W));
-      r = launch_prepare(packed_w, s.OC, s.C, s.KH, s.KW, 4, kw, st);
+      const int r = launch_w4a4_conv_inputs(packed_w, s.OC, s.C, s.KH, s.KW, kw, x, x_dtype, s.B * s.C * s.H * s.W,
+                                            sc, static_cast<int>(act_zp), q, st);
       if (r != DIMQ_OK) return r;
       return launch_conv_halo(q, DIMQ_F16, DIMQ_NCHW, s.B, s.C, s.H, s.W, kw, 4, codebook, cb_dtype, 1, 16, bias,
                               bias_dtype, s.OC, s.KH, s.KW, s.sh, s.ph, s.pw, s.OH, s.OW, y, DIMQ_F32, DIMQ_NCHW,
                               Epi{}, st, sc);
     }
+    const int r = launch_quantize_a4_f16(x, x_dtype, s.B * s.C * s.H * s.W, sc, static_cast<int>(act_zp), q, st);
+    if (r != DIMQ_OK) return r;
     GemmArgs p = conv_args(s, q, DIMQ_NCHW, packed_w, codebook, cb_dtype, 1, 16, bias, bias_dtype, y, DIMQ_F32,
                            DIMQ_NCHW);
     p.acc_scale = sc;

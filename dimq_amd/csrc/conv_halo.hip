@@ -22,10 +22,10 @@ __device__ __forceinline__ int field_of(int s, int j) {
   }
 }
 
+// Thread id's BITS words of the layout (ids past OC * 2 * chunks: none).
 template <int BITS>
-__global__ void prepare_kernel(const uint8_t* __restrict__ src, int OC, int C, int KH, int KW, int CC, int T,
-                               int chunks, uint32_t* __restrict__ out) {
-  const int64_t id = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void prepare_words(int64_t id, const uint8_t* __restrict__ src, int OC, int C, int KH,
+                                              int KW, int CC, int T, int chunks, uint32_t* __restrict__ out) {
   const int64_t total = (int64_t)OC * 2 * chunks;
   if (id >= total) return;
   const int chunk = static_cast<int>(id % chunks);
@@ -60,6 +60,33 @@ __global__ void prepare_kernel(const uint8_t* __restrict__ src, int OC, int C, i
   uint32_t* dst = out + id * BITS;
 #pragma unroll
   for (int w = 0; w < BITS; ++w) dst[w] = words[w];
+}
+
+template <int BITS>
+__global__ void prepare_kernel(const uint8_t* __restrict__ src, int OC, int C, int KH, int KW, int CC, int T,
+                               int chunks, uint32_t* __restrict__ out) {
+  prepare_words<BITS>(static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x, src, OC, C, KH, KW, CC, T, chunks,
+                      out);
+}
+
+// The two inputs of a W4A4 conv2d_lut call on the halo / band kernels in one
+// launch: work-groups [0, wblocks) lay out the 4-bit weight (prepare_words),
+// the rest quantize the activations to the fp16 integers q - zp
+// (quantize_a4_f16_groups, as quantize_a4_f16_kernel); the weight's few
+// work-groups then cost no launch of their own.
+template <int XT, bool VEC>
+__global__ __launch_bounds__(256) void w4a4_conv_inputs_kernel(const uint8_t* __restrict__ src, int OC, int C, int KH,
+                                                              int KW, int CC, int T, int chunks,
+                                                              uint32_t* __restrict__ kw, int wblocks,
+                                                              const void* __restrict__ x, int64_t n, float s, int zp,
+                                                              uint16_t* __restrict__ q) {
+  const int bid = static_cast<int>(blockIdx.x);
+  if (bid < wblocks) {
+    prepare_words<4>(static_cast<int64_t>(bid) * 256 + threadIdx.x, src, OC, C, KH, KW, CC, T, chunks, kw);
+    return;
+  }
+  quantize_a4_f16_groups<XT, VEC, kQa4Groups>(x, n, s, zp, q,
+                                              static_cast<int64_t>(bid - wblocks) * 256 * kQa4Groups + threadIdx.x, 256);
 }
 
 }  // namespace
@@ -198,6 +225,28 @@ int launch_conv_halo(const void* x, int x_dtype, int x_layout, int64_t B, int64_
     case 3: return launch_halo_b3(p, CC, (int)stride, mode, s);
     default: return launch_halo_b4(p, CC, (int)stride, mode, s);
   }
+}
+
+int launch_w4a4_conv_inputs(const uint8_t* src, int64_t OC, int64_t C, int64_t KH, int64_t KW, uint32_t* kw,
+                            const void* x, int x_dtype, int64_t n, float scale, int zp, uint16_t* q, hipStream_t s) {
+  const int CC = (int)(C / 16);
+  const int T = (int)(KH * KW * CC);
+  const int chunks = (T + 3) / 4;
+  const int64_t wblocks = (OC * 2 * chunks + 255) / 256;
+  const int64_t qblocks = ((n + 7) / 8 + 256 * kQa4Groups - 1) / (256 * kQa4Groups);
+  const dim3 grid(static_cast<unsigned>(wblocks + qblocks));
+  const bool vec = aligned(x, 16);
+#define DIMQ_W4A4_IN(XT, V)                                                                                      \
+  hipLaunchKernelGGL((w4a4_conv_inputs_kernel<XT, V>), grid, dim3(256), 0, s, src, (int)OC, (int)C, (int)KH,       \
+                     (int)KW, CC, T, chunks, kw, (int)wblocks, x, n, scale, zp, q)
+  switch (x_dtype) {
+    case DIMQ_F32: if (vec) DIMQ_W4A4_IN(DIMQ_F32, true); else DIMQ_W4A4_IN(DIMQ_F32, false); break;
+    case DIMQ_F16: if (vec) DIMQ_W4A4_IN(DIMQ_F16, true); else DIMQ_W4A4_IN(DIMQ_F16, false); break;
+    case DIMQ_BF16: if (vec) DIMQ_W4A4_IN(DIMQ_BF16, true); else DIMQ_W4A4_IN(DIMQ_BF16, false); break;
+    default: DIMQ_W4A4_IN(DIMQ_F64, false); break;
+  }
+#undef DIMQ_W4A4_IN
+  return check_launch("conv2d_lut (weight layout and activation quantization)");
 }
 
 int launch_prepare(const uint8_t* src, int64_t OC, int64_t C, int64_t KH, int64_t KW, int bits, uint32_t* out,

@@ -1048,6 +1048,10 @@ int launch_conv_stem(const void* x, int x_dtype, int x_layout, int64_t B, int64_
 
 // quant.hip: W4A4 activations as the fp16 integers a - zp (out 16-byte aligned)
 int launch_quantize_a4_f16(const void* x, int x_dtype, int64_t n, float s, int zp, uint16_t* out, hipStream_t st);
+// One launch: the 4-bit halo weight layout of launch_prepare into kw and the
+// activations' W4A4 form of launch_quantize_a4_f16 into q (16-byte aligned).
+int launch_w4a4_conv_inputs(const uint8_t* src, int64_t OC, int64_t C, int64_t KH, int64_t KW, uint32_t* kw,
+                            const void* x, int x_dtype, int64_t n, float scale, int zp, uint16_t* q, hipStream_t s);
 // lut_act.hip: index x index LUT gather of the weight x activation codebook Linear
 bool lut_act_supported(int64_t M, int64_t K, int bits, int64_t cb_rows, int64_t Ka);
 int launch_lut_act(const uint8_t* aidx, int64_t M, int64_t K, const uint8_t* w, int bits, const void* cw, int cw_dt,

@@ -39,43 +39,15 @@ __global__ __launch_bounds__(kThreads) void quantize_act_kernel(const void* __re
 // q = clamp(rint(x / s) + zp, 0, 15), the same code as quantize_act_kernel.
 // q - zp is an integer in [-15, 15], exact in fp16, so a weight-only GEMM/conv
 // over these values times s equals sum_k C[w] * (s * (a - zp)) up to fp32
-// summation order.  8 activations per thread, one 16-byte store; VEC: x is
+// summation order.  kQa4Groups groups of 8 activations per thread, group u of
+// thread t of work-group b at (b * kQa4Groups + u) * kThreads + t (loads
+// coalesced per u, all of a thread's loads in flight at once); VEC: x is
 // 16-byte aligned (vector loads of the 8 inputs).
 template <int XT, bool VEC>
 __global__ __launch_bounds__(kThreads) void quantize_a4_f16_kernel(const void* __restrict__ x, int64_t n, float s,
                                                                    int zp, uint16_t* __restrict__ out) {
-  const int64_t base = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * 8;
-  if (base >= n) return;
-  if (base + 8 <= n) {
-    float v[8];
-    if constexpr (VEC && XT == DIMQ_F32) {
-      const float4 a = reinterpret_cast<const float4*>(static_cast<const float*>(x) + base)[0];
-      const float4 b = reinterpret_cast<const float4*>(static_cast<const float*>(x) + base)[1];
-      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-      v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-    } else if constexpr (VEC && (XT == DIMQ_F16 || XT == DIMQ_BF16)) {
-      const uint4 a = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + base);
-      const uint32_t w[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[2 * j] = XT == DIMQ_F16 ? f16_bits_to_float(w[j] & 0xffffu) : bf16_bits_to_float(w[j] & 0xffffu);
-        v[2 * j + 1] = XT == DIMQ_F16 ? f16_bits_to_float(w[j] >> 16) : bf16_bits_to_float(w[j] >> 16);
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = load_as_float(x, XT, base + j);
-    }
-    u4_codes<8>(v, s, zp);
-    uint32_t h[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) h[j] = f16x2_rne(v[2 * j], v[2 * j + 1]);
-    *reinterpret_cast<uint4*>(out + base) = make_uint4(h[0], h[1], h[2], h[3]);
-  } else {
-    for (int64_t i = base; i < n; ++i) {
-      const float v = load_as_float(x, XT, i);
-      out[i] = (uint16_t)float_to_f16_bits((float)(quantize_u4(v, s, zp) - zp));
-    }
-  }
+  quantize_a4_f16_groups<XT, VEC, kQa4Groups>(
+      x, n, s, zp, out, static_cast<int64_t>(blockIdx.x) * kThreads * kQa4Groups + threadIdx.x, kThreads);
 }
 
 // table[g][w][a] = C[g][w] * (s * (a - zp)), fp32, same operation order as
@@ -227,7 +199,7 @@ int launch_act_codebook(const void* x, int x_dtype, int64_t n, const float* cent
 // Launches quantize_a4_f16_kernel; out must be 16-byte aligned.
 int launch_quantize_a4_f16(const void* x, int x_dtype, int64_t n, float s, int zp, uint16_t* out, hipStream_t st) {
   if (n == 0) return DIMQ_OK;
-  const int64_t blocks = ((n + 7) / 8 + kThreads - 1) / kThreads;
+  const int64_t blocks = ((n + 7) / 8 + kThreads * kQa4Groups - 1) / (kThreads * kQa4Groups);
   const bool vec = aligned(x, 16);
   const dim3 grid(static_cast<unsigned>(blocks));
 #define DIMQ_QA4(XT)                                                                                 \

@@ -63,6 +63,10 @@ def test_quantize_activation_f16_matches_reference_codes(gpu):
             q = ops.quantize_activation_f16(x.to(dt).to(gpu), s, zp)
             assert q.dtype == torch.float16 and q.shape == x.shape
             assert torch.equal(q.cpu().float(), _codes(x.to(dt).float(), s, zp))
+            # a view one element into its storage: the element-wise (unaligned) loads
+            xv = x.to(dt).to(gpu).flatten()[1:]
+            qv = ops.quantize_activation_f16(xv, s, zp)
+            assert torch.equal(qv.cpu().float(), _codes(x.to(dt).flatten()[1:].float(), s, zp))
 
 
 def test_quantize_codes_at_rounding_ties(gpu):

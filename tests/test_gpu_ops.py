@@ -395,6 +395,29 @@ def test_conv2d_lut_fp16_codebook_fast_path(gpu, case, xdt):
     _a4_exact_check(y, ref, exact, shape[1] * shape[2] * shape[3])
 
 
+@pytest.mark.parametrize("xdt", [torch.float32, torch.float16])
+def test_conv2d_lut_fast_path_unaligned_input(gpu, xdt):
+    """The W4A4 fast path's one launch that quantizes the activations and lays out the 4-bit weight: an input
+    view one element into its storage (element-wise loads) gives the same output, bit for bit, as an aligned
+    copy, and both match the oracle."""
+    ops = _ops()
+    g = _gen(77)
+    B, C, H, W, OC = 2, 64, 20, 24, 64
+    shape = (OC, C, 3, 3)
+    flat = torch.randn(B * C * H * W + 1, generator=g).to(xdt).to(gpu)
+    xv = flat[1:].view(B, C, H, W)
+    idx = torch.randint(0, 16, shape, generator=g, dtype=torch.uint8)
+    cb = torch.linspace(-0.7, 0.6, 16).half()
+    packed = torch.from_numpy(oracle.pack_bits(idx, 4))
+    args = (packed.to(gpu), cb.to(gpu), 0.25, 7, None, shape, (1, 1), (1, 1), (1, 1), 1)
+    y_view = ops.dimq_conv2d_lut(xv, *args)
+    y_copy = ops.dimq_conv2d_lut(xv.clone(), *args)
+    assert torch.equal(y_view, y_copy)
+    ref = oracle.conv2d_lut(xv.cpu().float(), packed, cb.float(), 0.25, 7, None, shape, (1, 1), (1, 1), (1, 1), 1)
+    exact = torch.nn.functional.conv2d(_a4_levels(xv.cpu(), 0.25, 7), cb.double()[idx.long()], None, 1, 1, 1, 1)
+    _a4_exact_check(y_view, ref, exact, C * 9)
+
+
 # ---------------------------------------------------------------- weight-only codebook Linear
 def _codebook_case(N, K, bits, per_channel, g, cb_entries=None):
     Kc = cb_entries or (1 << bits)

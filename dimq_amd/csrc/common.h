@@ -277,10 +277,22 @@ __device__ __forceinline__ float epi_quant(const Epi& e, float v) {
 // the whole group: t = v * RN(1/s) rounded and clamped with v_med3; a lane
 // with a value within 2^-15 of a tie, a NaN / inf, or a scale whose
 // reciprocal is subnormal redoes its values with quantize_u4.
+// A power-of-two scale (with a normal reciprocal) needs no test: v * RN(1/s)
+// is then v / s exactly (or both overflow alike, or both are below 1/2), so
+// its rint is the IEEE quotient's code, ties included; a NaN gives code zp.
 template <int N>
 __device__ __forceinline__ void u4_codes(float (&v)[N], float s, int zp) {
   const float rcp = 1.0f / s;
   const float lo = (float)(-zp), hi = (float)(15 - zp);
+  const uint32_t sb = __float_as_uint(s);
+  if ((sb & 0x007fffffu) == 0u && (sb & 0x7f800000u) != 0u && fabsf(rcp) >= 0x1p-126f) {  // uniform
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const float t = v[i] * rcp;
+      v[i] = t == t ? __builtin_amdgcn_fmed3f(__builtin_rintf(t), lo, hi) : 0.0f;
+    }
+    return;
+  }
   bool exact = !(fabsf(rcp) >= 0x1p-126f);
   float c[N];
 #pragma unroll

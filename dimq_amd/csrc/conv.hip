@@ -464,7 +464,7 @@ extern "C" int dimq_conv2d_codebook_ex(const void* x, int x_dtype, int x_layout,
   }
   if (variant != DIMQ_VARIANT_SMALL_M &&
       stem_eligible(s.C, s.OC, s.KH, s.KW, s.sh, s.sw, s.pw, s.dh, s.dw, s.groups, s.OH, s.OW, bits, x_dtype, y_dtype, x, y,
-                    epi_mode(epi))) {
+                    epi_mode(epi), packed_w, packed_numel, codebook, cb_dtype, cb_rows, cb_size)) {
     return launch_conv_stem(x, x_dtype, x_layout, s.B, s.C, s.H, s.W, packed_w, packed_numel, bits, codebook,
                             cb_dtype, cb_rows, cb_size, bias, bias_dtype, s.OC, s.KH, s.KW, s.ph, s.pw, s.OH, s.OW,
                             y, y_dtype, y_layout, epi, as_stream(stream));

@@ -52,6 +52,7 @@ struct StemArgs {
   int bits;
   const void* cb;
   int cb_dt, cb_rows, cb_size;
+  int cb_pass;  // decode: output channels per pass whose codebook rows are staged in LDS
   const void* bias;
   int bias_dt;
   void* y;
@@ -199,19 +200,16 @@ __global__ __launch_bounds__(kStemThreads, 2) void conv_stem_kernel(const StemAr
   float* otile = otile_all + wave * kStemOutFloats;
 
   // ---- decode the layer's weights into fragment order (thread: channel oc, pair o)
-  for (int item = tid; item < 64 * NP; item += kStemThreads) {
+  // One item: its 8 KH taps' indices and codebook entries, read from LDS
+  // (taps outside the kernel read index 0 and are zeroed by a select);
+  // index_bytes(flat) returns the two stream bytes holding index `flat`,
+  // entry(oc, i) entry i of oc's codebook row.
+  auto decode_item = [&](int item, auto&& index_bytes, auto&& entry) {
     const int oc = item / NP;
     const int o = item - oc * NP;
     const bool ocv = oc < p.OC;
-    const int row = (p.cb_rows == 1) ? 0 : oc;
-    // every index's stream bytes, then every codebook entry, each set issued
-    // before any of it is used (taps outside the kernel read index 0 and are
-    // zeroed by a select): a branch around each load made the weight decode
-    // a chain of KH x 8 dependent round trips (~20 us per work-group at the
-    // ResNet stem)
-    int flat[KH][8];
     bool tap[KH][8];
-    uint32_t ib[KH][8];
+    float v[KH][8];
 #pragma unroll
     for (int kh = 0; kh < KH; ++kh) {
 #pragma unroll
@@ -219,44 +217,12 @@ __global__ __launch_bounds__(kStemThreads, 2) void conv_stem_kernel(const StemAr
         const int px = e >= p.C ? 1 : 0;
         const int c = e - px * p.C;
         const int kw = 2 * o + px - p.par;
-        tap[kh][e] = ocv && e < 2 * p.C && kw >= 0 && kw < p.KW;
-        flat[kh][e] = tap[kh][e] ? ((oc * p.C + c) * KH + kh) * p.KW + kw : 0;
-        ib[kh][e] = stem_index_bytes(p, flat[kh][e]);
+        const bool in = ocv && e < 2 * p.C && kw >= 0 && kw < p.KW;
+        const int flat = in ? ((oc * p.C + c) * KH + kh) * p.KW + kw : 0;
+        const int i = stem_index_of(p, flat, index_bytes(flat));
+        tap[kh][e] = in && i < p.cb_size;
+        v[kh][e] = entry(oc, tap[kh][e] ? i : 0);
       }
-    }
-    int idx[KH][8];
-#pragma unroll
-    for (int kh = 0; kh < KH; ++kh)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int i = stem_index_of(p, flat[kh][e], ib[kh][e]);
-        tap[kh][e] = tap[kh][e] && i < p.cb_size;
-        idx[kh][e] = tap[kh][e] ? i : 0;
-      }
-    float v[KH][8];
-    if (p.cb_dt == DIMQ_F32) {
-      const float* cbf = reinterpret_cast<const float*>(p.cb) + row * p.cb_size;
-#pragma unroll
-      for (int kh = 0; kh < KH; ++kh)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[kh][e] = cbf[idx[kh][e]];
-    } else if (p.cb_dt == DIMQ_F16 || p.cb_dt == DIMQ_BF16) {
-      const uint16_t* cbh = reinterpret_cast<const uint16_t*>(p.cb) + row * p.cb_size;
-      uint32_t h[KH][8];
-#pragma unroll
-      for (int kh = 0; kh < KH; ++kh)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) h[kh][e] = cbh[idx[kh][e]];
-#pragma unroll
-      for (int kh = 0; kh < KH; ++kh)
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          v[kh][e] = p.cb_dt == DIMQ_F16 ? f16_bits_to_float(h[kh][e]) : bf16_bits_to_float(h[kh][e]);
-    } else {
-#pragma unroll
-      for (int kh = 0; kh < KH; ++kh)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[kh][e] = load_as_float(p.cb, p.cb_dt, row * p.cb_size + idx[kh][e]);
     }
     float mx = 0.0f;
 #pragma unroll
@@ -283,6 +249,86 @@ __global__ __launch_bounds__(kStemThreads, 2) void conv_stem_kernel(const StemAr
       const int l = (oc & 31) + 32 * (o & 1);
       wdec[((oc >> 5) * T + t) * 64 + l] =
           make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+    }
+  };
+  {
+    // The packed stream and, p.cb_pass output channels at a time, their
+    // codebook rows are first copied into LDS behind the decode area with
+    // coalesced 16-byte loads (all of a thread's loads of a batch in flight);
+    // the items then gather from LDS.  Gathered from global memory, each
+    // wave-wide load of 64 lanes' indices or entries touched ~30 cache lines
+    // (ResNet-18 stem: ~17.6 us of decode per work-group).
+    uint8_t* wst = reinterpret_cast<uint8_t*>(stem_lds + wdec_units);
+    const int wb = static_cast<int>(p.w_bytes);
+    float* cbs = reinterpret_cast<float*>(wst + ((wb + 15) & ~15));
+    const int nfull = wb >> 4;
+    if (nfull > 0) {
+      for (int c0 = 0; c0 < nfull; c0 += kStemThreads * 4) {
+        uint4 t[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int ci = c0 + j * kStemThreads + tid;
+          t[j] = *reinterpret_cast<const uint4*>(p.w + 16 * (ci < nfull ? ci : nfull - 1));
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int ci = c0 + j * kStemThreads + tid;
+          if (ci < nfull) *reinterpret_cast<uint4*>(wst + 16 * ci) = t[j];
+        }
+      }
+    }
+    if (tid < (wb & 15)) wst[(nfull << 4) + tid] = p.w[(nfull << 4) + tid];
+    const bool f32 = p.cb_dt == DIMQ_F32;
+    const int per = f32 ? 4 : 8;  // entries per 16-byte chunk
+    const int rows = p.cb_rows == 1 ? 1 : p.cb_pass;
+    const int dsz = f32 ? 4 : 2;
+    for (int r0 = 0; r0 < 64; r0 += p.cb_pass) {
+      const int nrows = p.cb_rows == 1 ? 1 : (r0 + rows <= p.cb_rows ? rows : p.cb_rows - r0);
+      if (nrows > 0) {
+        const int nch = nrows * p.cb_size / per;
+        const uint8_t* src = static_cast<const uint8_t*>(p.cb) + (size_t)(p.cb_rows == 1 ? 0 : r0) * p.cb_size * dsz;
+        for (int c0 = 0; c0 < nch; c0 += kStemThreads * 8) {
+          uint4 t[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int ci = c0 + j * kStemThreads + tid;
+            t[j] = *reinterpret_cast<const uint4*>(src + 16 * (ci < nch ? ci : nch - 1));
+          }
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int ci = c0 + j * kStemThreads + tid;
+            if (ci >= nch) continue;
+            if (f32) {
+              *reinterpret_cast<uint4*>(cbs + 4 * ci) = t[j];
+            } else {
+              const uint32_t u[4] = {t[j].x, t[j].y, t[j].z, t[j].w};
+              float f[8];
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                const bool h16 = p.cb_dt == DIMQ_F16;
+                f[2 * q] = h16 ? f16_bits_to_float(u[q] & 0xffffu) : bf16_bits_to_float(u[q] & 0xffffu);
+                f[2 * q + 1] = h16 ? f16_bits_to_float(u[q] >> 16) : bf16_bits_to_float(u[q] >> 16);
+              }
+              *reinterpret_cast<float4*>(cbs + 8 * ci) = make_float4(f[0], f[1], f[2], f[3]);
+              *reinterpret_cast<float4*>(cbs + 8 * ci + 4) = make_float4(f[4], f[5], f[6], f[7]);
+            }
+          }
+        }
+      }
+      __syncthreads();  // stream and rows staged
+      for (int item = tid; item < 64 * NP; item += kStemThreads) {
+        const int oc = item / NP;
+        if (oc < r0 || oc >= r0 + p.cb_pass) continue;  // whole channels: NP consecutive lanes
+        decode_item(
+            item,
+            [&](int flat) {
+              const int byte = (flat * p.bits) >> 3;
+              const int next = byte + 1 < wb ? byte + 1 : byte;
+              return static_cast<uint32_t>(wst[byte]) | (static_cast<uint32_t>(wst[next]) << 8);
+            },
+            [&](int ch, int i) { return cbs[(p.cb_rows == 1 ? 0 : ch - r0) * p.cb_size + i]; });
+      }
+      __syncthreads();  // the next pass overwrites the rows
     }
   }
   __syncthreads();
@@ -502,11 +548,41 @@ int64_t stem_rows(int64_t KH, int64_t OH, int64_t OW, int np) {
   return 0;
 }
 
+// Dynamic LDS of a band: the staged input rows or the decode area, then the
+// four epilogue tiles.
+size_t stem_band_lds(int64_t KH, int64_t OH, int64_t OW, int np) {
+  const int64_t th = stem_rows(KH, OH, OW, np);
+  const int64_t units = std::max<int64_t>((2 * (th - 1) + KH) * (OW + np - 1), KH * np * 64);
+  return (size_t)units * 16 + 4 * kStemOutFloats * sizeof(float);
+}
+
+// Output channels per decode pass: the packed stream and the codebook rows of
+// that many channels are staged behind the decode area (2 T 64 16-byte
+// units), the most that fit in the band's LDS or in 80 KB (two work-groups
+// per CU); *lds gets the LDS bytes the launch needs.  0: the stream or the
+// codebook is not 16-byte aligned, or a row is not whole 16-byte chunks.
+int stem_cb_pass(int64_t KH, int np, size_t band_lds, const void* w, int64_t w_bytes, const void* cb, int cb_dtype,
+                 int64_t cb_rows, int64_t cb_size, size_t* lds) {
+  const int64_t esz = cb_dtype == DIMQ_F32 ? 4 : (cb_dtype == DIMQ_F16 || cb_dtype == DIMQ_BF16 ? 2 : 0);
+  if (esz == 0 || !aligned(w, 16) || !aligned(cb, 16) || cb_size < 1 || (cb_size * esz) % 16 != 0) return 0;
+  const size_t limit = std::max<size_t>(band_lds, 80 * 1024);
+  for (int pass = 64; pass >= 8; pass /= 2) {
+    const size_t rows = cb_rows == 1 ? 1 : (size_t)pass;
+    const size_t need = (size_t)KH * np * 64 * 16 + (((size_t)w_bytes + 15) & ~(size_t)15) + rows * cb_size * 4;
+    if (need <= limit) {
+      *lds = std::max(band_lds, need);
+      return pass;
+    }
+  }
+  return 0;
+}
+
 }  // namespace
 
 bool stem_eligible(int64_t C, int64_t OC, int64_t KH, int64_t KW, int64_t sh, int64_t sw, int64_t pw,
                    int64_t dh, int64_t dw, int64_t groups, int64_t OH, int64_t OW, int bits, int x_dtype,
-                   int y_dtype, const void* x, const void* y, int epi_mode_) {
+                   int y_dtype, const void* x, const void* y, int epi_mode_, const void* w, int64_t w_bytes,
+                   const void* cb, int cb_dtype, int64_t cb_rows, int64_t cb_size) {
   if (epi_mode_ != kEpiNone && epi_mode_ != kEpiRelu) return false;  // other epilogues: generic kernel
   if (x_dtype != DIMQ_F16) return false;  // fp16 staging (other dtypes: the guarded generic kernel)
   if (groups != 1 || C < 1 || C > 4 || OC < 1 || OC > 64 || OC % 8 != 0) return false;
@@ -516,7 +592,9 @@ bool stem_eligible(int64_t C, int64_t OC, int64_t KH, int64_t KW, int64_t sh, in
   if (!((KH == 7 && np == 4) || (KH == 3 && np == 2))) return false;
   if (!aligned(x, 4) || !aligned(y, 16)) return false;
   (void)y_dtype;
-  return stem_rows(KH, OH, OW, np) > 0;
+  if (stem_rows(KH, OH, OW, np) <= 0) return false;
+  size_t lds = 0;
+  return stem_cb_pass(KH, np, stem_band_lds(KH, OH, OW, np), w, w_bytes, cb, cb_dtype, cb_rows, cb_size, &lds) > 0;
 }
 
 int launch_conv_stem(const void* x, int x_dtype, int x_layout, int64_t B, int64_t C, int64_t H, int64_t W,
@@ -564,9 +642,9 @@ int launch_conv_stem(const void* x, int x_dtype, int x_layout, int64_t B, int64_
   G = std::max<int64_t>(8, (G + 7) / 8 * 8);
   p.per_xcd = (int)((nbands + 7) / 8);
 
-  const int T = (int)KH * np / 2;
-  const int64_t units = std::max<int64_t>((int64_t)p.IR * p.npairs, 2LL * T * 64);
-  const size_t lds = (size_t)units * 16 + 4 * kStemOutFloats * sizeof(float);
+  size_t lds = 0;
+  p.cb_pass = stem_cb_pass(KH, np, stem_band_lds(KH, OH, OW, np), w, w_bytes, cb, cb_dtype, cb_rows, cb_size, &lds);
+  if (p.cb_pass == 0) return set_error(DIMQ_ERR_UNSUPPORTED, "conv stem kernel: codebook or stream not stageable");
   const bool relu = epi_mode(epi) == kEpiRelu;
   auto k = KH == 7 ? (relu ? conv_stem_kernel<7, 4, kEpiRelu> : conv_stem_kernel<7, 4, kEpiNone>)
                    : (relu ? conv_stem_kernel<3, 2, kEpiRelu> : conv_stem_kernel<3, 2, kEpiNone>);

@@ -1039,7 +1039,8 @@ int launch_prepare(const uint8_t* src, int64_t OC, int64_t C, int64_t KH, int64_
 // conv_stem.hip
 bool stem_eligible(int64_t C, int64_t OC, int64_t KH, int64_t KW, int64_t sh, int64_t sw, int64_t pw,
                    int64_t dh, int64_t dw, int64_t groups, int64_t OH, int64_t OW, int bits, int x_dtype,
-                   int y_dtype, const void* x, const void* y, int epi_mode);
+                   int y_dtype, const void* x, const void* y, int epi_mode, const void* w, int64_t w_bytes,
+                   const void* cb, int cb_dtype, int64_t cb_rows, int64_t cb_size);
 int launch_conv_stem(const void* x, int x_dtype, int x_layout, int64_t B, int64_t C, int64_t H, int64_t W,
                      const uint8_t* w, int64_t w_bytes, int bits, const void* cb, int cb_dtype, int64_t cb_rows,
                      int64_t cb_size, const void* bias, int bias_dtype, int64_t OC, int64_t KH, int64_t KW,

@@ -749,6 +749,13 @@ def test_conv2d_prepared_variants_agree(gpu, variant):
     dict(B=2, C=3, H=33, W=35, OC=32, K=7, p=3, bits=4, dt=torch.float16, out=torch.float16, pc=True),    # odd W
     dict(B=1, C=1, H=31, W=29, OC=16, K=3, p=0, bits=8, dt=torch.float32, out=torch.float32, pc=True),    # fp32 input
     dict(B=2, C=2, H=20, W=18, OC=40, K=7, p=3, bits=8, dt=torch.float16, out=torch.float16, pc=True, cbn=200),
+    # 16-bit codebooks (staged in LDS as floats), a per-layer one, and a packed stream one byte into its
+    # storage (not 16-byte aligned: the generic kernel)
+    dict(B=2, C=3, H=64, W=64, OC=64, K=7, p=3, bits=8, dt=torch.float16, out=torch.float16, pc=True,
+         cbdt=torch.float16),
+    dict(B=1, C=3, H=40, W=44, OC=32, K=7, p=3, bits=4, dt=torch.float16, out=torch.float32, pc=False,
+         cbdt=torch.bfloat16),
+    dict(B=1, C=3, H=30, W=30, OC=64, K=7, p=3, bits=8, dt=torch.float16, out=torch.float16, pc=True, woff=1),
 ])
 @pytest.mark.parametrize("layout", ["nchw", "nhwc"])
 def test_conv2d_stem_vs_oracle(gpu, case, layout):
@@ -761,16 +768,21 @@ def test_conv2d_stem_vs_oracle(gpu, case, layout):
     x = torch.randn(case["B"], case["C"], case["H"], case["W"], generator=g).to(case["dt"])
     cb, idx, packed = _codebook_case(case["OC"], case["C"] * K * K, case["bits"], case["pc"], g,
                                      cb_entries=case.get("cbn"))
+    if case.get("cbdt") is not None:
+        cb = cb.to(case["cbdt"])
     bias = torch.randn(case["OC"], generator=g) * 0.1
     xd = x.to(gpu)
     if layout == "nhwc":
         xd = xd.to(memory_format=torch.channels_last)
-    args = (xd, packed.to(gpu), cb.to(gpu), case["bits"], bias.to(gpu), shape, (2, 2), (pad, pad), (1, 1), 1)
+    pd = packed.to(gpu)
+    if case.get("woff"):
+        pd = torch.cat([torch.zeros(case["woff"], dtype=torch.uint8), packed]).to(gpu)[case["woff"]:]
+    args = (xd, pd, cb.to(gpu), case["bits"], bias.to(gpu), shape, (2, 2), (pad, pad), (1, 1), 1)
     y = ops.dimq_conv2d_codebook(*args, out_dtype=case["out"])
     assert y.dtype == case["out"]
     if layout == "nhwc" and case["C"] > 1:  # a 1-channel input is NCHW- and NHWC-contiguous at once
         assert y.is_contiguous(memory_format=torch.channels_last)
-    ref = oracle.conv2d_dequant_reference(x.float(), packed, case["bits"], cb, shape, bias, 2, pad, 1, 1)
+    ref = oracle.conv2d_dequant_reference(x.float(), packed, case["bits"], cb.float(), shape, bias, 2, pad, 1, 1)
     assert y.shape == ref.shape
     tol = out_tol(case["out"])
     assert oracle.rel_err(y.float(), ref) <= tol, oracle.rel_err(y.float(), ref)

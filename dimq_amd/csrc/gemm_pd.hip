@@ -63,10 +63,10 @@ __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds) {
   asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gptr), "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
 }
 
-constexpr int kPdRows = 2;     // weight rows per predecode work-group
+constexpr int kPdRows = 4;     // weight rows per predecode work-group (2: 10.1 us, 4: 9.3, 8: slower, per ViT-B/16 block)
 constexpr int kPdGroups = 16;  // 8-index groups per thread held in registers (K <= 4096 in one pass)
 
-// Weight rows 2 b, 2 b + 1 -> fp16 in wd, their factors acc_scale 2^-e in rs.
+// Weight rows kPdRows b .. kPdRows b + kPdRows - 1 -> fp16 in wd, their factors acc_scale 2^-e in rs.
 template <int BITS>
 __device__ __forceinline__ void predecode_rows(const uint8_t* __restrict__ w, const void* cb, int cb_dt,
                                                int64_t cb_rows, int cb_size, int64_t N, int64_t K, float acc_scale,

@@ -145,11 +145,13 @@ int launch_prepare_tapmajor(const uint8_t* src, int64_t src_bytes, int64_t OC, i
 
 
 // Tile of the implicit-GEMM conv: 128x128 when that fills every CU, else 64x128.
-// A single 64-wide k stage (K <= 64) also takes 64x128: ResNet-18's layer2
-// downsample (1x1/2, C 64, bs128) 20.3 -> 18.0 us same process; at K 128
-// (layer3's) both tiles measured alike.
+// At most 128 output channels, or a single 64-wide k stage (K <= 64), also
+// take 64x128 (ResNet-18 bs128, same process: layer2 3x3 C 128 56.9 -> 49.8
+// us, with the residual 59.9 -> 52.9; layer2 downsample 1x1/2 C 64 20.3 ->
+// 18.0); at layer3 (N 256) both tiles measured alike, at layer4 (N 512) the
+// 128x128 grid does not fill the CUs and 64x128 is faster (58.3 against 69.4).
 int gemm_conv_tile(int64_t M, int64_t N, int64_t K) {
-  if (K <= 64) return 1;
+  if (K <= 64 || N <= 128) return 1;
   const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
   return t128 >= device_cus() ? 0 : 1;
 }

@@ -508,17 +508,23 @@ struct PdTile<3> {
 //   4: 160 x 256, 10 waves of 32 x 128 (the last of a stage's six 16-byte
 //      loads per lane covers two waves): N 768 as 237 tiles instead of 198
 //      on 256 CUs; proj (K 768) 40.3-41.5 -> 37.9-38.1 us, both launches,
-//      same box; fc2 (K 3072) no faster, its main loop dominating (wave tiles
-//      of 32 x 128 read 1.25 fragments per MFMA against 0.83).
+//      same box; fc2 (K 3072) was first no faster (wave tiles of 32 x 128
+//      read 1.25 fragments per MFMA against 0.83), and with the current
+//      epilogue 81.2 against 84.7 us on tile 2 (ViT-B/16 forward 4.16-4.18
+//      -> 4.14 ms, same box).
 template <>
 struct PdTile<4> {
   static constexpr int WGM = 5, WGN = 2, MBLK = 1, NBLK = 4, S = 2, CH = 8;
 };
 
 // Tiles 0, 2 and 4 stage 64 k at a time (two slots) and need K % 64 == 0.
+// Tile sweep at the ViT-B/16 shapes (M 12,608, fp16 x, 4-bit, one process,
+// both launches): qkv 68.4 us on tile 0 (tiles 1-4: 76.5-81.5), proj 30.7 on
+// tile 4 (30.4 on 2), fc1 110.9 on tile 1 (118.2-129.1), fc2 (K 3072) 81.2 on
+// tile 4 against 84.7 on tile 2.
 int pd_pick_tile(int64_t M, int64_t N, int64_t K) {
   const bool k64 = K % 64 == 0;
-  if (k64 && N % 256 == 0 && N <= 768 && K <= 1024 && M >= 4096) return 4;
+  if (k64 && N % 256 == 0 && N <= 768 && M >= 4096) return 4;
   if (k64 && N % 384 == 0 && N <= 1536) return 2;
   if (N <= 128 || ((M + 127) / 128) * ((N + 255) / 256) < 256) return 3;
   const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);

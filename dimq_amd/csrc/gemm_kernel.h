@@ -371,10 +371,13 @@ __device__ __forceinline__ int load_codebook_row(const GemmArgs& p, int64_t row,
                                                  CodebookRegs<BITS>& lo) {
   constexpr int E = 1 << BITS;
   float c[E];
+  // rows past N read row 0 (always present) and are zeroed: no branch
+  // between the E loads (load_cb_row)
+  load_cb_row<E>(p.cb, p.cb_dt, valid ? row : 0, p.cb_size, c);
   float mx = 0.0f;
 #pragma unroll
   for (int j = 0; j < E; ++j) {
-    c[j] = (valid && j < p.cb_size) ? load_as_float(p.cb, p.cb_dt, row * p.cb_size + j) : 0.0f;
+    c[j] = valid ? c[j] : 0.0f;
     mx = fmaxf(mx, fabsf(c[j]));
   }
   const int e = cb_exponent(mx);
@@ -572,19 +575,42 @@ __global__ __launch_bounds__(256) void gemm_cb8_kernel(const GemmArgs p) {
 
   // codebook rows -> LDS (fp16, scaled by a per-row power of two).  One
   // pass: thread (row r = tid / 4, quarter part) loads its 64 entries back to
-  // back into registers (every load in flight at once), the row maxima meet
-  // in LDS, and the scaled entries go out from the registers.
+  // back into registers, the row maxima meet in LDS, and the scaled entries go
+  // out from the registers.  The dtype is switched on once and rows past N /
+  // entries past cb_size re-load a valid entry and are zeroed by a select, so
+  // no branch separates the 64 loads (a branch around each load makes the
+  // compiler wait for every load before the next: 64 round trips in a row).
   static_assert(ROWS == 64, "one codebook row per 4 threads");
   {
     const int r = tid >> 2, part = tid & 3;
     const int64_t n = n0 + r;
-    const int64_t row = (p.cb_rows == 1) ? 0 : nz + n;
+    const bool live = n < p.N;
+    const int64_t base = ((p.cb_rows == 1) ? 0 : nz + (live ? n : p.N - 1)) * p.cb_size;
+    const int last = p.cb_size - 1;
     float cv[64];
+    if (p.cb_dt == DIMQ_F32) {
+      const float* q = reinterpret_cast<const float*>(p.cb) + base;
 #pragma unroll
-    for (int i = 0; i < 64; ++i) {
-      const int j = part + 4 * i;
-      cv[i] = (n < p.N && j < p.cb_size) ? load_as_float(p.cb, p.cb_dt, row * p.cb_size + j) : 0.0f;
+      for (int i = 0; i < 64; ++i) cv[i] = q[min(part + 4 * i, last)];
+    } else if (p.cb_dt == DIMQ_F16 || p.cb_dt == DIMQ_BF16) {
+      const uint16_t* q = reinterpret_cast<const uint16_t*>(p.cb) + base;
+      uint32_t h[64];
+#pragma unroll
+      for (int i = 0; i < 64; ++i) h[i] = q[min(part + 4 * i, last)];
+      if (p.cb_dt == DIMQ_F16) {
+#pragma unroll
+        for (int i = 0; i < 64; ++i) cv[i] = f16_bits_to_float(h[i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 64; ++i) cv[i] = bf16_bits_to_float(h[i]);
+      }
+    } else {
+      const double* q = reinterpret_cast<const double*>(p.cb) + base;
+#pragma unroll
+      for (int i = 0; i < 64; ++i) cv[i] = static_cast<float>(q[min(part + 4 * i, last)]);
     }
+#pragma unroll
+    for (int i = 0; i < 64; ++i) cv[i] = (live && part + 4 * i <= last) ? cv[i] : 0.0f;
     float mx = 0.0f;
 #pragma unroll
     for (int i = 0; i < 64; ++i) mx = fmaxf(mx, fabsf(cv[i]));

@@ -573,6 +573,49 @@ __global__ __launch_bounds__(256) void gemm_cb8_kernel(const GemmArgs p) {
   const int64_t nz = static_cast<int64_t>(blockIdx.z) * p.N;
   const int64_t cbase = static_cast<int64_t>(blockIdx.z) * p.cICg;
 
+  floatx4 acc[MB][NB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const int64_t nk = (p.K + kKM - 1) / kKM;
+  uint32_t a_st[A_PER_T][8];
+  uint32_t bc[NB][BITS], bn[NB][BITS];
+  uint32_t trk = 0;
+  auto load_a = [&](int64_t kt) {
+#pragma unroll
+    for (int i = 0; i < A_PER_T; ++i) {
+      const int task = tid + 256 * i;
+      if (A_TASKS % 256 == 0 || task < A_TASKS) {
+        const int m = task >> 3, kg = task & 7;
+        load_a_group<BITS, XT, false>(p, m0 + m, kt * kKM + 16 * kg, cbase, a_st[i], trk);
+      }
+    }
+  };
+  auto store_a = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_PER_T; ++i) {
+      const int task = tid + 256 * i;
+      if (A_TASKS % 256 == 0 || task < A_TASKS) {
+        const int m = task >> 3, kg = task & 7;
+        uint4* dst = reinterpret_cast<uint4*>(&As[buf][m * kLDA + 16 * kg]);
+        dst[0] = make_uint4(a_st[i][0], a_st[i][1], a_st[i][2], a_st[i][3]);
+        dst[1] = make_uint4(a_st[i][4], a_st[i][5], a_st[i][6], a_st[i][7]);
+      }
+    }
+  };
+  auto load_b = [&](int64_t kt, uint32_t (&dst)[NB][BITS]) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+      load_b_chunk<BITS>(p, nw0 + nb * 16 + col, nz + nw0 + nb * 16 + col, kt * kKM + 32 * g, dst[nb]);
+  };
+
+  // the first k tile is requested before the codebook rows, so both are in
+  // flight together
+  load_a(0);
+  load_b(0, bc);
+
   // codebook rows -> LDS (fp16, scaled by a per-row power of two).  One
   // pass: thread (row r = tid / 4, quarter part) loads its 64 entries back to
   // back into registers, the row maxima meet in LDS, and the scaled entries go
@@ -622,57 +665,16 @@ __global__ __launch_bounds__(256) void gemm_cb8_kernel(const GemmArgs p) {
     for (int i = 0; i < 64; ++i) cbs[r * 256 + part + 4 * i] = (uint16_t)float_to_f16_bits(ldexpf(cv[i], e));
     if (part == 0) rscale[r] = ldexpf(p.acc_scale, -e);
   }
-
-  floatx4 acc[MB][NB];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-
-  const int64_t nk = (p.K + kKM - 1) / kKM;
-  uint32_t a_st[A_PER_T][8];
-  uint32_t bc[NB][BITS], bn[NB][BITS];
-  uint32_t trk = 0;
-  auto load_a = [&](int64_t kt) {
-#pragma unroll
-    for (int i = 0; i < A_PER_T; ++i) {
-      const int task = tid + 256 * i;
-      if (A_TASKS % 256 == 0 || task < A_TASKS) {
-        const int m = task >> 3, kg = task & 7;
-        load_a_group<BITS, XT, false>(p, m0 + m, kt * kKM + 16 * kg, cbase, a_st[i], trk);
-      }
-    }
-  };
-  auto store_a = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < A_PER_T; ++i) {
-      const int task = tid + 256 * i;
-      if (A_TASKS % 256 == 0 || task < A_TASKS) {
-        const int m = task >> 3, kg = task & 7;
-        uint4* dst = reinterpret_cast<uint4*>(&As[buf][m * kLDA + 16 * kg]);
-        dst[0] = make_uint4(a_st[i][0], a_st[i][1], a_st[i][2], a_st[i][3]);
-        dst[1] = make_uint4(a_st[i][4], a_st[i][5], a_st[i][6], a_st[i][7]);
-      }
-    }
-  };
-  auto load_b = [&](int64_t kt, uint32_t (&dst)[NB][BITS]) {
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-      load_b_chunk<BITS>(p, nw0 + nb * 16 + col, nz + nw0 + nb * 16 + col, kt * kKM + 32 * g, dst[nb]);
-  };
-
-  load_a(0);
   store_a(0);
-  load_b(0, bc);
   __syncthreads();
 
   for (int64_t kt = 0; kt < nk; ++kt) {
     const int buf = static_cast<int>(kt & 1);
-    const bool more = kt + 1 < nk;
-    if (more) {
-      load_a(kt + 1);
-      load_b(kt + 1, bn);
-    }
+    // the next tile's loads are issued unconditionally (the last trip
+    // re-reads its own tile into the unused buffer): no branch around them
+    const int64_t kn = kt + 1 < nk ? kt + 1 : kt;
+    load_a(kn);
+    load_b(kn, bn);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       half8 bf[NB];
@@ -695,13 +697,11 @@ __global__ __launch_bounds__(256) void gemm_cb8_kernel(const GemmArgs p) {
         for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = mfma16x16x32(af, bf[nb], acc[mb][nb]);
       }
     }
-    if (more) {
-      store_a(buf ^ 1);
+    store_a(buf ^ 1);
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
+    for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-        for (int w = 0; w < BITS; ++w) bc[nb][w] = bn[nb][w];
-    }
+      for (int w = 0; w < BITS; ++w) bc[nb][w] = bn[nb][w];
     __syncthreads();
   }
 

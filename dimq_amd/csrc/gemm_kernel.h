@@ -487,11 +487,11 @@ __global__ __launch_bounds__(256) void gemm_cb_kernel(const GemmArgs p) {
 
   for (int64_t kt = 0; kt < nk; ++kt) {
     const int buf = static_cast<int>(kt & 1);
-    const bool more = kt + 1 < nk;
-    if (more) {
-      load_a(kt + 1);
-      load_b(kt + 1, bn);
-    }
+    // the next tile's loads are issued unconditionally (the last trip
+    // re-reads its own tile into the unused buffer): no branch around them
+    const int64_t kn = kt + 1 < nk ? kt + 1 : kt;
+    load_a(kn);
+    load_b(kn, bn);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       half8 bf[NB][NCB];
@@ -508,13 +508,11 @@ __global__ __launch_bounds__(256) void gemm_cb_kernel(const GemmArgs p) {
           for (int c = 0; c < NCB; ++c) acc[mb][nb] = mfma16x16x32(af, bf[nb][c], acc[mb][nb]);
       }
     }
-    if (more) {
-      store_a(buf ^ 1);
+    store_a(buf ^ 1);
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
+    for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-        for (int w = 0; w < BITS; ++w) bc[nb][w] = bn[nb][w];
-    }
+      for (int w = 0; w < BITS; ++w) bc[nb][w] = bn[nb][w];
     __syncthreads();
   }
 
